@@ -1,0 +1,228 @@
+"""Benchmark of the MI355X weight-heavy decode path.
+
+One "step" is the RMSNorm(3072) + Q5_K QKV GEMV (5120x3072) + Q6_K FFN-down
+GEMV (3072x8192) workload at batch 1, over seeded synthetic inputs resident
+in HBM.  Consecutive steps rotate through `--copies` distinct copies of the
+two weight matrices (32 x 31.5 MB by default), so every step streams its
+weights from HBM rather than from the 256 MB Infinity Cache.  The timed
+steps are one HIP graph replay bracketed by a device sync and HIP events on
+the library's stream.
+
+Printed: one JSON line with value = algorithmic bytes / time in GB/s, the
+roofline of the dominant kernel (the Q6_K GEMV, timed alone the same way),
+a CPU baseline (the oracle's composed dequant+dot path on the host cores,
+bounded sample) and the other workloads under "extra".
+
+    python bench.py [--gpus 1] [--steps 1280] [--warmup 128] [--no-cpu] [--no-sweep]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "recursive-routing-racer-rs_amd")
+for _p in (REPO, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+import rrr_hip  # noqa: E402
+from rrr_hip import synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+D, QKV, FFN = 3072, 5120, 8192
+SEED = 2  # configs are seeded 1..5; this is the second one
+
+# Algorithmic bytes (raw GGUF weight bytes + activations once).
+B_NORM = 3 * D * 4                                         # 36,864
+B_QKV = rrr_hip.tensor_bytes(rrr_hip.Q5_K, D, QKV) + D * 4 + QKV * 4   # 10,846,208
+B_DOWN = rrr_hip.tensor_bytes(rrr_hip.Q6_K, FFN, D) + FFN * 4 + D * 4  # 20,688,896
+B_STEP = B_NORM + B_QKV + B_DOWN                            # 31,571,968
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed_graph(ctx, record, n):
+    """Capture `record(i)` for i < n as one graph, replay it once untimed and
+    once timed; returns milliseconds of the timed replay."""
+    ctx.graph_begin()
+    for i in range(n):
+        record(i)
+    g = ctx.graph_end()
+    g.launch()
+    ctx.sync()
+    ctx.timer_start()
+    g.launch()
+    ms = ctx.timer_stop()
+    g.destroy()
+    return ms
+
+
+class Config2:
+    """RMSNorm + Q5_K QKV GEMV + Q6_K down GEMV (batch 1)."""
+
+    def __init__(self, ctx, copies):
+        self.ctx, self.copies = ctx, copies
+        self.wq = [ctx.weight_upload(rrr_hip.Q5_K, D, QKV, synth.weight(SEED, 10 + c, rrr_hip.Q5_K, D, QKV))
+                   for c in range(copies)]
+        self.wd = [ctx.weight_upload(rrr_hip.Q6_K, FFN, D, synth.weight(SEED, 100 + c, rrr_hip.Q6_K, FFN, D))
+                   for c in range(copies)]
+        self.x = ctx.to_device(synth.normal_f32(SEED, 1, D))
+        self.g = ctx.to_device(synth.normal_f32(SEED, 2, D, 1.0, 0.1))
+        self.x2 = ctx.to_device(synth.normal_f32(SEED, 3, FFN))
+        self.normed = ctx.alloc(D * 4)
+        self.qkv = ctx.alloc(QKV * 4)
+        self.down = ctx.alloc(D * 4)
+
+    def step(self, i):
+        c = self.ctx
+        c.rmsnorm(self.x, self.g, self.normed, 1, D, 1e-5)
+        c.gemv(self.normed, self.wq[i % self.copies], rrr_hip.Q5_K, self.qkv, D, QKV)
+        c.gemv(self.x2, self.wd[i % self.copies], rrr_hip.Q6_K, self.down, FFN, D)
+
+    def q6k_only(self, i):
+        self.ctx.gemv(self.x2, self.wd[i % self.copies], rrr_hip.Q6_K, self.down, FFN, D)
+
+    def q5k_only(self, i):
+        self.ctx.gemv(self.normed, self.wq[i % self.copies], rrr_hip.Q5_K, self.qkv, D, QKV)
+
+    def norm_only(self, i):
+        self.ctx.rmsnorm(self.x, self.g, self.normed, 1, D, 1e-5)
+
+
+def cpu_baseline(budget_s=12.0):
+    """The oracle's composed dequant+dot path (restated phi4.rs formulas,
+    rows split over threads like rayon par_chunks) on this host, one config-2
+    step at a time, until `budget_s` seconds of work or 200 steps."""
+    import oracle.oracle as orc
+    threads = max(1, min(16, os.cpu_count() or 1))
+    wq = synth.weight(SEED, 10, rrr_hip.Q5_K, D, QKV)
+    wd = synth.weight(SEED, 100, rrr_hip.Q6_K, FFN, D)
+    x = synth.normal_f32(SEED, 1, D)
+    g = synth.normal_f32(SEED, 2, D, 1.0, 0.1)
+    x2 = synth.normal_f32(SEED, 3, FFN)
+
+    def one(th):
+        n = orc.rms_norm(x, g)
+        orc.gemv(rrr_hip.Q5_K, wq, n, D, QKV, 1, th)
+        orc.gemv(rrr_hip.Q6_K, wd, x2, FFN, D, 1, th)
+
+    res = {}
+    for th, budget in ((threads, budget_s * 0.75), (1, budget_s * 0.25)):
+        one(th)
+        times, t_end = [], time.perf_counter() + budget
+        while time.perf_counter() < t_end and len(times) < 200:
+            t0 = time.perf_counter()
+            one(th)
+            times.append(time.perf_counter() - t0)
+        res[th] = (float(np.median(times)), len(times))
+    med, n = res[threads]
+    med1, n1 = res[1]
+    return {
+        "value": round(B_STEP / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"median of {n} config-2 steps (RMSNorm 3072 + Q5_K 5120x3072 + Q6_K 3072x8192 GEMV) "
+                  f"on {threads} host threads; same weights each step",
+        "ms_per_step": round(med * 1e3, 3),
+        "single_thread": {"value": round(B_STEP / med1 / 1e9, 3), "unit": "GB/s", "ms_per_step": round(med1 * 1e3, 3),
+                          "steps": n1},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1280)
+    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--copies", type=int, default=32)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the decode path is single-device; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    ctx = rrr_hip.Context(0)
+    ctx.set_async(True)
+    log(f"[bench] generating config-2 inputs, {args.copies} weight copies")
+    cfg = Config2(ctx, args.copies)
+    ctx.sync()
+
+    # warmup: W untimed steps
+    ctx.graph_begin()
+    for i in range(args.warmup):
+        cfg.step(i)
+    warm = ctx.graph_end()
+    warm.launch()
+    ctx.sync()
+    warm.destroy()
+
+    # timed: exactly K steps in one graph, bracketed by a sync and HIP events
+    ctx.graph_begin()
+    for i in range(args.steps):
+        cfg.step(i)
+    timed = ctx.graph_end()
+    ctx.sync()
+    ctx.timer_start()
+    timed.launch()
+    ms = ctx.timer_stop()
+    ctx.sync()
+    timed.destroy()
+    ms_step = ms / args.steps
+    value = B_STEP / (ms_step * 1e-3) / 1e9
+    log(f"[bench] config 2: {ms_step * 1e3:.2f} us/step, {value:.1f} GB/s")
+
+    # dominant kernel alone, same rotation: average launch duration
+    n_k = args.steps
+    ms_q6 = timed_graph(ctx, cfg.q6k_only, n_k) / n_k
+    ms_q5 = timed_graph(ctx, cfg.q5k_only, n_k) / n_k
+    ms_nm = timed_graph(ctx, cfg.norm_only, n_k) / n_k
+    ach = B_DOWN / (ms_q6 * 1e-3) / 1e9
+    log(f"[bench] q6k gemv {ms_q6 * 1e3:.2f} us ({ach:.0f} GB/s); q5k gemv {ms_q5 * 1e3:.2f} us; "
+        f"rmsnorm {ms_nm * 1e3:.2f} us")
+
+    extra = {
+        "q6k_gemv_3072x8192": {"us": round(ms_q6 * 1e3, 3), "GBs": round(ach, 1),
+                               "frac_hbm": round(ach / HBM_PEAK_GBS, 4), "bytes": B_DOWN},
+        "q5k_gemv_5120x3072": {"us": round(ms_q5 * 1e3, 3), "GBs": round(B_QKV / (ms_q5 * 1e-3) / 1e9, 1),
+                               "frac_hbm": round(B_QKV / (ms_q5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": B_QKV},
+        "rmsnorm_3072": {"us": round(ms_nm * 1e3, 3), "bytes": B_NORM},
+    }
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline()
+
+    out = {
+        "metric": "K-quant GEMV GB/s (% of HBM peak); decode ms/token, Phi-4-mini shape",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded splitmix64: K-quant blocks per the config recipe, N(0,1) activations)",
+        "config": {"workload": "rmsnorm_3072 + q5k_gemv_5120x3072 + q6k_gemv_3072x8192, batch 1",
+                   "weight_copies": args.copies, "bytes_per_step": B_STEP, "seed": SEED},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_kernel<DecQ6K> 3072x8192", "bytes_per_launch": B_DOWN},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,266 @@
+/*
+ * rrr_hip.h -- C ABI of librrr_hip.so, the MI355X (gfx950) replacement for the
+ * reference's Vulkan compute engine on the weight-heavy decode path.
+ *
+ * The reference host (src/model/phi4.rs) reaches the GPU only through
+ * ComputeEngine / GpuBuffer / DescSetHandle (src/gpu/mod.rs:3).  Every entry
+ * point below names the reference interface it replaces.  All functions:
+ *   - return an int status (RRR_OK = 0, negative on error) and never abort;
+ *   - validate every argument before any HIP call, so the error paths run on a
+ *     machine without a GPU;
+ *   - record a human-readable message retrievable with rrr_last_error()
+ *     (thread-local).
+ *
+ * Weights are the raw GGUF bytes uploaded unchanged (no host repack):
+ * N rows of K/256 super-blocks, row n's blocks contiguous (GGUF ne0 = K inner,
+ * ne1 = N rows; phi4.rs:748-749).  Activations and outputs are f32 row-major
+ * per token, as in phi4.rs:1236-1238.
+ *
+ * Threading: one context = one HIP stream.  A context must not be used from
+ * two threads at once (the reference engine has the same restriction: one
+ * shared command buffer and fence, engine.rs:21-23).  By default every call
+ * that launches work waits for it before returning, matching the reference's
+ * submit + wait_for_fences on every dispatch (engine.rs:312, :369, :470,
+ * :550).  rrr_set_async(ctx, 1) turns that off; rrr_sync() then waits.
+ */
+#ifndef RRR_HIP_H
+#define RRR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RRR_ABI_VERSION 1
+
+typedef enum rrr_status {
+    RRR_OK = 0,
+    RRR_ERR_INVALID_ARG = -1,  /* bad size, count, flag or range */
+    RRR_ERR_BAD_TYPE = -2,     /* ggml type not in {0, 12, 13, 14} */
+    RRR_ERR_BAD_SHAPE = -3,    /* K % 256 != 0 for a K-quant, zero dims, ... */
+    RRR_ERR_SHORT_BUFFER = -4, /* a buffer is smaller than the op reads/writes */
+    RRR_ERR_NULL = -5,         /* null handle or pointer */
+    RRR_ERR_HIP = -6,          /* a HIP runtime call failed */
+    RRR_ERR_UNSUPPORTED = -7,  /* pipeline name or shape this build does not run */
+    RRR_ERR_NO_DEVICE = -8,    /* no such HIP device */
+    RRR_ERR_STATE = -9,        /* call not allowed in the context's state */
+    RRR_ERR_STALE = -10        /* handle already destroyed */
+} rrr_status;
+
+/* GGUF tensor types on the path (gguf.rs:179, :187-189). */
+typedef enum rrr_ggml_type {
+    RRR_TYPE_F32 = 0,
+    RRR_TYPE_Q4_K = 12,
+    RRR_TYPE_Q5_K = 13,
+    RRR_TYPE_Q6_K = 14
+} rrr_ggml_type;
+
+/* Logits weight layouts. */
+typedef enum rrr_logits_layout {
+    RRR_LOGITS_ROWS = 0,    /* E[v][d], V rows of K f32 (token_embd order) */
+    RRR_LOGITS_CHUNKED = 1  /* reference chunks: B_c[d*n + v] = E[(c*chunk+v)*K + d]
+                               (phi4.rs:874-893), chunks back to back */
+} rrr_logits_layout;
+
+typedef struct rrr_ctx rrr_ctx;
+typedef struct rrr_buf rrr_buf;
+typedef struct rrr_graph rrr_graph;
+
+/* ---- engine lifetime ------------------------------------------------- */
+
+/* Replaces ComputeEngine::new (engine.rs:49-128): picks HIP device `device`
+ * (the reference always takes pdevices[0], engine.rs:62-63) and creates the
+ * context's stream.  device == RRR_DEVICE_NONE creates a validation-only
+ * context: buffers are placeholders with a size and no memory, every call
+ * validates its arguments as usual and then returns RRR_ERR_NO_DEVICE instead
+ * of touching a GPU. */
+#define RRR_DEVICE_NONE (-1)
+int rrr_init(int device, rrr_ctx **out);
+/* Replaces Drop for ComputeEngine (engine.rs:557-579): waits for the device,
+ * frees every buffer and graph still owned by the context. */
+int rrr_destroy(rrr_ctx *ctx);
+/* Thread-local text of the last error ("" if none). */
+const char *rrr_last_error(void);
+int rrr_abi_version(void);
+/* Number of HIP devices visible (0 when there is no GPU); never fails. */
+int rrr_device_count(void);
+
+/* ---- buffers --------------------------------------------------------- */
+
+/* Replaces ComputeEngine::alloc_buffer (engine.rs:200-229).  The reference
+ * allocates host-visible mapped memory; here buffers live in device HBM,
+ * 256-byte aligned, and data moves with rrr_buf_upload / rrr_buf_download. */
+int rrr_buf_alloc(rrr_ctx *ctx, uint64_t bytes, rrr_buf **out);
+/* A view of [offset, offset+bytes) of `parent`; it shares the parent's memory
+ * and must not outlive it.  Used where the reference binds sub-ranges. */
+int rrr_buf_view(rrr_ctx *ctx, rrr_buf *parent, uint64_t offset, uint64_t bytes, rrr_buf **out);
+/* Frees a buffer or view (the reference only frees pooled buffers at Drop,
+ * engine.rs:557-566). */
+int rrr_buf_free(rrr_ctx *ctx, rrr_buf *buf);
+/* Size in bytes (GpuBuffer.capacity, engine.rs:42); 0 for a null handle. */
+uint64_t rrr_buf_size(const rrr_buf *buf);
+/* Replaces upload / upload_bytes (phi4.rs:616-622): memcpy into .mapped. */
+int rrr_buf_upload(rrr_ctx *ctx, rrr_buf *buf, uint64_t offset, const void *src, uint64_t bytes);
+/* Replaces download (phi4.rs:624-626) and the zero-copy reads of mapped
+ * logits (phi4.rs:1178, :1190). */
+int rrr_buf_download(rrr_ctx *ctx, const rrr_buf *buf, uint64_t offset, void *dst, uint64_t bytes);
+/* Fills bytes [offset, offset+bytes) with a 32-bit pattern (offset and bytes
+ * multiples of 4).  Uses a kernel, never hipMemset, so it may be captured. */
+int rrr_buf_fill_u32(rrr_ctx *ctx, rrr_buf *buf, uint64_t offset, uint64_t bytes, uint32_t value);
+
+/* ---- weights --------------------------------------------------------- */
+
+/* Bytes of an N x K tensor of `type`: N * (K/256) * {144,176,210} for the
+ * K-quants (gguf.rs:187-189), N * K * 4 for F32.  Returns 0 for an invalid
+ * type or K. */
+uint64_t rrr_tensor_bytes(uint32_t type, uint32_t K, uint32_t N);
+/* Replaces load_weight_gpu (phi4.rs:744-771) without its repack step
+ * (phi4.rs:752-755): the raw GGUF bytes are copied to HBM unchanged.
+ * Checks type, K % 256 == 0 for K-quants and bytes >= rrr_tensor_bytes(). */
+int rrr_weight_upload(rrr_ctx *ctx, uint32_t type, uint32_t K, uint32_t N, const void *raw,
+                      uint64_t bytes, rrr_buf **out);
+
+/* ---- typed ops (each a single kernel launch on the context stream) --- */
+
+/* Dequantize n_elements (multiple of 256) of raw `type` blocks to f32,
+ * bit-exact with dequant_q4_k / dequant_q5_k / dequant_q6_k
+ * (phi4.rs:444-542) and dequant_tensor_f32 (phi4.rs:572-587). */
+int rrr_dequant(rrr_ctx *ctx, uint32_t type, const rrr_buf *W, rrr_buf *out, uint64_t n_elements);
+
+/* Y[m][n] = sum_k X[m][k] * W[n][k] for m < M, n < N.
+ * M == 1 replaces matmul_q{4,5,6}k / matmul_gpuq{4,5,6} (push [K, N], grid
+ * [N,1,1]; phi4.rs:631-658, :1081-1096) and matmul_tiled for F32 weights
+ * (phi4.rs:641-646).  M > 1 replaces matmul_gpuq*_batch (push [K, N, M],
+ * grid [N, M, 1]; phi4.rs:1257-1268, :1346-1391).  type 0 means F32 W stored
+ * row-major N x K. */
+int rrr_gemv(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t type, rrr_buf *Y,
+             uint32_t K, uint32_t N, uint32_t M);
+
+/* Y[m][n] = sum_k float(X_bf16[m][k]) * W[n][k]: the prefill dequant-GEMM
+ * (MFMA, fp16 tiles, fp32 accumulate).  No reference counterpart exists for the
+ * MFMA kernel; its call shape is the batched one above with X in bf16. */
+int rrr_gemm_bf16(rrr_ctx *ctx, const rrr_buf *X_bf16, const rrr_buf *W, uint32_t type,
+                  rrr_buf *Y, uint32_t K, uint32_t N, uint32_t M);
+
+/* y[r] = (gamma * x[r]) / sqrt(mean(x[r]^2) + eps) for r < rows.
+ * Replaces the rmsnorm pipeline (push [rows, d]; phi4.rs:1006, :1043-1047;
+ * CPU twin rms_norm phi4.rs:593-599 with eps RMS_EPS = 1e-5, :111). */
+int rrr_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, rrr_buf *y,
+                uint32_t rows, uint32_t d, float eps);
+
+/* mid[r][i] = silu(gu[r][i]) * gu[r][F + i]: replaces silu_gate (push [F];
+ * phi4.rs:1028-1029; CPU twin :1369-1373). */
+int rrr_silu_gate(rrr_ctx *ctx, const rrr_buf *gate_up, rrr_buf *mid, uint32_t rows, uint32_t F);
+
+/* out = a + b over n floats (out may alias a): replaces residual_add
+ * (push [d]; phi4.rs:1023, :1033; CPU twin elemwise_add :608-610). */
+int rrr_residual_add(rrr_ctx *ctx, const rrr_buf *a, const rrr_buf *b, rrr_buf *out, uint32_t n);
+
+/* logits[v] = sum_d x[d] * E[v][d] for v < V in one launch.  Replaces the
+ * chunked matmul_tiled logit dispatches (phi4.rs:1049-1064, :1416-1434):
+ * layout RRR_LOGITS_CHUNKED accepts the reference's transposed chunks of
+ * `chunk` rows (8192 in the reference) back to back, RRR_LOGITS_ROWS the
+ * untransposed E. */
+int rrr_logits_f32(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *E, rrr_buf *logits, uint32_t K,
+                   uint32_t V, uint32_t layout, uint32_t chunk);
+
+/* Index of the largest logit (first on ties, NaN never wins), written as a
+ * u32 to out_index: replaces the CPU argmax over the mapped logit chunks
+ * (phi4.rs:1172-1183). */
+int rrr_argmax_f32(rrr_ctx *ctx, const rrr_buf *logits, uint32_t V, rrr_buf *out_index);
+
+/* ---- fused decode-sweep ops (the four launches per layer) ------------ */
+
+/* Y = W . rmsnorm(x, gamma, eps): RMSNorm folded into the GEMV's activation
+ * staging (the reference registers fused_norm_matmul_q{4,5,6}k, phi4.rs:725-727,
+ * but never dispatches them).  Y is bit-identical to rrr_rmsnorm followed by
+ * rrr_gemv. */
+int rrr_gemv_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps,
+                     const rrr_buf *W, uint32_t type, rrr_buf *Y, uint32_t K, uint32_t N);
+/* hidden[n] += sum_k act(x)[k] * W[n][k] (residual_add folded into the GEMV's
+ * epilogue, phi4.rs:1020-1023 and :1030-1033).  act_kind:
+ *   RRR_ACT_IDENTITY  act(x) = x[0..K)
+ *   RRR_ACT_SILU_GATE act(x)[k] = silu(x[k]) * x[K + k]   (silu_gate, :1028-1029)
+ *   RRR_ACT_GQA_V     act(x)[k] = x[K + K/hpk + (k / (hd*hpk))*hd + k % hd], the
+ *                     output of single-query GQA attention at position 0 (the
+ *                     softmax over one key is 1, so head h returns V of kv head
+ *                     h / hpk); x is the fused QKV vector [q(K) | k(K/hpk) | v(K/hpk)].
+ *                     act_param = hd | (hpk << 16), hd % 16 == 0.
+ * act_param is ignored for the other kinds. */
+enum { RRR_ACT_IDENTITY = 0, RRR_ACT_SILU_GATE = 1, RRR_ACT_GQA_V = 2 };
+int rrr_gemv_residual(rrr_ctx *ctx, const rrr_buf *x, uint32_t act_kind, uint32_t act_param,
+                      const rrr_buf *W, uint32_t type, rrr_buf *hidden, uint32_t K, uint32_t N);
+/* logits = E . rmsnorm(x, gamma, eps), E in RRR_LOGITS_ROWS or CHUNKED. */
+int rrr_logits_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps,
+                       const rrr_buf *E, rrr_buf *logits, uint32_t K, uint32_t V, uint32_t layout,
+                       uint32_t chunk);
+
+/* ---- name-keyed dispatch shim ---------------------------------------- */
+
+/* Replaces dispatch_by_name (engine.rs:476-486) for the reference's pipelines,
+ * with their exact binding order and little-endian u32 push layouts:
+ *   matmul_q4k/q5k/q6k, matmul_gpuq4/5/6  bufs [x, W, y],  push [K, N]
+ *   matmul_gpuq{4,5,6}_batch              bufs [X, W, Y],  push [K, N, M]
+ *   matmul_tiled                          bufs [A, B, C],  push [M, K, N]
+ *     (B is K x N row-major, as the logit chunks are; phi4.rs:886)
+ *   rmsnorm                               bufs [x, g, y],  push [rows, d]
+ *   silu_gate                             bufs [gu, mid],  push [F]
+ *   residual_add                          bufs [a, b, out], push [d]
+ * The matmul_gpuq* names take RAW GGUF bytes here (the repack is gone) with
+ * the type implied by the name.  The grid argument is accepted for call-shape
+ * compatibility and checked against the push constants; launch geometry is
+ * chosen by the library.  Unknown names and the out-of-scope pipelines
+ * (rope, rope_kv_store, kv_store, attention) return RRR_ERR_UNSUPPORTED.
+ * rmsnorm uses eps = 1e-5, baked in as the reference's shader does. */
+int rrr_dispatch(rrr_ctx *ctx, const char *name, rrr_buf *const *bufs, uint32_t n_bufs,
+                 const void *push, uint32_t push_bytes, const uint32_t groups[3]);
+
+/* One entry of a dispatch batch: replaces the tuples of
+ * dispatch_batch_persistent_v2 (engine.rs:317-370) / dispatch_batch
+ * (engine.rs:380-386).  `barrier` is accepted for shape compatibility; every
+ * launch on the context stream is ordered after the previous one. */
+typedef struct rrr_dispatch_desc {
+    const char *name;
+    rrr_buf *const *bufs;
+    uint32_t n_bufs;
+    const void *push;
+    uint32_t push_bytes;
+    uint32_t groups[3];
+    uint32_t barrier;
+} rrr_dispatch_desc;
+/* Launches all entries in order, then waits once (one "submit"). */
+int rrr_dispatch_batch(rrr_ctx *ctx, const rrr_dispatch_desc *descs, uint32_t n);
+
+/* ---- HIP graphs (replace the pre-built mega-batch table) ------------- */
+
+/* Between rrr_graph_begin and rrr_graph_end every op above is recorded into a
+ * HIP graph instead of run (no waits inside).  rrr_graph_launch replays it,
+ * the MI355X counterpart of replaying mega_dispatches through
+ * dispatch_batch_persistent_v2 (phi4.rs:972-1064, :1163-1168). */
+int rrr_graph_begin(rrr_ctx *ctx);
+int rrr_graph_end(rrr_ctx *ctx, rrr_graph **out);
+int rrr_graph_launch(rrr_ctx *ctx, rrr_graph *g);
+int rrr_graph_destroy(rrr_ctx *ctx, rrr_graph *g);
+
+/* ---- synchronisation and timing -------------------------------------- */
+
+int rrr_set_async(rrr_ctx *ctx, int async);
+int rrr_sync(rrr_ctx *ctx);
+/* HIP events recorded on the context stream; elapsed milliseconds between the
+ * last rrr_timer_start and rrr_timer_stop (waits for the stop event). */
+int rrr_timer_start(rrr_ctx *ctx);
+int rrr_timer_stop(rrr_ctx *ctx, float *ms);
+
+/* ---- one-call helper ---------------------------------------------------- */
+
+/* Mirror of gpu_matmul_kquant (phi4.rs:631-658): upload a[K] into buf_a, run
+ * the GEMV against weight_buf, download c[N] from buf_c. */
+int rrr_matmul_kquant(rrr_ctx *ctx, rrr_buf *buf_a, const rrr_buf *weight_buf, rrr_buf *buf_c,
+                      uint32_t type, const float *a, float *c, uint32_t K, uint32_t N);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

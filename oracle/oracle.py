@@ -1,0 +1,175 @@
+"""ctypes wrapper of liboracle.so -- TEST INFRASTRUCTURE ONLY.
+
+The CPU oracle restates the reference's CPU formulas (src/model/phi4.rs);
+see rrr_oracle.h for the function-by-function citations and the checks that
+pin each function.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module, and only as the checker.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_u32 = ctypes.c_uint32
+_sz = ctypes.c_size_t
+
+_SIG = {
+    "rrr_o_block_bytes": (_u32, [_u32]),
+    "rrr_o_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "rrr_o_bf16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+    "rrr_o_scale_min_k4": (None, [ctypes.c_int, _u8p, _u8p, _u8p]),
+    "rrr_o_dequant": (ctypes.c_int, [_u32, _u8p, _sz, _f32p]),
+    "rrr_o_repack_q4k": (None, [_u8p, _sz, _u8p]),
+    "rrr_o_repack_q5k": (None, [_u8p, _sz, _u8p]),
+    "rrr_o_repack_q6k": (None, [_u8p, _sz, _u8p]),
+    "rrr_o_dequant_gpuq4": (None, [_u8p, _sz, _f32p]),
+    "rrr_o_dequant_gpuq5": (None, [_u8p, _sz, _f32p]),
+    "rrr_o_dequant_gpuq6": (None, [_u8p, _sz, _f32p]),
+    "rrr_o_rms_norm_rows": (None, [_f32p, _f32p, _f32p, _sz, _sz, ctypes.c_float]),
+    "rrr_o_silu_gate": (None, [_f32p, _f32p, _sz, _sz]),
+    "rrr_o_residual_add": (None, [_f32p, _f32p, _f32p, _sz]),
+    "rrr_o_gemv": (ctypes.c_int, [_u32, _u8p, _f32p, _f32p, _u32, _u32, _u32, ctypes.c_int]),
+    "rrr_o_gemv_f64": (ctypes.c_int, [_u32, _u8p, _f32p, _f64p, _u32, _u32, _u32, ctypes.c_int]),
+    "rrr_o_logits_f32": (ctypes.c_int, [_f32p, _f32p, _f32p, _u32, _u32, _u32, _u32, ctypes.c_int]),
+    "rrr_o_logits_f64": (ctypes.c_int, [_f32p, _f32p, _f64p, _u32, _u32, _u32, _u32, ctypes.c_int]),
+    "rrr_o_logits_chunk_build": (None, [_f32p, _u32, _u32, _u32, _f32p]),
+}
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        l = ctypes.CDLL(LIB)
+        for name, (res, args) in _SIG.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t)
+
+
+def block_bytes(qtype):
+    return int(lib().rrr_o_block_bytes(qtype))
+
+
+def f16_to_f32(bits):
+    return lib().rrr_o_f16_to_f32(int(bits))
+
+
+def scale_min_k4(j, q12):
+    q = np.ascontiguousarray(q12, dtype=np.uint8)
+    sc, mn = ctypes.c_uint8(), ctypes.c_uint8()
+    lib().rrr_o_scale_min_k4(j, _p(q, _u8p), ctypes.byref(sc), ctypes.byref(mn))
+    return sc.value, mn.value
+
+
+def dequant(qtype, raw, n):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    if lib().rrr_o_dequant(qtype, _p(raw, _u8p), n, _p(out, _f32p)) != 0:
+        raise ValueError(f"type {qtype}")
+    return out
+
+
+_REPACK = {12: ("rrr_o_repack_q4k", "rrr_o_dequant_gpuq4", 192),
+           13: ("rrr_o_repack_q5k", "rrr_o_dequant_gpuq5", 320),
+           14: ("rrr_o_repack_q6k", "rrr_o_dequant_gpuq6", 320)}
+
+
+def dequant_via_repack(qtype, raw, n):
+    """Dequantize through the reference's repacked GPU layout (phi4.rs:278-436)."""
+    rp, rd, bs = _REPACK[qtype]
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    rep = np.zeros(n // 256 * bs, dtype=np.uint8)
+    getattr(lib(), rp)(_p(raw, _u8p), n, _p(rep, _u8p))
+    out = np.empty(n, dtype=np.float32)
+    getattr(lib(), rd)(_p(rep, _u8p), n, _p(out, _f32p))
+    return out
+
+
+def rms_norm(x, w, eps=1e-5):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    d = w.shape[0]
+    out = np.empty_like(x)
+    lib().rrr_o_rms_norm_rows(_p(x, _f32p), _p(w, _f32p), _p(out, _f32p), x.size // d, d, eps)
+    return out
+
+
+def silu_gate(gu, F):
+    gu = np.ascontiguousarray(gu, dtype=np.float32)
+    rows = gu.size // (2 * F)
+    out = np.empty(rows * F, dtype=np.float32)
+    lib().rrr_o_silu_gate(_p(gu, _f32p), _p(out, _f32p), rows, F)
+    return out
+
+
+def residual_add(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out = np.empty_like(a)
+    lib().rrr_o_residual_add(_p(a, _f32p), _p(b, _f32p), _p(out, _f32p), a.size)
+    return out
+
+
+def gemv(qtype, W, X, K, N, M=1, threads=1, f64=False):
+    """Y[M, N] from raw W (N x K of qtype) and X[M, K]."""
+    W = np.ascontiguousarray(W).view(np.uint8)
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    if f64:
+        Y = np.empty(M * N, dtype=np.float64)
+        rc = lib().rrr_o_gemv_f64(qtype, _p(W, _u8p), _p(X, _f32p), _p(Y, _f64p), K, N, M, threads)
+    else:
+        Y = np.empty(M * N, dtype=np.float32)
+        rc = lib().rrr_o_gemv(qtype, _p(W, _u8p), _p(X, _f32p), _p(Y, _f32p), K, N, M, threads)
+    if rc != 0:
+        raise ValueError("oracle gemv rejected its arguments")
+    return Y.reshape(M, N)
+
+
+def logits(x, E, K, V, layout=0, chunk=8192, threads=1, f64=False):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    E = np.ascontiguousarray(E, dtype=np.float32)
+    if f64:
+        y = np.empty(V, dtype=np.float64)
+        rc = lib().rrr_o_logits_f64(_p(x, _f32p), _p(E, _f32p), _p(y, _f64p), K, V, layout, chunk, threads)
+    else:
+        y = np.empty(V, dtype=np.float32)
+        rc = lib().rrr_o_logits_f32(_p(x, _f32p), _p(E, _f32p), _p(y, _f32p), K, V, layout, chunk, threads)
+    if rc != 0:
+        raise ValueError("oracle logits rejected its arguments")
+    return y
+
+
+def logits_chunk_build(E, K, V, chunk=8192):
+    E = np.ascontiguousarray(E, dtype=np.float32)
+    out = np.empty(V * K, dtype=np.float32)
+    lib().rrr_o_logits_chunk_build(_p(E, _f32p), K, V, chunk, _p(out, _f32p))
+    return out
+
+
+def normwise_err(got, ref):
+    """max_i |got_i - ref_i| / max_i |ref_i| (the tolerance metric)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.max(np.abs(ref))
+    return float(np.max(np.abs(got - ref)) / (den if den > 0 else 1.0))

@@ -1,0 +1,866 @@
+// api.cpp -- the C ABI of librrr_hip.so (declared in include/rrr_hip.h).
+//
+// Every entry point validates its arguments completely before the first HIP
+// call, so a validation-only context (RRR_DEVICE_NONE) exercises all error
+// paths on a machine without a GPU.
+#include "rrr_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_set>
+
+#include "internal.h"
+
+using namespace rrr;
+
+namespace {
+
+constexpr uint32_t CTX_MAGIC = 0x52525243u, BUF_MAGIC = 0x52525242u, GRAPH_MAGIC = 0x52525247u;
+
+thread_local std::string g_err;
+std::mutex g_mu;
+std::unordered_set<rrr_ctx *> g_ctxs;
+
+int fail(int code, const char *fmt, ...)
+{
+    char msg[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+    g_err = msg;
+    return code;
+}
+
+int ok()
+{
+    g_err.clear();
+    return RRR_OK;
+}
+
+}  // namespace
+
+struct rrr_buf {
+    uint32_t magic;
+    rrr_ctx *ctx;
+    void *ptr;        // device pointer (nullptr in a validation-only context)
+    uint64_t bytes;
+    rrr_buf *parent;  // non-null for views
+};
+
+struct rrr_graph {
+    uint32_t magic;
+    rrr_ctx *ctx;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+struct rrr_ctx {
+    uint32_t magic;
+    int device;
+    bool nodevice;
+    bool async;
+    bool capturing;
+    bool timer_started;
+    hipStream_t stream;
+    hipEvent_t ev0, ev1;
+    void *scratch;  // argmax partial candidates
+    std::unordered_set<rrr_buf *> bufs;
+    std::unordered_set<rrr_graph *> graphs;
+};
+
+namespace {
+
+int check_ctx(rrr_ctx *ctx)
+{
+    if (!ctx) return fail(RRR_ERR_NULL, "null context");
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_ctxs.count(ctx) || ctx->magic != CTX_MAGIC) return fail(RRR_ERR_STALE, "context already destroyed");
+    return RRR_OK;
+}
+
+int check_buf(rrr_ctx *ctx, const rrr_buf *b, const char *what)
+{
+    if (!b) return fail(RRR_ERR_NULL, "%s: null buffer", what);
+    if (!ctx->bufs.count(const_cast<rrr_buf *>(b)) || b->magic != BUF_MAGIC)
+        return fail(RRR_ERR_STALE, "%s: buffer already freed or not owned by this context", what);
+    return RRR_OK;
+}
+
+int need(const rrr_buf *b, uint64_t bytes, const char *what)
+{
+    if (b->bytes < bytes)
+        return fail(RRR_ERR_SHORT_BUFFER, "%s: buffer holds %llu bytes, the op needs %llu", what,
+                    (unsigned long long)b->bytes, (unsigned long long)bytes);
+    return RRR_OK;
+}
+
+int need_f32(const rrr_buf *b, uint64_t count, const char *what)
+{
+    if (int rc = need(b, count * 4, what)) return rc;
+    if (b->ptr && ((uintptr_t)b->ptr & 15))
+        return fail(RRR_ERR_INVALID_ARG, "%s: f32 vector buffers must be 16-byte aligned", what);
+    return RRR_OK;
+}
+
+bool valid_type(uint32_t t) { return t == RRR_TYPE_F32 || t == RRR_TYPE_Q4_K || t == RRR_TYPE_Q5_K || t == RRR_TYPE_Q6_K; }
+
+int check_shape(uint32_t type, uint32_t K, uint32_t N)
+{
+    if (!valid_type(type)) return fail(RRR_ERR_BAD_TYPE, "ggml type %u is not one of 0, 12, 13, 14", type);
+    if (K == 0 || N == 0) return fail(RRR_ERR_BAD_SHAPE, "K and N must be positive (K=%u N=%u)", K, N);
+    if (K % 256) return fail(RRR_ERR_BAD_SHAPE, "K=%u is not a multiple of the 256-element super-block", K);
+    if (K > 65536) return fail(RRR_ERR_UNSUPPORTED, "K=%u exceeds 65536", K);
+    return RRR_OK;
+}
+
+// Launch epilogue: report launch errors, then wait unless async or capturing.
+int finish(rrr_ctx *ctx, hipError_t e, const char *what)
+{
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    if (!ctx->async && !ctx->capturing) {
+        e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    }
+    return ok();
+}
+
+int device_ready(rrr_ctx *ctx)
+{
+    if (ctx->nodevice) return fail(RRR_ERR_NO_DEVICE, "validation-only context has no device");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "hipSetDevice: %s", hipGetErrorString(e));
+    return RRR_OK;
+}
+
+#define TRY(x)                     \
+    do {                           \
+        int rc_ = (x);             \
+        if (rc_ != RRR_OK) return rc_; \
+    } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int rrr_abi_version(void) { return RRR_ABI_VERSION; }
+
+const char *rrr_last_error(void) { return g_err.c_str(); }
+
+int rrr_device_count(void)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+uint64_t rrr_tensor_bytes(uint32_t type, uint32_t K, uint32_t N)
+{
+    if (!valid_type(type) || K == 0 || K % 256) return 0;
+    return (uint64_t)N * (K / 256) * block_bytes(type);
+}
+
+int rrr_init(int device, rrr_ctx **out)
+{
+    if (!out) return fail(RRR_ERR_NULL, "rrr_init: null output pointer");
+    *out = nullptr;
+    if (device < RRR_DEVICE_NONE) return fail(RRR_ERR_INVALID_ARG, "rrr_init: device %d", device);
+    rrr_ctx *ctx = new rrr_ctx();
+    ctx->magic = CTX_MAGIC;
+    ctx->device = device;
+    ctx->nodevice = device == RRR_DEVICE_NONE;
+    ctx->async = ctx->capturing = ctx->timer_started = false;
+    ctx->stream = nullptr;
+    ctx->ev0 = ctx->ev1 = nullptr;
+    ctx->scratch = nullptr;
+    if (!ctx->nodevice) {
+        int n = rrr_device_count();
+        if (device >= n) {
+            delete ctx;
+            return fail(RRR_ERR_NO_DEVICE, "rrr_init: device %d requested, %d visible", device, n);
+        }
+        hipError_t e = hipSetDevice(device);
+        if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreate(&ctx->ev0);
+        if (e == hipSuccess) e = hipEventCreate(&ctx->ev1);
+        if (e == hipSuccess) e = hipMalloc(&ctx->scratch, argmax_partials_bytes());
+        if (e != hipSuccess) {
+            if (ctx->scratch) (void)hipFree(ctx->scratch);
+            if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
+            if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
+            if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+            delete ctx;
+            return fail(RRR_ERR_HIP, "rrr_init: %s", hipGetErrorString(e));
+        }
+    }
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_ctxs.insert(ctx);
+    }
+    *out = ctx;
+    return ok();
+}
+
+int rrr_destroy(rrr_ctx *ctx)
+{
+    TRY(check_ctx(ctx));
+    if (!ctx->nodevice) {
+        (void)hipSetDevice(ctx->device);
+        if (ctx->capturing) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(ctx->stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+        }
+        (void)hipStreamSynchronize(ctx->stream);
+        for (rrr_graph *g : ctx->graphs) {
+            (void)hipGraphExecDestroy(g->exec);
+            (void)hipGraphDestroy(g->graph);
+            g->magic = 0;
+            delete g;
+        }
+        for (rrr_buf *b : ctx->bufs)
+            if (!b->parent && b->ptr) (void)hipFree(b->ptr);
+        (void)hipFree(ctx->scratch);
+        (void)hipEventDestroy(ctx->ev0);
+        (void)hipEventDestroy(ctx->ev1);
+        (void)hipStreamDestroy(ctx->stream);
+    } else {
+        for (rrr_graph *g : ctx->graphs) delete g;
+    }
+    for (rrr_buf *b : ctx->bufs) {
+        b->magic = 0;
+        delete b;
+    }
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_ctxs.erase(ctx);
+    }
+    ctx->magic = 0;
+    delete ctx;
+    return ok();
+}
+
+// ---- buffers ---------------------------------------------------------------
+
+int rrr_buf_alloc(rrr_ctx *ctx, uint64_t bytes, rrr_buf **out)
+{
+    TRY(check_ctx(ctx));
+    if (!out) return fail(RRR_ERR_NULL, "rrr_buf_alloc: null output pointer");
+    *out = nullptr;
+    if (bytes == 0) return fail(RRR_ERR_INVALID_ARG, "rrr_buf_alloc: zero bytes");
+    if (ctx->capturing) return fail(RRR_ERR_STATE, "rrr_buf_alloc: not allowed during graph capture");
+    void *p = nullptr;
+    if (!ctx->nodevice) {
+        TRY(device_ready(ctx));
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return fail(RRR_ERR_HIP, "hipMalloc(%llu): %s", (unsigned long long)bytes, hipGetErrorString(e));
+    }
+    rrr_buf *b = new rrr_buf{BUF_MAGIC, ctx, p, bytes, nullptr};
+    ctx->bufs.insert(b);
+    *out = b;
+    return ok();
+}
+
+int rrr_buf_view(rrr_ctx *ctx, rrr_buf *parent, uint64_t offset, uint64_t bytes, rrr_buf **out)
+{
+    TRY(check_ctx(ctx));
+    if (!out) return fail(RRR_ERR_NULL, "rrr_buf_view: null output pointer");
+    *out = nullptr;
+    TRY(check_buf(ctx, parent, "rrr_buf_view"));
+    if (bytes == 0 || offset > parent->bytes || bytes > parent->bytes - offset)
+        return fail(RRR_ERR_INVALID_ARG, "rrr_buf_view: range [%llu, +%llu) outside a %llu-byte buffer",
+                    (unsigned long long)offset, (unsigned long long)bytes, (unsigned long long)parent->bytes);
+    if (offset % 4) return fail(RRR_ERR_INVALID_ARG, "rrr_buf_view: offset must be a multiple of 4");
+    rrr_buf *root = parent->parent ? parent->parent : parent;
+    void *p = parent->ptr ? (void *)((char *)parent->ptr + offset) : nullptr;
+    rrr_buf *b = new rrr_buf{BUF_MAGIC, ctx, p, bytes, root};
+    ctx->bufs.insert(b);
+    *out = b;
+    return ok();
+}
+
+int rrr_buf_free(rrr_ctx *ctx, rrr_buf *buf)
+{
+    TRY(check_ctx(ctx));
+    TRY(check_buf(ctx, buf, "rrr_buf_free"));
+    if (ctx->capturing) return fail(RRR_ERR_STATE, "rrr_buf_free: not allowed during graph capture");
+    if (!buf->parent) {
+        for (rrr_buf *b : ctx->bufs)
+            if (b->parent == buf) return fail(RRR_ERR_STATE, "rrr_buf_free: free the views of this buffer first");
+    }
+    if (!ctx->nodevice && !buf->parent && buf->ptr) {
+        TRY(device_ready(ctx));
+        (void)hipStreamSynchronize(ctx->stream);
+        hipError_t e = hipFree(buf->ptr);
+        if (e != hipSuccess) return fail(RRR_ERR_HIP, "hipFree: %s", hipGetErrorString(e));
+    }
+    ctx->bufs.erase(buf);
+    buf->magic = 0;
+    delete buf;
+    return ok();
+}
+
+uint64_t rrr_buf_size(const rrr_buf *buf) { return buf && buf->magic == BUF_MAGIC ? buf->bytes : 0; }
+
+static int copy_check(rrr_ctx *ctx, const rrr_buf *buf, uint64_t offset, const void *host, uint64_t bytes,
+                      const char *what)
+{
+    TRY(check_ctx(ctx));
+    TRY(check_buf(ctx, buf, what));
+    if (!host && bytes) return fail(RRR_ERR_NULL, "%s: null host pointer", what);
+    if (offset > buf->bytes || bytes > buf->bytes - offset)
+        return fail(RRR_ERR_SHORT_BUFFER, "%s: range [%llu, +%llu) outside a %llu-byte buffer", what,
+                    (unsigned long long)offset, (unsigned long long)bytes, (unsigned long long)buf->bytes);
+    if (ctx->capturing) return fail(RRR_ERR_STATE, "%s: host copies are not allowed during graph capture", what);
+    return RRR_OK;
+}
+
+int rrr_buf_upload(rrr_ctx *ctx, rrr_buf *buf, uint64_t offset, const void *src, uint64_t bytes)
+{
+    TRY(copy_check(ctx, buf, offset, src, bytes, "rrr_buf_upload"));
+    if (bytes == 0) return ok();
+    TRY(device_ready(ctx));
+    hipError_t e = hipMemcpyAsync((char *)buf->ptr + offset, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "rrr_buf_upload: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int rrr_buf_download(rrr_ctx *ctx, const rrr_buf *buf, uint64_t offset, void *dst, uint64_t bytes)
+{
+    TRY(copy_check(ctx, buf, offset, dst, bytes, "rrr_buf_download"));
+    if (bytes == 0) return ok();
+    TRY(device_ready(ctx));
+    hipError_t e = hipMemcpyAsync(dst, (const char *)buf->ptr + offset, bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "rrr_buf_download: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int rrr_buf_fill_u32(rrr_ctx *ctx, rrr_buf *buf, uint64_t offset, uint64_t bytes, uint32_t value)
+{
+    TRY(check_ctx(ctx));
+    TRY(check_buf(ctx, buf, "rrr_buf_fill_u32"));
+    if (offset % 4 || bytes % 4) return fail(RRR_ERR_INVALID_ARG, "rrr_buf_fill_u32: offset and bytes must be multiples of 4");
+    if (offset > buf->bytes || bytes > buf->bytes - offset)
+        return fail(RRR_ERR_SHORT_BUFFER, "rrr_buf_fill_u32: range outside the buffer");
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_fill_u32((uint32_t *)((char *)buf->ptr + offset), bytes / 4, value, ctx->stream),
+                  "rrr_buf_fill_u32");
+}
+
+// ---- weights ---------------------------------------------------------------
+
+int rrr_weight_upload(rrr_ctx *ctx, uint32_t type, uint32_t K, uint32_t N, const void *raw, uint64_t bytes,
+                      rrr_buf **out)
+{
+    TRY(check_ctx(ctx));
+    if (!out) return fail(RRR_ERR_NULL, "rrr_weight_upload: null output pointer");
+    *out = nullptr;
+    if (!raw) return fail(RRR_ERR_NULL, "rrr_weight_upload: null source");
+    TRY(check_shape(type, K, N));
+    const uint64_t need_bytes = rrr_tensor_bytes(type, K, N);
+    if (bytes < need_bytes)
+        return fail(RRR_ERR_SHORT_BUFFER, "rrr_weight_upload: %llu bytes given, a %ux%u type-%u tensor has %llu",
+                    (unsigned long long)bytes, N, K, type, (unsigned long long)need_bytes);
+    rrr_buf *b = nullptr;
+    TRY(rrr_buf_alloc(ctx, need_bytes, &b));
+    int rc = rrr_buf_upload(ctx, b, 0, raw, need_bytes);
+    if (rc != RRR_OK) {
+        std::string msg = g_err;
+        rrr_buf_free(ctx, b);
+        return fail(rc, "%s", msg.c_str());
+    }
+    *out = b;
+    return ok();
+}
+
+// ---- typed ops ---------------------------------------------------------------
+
+int rrr_dequant(rrr_ctx *ctx, uint32_t type, const rrr_buf *W, rrr_buf *out, uint64_t n)
+{
+    TRY(check_ctx(ctx));
+    TRY(check_buf(ctx, W, "rrr_dequant W"));
+    TRY(check_buf(ctx, out, "rrr_dequant out"));
+    if (!valid_type(type)) return fail(RRR_ERR_BAD_TYPE, "rrr_dequant: ggml type %u", type);
+    if (n == 0 || n % 256) return fail(RRR_ERR_BAD_SHAPE, "rrr_dequant: n_elements=%llu is not a positive multiple of 256", (unsigned long long)n);
+    TRY(need(W, n / 256 * block_bytes(type), "rrr_dequant W"));
+    TRY(need_f32(out, n, "rrr_dequant out"));
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_dequant(type, (const uint8_t *)W->ptr, W->bytes, (float *)out->ptr, n, ctx->stream),
+                  "rrr_dequant");
+}
+
+static int gemv_common(rrr_ctx *ctx, const rrr_buf *X, uint64_t x_floats, const rrr_buf *gamma, float eps,
+                       uint32_t act, uint32_t hd, uint32_t hpk, const rrr_buf *W, uint32_t type, rrr_buf *Y,
+                       uint32_t K, uint32_t N, uint32_t M, uint32_t residual, const char *what)
+{
+    TRY(check_buf(ctx, X, what));
+    TRY(check_buf(ctx, W, what));
+    TRY(check_buf(ctx, Y, what));
+    if (gamma) TRY(check_buf(ctx, gamma, what));
+    TRY(check_shape(type, K, N));
+    if (M == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: M must be positive", what);
+    if (M > 65535) return fail(RRR_ERR_UNSUPPORTED, "%s: M=%u exceeds 65535", what, M);
+    TRY(need(W, rrr_tensor_bytes(type, K, N), what));
+    TRY(need_f32(X, x_floats, what));
+    TRY(need_f32(Y, (uint64_t)M * N, what));
+    if (gamma) TRY(need_f32(gamma, K, what));
+    if (act == ACT_RMSNORM && !(std::isfinite(eps) && eps >= 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: eps", what);
+    TRY(device_ready(ctx));
+    GemvArgs a{};
+    a.type = type;
+    a.x = (const float *)X->ptr;
+    a.gamma = gamma ? (const float *)gamma->ptr : nullptr;
+    a.eps = eps;
+    a.head_dim = hd;
+    a.heads_per_kv = hpk;
+    a.W = (const uint8_t *)W->ptr;
+    a.w_bytes = W->bytes;
+    a.y = (float *)Y->ptr;
+    a.K = K;
+    a.N = N;
+    a.M = M;
+    a.residual = residual;
+    return finish(ctx, launch_gemv(a, act, ctx->stream), what);
+}
+
+int rrr_gemv(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t type, rrr_buf *Y, uint32_t K, uint32_t N,
+             uint32_t M)
+{
+    TRY(check_ctx(ctx));
+    return gemv_common(ctx, X, (uint64_t)M * K, nullptr, 0.0f, ACT_PLAIN, 0, 0, W, type, Y, K, N, M, 0, "rrr_gemv");
+}
+
+int rrr_gemv_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps, const rrr_buf *W, uint32_t type,
+                     rrr_buf *Y, uint32_t K, uint32_t N)
+{
+    TRY(check_ctx(ctx));
+    if (!gamma) return fail(RRR_ERR_NULL, "rrr_gemv_rmsnorm: null gamma");
+    return gemv_common(ctx, x, K, gamma, eps, ACT_RMSNORM, 0, 0, W, type, Y, K, N, 1, 0, "rrr_gemv_rmsnorm");
+}
+
+int rrr_gemv_residual(rrr_ctx *ctx, const rrr_buf *x, uint32_t act_kind, uint32_t act_param, const rrr_buf *W,
+                      uint32_t type, rrr_buf *hidden, uint32_t K, uint32_t N)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_gemv_residual";
+    switch (act_kind) {
+    case RRR_ACT_IDENTITY:
+        return gemv_common(ctx, x, K, nullptr, 0.0f, ACT_PLAIN, 0, 0, W, type, hidden, K, N, 1, 1, what);
+    case RRR_ACT_SILU_GATE:
+        return gemv_common(ctx, x, 2ull * K, nullptr, 0.0f, ACT_SILU, 0, 0, W, type, hidden, K, N, 1, 1, what);
+    case RRR_ACT_GQA_V: {
+        const uint32_t hd = act_param & 0xFFFFu, hpk = act_param >> 16;
+        if (hd == 0 || hpk == 0 || hd % 16 || K % (hd * hpk) || (K / hpk) % 16)
+            return fail(RRR_ERR_INVALID_ARG, "%s: GQA params head_dim=%u heads_per_kv=%u do not tile K=%u", what, hd,
+                        hpk, K);
+        return gemv_common(ctx, x, (uint64_t)K + 2ull * (K / hpk), nullptr, 0.0f, ACT_GQA_V, hd, hpk, W, type, hidden,
+                           K, N, 1, 1, what);
+    }
+    default:
+        return fail(RRR_ERR_INVALID_ARG, "%s: act_kind %u", what, act_kind);
+    }
+}
+
+int rrr_gemm_bf16(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t type, rrr_buf *Y, uint32_t K, uint32_t N,
+                  uint32_t M)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_gemm_bf16";
+    TRY(check_buf(ctx, X, what));
+    TRY(check_buf(ctx, W, what));
+    TRY(check_buf(ctx, Y, what));
+    TRY(check_shape(type, K, N));
+    if (type == RRR_TYPE_F32) return fail(RRR_ERR_UNSUPPORTED, "%s: F32 weights are not a prefill shape", what);
+    if (M == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: M must be positive", what);
+    TRY(need(W, rrr_tensor_bytes(type, K, N), what));
+    TRY(need(X, (uint64_t)M * K * 2, what));
+    TRY(need_f32(Y, (uint64_t)M * N, what));
+    TRY(device_ready(ctx));
+    hipError_t e = launch_gemm_bf16((const uint16_t *)X->ptr, (const uint8_t *)W->ptr, W->bytes, type, (float *)Y->ptr,
+                                    K, N, M, ctx->stream);
+    if (e == hipErrorNotSupported) return fail(RRR_ERR_UNSUPPORTED, "%s: shape not supported by this build", what);
+    return finish(ctx, e, what);
+}
+
+int rrr_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, rrr_buf *y, uint32_t rows, uint32_t d, float eps)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_rmsnorm";
+    TRY(check_buf(ctx, x, what));
+    TRY(check_buf(ctx, gamma, what));
+    TRY(check_buf(ctx, y, what));
+    if (rows == 0 || d == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: rows and d must be positive", what);
+    if (!(std::isfinite(eps) && eps >= 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: eps must be finite and >= 0", what);
+    TRY(need_f32(x, (uint64_t)rows * d, what));
+    TRY(need_f32(gamma, d, what));
+    TRY(need_f32(y, (uint64_t)rows * d, what));
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_rmsnorm((const float *)x->ptr, (const float *)gamma->ptr, (float *)y->ptr, rows, d, eps,
+                                      ctx->stream),
+                  what);
+}
+
+int rrr_silu_gate(rrr_ctx *ctx, const rrr_buf *gu, rrr_buf *mid, uint32_t rows, uint32_t F)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_silu_gate";
+    TRY(check_buf(ctx, gu, what));
+    TRY(check_buf(ctx, mid, what));
+    if (rows == 0 || F == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: rows and F must be positive", what);
+    TRY(need_f32(gu, 2ull * rows * F, what));
+    TRY(need_f32(mid, (uint64_t)rows * F, what));
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_silu_gate((const float *)gu->ptr, (float *)mid->ptr, rows, F, ctx->stream), what);
+}
+
+int rrr_residual_add(rrr_ctx *ctx, const rrr_buf *a, const rrr_buf *b, rrr_buf *out, uint32_t n)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_residual_add";
+    TRY(check_buf(ctx, a, what));
+    TRY(check_buf(ctx, b, what));
+    TRY(check_buf(ctx, out, what));
+    if (n == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: n must be positive", what);
+    TRY(need_f32(a, n, what));
+    TRY(need_f32(b, n, what));
+    TRY(need_f32(out, n, what));
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_residual_add((const float *)a->ptr, (const float *)b->ptr, (float *)out->ptr, n, ctx->stream),
+                  what);
+}
+
+static int logits_common(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps, const rrr_buf *E,
+                         rrr_buf *y, uint32_t K, uint32_t V, uint32_t layout, uint32_t chunk, const char *what)
+{
+    TRY(check_buf(ctx, x, what));
+    TRY(check_buf(ctx, E, what));
+    TRY(check_buf(ctx, y, what));
+    if (gamma) TRY(check_buf(ctx, gamma, what));
+    if (K == 0 || V == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: K and V must be positive", what);
+    if (layout > RRR_LOGITS_CHUNKED) return fail(RRR_ERR_INVALID_ARG, "%s: layout %u", what, layout);
+    if (gamma && !(std::isfinite(eps) && eps >= 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: eps", what);
+    TRY(need_f32(x, K, what));
+    TRY(need_f32(y, V, what));
+    if (gamma) TRY(need_f32(gamma, K, what));
+    TRY(need(E, (uint64_t)V * K * 4, what));
+    if (layout == RRR_LOGITS_ROWS) {
+        if (K % 256) return fail(RRR_ERR_BAD_SHAPE, "%s: row layout needs K %% 256 == 0 (K=%u)", what, K);
+        TRY(device_ready(ctx));
+        GemvArgs a{};
+        a.type = T_F32;
+        a.x = (const float *)x->ptr;
+        a.gamma = gamma ? (const float *)gamma->ptr : nullptr;
+        a.eps = eps;
+        a.W = (const uint8_t *)E->ptr;
+        a.w_bytes = E->bytes;
+        a.y = (float *)y->ptr;
+        a.K = K;
+        a.N = V;
+        a.M = 1;
+        return finish(ctx, launch_gemv(a, gamma ? ACT_RMSNORM : ACT_PLAIN, ctx->stream), what);
+    }
+    if (chunk == 0) return fail(RRR_ERR_INVALID_ARG, "%s: chunk must be positive", what);
+    if (chunk % 256 && chunk < V) return fail(RRR_ERR_UNSUPPORTED, "%s: chunk=%u must be a multiple of 256", what, chunk);
+    if (K % 4) return fail(RRR_ERR_BAD_SHAPE, "%s: chunked layout needs K %% 4 == 0", what);
+    if (K > 12288) return fail(RRR_ERR_UNSUPPORTED, "%s: K=%u exceeds 12288", what, K);
+    const uint64_t cn = chunk < V ? chunk : V;
+    if (cn * K * 4 > 0xFFFFFFFFull) return fail(RRR_ERR_UNSUPPORTED, "%s: one chunk exceeds 4 GiB", what);
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_logits_chunked((const float *)x->ptr, gamma ? (const float *)gamma->ptr : nullptr, eps,
+                                             (const float *)E->ptr, (float *)y->ptr, K, V, (uint32_t)cn, ctx->stream),
+                  what);
+}
+
+int rrr_logits_f32(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *E, rrr_buf *logits, uint32_t K, uint32_t V,
+                   uint32_t layout, uint32_t chunk)
+{
+    TRY(check_ctx(ctx));
+    return logits_common(ctx, x, nullptr, 0.0f, E, logits, K, V, layout, chunk, "rrr_logits_f32");
+}
+
+int rrr_logits_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps, const rrr_buf *E,
+                       rrr_buf *logits, uint32_t K, uint32_t V, uint32_t layout, uint32_t chunk)
+{
+    TRY(check_ctx(ctx));
+    if (!gamma) return fail(RRR_ERR_NULL, "rrr_logits_rmsnorm: null gamma");
+    return logits_common(ctx, x, gamma, eps, E, logits, K, V, layout, chunk, "rrr_logits_rmsnorm");
+}
+
+int rrr_argmax_f32(rrr_ctx *ctx, const rrr_buf *logits, uint32_t V, rrr_buf *out_index)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_argmax_f32";
+    TRY(check_buf(ctx, logits, what));
+    TRY(check_buf(ctx, out_index, what));
+    if (V == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: V must be positive", what);
+    TRY(need_f32(logits, V, what));
+    TRY(need(out_index, 4, what));
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_argmax((const float *)logits->ptr, V, ctx->scratch, (uint32_t *)out_index->ptr, ctx->stream),
+                  what);
+}
+
+// ---- name-keyed dispatch shim ----------------------------------------------
+
+static int push_u32(const void *push, uint32_t push_bytes, uint32_t n, uint32_t *out, const char *name)
+{
+    if (push_bytes != 4 * n) return fail(RRR_ERR_INVALID_ARG, "%s: expects %u push bytes, got %u", name, 4 * n, push_bytes);
+    if (!push) return fail(RRR_ERR_NULL, "%s: null push constants", name);
+    const unsigned char *p = (const unsigned char *)push;
+    for (uint32_t i = 0; i < n; i++)
+        out[i] = (uint32_t)p[4 * i] | ((uint32_t)p[4 * i + 1] << 8) | ((uint32_t)p[4 * i + 2] << 16) |
+                 ((uint32_t)p[4 * i + 3] << 24);
+    return RRR_OK;
+}
+
+static int want_bufs(uint32_t n_bufs, uint32_t n, rrr_buf *const *bufs, const char *name)
+{
+    if (n_bufs != n) return fail(RRR_ERR_INVALID_ARG, "%s: expects %u buffers, got %u", name, n, n_bufs);
+    if (!bufs) return fail(RRR_ERR_NULL, "%s: null buffer list", name);
+    return RRR_OK;
+}
+
+static int want_grid(const uint32_t *g, uint32_t x, uint32_t y, uint32_t z, const char *name)
+{
+    if (!g) return fail(RRR_ERR_NULL, "%s: null grid", name);
+    if (g[0] != x || g[1] != y || g[2] != z)
+        return fail(RRR_ERR_INVALID_ARG, "%s: grid [%u,%u,%u] does not match the push constants (expected [%u,%u,%u])",
+                    name, g[0], g[1], g[2], x, y, z);
+    return RRR_OK;
+}
+
+static int dispatch_one(rrr_ctx *ctx, const char *name, rrr_buf *const *bufs, uint32_t n_bufs, const void *push,
+                        uint32_t push_bytes, const uint32_t *groups)
+{
+    if (!name) return fail(RRR_ERR_NULL, "rrr_dispatch: null pipeline name");
+    uint32_t pc[3];
+    struct KQ { const char *name; uint32_t type; bool batch; };
+    static const KQ kq[] = {
+        {"matmul_q4k", RRR_TYPE_Q4_K, false},        {"matmul_q5k", RRR_TYPE_Q5_K, false},
+        {"matmul_q6k", RRR_TYPE_Q6_K, false},        {"matmul_gpuq4", RRR_TYPE_Q4_K, false},
+        {"matmul_gpuq5", RRR_TYPE_Q5_K, false},      {"matmul_gpuq6", RRR_TYPE_Q6_K, false},
+        {"matmul_gpuq4_batch", RRR_TYPE_Q4_K, true}, {"matmul_gpuq5_batch", RRR_TYPE_Q5_K, true},
+        {"matmul_gpuq6_batch", RRR_TYPE_Q6_K, true},
+    };
+    for (const KQ &q : kq) {
+        if (strcmp(name, q.name)) continue;
+        TRY(want_bufs(n_bufs, 3, bufs, name));
+        if (!q.batch) {
+            TRY(push_u32(push, push_bytes, 2, pc, name));
+            TRY(want_grid(groups, pc[1], 1, 1, name));
+            return gemv_common(ctx, bufs[0], pc[0], nullptr, 0.0f, ACT_PLAIN, 0, 0, bufs[1], q.type, bufs[2], pc[0], pc[1],
+                               1, 0, name);
+        }
+        TRY(push_u32(push, push_bytes, 3, pc, name));
+        TRY(want_grid(groups, pc[1], pc[2], 1, name));
+        return gemv_common(ctx, bufs[0], (uint64_t)pc[2] * pc[0], nullptr, 0.0f, ACT_PLAIN, 0, 0, bufs[1], q.type,
+                           bufs[2], pc[0], pc[1], pc[2], 0, name);
+    }
+    if (!strcmp(name, "matmul_tiled")) {
+        TRY(want_bufs(n_bufs, 3, bufs, name));
+        TRY(push_u32(push, push_bytes, 3, pc, name));  // [M, K, N]
+        const uint32_t M = pc[0], K = pc[1], N = pc[2];
+        TRY(want_grid(groups, (N + 15) / 16, (M + 15) / 16, 1, name));
+        if (M != 1) return fail(RRR_ERR_UNSUPPORTED, "%s: only M = 1 (the logit shape) is supported", name);
+        return logits_common(ctx, bufs[0], nullptr, 0.0f, bufs[1], bufs[2], K, N, RRR_LOGITS_CHUNKED, N, name);
+    }
+    if (!strcmp(name, "rmsnorm")) {
+        TRY(want_bufs(n_bufs, 3, bufs, name));
+        TRY(push_u32(push, push_bytes, 2, pc, name));
+        TRY(want_grid(groups, 1, 1, 1, name));
+        return rrr_rmsnorm(ctx, bufs[0], bufs[1], bufs[2], pc[0], pc[1], 1e-5f);
+    }
+    if (!strcmp(name, "silu_gate")) {
+        TRY(want_bufs(n_bufs, 2, bufs, name));
+        TRY(push_u32(push, push_bytes, 1, pc, name));
+        TRY(want_grid(groups, (pc[0] + 255) / 256, 1, 1, name));
+        return rrr_silu_gate(ctx, bufs[0], bufs[1], 1, pc[0]);
+    }
+    if (!strcmp(name, "residual_add")) {
+        TRY(want_bufs(n_bufs, 3, bufs, name));
+        TRY(push_u32(push, push_bytes, 1, pc, name));
+        TRY(want_grid(groups, (pc[0] + 255) / 256, 1, 1, name));
+        return rrr_residual_add(ctx, bufs[0], bufs[1], bufs[2], pc[0]);
+    }
+    static const char *out_of_scope[] = {"rope", "rope_kv_store", "kv_store", "attention", "fused_norm_matmul_q4k",
+                                         "fused_norm_matmul_q5k", "fused_norm_matmul_q6k"};
+    for (const char *o : out_of_scope)
+        if (!strcmp(name, o))
+            return fail(RRR_ERR_UNSUPPORTED, "rrr_dispatch: pipeline '%s' is outside the weight-heavy decode path", name);
+    return fail(RRR_ERR_UNSUPPORTED, "rrr_dispatch: unknown pipeline '%s'", name);
+}
+
+int rrr_dispatch(rrr_ctx *ctx, const char *name, rrr_buf *const *bufs, uint32_t n_bufs, const void *push,
+                 uint32_t push_bytes, const uint32_t groups[3])
+{
+    TRY(check_ctx(ctx));
+    return dispatch_one(ctx, name, bufs, n_bufs, push, push_bytes, groups);
+}
+
+int rrr_dispatch_batch(rrr_ctx *ctx, const rrr_dispatch_desc *descs, uint32_t n)
+{
+    TRY(check_ctx(ctx));
+    if (!descs && n) return fail(RRR_ERR_NULL, "rrr_dispatch_batch: null descriptor list");
+    const bool was_async = ctx->async;
+    ctx->async = true;
+    for (uint32_t i = 0; i < n; i++) {
+        const rrr_dispatch_desc &d = descs[i];
+        int rc = dispatch_one(ctx, d.name, d.bufs, d.n_bufs, d.push, d.push_bytes, d.groups);
+        if (rc != RRR_OK) {
+            ctx->async = was_async;
+            std::string msg = g_err;
+            return fail(rc, "rrr_dispatch_batch entry %u: %s", i, msg.c_str());
+        }
+    }
+    ctx->async = was_async;
+    if (ctx->nodevice || ctx->capturing || ctx->async) return ok();
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "rrr_dispatch_batch: %s", hipGetErrorString(e));
+    return ok();
+}
+
+// ---- graphs ------------------------------------------------------------------
+
+int rrr_graph_begin(rrr_ctx *ctx)
+{
+    TRY(check_ctx(ctx));
+    if (ctx->capturing) return fail(RRR_ERR_STATE, "rrr_graph_begin: already capturing");
+    TRY(device_ready(ctx));
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "rrr_graph_begin: %s", hipGetErrorString(e));
+    ctx->capturing = true;
+    return ok();
+}
+
+int rrr_graph_end(rrr_ctx *ctx, rrr_graph **out)
+{
+    TRY(check_ctx(ctx));
+    if (!out) return fail(RRR_ERR_NULL, "rrr_graph_end: null output pointer");
+    *out = nullptr;
+    if (!ctx->capturing) return fail(RRR_ERR_STATE, "rrr_graph_end: no capture in progress");
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ex = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (e == hipSuccess) e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return fail(RRR_ERR_HIP, "rrr_graph_end: %s", hipGetErrorString(e));
+    }
+    rrr_graph *gr = new rrr_graph{GRAPH_MAGIC, ctx, g, ex};
+    ctx->graphs.insert(gr);
+    *out = gr;
+    return ok();
+}
+
+static int check_graph(rrr_ctx *ctx, rrr_graph *g, const char *what)
+{
+    if (!g) return fail(RRR_ERR_NULL, "%s: null graph", what);
+    if (!ctx->graphs.count(g) || g->magic != GRAPH_MAGIC) return fail(RRR_ERR_STALE, "%s: graph already destroyed", what);
+    return RRR_OK;
+}
+
+int rrr_graph_launch(rrr_ctx *ctx, rrr_graph *g)
+{
+    TRY(check_ctx(ctx));
+    TRY(check_graph(ctx, g, "rrr_graph_launch"));
+    if (ctx->capturing) return fail(RRR_ERR_STATE, "rrr_graph_launch: not allowed during capture");
+    TRY(device_ready(ctx));
+    return finish(ctx, hipGraphLaunch(g->exec, ctx->stream), "rrr_graph_launch");
+}
+
+int rrr_graph_destroy(rrr_ctx *ctx, rrr_graph *g)
+{
+    TRY(check_ctx(ctx));
+    TRY(check_graph(ctx, g, "rrr_graph_destroy"));
+    if (!ctx->nodevice) {
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipGraphExecDestroy(g->exec);
+        (void)hipGraphDestroy(g->graph);
+    }
+    ctx->graphs.erase(g);
+    g->magic = 0;
+    delete g;
+    return ok();
+}
+
+// ---- sync and timing ----------------------------------------------------------
+
+int rrr_set_async(rrr_ctx *ctx, int async)
+{
+    TRY(check_ctx(ctx));
+    ctx->async = async != 0;
+    return ok();
+}
+
+int rrr_sync(rrr_ctx *ctx)
+{
+    TRY(check_ctx(ctx));
+    if (ctx->capturing) return fail(RRR_ERR_STATE, "rrr_sync: not allowed during capture");
+    TRY(device_ready(ctx));
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "rrr_sync: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int rrr_timer_start(rrr_ctx *ctx)
+{
+    TRY(check_ctx(ctx));
+    if (ctx->capturing) return fail(RRR_ERR_STATE, "rrr_timer_start: not allowed during capture");
+    TRY(device_ready(ctx));
+    hipError_t e = hipEventRecord(ctx->ev0, ctx->stream);
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "rrr_timer_start: %s", hipGetErrorString(e));
+    ctx->timer_started = true;
+    return ok();
+}
+
+int rrr_timer_stop(rrr_ctx *ctx, float *ms)
+{
+    TRY(check_ctx(ctx));
+    if (!ms) return fail(RRR_ERR_NULL, "rrr_timer_stop: null output");
+    if (!ctx->timer_started) return fail(RRR_ERR_STATE, "rrr_timer_stop: timer not started");
+    TRY(device_ready(ctx));
+    hipError_t e = hipEventRecord(ctx->ev1, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(ctx->ev1);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, ctx->ev0, ctx->ev1);
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "rrr_timer_stop: %s", hipGetErrorString(e));
+    ctx->timer_started = false;
+    return ok();
+}
+
+// ---- one-call helper ------------------------------------------------------------
+
+int rrr_matmul_kquant(rrr_ctx *ctx, rrr_buf *buf_a, const rrr_buf *weight_buf, rrr_buf *buf_c, uint32_t type,
+                      const float *a, float *c, uint32_t K, uint32_t N)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_matmul_kquant";
+    if (!a || !c) return fail(RRR_ERR_NULL, "%s: null host vector", what);
+    TRY(check_buf(ctx, buf_a, what));
+    TRY(check_buf(ctx, buf_c, what));
+    TRY(check_buf(ctx, weight_buf, what));
+    TRY(check_shape(type, K, N));
+    TRY(need(weight_buf, rrr_tensor_bytes(type, K, N), what));
+    TRY(need_f32(buf_a, K, what));
+    TRY(need_f32(buf_c, N, what));
+    if (ctx->capturing) return fail(RRR_ERR_STATE, "%s: not allowed during capture", what);
+    TRY(rrr_buf_upload(ctx, buf_a, 0, a, (uint64_t)K * 4));
+    const bool was_async = ctx->async;
+    ctx->async = false;
+    int rc = rrr_gemv(ctx, buf_a, weight_buf, type, buf_c, K, N, 1);
+    ctx->async = was_async;
+    TRY(rc);
+    return rrr_buf_download(ctx, buf_c, 0, c, (uint64_t)N * 4);
+}
+
+}  // extern "C"

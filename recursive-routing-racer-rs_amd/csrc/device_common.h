@@ -1,0 +1,106 @@
+// device_common.h -- gfx950 device helpers shared by the decode-path kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef char i8x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define RRR_WAVE 64
+
+// Buffer resource descriptor (V#) for raw byte addressing on gfx9: stride 0,
+// num_records = bytes, DST_SEL/format word 0x00020000.  Loads past
+// num_records return zero instead of faulting, which bounds every weight read
+// to the tensor the caller passed.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, uint64_t bytes)
+{
+    uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)n, 0x00020000);
+}
+
+// 16-byte load at any byte offset (the hardware runs in unaligned-access mode
+// under ROCm, so Q6_K's 2-byte-aligned 210-byte blocks need no realignment).
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+// IEEE binary16 -> binary32 (exact; v_cvt_f32_f16).
+__device__ __forceinline__ float h2f(uint32_t bits16)
+{
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits16 & 0xFFFFu));
+}
+
+// u32 bits -> f32.  Take the argument by value: applying __builtin_bit_cast
+// directly to an ext-vector swizzle such as v.y reads element 0 instead.
+__device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, uint32_t i) { return (w >> (8u * i)) & 0xFFu; }
+
+// 6-bit scale/min pair j (0..7) from the 12 packed bytes held in three
+// little-endian dwords (bytes 4..15 of a Q4_K/Q5_K block).  Restates the
+// get_scale_min step of phi4.rs:492-498.
+__device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             uint32_t &sc, uint32_t &mn)
+{
+    // q[i] for i in 0..11 is byte (i & 3) of dword s[i >> 2]
+    if (j < 4) {
+        sc = byte_of(s0, j) & 63u;
+        mn = byte_of(s1, j) & 63u;
+    } else {
+        uint32_t i = j - 4;
+        uint32_t q8 = byte_of(s2, i), q0 = byte_of(s0, i), q4 = byte_of(s1, i);
+        sc = (q8 & 0x0Fu) | ((q0 >> 6) << 4);
+        mn = (q8 >> 4) | ((q4 >> 6) << 4);
+    }
+}
+
+// Deterministic full-wave sum: fixed butterfly order, identical on every call.
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, RRR_WAVE);
+    return v;
+}
+
+// Sum of squares of x[0..d) by a 256-thread workgroup, in a fixed order that
+// does not depend on the caller: thread t accumulates x[t + 256 i] for
+// increasing i with fmaf, then a wave butterfly, then waves 0..3 in order.
+// `red` is 4 floats of LDS.  Every thread returns the same value.
+__device__ __forceinline__ float block_sumsq_256(const float *__restrict__ x, uint32_t d, float *red)
+{
+    const uint32_t t = threadIdx.x;
+    float acc = 0.0f;
+    for (uint32_t i = t; i < d; i += 256) acc = __builtin_fmaf(x[i], x[i], acc);
+    acc = wave_sum(acc);
+    __syncthreads();
+    if ((t & 63) == 0) red[t >> 6] = acc;
+    __syncthreads();
+    float s = ((red[0] + red[1]) + red[2]) + red[3];
+    __syncthreads();
+    return s;
+}
+
+// 1 / sqrt(sumsq / d + eps) with correctly rounded divide and square root,
+// the evaluation order of rms_norm (phi4.rs:596).
+__device__ __forceinline__ float rms_inv(float sumsq, uint32_t d, float eps)
+{
+    float mean = __fdiv_rn(sumsq, (float)d);
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+}
+
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }

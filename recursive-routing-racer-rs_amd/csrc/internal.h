@@ -1,0 +1,51 @@
+// internal.h -- launch interface between the C ABI (api.cpp) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rrr {
+
+enum GgmlType : uint32_t { T_F32 = 0, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
+
+// How a GEMV builds its activation vector before the dot products.
+enum ActKind : uint32_t {
+    ACT_PLAIN = 0,    // x as given (M rows of K)
+    ACT_SILU = 1,     // x[k] = silu(src[k]) * src[K + k]   (silu_gate)
+    ACT_GQA_V = 2,    // x[k] = src[K + K/hpk + (k / (hd*hpk)) * hd + k % hd]
+    ACT_RMSNORM = 3   // x[k] = (gamma[k] * src[k]) * inv_rms(src)
+};
+
+struct GemvArgs {
+    uint32_t type;        // GgmlType of W
+    const float *x;       // activation source
+    const float *gamma;   // ACT_RMSNORM weights
+    float eps;
+    uint32_t head_dim, heads_per_kv;  // ACT_GQA_V
+    const uint8_t *W;
+    uint64_t w_bytes;
+    float *y;
+    uint32_t K, N, M;
+    uint32_t residual;    // y += result instead of y = result
+};
+
+uint64_t block_bytes(uint32_t type);  // 144/176/210 per 256 elements, 1024 for F32
+
+hipError_t launch_gemv(const GemvArgs &a, uint32_t act, hipStream_t s);
+hipError_t launch_dequant(uint32_t type, const uint8_t *W, uint64_t w_bytes, float *out,
+                          uint64_t n_elements, hipStream_t s);
+hipError_t launch_rmsnorm(const float *x, const float *g, float *y, uint32_t rows, uint32_t d,
+                          float eps, hipStream_t s);
+hipError_t launch_silu_gate(const float *gu, float *mid, uint32_t rows, uint32_t F, hipStream_t s);
+hipError_t launch_residual_add(const float *a, const float *b, float *out, uint32_t n, hipStream_t s);
+hipError_t launch_fill_u32(uint32_t *p, uint64_t n_words, uint32_t v, hipStream_t s);
+// Transposed-chunk logits (layout 1).  gamma != nullptr fuses the RMSNorm.
+hipError_t launch_logits_chunked(const float *x, const float *gamma, float eps, const float *E,
+                                 float *y, uint32_t K, uint32_t V, uint32_t chunk, hipStream_t s);
+// Argmax: `partials` holds at least argmax_partials_bytes() bytes.
+uint64_t argmax_partials_bytes();
+hipError_t launch_argmax(const float *v, uint32_t n, void *partials, uint32_t *out, hipStream_t s);
+hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint64_t w_bytes, uint32_t type,
+                            float *Y, uint32_t K, uint32_t N, uint32_t M, hipStream_t s);
+
+}  // namespace rrr

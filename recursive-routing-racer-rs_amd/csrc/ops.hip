@@ -1,0 +1,299 @@
+// ops.hip -- dequant, RMSNorm, SwiGLU glue, residual add, fill, transposed
+// logits and argmax kernels of the decode path.
+#include "device_common.h"
+#include "internal.h"
+
+namespace rrr {
+
+// ---------------------------------------------------------------------------
+// Standalone dequant to f32: bit-exact with phi4.rs:444-542.  One thread per
+// 16 consecutive output elements.  Every product below is exact in f32
+// (11-bit d times a 6-bit scale times a 6-bit quant), so each output carries
+// at most the single rounding of `q*s - m` that the Rust code performs.
+template <uint32_t TYPE>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict__ W, uint64_t w_bytes,
+                                                       float *__restrict__ out, uint64_t n_groups)
+{
+    const uint64_t gid = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= n_groups) return;
+    const uint64_t blk = gid >> 4;
+    const uint32_t e0 = (uint32_t)(gid & 15) * 16;
+    float v[16];
+    if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) {
+        const uint32_t BS = TYPE == T_Q4_K ? 144 : 176;
+        const uint8_t *b = W + blk * BS;
+        const float d = h2f(b[0] | (b[1] << 8)), dmin = h2f(b[2] | (b[3] << 8));
+        const uint32_t sub = e0 / 32, j0 = e0 % 32, pair = sub / 2;
+        uint32_t sc, mn;
+        const uint8_t *q = b + 4;
+        if (sub < 4) {
+            sc = q[sub] & 63u;
+            mn = q[sub + 4] & 63u;
+        } else {
+            const uint32_t i = sub - 4;
+            sc = (q[8 + i] & 0x0Fu) | ((uint32_t)(q[i] >> 6) << 4);
+            mn = (q[8 + i] >> 4) | ((uint32_t)(q[4 + i] >> 6) << 4);
+        }
+        const float s = __fmul_rn(d, (float)sc), m = __fmul_rn(dmin, (float)mn);
+        const uint8_t *qs = b + (TYPE == T_Q4_K ? 16 : 48);
+        for (int i = 0; i < 16; i++) {
+            const uint32_t j = j0 + i;
+            const uint8_t qb = qs[pair * 32 + j];
+            uint32_t qi = (sub & 1) ? (qb >> 4) : (qb & 0xFu);
+            if constexpr (TYPE == T_Q5_K) qi |= ((uint32_t)(b[16 + j] >> sub) & 1u) << 4;
+            v[i] = __fsub_rn(__fmul_rn((float)qi, s), m);
+        }
+    } else if constexpr (TYPE == T_Q6_K) {
+        const uint8_t *b = W + blk * 210;
+        const float d = h2f(b[208] | (b[209] << 8));
+        const uint32_t g = e0 / 128, quad = (e0 % 128) / 32, l0 = e0 % 32;
+        const uint32_t is = g * 8 + l0 / 16 + 2 * quad;
+        const float ds = __fmul_rn(d, (float)(int8_t)b[192 + is]);
+        for (int i = 0; i < 16; i++) {
+            const uint32_t l = l0 + i;
+            const uint8_t qlb = b[g * 64 + l + (quad & 1) * 32];
+            const uint32_t lo = (quad < 2) ? (qlb & 0xFu) : (qlb >> 4);
+            const uint32_t hi = (b[128 + g * 32 + l] >> (2 * quad)) & 3u;
+            v[i] = __fmul_rn(ds, (float)((int)(lo | (hi << 4)) - 32));
+        }
+    } else {
+        const float *f = (const float *)W + gid * 16;
+        for (int i = 0; i < 16; i++) v[i] = f[i];
+    }
+    float4 *o = (float4 *)(out + gid * 16);
+    for (int i = 0; i < 4; i++) o[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+
+hipError_t launch_dequant(uint32_t type, const uint8_t *W, uint64_t w_bytes, float *out, uint64_t n,
+                          hipStream_t s)
+{
+    const uint64_t ng = n / 16;
+    const dim3 grid((unsigned)((ng + 255) / 256));
+    switch (type) {
+    case T_Q4_K: hipLaunchKernelGGL(dequant_kernel<T_Q4_K>, grid, dim3(256), 0, s, W, w_bytes, out, ng); break;
+    case T_Q5_K: hipLaunchKernelGGL(dequant_kernel<T_Q5_K>, grid, dim3(256), 0, s, W, w_bytes, out, ng); break;
+    case T_Q6_K: hipLaunchKernelGGL(dequant_kernel<T_Q6_K>, grid, dim3(256), 0, s, W, w_bytes, out, ng); break;
+    case T_F32: hipLaunchKernelGGL(dequant_kernel<T_F32>, grid, dim3(256), 0, s, W, w_bytes, out, ng); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm (phi4.rs:593-599): one 256-thread workgroup per row; the sum of
+// squares uses the same fixed-order reduction as the fused GEMV staging, so
+// rmsnorm -> gemv and the fused gemv_rmsnorm produce identical bits.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ g,
+                                                      float *__restrict__ y, uint32_t d, float eps)
+{
+    __shared__ float red[4];
+    const float *xr = x + (uint64_t)blockIdx.x * d;
+    float *yr = y + (uint64_t)blockIdx.x * d;
+    const float inv = rms_inv(block_sumsq_256(xr, d, red), d, eps);
+    for (uint32_t i = threadIdx.x; i < d; i += 256) yr[i] = __fmul_rn(__fmul_rn(g[i], xr[i]), inv);
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *g, float *y, uint32_t rows, uint32_t d, float eps,
+                          hipStream_t s)
+{
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, g, y, d, eps);
+    return hipGetLastError();
+}
+
+// silu_gate (phi4.rs:1369-1373): rows of [gate(F) | up(F)] -> rows of F.
+__global__ __launch_bounds__(256) void silu_gate_kernel(const float *__restrict__ gu, float *__restrict__ mid,
+                                                        uint32_t F, uint64_t total)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const uint64_t r = i / F, c = i - r * F;
+    const float *row = gu + r * 2 * F;
+    mid[i] = silu_f(row[c]) * row[F + c];
+}
+
+hipError_t launch_silu_gate(const float *gu, float *mid, uint32_t rows, uint32_t F, hipStream_t s)
+{
+    const uint64_t total = (uint64_t)rows * F;
+    hipLaunchKernelGGL(silu_gate_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, gu, mid, F, total);
+    return hipGetLastError();
+}
+
+// residual_add (phi4.rs:608-610); out may alias a.
+__global__ __launch_bounds__(256) void residual_add_kernel(const float *a, const float *b, float *out, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+hipError_t launch_residual_add(const float *a, const float *b, float *out, uint32_t n, hipStream_t s)
+{
+    hipLaunchKernelGGL(residual_add_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a, b, out, n);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t *p, uint64_t n, uint32_t v)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) p[i] = v;
+}
+
+hipError_t launch_fill_u32(uint32_t *p, uint64_t n, uint32_t v, hipStream_t s)
+{
+    uint64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Logits over the reference's transposed chunks (phi4.rs:874-893):
+// chunk c holds n_c = min(chunk, V - c*chunk) vocab rows as B_c[d*n_c + v].
+// A workgroup owns 256 consecutive vocab entries of one chunk (lane = 4
+// entries, one 16-byte load per d), wave w sums d in [w*K/4, (w+1)*K/4), and
+// the four partials are added in wave order through LDS.  The activation
+// (optionally RMS-normalised in place) sits in LDS.
+__global__ __launch_bounds__(256) void logits_chunked_kernel(const float *__restrict__ x, const float *__restrict__ gamma,
+                                                             float eps, const float *__restrict__ E,
+                                                             float *__restrict__ y, uint32_t K, uint32_t V,
+                                                             uint32_t chunk)
+{
+    extern __shared__ float sm[];
+    float *xs = sm;             // K
+    float *part = xs + K;       // 4 * 256
+    float *red = part + 1024;   // 4
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    float inv = 1.0f;
+    if (gamma) inv = rms_inv(block_sumsq_256(x, K, red), K, eps);
+    for (uint32_t i = t; i < K; i += 256) xs[i] = gamma ? __fmul_rn(__fmul_rn(gamma[i], x[i]), inv) : x[i];
+    __syncthreads();
+
+    const uint32_t v0 = blockIdx.x * 256;
+    const uint32_t c = v0 / chunk, cstart = c * chunk;
+    const uint32_t n = (V - cstart) < chunk ? (V - cstart) : chunk;
+    const uint32_t vin = v0 - cstart + 4 * lane;  // index inside the chunk
+    const uint64_t cbase = (uint64_t)cstart * K;  // chunk c starts after c full chunks
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(E + cbase, (uint64_t)n * K * 4);
+    const uint32_t dq = K / 4, d0 = wave * dq;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    if (vin < n) {
+        uint32_t off = (d0 * n + vin) * 4;
+        const uint32_t step = n * 4;
+        uint32_t dd = 0;
+        for (; dd + 8 <= dq; dd += 8) {
+            u32x4 w[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) w[u] = bload16(rs, off + u * step);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float xv = xs[d0 + dd + u];
+                a0 = fmaf(xv, u2f(w[u].x), a0);
+                a1 = fmaf(xv, u2f(w[u].y), a1);
+                a2 = fmaf(xv, u2f(w[u].z), a2);
+                a3 = fmaf(xv, u2f(w[u].w), a3);
+            }
+            off += 8 * step;
+        }
+        for (; dd < dq; dd++) {
+            const u32x4 w = bload16(rs, off);
+            const float xv = xs[d0 + dd];
+            a0 = fmaf(xv, u2f(w.x), a0);
+            a1 = fmaf(xv, u2f(w.y), a1);
+            a2 = fmaf(xv, u2f(w.z), a2);
+            a3 = fmaf(xv, u2f(w.w), a3);
+            off += step;
+        }
+    }
+    float4 *p4 = (float4 *)part;
+    p4[wave * 64 + lane] = make_float4(a0, a1, a2, a3);
+    __syncthreads();
+    if (wave == 0 && vin < n) {
+        float r[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            r[e] = ((part[4 * lane + e] + part[256 + 4 * lane + e]) + part[512 + 4 * lane + e]) + part[768 + 4 * lane + e];
+        for (int e = 0; e < 4; e++)
+            if (vin + e < n) y[cstart + vin + e] = r[e];
+    }
+}
+
+hipError_t launch_logits_chunked(const float *x, const float *gamma, float eps, const float *E, float *y,
+                                 uint32_t K, uint32_t V, uint32_t chunk, hipStream_t s)
+{
+    const size_t lds = ((size_t)K + 1024 + 4) * sizeof(float);
+    const uint32_t nwg = (V + 255) / 256;
+    hipLaunchKernelGGL(logits_chunked_kernel, dim3(nwg), dim3(256), lds, s, x, gamma, eps, E, y, K, V, chunk);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Argmax with the semantics of the sequential loop at phi4.rs:1172-1183:
+// start from (value -inf, index 0), replace only on strictly greater, so the
+// first maximal index wins and NaN never wins.  Pass 1: one candidate per
+// workgroup; pass 2: one workgroup reduces the candidates in index order.
+struct Cand { float v; uint32_t i; };
+
+__device__ __forceinline__ Cand better(Cand a, Cand b)
+{
+    // a precedes b in index order whenever both are live candidates
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+
+__device__ __forceinline__ Cand wave_best(Cand c)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        Cand d;
+        d.v = __shfl_xor(c.v, o, 64);
+        d.i = __shfl_xor(c.i, o, 64);
+        c = better(c, d);
+    }
+    return c;
+}
+
+__device__ Cand block_best(Cand c, Cand *sm)
+{
+    c = wave_best(c);
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = c;
+    __syncthreads();
+    Cand r = sm[0];
+    for (int w = 1; w < 4; w++) r = better(r, sm[w]);
+    return r;
+}
+
+constexpr uint32_t ARGMAX_WG = 1024;
+
+__global__ __launch_bounds__(256) void argmax_pass1(const float *__restrict__ v, uint32_t n, Cand *part)
+{
+    __shared__ Cand sm[4];
+    Cand c = {-__builtin_inff(), 0u};
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        const float x = v[i];
+        if (x > c.v) { c.v = x; c.i = i; }
+    }
+    c = block_best(c, sm);
+    if (threadIdx.x == 0) part[blockIdx.x] = c;
+}
+
+__global__ __launch_bounds__(256) void argmax_pass2(const Cand *part, uint32_t np, uint32_t *out)
+{
+    __shared__ Cand sm[4];
+    Cand c = {-__builtin_inff(), 0u};
+    for (uint32_t i = threadIdx.x; i < np; i += 256) c = better(c, part[i]);
+    c = block_best(c, sm);
+    if (threadIdx.x == 0) out[0] = c.i;
+}
+
+uint64_t argmax_partials_bytes() { return ARGMAX_WG * sizeof(Cand); }
+
+hipError_t launch_argmax(const float *v, uint32_t n, void *partials, uint32_t *out, hipStream_t s)
+{
+    uint32_t wg = (n + 255) / 256;
+    if (wg > ARGMAX_WG) wg = ARGMAX_WG;
+    if (wg == 0) wg = 1;
+    hipLaunchKernelGGL(argmax_pass1, dim3(wg), dim3(256), 0, s, v, n, (Cand *)partials);
+    hipLaunchKernelGGL(argmax_pass2, dim3(1), dim3(256), 0, s, (const Cand *)partials, wg, out);
+    return hipGetLastError();
+}
+
+}  // namespace rrr

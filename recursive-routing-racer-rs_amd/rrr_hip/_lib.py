@@ -1,0 +1,114 @@
+"""ctypes loader for librrr_hip.so and librrr_synth.so.
+
+The product path is the HIP library: if it has not been built, loading raises
+instead of falling back to anything else.
+"""
+import ctypes
+import os
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+HIP_LIB = os.path.join(LIB_DIR, "librrr_hip.so")
+SYNTH_LIB = os.path.join(LIB_DIR, "librrr_synth.so")
+
+c_ctx_p = ctypes.c_void_p
+c_buf_p = ctypes.c_void_p
+u32 = ctypes.c_uint32
+u64 = ctypes.c_uint64
+i32 = ctypes.c_int
+f32 = ctypes.c_float
+vp = ctypes.c_void_p
+
+
+class DispatchDesc(ctypes.Structure):
+    """rrr_dispatch_desc (include/rrr_hip.h)."""
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("bufs", ctypes.POINTER(c_buf_p)),
+        ("n_bufs", u32),
+        ("push", vp),
+        ("push_bytes", u32),
+        ("groups", u32 * 3),
+        ("barrier", u32),
+    ]
+
+
+# name -> (restype, argtypes); every symbol include/rrr_hip.h declares.
+SIGNATURES = {
+    "rrr_init": (i32, [i32, ctypes.POINTER(c_ctx_p)]),
+    "rrr_destroy": (i32, [c_ctx_p]),
+    "rrr_last_error": (ctypes.c_char_p, []),
+    "rrr_abi_version": (i32, []),
+    "rrr_device_count": (i32, []),
+    "rrr_buf_alloc": (i32, [c_ctx_p, u64, ctypes.POINTER(c_buf_p)]),
+    "rrr_buf_view": (i32, [c_ctx_p, c_buf_p, u64, u64, ctypes.POINTER(c_buf_p)]),
+    "rrr_buf_free": (i32, [c_ctx_p, c_buf_p]),
+    "rrr_buf_size": (u64, [c_buf_p]),
+    "rrr_buf_upload": (i32, [c_ctx_p, c_buf_p, u64, vp, u64]),
+    "rrr_buf_download": (i32, [c_ctx_p, c_buf_p, u64, vp, u64]),
+    "rrr_buf_fill_u32": (i32, [c_ctx_p, c_buf_p, u64, u64, u32]),
+    "rrr_tensor_bytes": (u64, [u32, u32, u32]),
+    "rrr_weight_upload": (i32, [c_ctx_p, u32, u32, u32, vp, u64, ctypes.POINTER(c_buf_p)]),
+    "rrr_dequant": (i32, [c_ctx_p, u32, c_buf_p, c_buf_p, u64]),
+    "rrr_gemv": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, c_buf_p, u32, u32, u32]),
+    "rrr_gemm_bf16": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, c_buf_p, u32, u32, u32]),
+    "rrr_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, u32, f32]),
+    "rrr_silu_gate": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, u32]),
+    "rrr_residual_add": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32]),
+    "rrr_logits_f32": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, u32, u32, u32]),
+    "rrr_argmax_f32": (i32, [c_ctx_p, c_buf_p, u32, c_buf_p]),
+    "rrr_gemv_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, u32, c_buf_p, u32, u32]),
+    "rrr_gemv_residual": (i32, [c_ctx_p, c_buf_p, u32, u32, c_buf_p, u32, c_buf_p, u32, u32]),
+    "rrr_logits_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, c_buf_p, u32, u32, u32, u32]),
+    "rrr_dispatch": (i32, [c_ctx_p, ctypes.c_char_p, ctypes.POINTER(c_buf_p), u32, vp, u32,
+                           ctypes.POINTER(u32)]),
+    "rrr_dispatch_batch": (i32, [c_ctx_p, ctypes.POINTER(DispatchDesc), u32]),
+    "rrr_graph_begin": (i32, [c_ctx_p]),
+    "rrr_graph_end": (i32, [c_ctx_p, ctypes.POINTER(vp)]),
+    "rrr_graph_launch": (i32, [c_ctx_p, vp]),
+    "rrr_graph_destroy": (i32, [c_ctx_p, vp]),
+    "rrr_set_async": (i32, [c_ctx_p, i32]),
+    "rrr_sync": (i32, [c_ctx_p]),
+    "rrr_timer_start": (i32, [c_ctx_p]),
+    "rrr_timer_stop": (i32, [c_ctx_p, ctypes.POINTER(f32)]),
+    "rrr_matmul_kquant": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, vp, vp, u32, u32]),
+}
+
+SYNTH_SIGNATURES = {
+    "rrr_synth_word": (u64, [u64, u64, u64]),
+    "rrr_synth_f32_to_f16": (ctypes.c_uint16, [f32]),
+    "rrr_synth_normal_f32": (None, [u64, u64, f32, f32, vp, u64, i32]),
+    "rrr_synth_normal_bf16": (None, [u64, u64, f32, f32, vp, u64, i32]),
+    "rrr_synth_kquant": (i32, [u64, u64, u32, vp, u64, i32]),
+}
+
+_hip = None
+_synth = None
+
+
+def _bind(lib, table):
+    for name, (res, args) in table.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def hip():
+    """The loaded librrr_hip.so (raises if it has not been built)."""
+    global _hip
+    if _hip is None:
+        if not os.path.exists(HIP_LIB):
+            raise RuntimeError(f"{HIP_LIB} is missing: build it with `make -C {PKG_DIR}/csrc` "
+                               "(or __graft_entry__.build())")
+        _hip = _bind(ctypes.CDLL(HIP_LIB), SIGNATURES)
+    return _hip
+
+
+def synth():
+    global _synth
+    if _synth is None:
+        if not os.path.exists(SYNTH_LIB):
+            raise RuntimeError(f"{SYNTH_LIB} is missing: build it with `make -C {PKG_DIR}/csrc`")
+        _synth = _bind(ctypes.CDLL(SYNTH_LIB), SYNTH_SIGNATURES)
+    return _synth

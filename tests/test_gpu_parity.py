@@ -1,0 +1,341 @@
+"""GPU parity of the HIP decode path against the CPU oracle.
+
+Bars: dequantized weights bit-exact; GEMV / batched GEMV / RMSNorm / logits
+within 1e-4 normwise relative error max|got - ref| / max|ref| against the
+oracle evaluated in fp64 (TOL below); fused kernels bit-identical to the
+unfused sequence they replace.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle.oracle as orc
+import rrr_hip
+from rrr_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+THREADS = 16
+
+
+def err(got, ref):
+    return orc.normwise_err(got, ref)
+
+
+def same_bits_or_both_nan(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(nan | (a.view(np.uint32) == b.view(np.uint32))))
+
+
+def weights(qtype, K, N, seed=1, stream=0):
+    if qtype == rrr_hip.F32:
+        return synth.normal_f32(seed, stream, N * K, 0.0, 0.02).view(np.uint8)
+    return synth.weight(seed, stream, qtype, K, N)
+
+
+# ---- dequant: bit-exact -------------------------------------------------------
+
+@pytest.mark.parametrize("name,qtype", [("q4k", 12), ("q5k", 13), ("q6k", 14)])
+def test_dequant_known_answer_blocks(ctx, name, qtype):
+    z = np.load(os.path.join(GOLDEN, f"kat_{name}.npz"))
+    blocks, expected = z["blocks"], z["expected"]
+    n = blocks.shape[0] * 256
+    W = ctx.weight_upload(qtype, 256, blocks.shape[0], blocks.reshape(-1))
+    out = ctx.alloc(n * 4)
+    ctx.dequant(qtype, W, out, n)
+    assert same_bits_or_both_nan(ctx.download(out).reshape(-1, 256), expected)
+    W.free(); out.free()
+
+
+@pytest.mark.parametrize("qtype,K,N", [(12, 3072, 3072), (13, 3072, 5120), (14, 8192, 3072), (14, 3072, 77)])
+def test_dequant_seeded_bit_exact(ctx, qtype, K, N):
+    raw = weights(qtype, K, N, seed=2)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    out = ctx.alloc(K * N * 4)
+    ctx.dequant(qtype, W, out, K * N)
+    assert same_bits_or_both_nan(ctx.download(out), orc.dequant(qtype, raw, K * N))
+    W.free(); out.free()
+
+
+# ---- GEMV (M = 1) ---------------------------------------------------------------
+
+GEMV_SHAPES = [
+    (12, 3072, 3072),   # config 1 / O-proj
+    (13, 3072, 5120),   # QKV
+    (14, 8192, 3072),   # down, Q6_K
+    (12, 8192, 3072),   # down, Q4_K layers
+    (12, 3072, 16384),  # gate+up
+    (0, 3072, 4096),    # F32 rows
+    # ragged and edge shapes
+    (12, 256, 1), (13, 256, 3), (14, 256, 5), (0, 256, 7),
+    (12, 768, 17), (13, 1280, 33), (14, 3072, 1001), (14, 2560, 9),
+    (12, 12288, 64), (14, 16384, 40), (0, 12288, 9),
+]
+
+
+@pytest.mark.parametrize("qtype,K,N", GEMV_SHAPES)
+def test_gemv_parity(ctx, qtype, K, N):
+    raw = weights(qtype, K, N, seed=3, stream=qtype)
+    x = synth.normal_f32(3, 100 + qtype, K)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    xb = ctx.to_device(x)
+    yb = ctx.alloc(N * 4)
+    ctx.gemv(xb, W, qtype, yb, K, N)
+    y = ctx.download(yb)
+    ref = orc.gemv(qtype, raw, x, K, N, 1, THREADS, f64=True)[0]
+    e = err(y, ref)
+    assert e < TOL, e
+    # the oracle's own f32 path sits inside the same bar
+    assert err(orc.gemv(qtype, raw, x, K, N, 1, THREADS)[0], ref) < TOL
+    W.free(); xb.free(); yb.free()
+
+
+@pytest.mark.parametrize("qtype", [12, 13, 14, 0])
+def test_gemv_one_hot_is_bit_exact_column(ctx, qtype):
+    K, N = 1024, 96
+    raw = weights(qtype, K, N, seed=4, stream=qtype)
+    deq = (orc.dequant(qtype, raw, K * N) if qtype else raw.view(np.float32)).reshape(N, K)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    xb, yb = ctx.alloc(K * 4), ctx.alloc(N * 4)
+    for k in (0, 15, 16, 31, 32, 200, 255, 256, 513, 1023):
+        x = np.zeros(K, np.float32)
+        x[k] = 1.0
+        ctx.upload(xb, x)
+        ctx.gemv(xb, W, qtype, yb, K, N)
+        # equal values (a -0.0 weight cannot survive as -0.0 through a sum)
+        assert np.array_equal(ctx.download(yb), deq[:, k]), k
+    W.free(); xb.free(); yb.free()
+
+
+def test_matmul_kquant_helper_and_dispatch_names(ctx):
+    # gpu_matmul_kquant (phi4.rs:631-658) and the name-keyed shaders
+    K, N = 3072, 640
+    for qtype, names in ((12, ("matmul_q4k", "matmul_gpuq4")), (13, ("matmul_q5k", "matmul_gpuq5")),
+                         (14, ("matmul_q6k", "matmul_gpuq6"))):
+        KK = 8192 if qtype == 14 else K
+        raw = weights(qtype, KK, N, seed=5, stream=qtype)
+        x = synth.normal_f32(5, qtype, KK)
+        W = ctx.weight_upload(qtype, KK, N, raw)
+        a, c = ctx.alloc(KK * 4), ctx.alloc(N * 4)
+        y = ctx.matmul_kquant(a, W, c, qtype, x, KK, N)
+        ref = orc.gemv(qtype, raw, x, KK, N, 1, THREADS, f64=True)[0]
+        assert err(y, ref) < TOL
+        for nm in names:
+            ctx.fill_u32(c, 0x7FC00000)
+            ctx.dispatch(nm, [a, W, c], [KK, N], [N, 1, 1])
+            assert np.array_equal(ctx.download(c), y)
+        W.free(); a.free(); c.free()
+
+
+# ---- batched GEMV / skinny ----------------------------------------------------------
+
+@pytest.mark.parametrize("qtype,K,N", [(12, 3072, 16384), (13, 3072, 5120), (14, 8192, 3072), (0, 3072, 2048),
+                                       (12, 512, 37)])
+@pytest.mark.parametrize("M", [2, 3, 4, 8, 32])
+def test_batched_gemv_parity(ctx, qtype, K, N, M):
+    raw = weights(qtype, K, N, seed=6, stream=qtype)
+    X = synth.normal_f32(6, 50 + M, M * K)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    Xb, Yb = ctx.to_device(X), ctx.alloc(M * N * 4)
+    ctx.gemv(Xb, W, qtype, Yb, K, N, M)
+    Y = ctx.download(Yb).reshape(M, N)
+    ref = orc.gemv(qtype, raw, X, K, N, M, THREADS, f64=True)
+    for m in range(M):
+        assert err(Y[m], ref[m]) < TOL, m
+    if qtype:
+        name = {12: "matmul_gpuq4_batch", 13: "matmul_gpuq5_batch", 14: "matmul_gpuq6_batch"}[qtype]
+        ctx.fill_u32(Yb, 0)
+        ctx.dispatch(name, [Xb, W, Yb], [K, N, M], [N, M, 1])
+        assert np.array_equal(ctx.download(Yb).reshape(M, N), Y)
+    W.free(); Xb.free(); Yb.free()
+
+
+# ---- RMSNorm, SwiGLU glue, residual ---------------------------------------------
+
+@pytest.mark.parametrize("rows,d", [(1, 3072), (5, 3072), (1, 8192), (3, 1000), (1, 1)])
+def test_rmsnorm_parity(ctx, rows, d):
+    x = synth.normal_f32(7, rows, rows * d)
+    g = synth.normal_f32(7, 100 + rows, d, 1.0, 0.1)
+    xb, gb, yb = ctx.to_device(x), ctx.to_device(g), ctx.alloc(rows * d * 4)
+    ctx.rmsnorm(xb, gb, yb, rows, d, 1e-5)
+    y = ctx.download(yb).reshape(rows, d)
+    xd = x.reshape(rows, d).astype(np.float64)
+    ref = g * xd / np.sqrt(np.mean(xd * xd, axis=1, keepdims=True) + 1e-5)
+    for r in range(rows):
+        assert err(y[r], ref[r]) < TOL
+    assert err(y, orc.rms_norm(x, g).reshape(rows, d)) < TOL
+    if rows == 1:
+        ctx.fill_u32(yb, 0)
+        ctx.dispatch("rmsnorm", [xb, gb, yb], [1, d], [1, 1, 1])
+        assert np.array_equal(ctx.download(yb), y[0])
+    xb.free(); gb.free(); yb.free()
+
+
+def test_silu_gate_and_residual(ctx):
+    F, rows = 8192, 3
+    gu = synth.normal_f32(8, 0, rows * 2 * F, 0.0, 3.0)
+    gub, mid = ctx.to_device(gu), ctx.alloc(rows * F * 4)
+    ctx.silu_gate(gub, mid, rows, F)
+    assert err(ctx.download(mid), orc.silu_gate(gu, F)) < 1e-6
+    a = synth.normal_f32(8, 1, 3072)
+    b = synth.normal_f32(8, 2, 3072)
+    ab, bb = ctx.to_device(a), ctx.to_device(b)
+    ctx.residual_add(ab, bb, ab, 3072)  # in place, as the reference does on gpu_hidden
+    assert np.array_equal(ctx.download(ab), orc.residual_add(a, b))
+    ctx.dispatch("residual_add", [ab, bb, ab], [3072], [12, 1, 1])
+    assert np.array_equal(ctx.download(ab), (a + b) + b)
+    one = ctx.alloc(F * 4)
+    ctx.dispatch("silu_gate", [gub, one], [F], [32, 1, 1])
+    assert np.array_equal(ctx.download(one), ctx.download(mid, count=F))
+    for bb_ in (gub, mid, ab, bb, one):
+        bb_.free()
+
+
+# ---- fused kernels are bit-identical to the unfused sequence ------------------------
+
+@pytest.mark.parametrize("qtype,K,N", [(13, 3072, 5120), (12, 3072, 16384), (14, 3072, 300), (0, 3072, 2000)])
+def test_gemv_rmsnorm_fused_bitwise(ctx, qtype, K, N):
+    raw = weights(qtype, K, N, seed=9, stream=qtype)
+    x = synth.normal_f32(9, 1, K)
+    g = synth.normal_f32(9, 2, K, 1.0, 0.1)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    xb, gb, nb = ctx.to_device(x), ctx.to_device(g), ctx.alloc(K * 4)
+    y1, y2 = ctx.alloc(N * 4), ctx.alloc(N * 4)
+    ctx.rmsnorm(xb, gb, nb, 1, K, 1e-5)
+    ctx.gemv(nb, W, qtype, y1, K, N)
+    ctx.gemv_rmsnorm(xb, gb, 1e-5, W, qtype, y2, K, N)
+    a, b = ctx.download(y1), ctx.download(y2)
+    assert np.array_equal(a, b)
+    ref = orc.gemv(qtype, raw, orc.rms_norm(x, g), K, N, 1, THREADS, f64=True)[0]
+    assert err(b, ref) < TOL
+    for t in (W, xb, gb, nb, y1, y2):
+        t.free()
+
+
+def test_gemv_residual_kinds(ctx):
+    K, N = 3072, 3072
+    # identity: O-proj + residual
+    raw = weights(12, K, N, seed=10, stream=1)
+    W = ctx.weight_upload(12, K, N, raw)
+    x = synth.normal_f32(10, 2, K)
+    h = synth.normal_f32(10, 3, N, 0.0, 100.0)
+    xb, hb = ctx.to_device(x), ctx.to_device(h)
+    ctx.gemv_residual(xb, rrr_hip.ACT_IDENTITY, 0, W, 12, hb, K, N)
+    ref = h.astype(np.float64) + orc.gemv(12, raw, x, K, N, 1, THREADS, f64=True)[0]
+    assert err(ctx.download(hb), ref) < TOL
+    # silu_gate + down (Q6_K) + residual
+    F = 8192
+    raw6 = weights(14, F, N, seed=10, stream=4)
+    W6 = ctx.weight_upload(14, F, N, raw6)
+    gu = synth.normal_f32(10, 5, 2 * F, 0.0, 2.0)
+    gub = ctx.to_device(gu)
+    ctx.upload(hb, h)
+    ctx.gemv_residual(gub, rrr_hip.ACT_SILU_GATE, 0, W6, 14, hb, F, N)
+    mid = orc.silu_gate(gu, F)
+    ref = h.astype(np.float64) + orc.gemv(14, raw6, mid, F, N, 1, THREADS, f64=True)[0]
+    assert err(ctx.download(hb), ref) < TOL
+    # position-0 GQA attention output (V gathered per kv head) + O-proj + residual
+    hd, hpk = 128, 3
+    qkv = synth.normal_f32(10, 6, K + 2 * (K // hpk))
+    qb = ctx.to_device(qkv)
+    ctx.upload(hb, h)
+    ctx.gemv_residual(qb, rrr_hip.ACT_GQA_V, hd | (hpk << 16), W, 12, hb, K, N)
+    v = qkv[K + K // hpk:]
+    attn = np.concatenate([v[(hh // hpk) * hd:(hh // hpk + 1) * hd] for hh in range(K // hd)])
+    ref = h.astype(np.float64) + orc.gemv(12, raw, attn, K, N, 1, THREADS, f64=True)[0]
+    assert err(ctx.download(hb), ref) < TOL
+    for t in (W, W6, xb, hb, gub, qb):
+        t.free()
+
+
+# ---- logits and argmax -------------------------------------------------------------
+
+@pytest.mark.parametrize("V,chunk", [(20000, 8192), (8192, 8192), (3456, 8192), (1000, 256), (700, 700)])
+def test_logits_parity_both_layouts(ctx, V, chunk):
+    K = 3072
+    E = synth.normal_f32(11, V, V * K, 0.0, 0.02)
+    x = synth.normal_f32(11, 1, K)
+    ref = orc.logits(x, E, K, V, threads=THREADS, f64=True)
+    xb, yb = ctx.to_device(x), ctx.alloc(V * 4)
+    Eb = ctx.to_device(E)
+    ctx.logits_f32(xb, Eb, yb, K, V, rrr_hip.LOGITS_ROWS)
+    y_rows = ctx.download(yb)
+    assert err(y_rows, ref) < TOL
+    Ec = orc.logits_chunk_build(E, K, V, chunk)
+    ctx.upload(Eb, Ec)
+    ctx.fill_u32(yb, 0)
+    ctx.logits_f32(xb, Eb, yb, K, V, rrr_hip.LOGITS_CHUNKED, chunk)
+    y_chunk = ctx.download(yb)
+    assert err(y_chunk, ref) < TOL
+    if V <= chunk:  # one chunk: the reference's matmul_tiled call shape
+        ctx.fill_u32(yb, 0)
+        ctx.dispatch("matmul_tiled", [xb, Eb, yb], [1, K, V], [(V + 15) // 16, 1, 1])
+        assert np.array_equal(ctx.download(yb), y_chunk)
+    xb.free(); yb.free(); Eb.free()
+
+
+def ref_argmax(v):
+    """The sequential loop of phi4.rs:1172-1183."""
+    best_val, best_id = -np.inf, 0
+    for j, x in enumerate(v):
+        if x > best_val:
+            best_val, best_id = x, j
+    return best_id
+
+
+@pytest.mark.parametrize("case", ["random", "ties", "nan", "all_neg_inf", "last", "single"])
+def test_argmax_semantics(ctx, case):
+    V = 200064
+    v = synth.normal_f32(12, 0, V)
+    if case == "ties":
+        v[[5, 77777, 199999]] = 9.0
+    elif case == "nan":
+        v[[0, 10]] = np.nan
+        v[123456] = 7.5
+    elif case == "all_neg_inf":
+        v[:] = -np.inf
+        v[3] = np.nan
+    elif case == "last":
+        v[-1] = 100.0
+    elif case == "single":
+        v = v[:1]
+        V = 1
+    vb, ob = ctx.to_device(v), ctx.alloc(4)
+    ctx.argmax_f32(vb, V, ob)
+    got = int(ctx.download(ob, np.uint32)[0])
+    exp = ref_argmax(v) if case in ("nan", "all_neg_inf", "single") else int(np.argmax(v))
+    assert got == exp
+    vb.free(); ob.free()
+
+
+# ---- graphs --------------------------------------------------------------------------
+
+def test_graph_replay_matches_eager(ctx):
+    K, N = 3072, 5120
+    raw = weights(13, K, N, seed=13)
+    W = ctx.weight_upload(13, K, N, raw)
+    x = synth.normal_f32(13, 1, K)
+    g = synth.normal_f32(13, 2, K, 1.0, 0.1)
+    xb, gb, yb, ob = ctx.to_device(x), ctx.to_device(g), ctx.alloc(N * 4), ctx.alloc(4)
+    ctx.gemv_rmsnorm(xb, gb, 1e-5, W, 13, yb, K, N)
+    ctx.argmax_f32(yb, N, ob)
+    eager_y, eager_i = ctx.download(yb), ctx.download(ob, np.uint32)
+    ctx.graph_begin()
+    ctx.fill_u32(yb, 0)
+    ctx.gemv_rmsnorm(xb, gb, 1e-5, W, 13, yb, K, N)
+    ctx.argmax_f32(yb, N, ob)
+    graph = ctx.graph_end()
+    for rep in range(5):
+        ctx.fill_u32(yb, 0x7FC00000)          # eager work between replays
+        ctx.fill_u32(ob, 0xFFFFFFFF)
+        graph.launch()
+        assert np.array_equal(ctx.download(yb), eager_y), rep
+        assert np.array_equal(ctx.download(ob, np.uint32), eager_i), rep
+    graph.destroy()
+    for t in (W, xb, gb, yb, ob):
+        t.free()

@@ -1,0 +1,250 @@
+"""CPU tests of the host side: the input generator, the C ABI's exports and
+its argument validation (through a validation-only context, no GPU), and the
+ComputeEngine mirror of the reference engine surface."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import rrr_hip
+from rrr_hip import _lib, synth
+from rrr_hip.engine import (ERR_BAD_SHAPE, ERR_BAD_TYPE, ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_NULL,
+                            ERR_SHORT_BUFFER, ERR_STALE, ERR_STATE, ERR_UNSUPPORTED)
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "rrr_hip.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rrr_[a-z0-9_]+)\s*\(", text)))
+
+
+# ---- generator ----------------------------------------------------------------
+
+def test_f32_to_f16_matches_numpy_rne():
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000),
+        np.array([0.0, -0.0, 65504.0, 65520.0, 65519.99, 1e-8, 5.96e-8, 2.98e-8, 6.1e-5, np.inf, -np.inf],
+                 np.float32),
+    ]).astype(np.float32)
+    # every f16 value and the midpoints between neighbours (ties to even)
+    allh = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = ((allh[:-1] + allh[1:]) / 2).astype(np.float32)
+    vals = np.concatenate([vals, allh.astype(np.float32), mids, -mids])
+    ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([synth.f32_to_f16_bits(v) for v in vals], np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_generator_is_deterministic_and_thread_independent():
+    a = synth.weight(1, 5, 12, 3072, 64, threads=1)
+    b = synth.weight(1, 5, 12, 3072, 64, threads=7)
+    assert np.array_equal(a, b)
+    n1 = synth.normal_f32(1, 9, 10001, threads=1)
+    n2 = synth.normal_f32(1, 9, 10001, threads=6)
+    assert np.array_equal(n1, n2)
+    assert not np.array_equal(synth.weight(1, 6, 12, 3072, 4), synth.weight(1, 5, 12, 3072, 4))
+
+
+def test_generator_recipes():
+    # Q4_K/Q5_K: d = f16(|N|*0.01), dmin = f16(|N|*0.005), finite and >= 0
+    for qt, bs in ((12, 144), (13, 176)):
+        b = synth.weight(2, qt, qt, 256 * 4000, 1).reshape(-1, bs)
+        d = b[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+        dmin = b[:, 2:4].copy().view(np.float16).astype(np.float64)[:, 0]
+        assert np.all(np.isfinite(d)) and np.all(d >= 0) and np.all(dmin >= 0)
+        assert 0.006 < d.mean() < 0.010 and 0.003 < dmin.mean() < 0.005  # E|N| = 0.798
+        # packed 6-bit fields are uniform: mean of all 16 fields ~ 31.5
+        assert 30.0 < b[:, 4:16].astype(np.float64).mean() < 133.0
+    b = synth.weight(2, 14, 14, 256 * 4000, 1).reshape(-1, 210)
+    sc = b[:, 192:208].view(np.int8)
+    assert sc.min() == -32 and sc.max() == 31
+    d = b[:, 208:210].copy().view(np.float16).astype(np.float64)[:, 0]
+    assert 0.003 < d.mean() < 0.005
+    x = synth.normal_f32(3, 0, 200000, 1.0, 0.1)
+    assert abs(x.mean() - 1.0) < 2e-3 and abs(x.std() - 0.1) < 2e-3
+    xb = synth.normal_bf16(3, 0, 1000)
+    xf = (xb.astype(np.uint32) << 16).view(np.float32)
+    assert np.allclose(xf, synth.normal_f32(3, 0, 1000), rtol=1 / 128)
+
+
+# ---- C ABI exports ------------------------------------------------------------
+
+def test_library_exports_every_header_symbol():
+    lib = ctypes.CDLL(_lib.HIP_LIB)
+    syms = header_symbols()
+    assert len(syms) >= 30
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, missing
+    # the Python binding declares a signature for each of them
+    assert sorted(_lib.SIGNATURES) == syms
+
+
+def test_abi_version_and_no_device_here():
+    lib = _lib.hip()
+    assert lib.rrr_abi_version() == 1
+    assert lib.rrr_device_count() >= 0
+    assert lib.rrr_tensor_bytes(12, 3072, 3072) == 5308416
+    assert lib.rrr_tensor_bytes(13, 3072, 5120) == 10813440
+    assert lib.rrr_tensor_bytes(14, 8192, 3072) == 20643840
+    assert lib.rrr_tensor_bytes(0, 3072, 200064) == 2458386432
+    assert lib.rrr_tensor_bytes(12, 3000, 1) == 0
+    assert lib.rrr_tensor_bytes(7, 256, 1) == 0
+
+
+# ---- validation (validation-only context) ----------------------------------------
+
+@pytest.fixture
+def vctx():
+    c = rrr_hip.Context(rrr_hip.DEVICE_NONE)
+    yield c
+    c.close()
+
+
+def code_of(fn, *args):
+    with pytest.raises(rrr_hip.RrrError) as ei:
+        fn(*args)
+    return ei.value.code
+
+
+def test_gemv_validation(vctx):
+    K, N = 3072, 64
+    x = vctx.alloc(K * 4)
+    y = vctx.alloc(N * 4)
+    W = vctx.alloc(rrr_hip.tensor_bytes(12, K, N))
+    assert code_of(vctx.gemv, x, W, 12, y, K, N) == ERR_NO_DEVICE          # valid call, no GPU
+    assert code_of(vctx.gemv, x, W, 11, y, K, N) == ERR_BAD_TYPE
+    assert code_of(vctx.gemv, x, W, 12, y, 3000, N) == ERR_BAD_SHAPE
+    assert code_of(vctx.gemv, x, W, 12, y, K, 0) == ERR_BAD_SHAPE
+    assert code_of(vctx.gemv, x, W, 12, y, K, N, 0) == ERR_BAD_SHAPE
+    assert code_of(vctx.gemv, x, W, 12, y, K, N + 1) == ERR_SHORT_BUFFER   # W too short
+    assert code_of(vctx.gemv, x, W, 13, y, K, N) == ERR_SHORT_BUFFER       # Q5_K needs more bytes
+    assert code_of(vctx.gemv, x, W, 12, y, K, N, 2) == ERR_SHORT_BUFFER    # X too short for M=2
+    small_y = vctx.alloc(N * 4 - 4)
+    assert code_of(vctx.gemv, x, W, 12, small_y, K, N) == ERR_SHORT_BUFFER
+    nullbuf = rrr_hip.Buffer(vctx, None, 0)
+    assert code_of(vctx.gemv, nullbuf, W, 12, y, K, N) == ERR_NULL
+    assert code_of(vctx.gemv, x, W, 12, y, 65536 + 256, N) in (ERR_UNSUPPORTED, ERR_SHORT_BUFFER)
+
+
+def test_stale_handles(vctx):
+    b = vctx.alloc(64)
+    h = b.handle
+    b.free()
+    stale = rrr_hip.Buffer(vctx, h, 64)
+    assert code_of(vctx.upload, stale, np.zeros(4, np.float32)) in (ERR_STALE,)
+    other = rrr_hip.Context(rrr_hip.DEVICE_NONE)
+    ob = other.alloc(64)
+    foreign = rrr_hip.Buffer(vctx, ob.handle, 64)
+    assert code_of(vctx.upload, foreign, np.zeros(4, np.float32)) == ERR_STALE
+    other.close()
+    # a destroyed context is rejected
+    lib = _lib.hip()
+    assert lib.rrr_buf_size(None) == 0
+    assert lib.rrr_sync(ctypes.c_void_p(other.handle or 0)) in (ERR_NULL,)
+
+
+def test_views_and_ranges(vctx):
+    b = vctx.alloc(4096)
+    v = vctx.view(b, 1024, 1024)
+    assert v.nbytes == 1024
+    assert code_of(vctx.view, b, 4000, 200) == ERR_INVALID_ARG
+    assert code_of(vctx.view, b, 2, 16) == ERR_INVALID_ARG
+    assert code_of(b.free) == ERR_STATE  # views first
+    v.free()
+    assert code_of(vctx.upload, b, np.zeros(2000, np.float32)) == ERR_SHORT_BUFFER
+    assert code_of(vctx.upload, b, np.zeros(16, np.float32)) == ERR_NO_DEVICE
+    assert code_of(vctx.fill_u32, b, 0, 2, 8) == ERR_INVALID_ARG
+    b.free()
+
+
+def test_weight_upload_validation(vctx):
+    raw = np.zeros(rrr_hip.tensor_bytes(14, 8192, 2), np.uint8)
+    assert code_of(vctx.weight_upload, 14, 8192, 2, raw) == ERR_NO_DEVICE
+    assert code_of(vctx.weight_upload, 14, 8192, 3, raw) == ERR_SHORT_BUFFER
+    assert code_of(vctx.weight_upload, 9, 8192, 2, raw) == ERR_BAD_TYPE
+    assert code_of(vctx.weight_upload, 14, 8000, 2, raw) == ERR_BAD_SHAPE
+
+
+def test_elementwise_and_logits_validation(vctx):
+    d = 3072
+    x, g, y = vctx.alloc(d * 4), vctx.alloc(d * 4), vctx.alloc(d * 4)
+    assert code_of(vctx.rmsnorm, x, g, y, 1, d) == ERR_NO_DEVICE
+    assert code_of(vctx.rmsnorm, x, g, y, 2, d) == ERR_SHORT_BUFFER
+    assert code_of(vctx.rmsnorm, x, g, y, 1, d, float("nan")) == ERR_INVALID_ARG
+    assert code_of(vctx.silu_gate, x, y, 1, d) == ERR_SHORT_BUFFER
+    assert code_of(vctx.residual_add, x, g, y, d + 1) == ERR_SHORT_BUFFER
+    V, K = 1000, 256
+    E = vctx.alloc(V * K * 4)
+    lg = vctx.alloc(V * 4)
+    xk = vctx.alloc(K * 4)
+    assert code_of(vctx.logits_f32, xk, E, lg, K, V, rrr_hip.LOGITS_ROWS) == ERR_NO_DEVICE
+    assert code_of(vctx.logits_f32, xk, E, lg, K, V, rrr_hip.LOGITS_CHUNKED, 300) == ERR_UNSUPPORTED
+    assert code_of(vctx.logits_f32, xk, E, lg, K, V, 2) == ERR_INVALID_ARG
+    assert code_of(vctx.logits_f32, xk, E, lg, K, V + 1, rrr_hip.LOGITS_ROWS) == ERR_SHORT_BUFFER
+    out = vctx.alloc(4)
+    assert code_of(vctx.argmax_f32, lg, V, out) == ERR_NO_DEVICE
+    assert code_of(vctx.argmax_f32, lg, V + 1, out) == ERR_SHORT_BUFFER
+
+
+def test_fused_validation(vctx):
+    K = 3072
+    qkv = vctx.alloc((K + 2048) * 4)
+    hid = vctx.alloc(K * 4)
+    W = vctx.alloc(rrr_hip.tensor_bytes(12, K, K))
+    param = 128 | (3 << 16)
+    assert code_of(vctx.gemv_residual, qkv, rrr_hip.ACT_GQA_V, param, W, 12, hid, K, K) == ERR_NO_DEVICE
+    assert code_of(vctx.gemv_residual, qkv, rrr_hip.ACT_GQA_V, 100 | (3 << 16), W, 12, hid, K, K) == ERR_INVALID_ARG
+    assert code_of(vctx.gemv_residual, qkv, 7, 0, W, 12, hid, K, K) == ERR_INVALID_ARG
+    assert code_of(vctx.gemv_residual, hid, rrr_hip.ACT_SILU_GATE, 0, W, 12, hid, K, K) == ERR_SHORT_BUFFER
+
+
+def test_dispatch_shim_validation(vctx):
+    K, N = 3072, 16
+    x, y = vctx.alloc(K * 4), vctx.alloc(N * 4)
+    W = vctx.alloc(rrr_hip.tensor_bytes(13, K, N))
+    assert code_of(vctx.dispatch, "matmul_q5k", [x, W, y], [K, N], [N, 1, 1]) == ERR_NO_DEVICE
+    assert code_of(vctx.dispatch, "matmul_gpuq5", [x, W, y], [K, N], [N, 1, 1]) == ERR_NO_DEVICE
+    assert code_of(vctx.dispatch, "matmul_q5k", [x, W, y], [K, N], [N + 1, 1, 1]) == ERR_INVALID_ARG
+    assert code_of(vctx.dispatch, "matmul_q5k", [x, W], [K, N], [N, 1, 1]) == ERR_INVALID_ARG
+    assert code_of(vctx.dispatch, "matmul_q5k", [x, W, y], [K], [N, 1, 1]) == ERR_INVALID_ARG
+    assert code_of(vctx.dispatch, "attention", [x, W, y, x], [1, 8, 3, 128], [24, 1, 1]) == ERR_UNSUPPORTED
+    assert code_of(vctx.dispatch, "no_such_shader", [x], [1], [1, 1, 1]) == ERR_UNSUPPORTED
+    assert code_of(vctx.dispatch, "rmsnorm", [x, x, x], [1, K], [1, 1, 1]) == ERR_NO_DEVICE
+    # batch: failing entry is named
+    with pytest.raises(rrr_hip.RrrError) as ei:
+        vctx.dispatch_batch([("matmul_q5k", [x, W, y], [K, N], [N, 1, 1], True),
+                             ("rope", [x, x], [0] * 5, [1, 1, 1], True)])
+    assert "entry 0" in ei.value.msg or ei.value.code == ERR_NO_DEVICE
+
+
+def test_graph_state_rules(vctx):
+    assert code_of(vctx.graph_end) == ERR_STATE
+    assert code_of(vctx.graph_begin) == ERR_NO_DEVICE
+    assert code_of(vctx.timer_stop) == ERR_STATE
+
+
+def test_compute_engine_mirror_requires_registration(monkeypatch):
+    # ComputeEngine on a validation-only context: pipelines must be registered
+    # (engine.rs:142 before engine.rs:476), buffer counts must match.
+    eng = rrr_hip.ComputeEngine.__new__(rrr_hip.ComputeEngine)
+    eng.ctx = rrr_hip.Context(rrr_hip.DEVICE_NONE)
+    eng.pipeline_cache, eng.persistent_desc_sets = {}, []
+    a = eng.alloc_buffer(3072 * 4)
+    assert a.capacity == 3072 * 4
+    with pytest.raises(rrr_hip.RrrError):
+        eng.dispatch_by_name("rmsnorm", [a, a, a], [a.capacity] * 3, b"\x01\0\0\0\0\x0c\0\0", [1, 1, 1])
+    eng.get_pipeline("rmsnorm", 3, 8)
+    with pytest.raises(rrr_hip.RrrError) as ei:
+        eng.dispatch_by_name("rmsnorm", [a, a, a], [a.capacity] * 3, b"\x01\0\0\0\0\x0c\0\0", [1, 1, 1])
+    assert ei.value.code == ERR_NO_DEVICE
+    h = eng.pre_allocate_desc_set("rmsnorm", [a, a, a], [a.capacity] * 3)
+    with pytest.raises(rrr_hip.RrrError) as ei:
+        eng.dispatch_batch_persistent_v2([("matmul_q4k", h, b"", [1, 1, 1], True)])
+    assert ei.value.code == ERR_INVALID_ARG
+    eng.close()
