@@ -77,22 +77,62 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
-// Sum of squares of x[0..d) by a 256-thread workgroup, in a fixed order that
-// does not depend on the caller: thread t accumulates x[t + 256 i] for
-// increasing i with fmaf, then a wave butterfly, then waves 0..3 in order.
-// `red` is 4 floats of LDS.  Every thread returns the same value.
-__device__ __forceinline__ float block_sumsq_256(const float *__restrict__ x, uint32_t d, float *red)
+// Workgroup (256 threads) sum of per-thread partials: a fixed wave butterfly,
+// then waves 0..3 in order.  `red` is 4 floats of LDS.  Every thread returns
+// the same value.
+__device__ __forceinline__ float block_sum_256(float acc, float *red)
+{
+    acc = wave_sum(acc);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    const float s = ((red[0] + red[1]) + red[2]) + red[3];
+    __syncthreads();
+    return s;
+}
+
+// Same for a workgroup of W waves (waves summed in order).  `red` holds W floats.
+template <int W>
+__device__ __forceinline__ float block_sum_w(float acc, float *red)
+{
+    acc = wave_sum(acc);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < W; w++) s = s + red[w];
+    __syncthreads();
+    return s;
+}
+
+// Canonical per-thread sum-of-squares order shared by every RMSNorm on the
+// path (standalone and fused), so that they agree bit for bit: for d % 4 == 0
+// thread t owns the float4s t, t + 256, t + 512, ... of the vector and
+// accumulates x^2 with fmaf float4 by float4, component by component;
+// otherwise it owns the elements t, t + 256, ...
+__device__ __forceinline__ float thread_sumsq(const float *__restrict__ x, uint32_t d)
 {
     const uint32_t t = threadIdx.x;
     float acc = 0.0f;
-    for (uint32_t i = t; i < d; i += 256) acc = __builtin_fmaf(x[i], x[i], acc);
-    acc = wave_sum(acc);
-    __syncthreads();
-    if ((t & 63) == 0) red[t >> 6] = acc;
-    __syncthreads();
-    float s = ((red[0] + red[1]) + red[2]) + red[3];
-    __syncthreads();
-    return s;
+    if (d % 4 == 0) {
+        const float4 *p = (const float4 *)x;
+        for (uint32_t f = t; f < d / 4; f += 256) {
+            const float4 v = p[f];
+            acc = __builtin_fmaf(v.x, v.x, acc);
+            acc = __builtin_fmaf(v.y, v.y, acc);
+            acc = __builtin_fmaf(v.z, v.z, acc);
+            acc = __builtin_fmaf(v.w, v.w, acc);
+        }
+    } else {
+        for (uint32_t i = t; i < d; i += 256) acc = __builtin_fmaf(x[i], x[i], acc);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float block_sumsq_256(const float *__restrict__ x, uint32_t d, float *red)
+{
+    return block_sum_256(thread_sumsq(x, d), red);
 }
 
 // 1 / sqrt(sumsq / d + eps) with correctly rounded divide and square root,

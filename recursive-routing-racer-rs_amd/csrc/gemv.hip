@@ -2,42 +2,47 @@
 //
 // Y[m][n] = sum_k X[m][k] * W[n][k]  (phi4.rs:628-630; batch shape :1257-1268)
 //
-// Layout: W is the raw GGUF tensor, N rows of K/256 super-blocks, uploaded
-// unchanged.  A 256-thread workgroup owns 4*R consecutive rows (R per wave)
-// and MT activation rows.  The activation tile is staged once per K-chunk in
-// LDS together with its 16-element partial sums; every lane then owns a fixed
-// 16-byte slice of each super-block it visits (selected per type below),
-// loads it with a bounds-checked buffer load, and multiplies it against the
-// matching LDS spans for all R rows and MT tokens.  The per-sub-block scale
-// and min are applied once per span:
+// W is the raw GGUF tensor, N rows of K/256 super-blocks, uploaded unchanged.
+// A 256-thread workgroup owns 4*R consecutive rows (R per wave).  Within a
+// wave, BPI super-blocks of a row are in flight per iteration and LPB lanes
+// share each super-block; every lane owns a fixed 16-byte slice of the block
+// (chosen per type below), loads it with a bounds-checked buffer load, and
+// multiplies it against the NS activation spans that slice covers.  The
+// sub-block scale and min are applied once per span:
 //     sum_j x_j * (q_j * s - m) = s * sum_j q_j x_j - m * sum_j x_j
-// so the inner loop is one conversion and one FMA per element.
-#include "device_common.h"
-#include "internal.h"
+// with the 16-element activation sums precomputed at staging, so the inner
+// loop is one int->float conversion and one FMA per weight.  A lane reads its
+// activation spans once per iteration and reuses them for all R rows.
+#include "act.h"
 
 namespace rrr {
 
 // ---------------------------------------------------------------------------
-// Per-type lane decoders.  LPB lanes share one super-block, BPI blocks are in
-// flight per wave iteration (LPB * BPI == 64).
+// Per-type lane decoders.  Lane = part * BPI + slot: `slot` picks the
+// super-block within the iteration, `part` the 16-byte slice within it.
+// span_off(j) is the offset of activation span j inside the 256-element block.
+// STR is the float4 row stride of the interleaved LDS layout used by the
+// batch-1 kernel (see gemv_pf_kernel).
 
 // Q4_K block (phi4.rs:481-510): {f16 d; f16 dmin; u8 sc[12]; u8 qs[128]}.
-// Lane c (0..7) takes qs bytes [16c, 16c+16): pair p = c/2, j0 = 16 (c&1);
-// low nibbles are sub-block 2p, high nibbles sub-block 2p+1, positions j0..j0+15.
+// Part c (0..7) takes qs bytes [16c, 16c+16): pair p = c/2, j0 = 16 (c&1);
+// its low nibbles are sub-block 2p (span 0), its high nibbles sub-block 2p+1
+// (span 1), positions j0..j0+15.
 struct DecQ4K {
-    static constexpr uint32_t BS = 144, LPB = 8, BPI = 8;
+    static constexpr uint32_t BS = 144, LPB = 8, BPI = 8, STR = 10;
+    static constexpr int NS = 2, SPAN = 16;
     struct Raw { u32x4 hdr, qs; };
     uint32_t c, p, j0;
-    __device__ explicit DecQ4K(uint32_t lane) : c(lane & 7), p((lane & 7) >> 1), j0((lane & 1) * 16) {}
-    __device__ static uint32_t slot(uint32_t lane) { return lane >> 3; }
+    __device__ explicit DecQ4K(uint32_t lane) : c(lane / BPI), p((lane / BPI) >> 1), j0(((lane / BPI) & 1) * 16) {}
+    __device__ static uint32_t slot(uint32_t lane) { return lane % BPI; }
+    __device__ uint32_t span_off(int j) const { return 64 * p + j0 + 32 * j; }
     __device__ void load(Raw &w, __amdgpu_buffer_rsrc_t rs, uint32_t boff) const
     {
         w.hdr = bload16(rs, boff);
         w.qs = bload16(rs, boff + 16 + 16 * c);
     }
     template <int MT>
-    __device__ void accum(const Raw &w, const float *xb, uint32_t xst, const float *gb, uint32_t gst,
-                          float *acc) const
+    __device__ void accum(const Raw &w, const float (*xr)[NS * SPAN], const float (*gr)[NS], float *acc) const
     {
         const float d = h2f(w.hdr.x), dmin = h2f(w.hdr.x >> 16);
         uint32_t sc0, mn0, sc1, mn1;
@@ -56,38 +61,33 @@ struct DecQ4K {
                 qh[4 * i + b] = (float)byte_of(hi, b);
             }
         }
-        const uint32_t xo = 64 * p + j0;
 #pragma unroll
         for (int m = 0; m < MT; m++) {
-            const float4 *xl = (const float4 *)(xb + m * xst + xo);
-            const float4 *xh = (const float4 *)(xb + m * xst + xo + 32);
             float dl = 0.0f, dh = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 a = xl[i], b = xh[i];
-                dl = fmaf(ql[4 * i + 0], a.x, dl); dl = fmaf(ql[4 * i + 1], a.y, dl);
-                dl = fmaf(ql[4 * i + 2], a.z, dl); dl = fmaf(ql[4 * i + 3], a.w, dl);
-                dh = fmaf(qh[4 * i + 0], b.x, dh); dh = fmaf(qh[4 * i + 1], b.y, dh);
-                dh = fmaf(qh[4 * i + 2], b.z, dh); dh = fmaf(qh[4 * i + 3], b.w, dh);
+            for (int i = 0; i < 16; i++) {
+                dl = fmaf(ql[i], xr[m][i], dl);
+                dh = fmaf(qh[i], xr[m][16 + i], dh);
             }
-            const float gl = gb[m * gst + xo / 16], gh = gb[m * gst + xo / 16 + 2];
             float r = acc[m];
-            r = fmaf(s0, dl, r); r = fmaf(-n0, gl, r);
-            r = fmaf(s1, dh, r); r = fmaf(-n1, gh, r);
+            r = fmaf(s0, dl, r); r = fmaf(-n0, gr[m][0], r);
+            r = fmaf(s1, dh, r); r = fmaf(-n1, gr[m][1], r);
             acc[m] = r;
         }
     }
 };
 
 // Q5_K block (phi4.rs:512-542): {d; dmin; sc[12]; qh[32]; qs[128]}.
-// Same lane split as Q4_K; the fifth bit of position j in sub-block s is bit s
-// of qh[j], so the lane also loads qh[j0..j0+15].
+// Same parts as Q4_K; the fifth bit of position j in sub-block s is bit s of
+// qh[j], so each lane also loads qh[j0..j0+15].
 struct DecQ5K {
-    static constexpr uint32_t BS = 176, LPB = 8, BPI = 8;
+    static constexpr uint32_t BS = 176, LPB = 8, BPI = 8, STR = 10;
+    static constexpr int NS = 2, SPAN = 16;
     struct Raw { u32x4 hdr, qh, qs; };
     uint32_t c, p, j0;
-    __device__ explicit DecQ5K(uint32_t lane) : c(lane & 7), p((lane & 7) >> 1), j0((lane & 1) * 16) {}
-    __device__ static uint32_t slot(uint32_t lane) { return lane >> 3; }
+    __device__ explicit DecQ5K(uint32_t lane) : c(lane / BPI), p((lane / BPI) >> 1), j0(((lane / BPI) & 1) * 16) {}
+    __device__ static uint32_t slot(uint32_t lane) { return lane % BPI; }
+    __device__ uint32_t span_off(int j) const { return 64 * p + j0 + 32 * j; }
     __device__ void load(Raw &w, __amdgpu_buffer_rsrc_t rs, uint32_t boff) const
     {
         w.hdr = bload16(rs, boff);
@@ -95,8 +95,7 @@ struct DecQ5K {
         w.qs = bload16(rs, boff + 48 + 16 * c);
     }
     template <int MT>
-    __device__ void accum(const Raw &w, const float *xb, uint32_t xst, const float *gb, uint32_t gst,
-                          float *acc) const
+    __device__ void accum(const Raw &w, const float (*xr)[NS * SPAN], const float (*gr)[NS], float *acc) const
     {
         const float d = h2f(w.hdr.x), dmin = h2f(w.hdr.x >> 16);
         uint32_t sc0, mn0, sc1, mn1;
@@ -116,41 +115,36 @@ struct DecQ5K {
                 qh[4 * i + b] = (float)byte_of(hi, b);
             }
         }
-        const uint32_t xo = 64 * p + j0;
 #pragma unroll
         for (int m = 0; m < MT; m++) {
-            const float4 *xl = (const float4 *)(xb + m * xst + xo);
-            const float4 *xh = (const float4 *)(xb + m * xst + xo + 32);
             float dl = 0.0f, dh = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 a = xl[i], b = xh[i];
-                dl = fmaf(ql[4 * i + 0], a.x, dl); dl = fmaf(ql[4 * i + 1], a.y, dl);
-                dl = fmaf(ql[4 * i + 2], a.z, dl); dl = fmaf(ql[4 * i + 3], a.w, dl);
-                dh = fmaf(qh[4 * i + 0], b.x, dh); dh = fmaf(qh[4 * i + 1], b.y, dh);
-                dh = fmaf(qh[4 * i + 2], b.z, dh); dh = fmaf(qh[4 * i + 3], b.w, dh);
+            for (int i = 0; i < 16; i++) {
+                dl = fmaf(ql[i], xr[m][i], dl);
+                dh = fmaf(qh[i], xr[m][16 + i], dh);
             }
-            const float gl = gb[m * gst + xo / 16], gh = gb[m * gst + xo / 16 + 2];
             float r = acc[m];
-            r = fmaf(s0, dl, r); r = fmaf(-n0, gl, r);
-            r = fmaf(s1, dh, r); r = fmaf(-n1, gh, r);
+            r = fmaf(s0, dl, r); r = fmaf(-n0, gr[m][0], r);
+            r = fmaf(s1, dh, r); r = fmaf(-n1, gr[m][1], r);
             acc[m] = r;
         }
     }
 };
 
 // Q6_K block (phi4.rs:444-479): {ql[128]; qh[64]; i8 sc[16]; f16 d}.
-// Lane G (0..3) takes half g = G/2 and positions l0 = 16 (G&1) .. l0+15 of it:
+// Part G (0..3) takes half g = G/2 and positions l0 = 16 (G&1) .. l0+15:
 // ql[64g + l0 ..], ql[64g + 32 + l0 ..] and qh[32g + l0 ..], i.e. all four
-// quads of those 16 positions.  Element g*128 + 32u + l uses scale
+// quads u of those positions (span u).  Element g*128 + 32u + l uses scale
 // sc[8g + l/16 + 2u], which is the is = g*8 + l/16 rule of phi4.rs:463.
 // Blocks are 210 bytes, so these 16-byte loads are 2-byte aligned.
 struct DecQ6K {
-    static constexpr uint32_t BS = 210, LPB = 4, BPI = 16;
+    static constexpr uint32_t BS = 210, LPB = 4, BPI = 16, STR = 17;
+    static constexpr int NS = 4, SPAN = 16;
     struct Raw { u32x4 qa, qb, qh; u32x2 sc; uint32_t d; };
     uint32_t g, l0;
-    __device__ explicit DecQ6K(uint32_t lane) : g((lane & 3) >> 1), l0((lane & 1) * 16) {}
-    __device__ static uint32_t slot(uint32_t lane) { return lane >> 2; }
+    __device__ explicit DecQ6K(uint32_t lane) : g((lane / BPI) >> 1), l0(((lane / BPI) & 1) * 16) {}
+    __device__ static uint32_t slot(uint32_t lane) { return lane % BPI; }
+    __device__ uint32_t span_off(int u) const { return 128 * g + l0 + 32 * u; }
     __device__ void load(Raw &w, __amdgpu_buffer_rsrc_t rs, uint32_t boff) const
     {
         w.qa = bload16(rs, boff + 64 * g + l0);
@@ -160,8 +154,7 @@ struct DecQ6K {
         w.d = bload2(rs, boff + 208);
     }
     template <int MT>
-    __device__ void accum(const Raw &w, const float *xb, uint32_t xst, const float *gb, uint32_t gst,
-                          float *acc) const
+    __device__ void accum(const Raw &w, const float (*xr)[NS * SPAN], const float (*gr)[NS], float *acc) const
     {
         const float d = h2f(w.d);
         const uint32_t h = l0 >> 4;
@@ -186,22 +179,16 @@ struct DecQ6K {
                 q[3][4 * i + k] = (float)byte_of(q4, k);
             }
         }
-        const uint32_t xo = 128 * g + l0;
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             float r = acc[m];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const float4 *xv = (const float4 *)(xb + m * xst + xo + 32 * u);
                 float dot = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float4 a = xv[i];
-                    dot = fmaf(q[u][4 * i + 0], a.x, dot); dot = fmaf(q[u][4 * i + 1], a.y, dot);
-                    dot = fmaf(q[u][4 * i + 2], a.z, dot); dot = fmaf(q[u][4 * i + 3], a.w, dot);
-                }
+                for (int i = 0; i < 16; i++) dot = fmaf(q[u][i], xr[m][16 * u + i], dot);
                 // stored values are q + 32 (0..63); remove the offset once per span
-                dot = fmaf(-32.0f, gb[m * gst + (xo + 32 * u) / 16], dot);
+                dot = fmaf(-32.0f, gr[m][u], dot);
                 r = fmaf(ds[u], dot, r);
             }
             acc[m] = r;
@@ -210,33 +197,34 @@ struct DecQ6K {
 };
 
 // F32 rows (matmul_tiled with M=1 on untransposed weights, phi4.rs:641-646,
-// and the row-major logits).  A "block" is 256 floats; lane c (0..15) takes
-// floats 4c + 64i (i = 0..3) so each load instruction covers contiguous 256 B.
+// and the row-major logits).  A "block" is 256 floats; part c (0..15) takes
+// floats 4c + 64i (span i, i = 0..3), so each load instruction covers
+// contiguous 256-byte runs.
 struct DecF32 {
-    static constexpr uint32_t BS = 1024, LPB = 16, BPI = 4;
+    static constexpr uint32_t BS = 1024, LPB = 16, BPI = 4, STR = 4;
+    static constexpr int NS = 4, SPAN = 4;
     struct Raw { u32x4 v[4]; };
     uint32_t c;
-    __device__ explicit DecF32(uint32_t lane) : c(lane & 15) {}
-    __device__ static uint32_t slot(uint32_t lane) { return lane >> 4; }
+    __device__ explicit DecF32(uint32_t lane) : c(lane / BPI) {}
+    __device__ static uint32_t slot(uint32_t lane) { return lane % BPI; }
+    __device__ uint32_t span_off(int i) const { return 4 * c + 64 * i; }
     __device__ void load(Raw &w, __amdgpu_buffer_rsrc_t rs, uint32_t boff) const
     {
 #pragma unroll
         for (int i = 0; i < 4; i++) w.v[i] = bload16(rs, boff + 16 * c + 256 * i);
     }
     template <int MT>
-    __device__ void accum(const Raw &w, const float *xb, uint32_t xst, const float *, uint32_t,
-                          float *acc) const
+    __device__ void accum(const Raw &w, const float (*xr)[NS * SPAN], const float (*)[NS], float *acc) const
     {
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             float r = acc[m];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float4 a = *(const float4 *)(xb + m * xst + 4 * c + 64 * i);
-                r = fmaf(u2f(w.v[i].x), a.x, r);
-                r = fmaf(u2f(w.v[i].y), a.y, r);
-                r = fmaf(u2f(w.v[i].z), a.z, r);
-                r = fmaf(u2f(w.v[i].w), a.w, r);
+                r = fmaf(u2f(w.v[i].x), xr[m][4 * i + 0], r);
+                r = fmaf(u2f(w.v[i].y), xr[m][4 * i + 1], r);
+                r = fmaf(u2f(w.v[i].z), xr[m][4 * i + 2], r);
+                r = fmaf(u2f(w.v[i].w), xr[m][4 * i + 3], r);
             }
             acc[m] = r;
         }
@@ -244,52 +232,80 @@ struct DecF32 {
 };
 
 // ---------------------------------------------------------------------------
-// Activation staging: 16 consecutive values of token m starting at k.
+// Activation sources.  src_load fetches the raw inputs of 16 consecutive
+// activations of token m at k; src_xform turns them into the activations.
+
+struct Src16 {
+    float4 a[4];  // x / gate / gathered V
+    float4 b[4];  // gamma (ACT_RMSNORM) or up (ACT_SILU)
+};
 
 template <int ACT>
-__device__ __forceinline__ void stage16(const GemvArgs &a, uint32_t m, uint32_t k, float inv, float *v)
+__device__ __forceinline__ void src_load(const GemvArgs &a, uint32_t m, uint32_t k, Src16 &s)
 {
-    if constexpr (ACT == ACT_PLAIN) {
-        const float4 *s = (const float4 *)(a.x + (uint64_t)m * a.K + k);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 t = s[i];
-            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-        }
-    } else if constexpr (ACT == ACT_RMSNORM) {
-        const float4 *s = (const float4 *)(a.x + k);
-        const float4 *g = (const float4 *)(a.gamma + k);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 t = s[i], w = g[i];
-            v[4 * i + 0] = __fmul_rn(__fmul_rn(w.x, t.x), inv);
-            v[4 * i + 1] = __fmul_rn(__fmul_rn(w.y, t.y), inv);
-            v[4 * i + 2] = __fmul_rn(__fmul_rn(w.z, t.z), inv);
-            v[4 * i + 3] = __fmul_rn(__fmul_rn(w.w, t.w), inv);
-        }
-    } else if constexpr (ACT == ACT_SILU) {
-        const float4 *gt = (const float4 *)(a.x + k);
-        const float4 *up = (const float4 *)(a.x + a.K + k);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 t = gt[i], u = up[i];
-            v[4 * i + 0] = silu_f(t.x) * u.x;
-            v[4 * i + 1] = silu_f(t.y) * u.y;
-            v[4 * i + 2] = silu_f(t.z) * u.z;
-            v[4 * i + 3] = silu_f(t.w) * u.w;
-        }
-    } else {  // ACT_GQA_V: 16 | head_dim, so the 16 values are contiguous
+    const float4 *pa;
+    if constexpr (ACT == ACT_GQA_V) {
+        // 16 | head_dim, so the 16 gathered values are contiguous
         const uint32_t hd = a.head_dim, hpk = a.heads_per_kv;
-        const uint32_t src = a.K + a.K / hpk + (k / (hd * hpk)) * hd + k % hd;
-        const float4 *s = (const float4 *)(a.x + src);
+        pa = (const float4 *)(a.x + a.K + a.K / hpk + (k / (hd * hpk)) * hd + k % hd);
+    } else {
+        pa = (const float4 *)(a.x + (uint64_t)m * a.K + k);
+    }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 t = s[i];
-            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    for (int i = 0; i < 4; i++) s.a[i] = pa[i];
+    if constexpr (ACT == ACT_RMSNORM) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) s.b[i] = ((const float4 *)(a.gamma + k))[i];
+    } else if constexpr (ACT == ACT_SILU) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) s.b[i] = ((const float4 *)(a.x + a.K + k))[i];
+    }
+}
+
+// sum of squares of the 16 raw values in order (the canonical RMSNorm order)
+__device__ __forceinline__ float src_sumsq(const Src16 &s, float acc)
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        acc = __builtin_fmaf(s.a[i].x, s.a[i].x, acc);
+        acc = __builtin_fmaf(s.a[i].y, s.a[i].y, acc);
+        acc = __builtin_fmaf(s.a[i].z, s.a[i].z, acc);
+        acc = __builtin_fmaf(s.a[i].w, s.a[i].w, acc);
+    }
+    return acc;
+}
+
+template <int ACT>
+__device__ __forceinline__ void src_xform(const Src16 &s, float inv, float4 *v)
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 x = s.a[i];
+        if constexpr (ACT == ACT_RMSNORM) {
+            const float4 w = s.b[i];
+            v[i] = make_float4(__fmul_rn(__fmul_rn(w.x, x.x), inv), __fmul_rn(__fmul_rn(w.y, x.y), inv),
+                               __fmul_rn(__fmul_rn(w.z, x.z), inv), __fmul_rn(__fmul_rn(w.w, x.w), inv));
+        } else if constexpr (ACT == ACT_SILU) {
+            const float4 u = s.b[i];
+            v[i] = make_float4(silu_f(x.x) * u.x, silu_f(x.y) * u.y, silu_f(x.z) * u.z, silu_f(x.w) * u.w);
+        } else {
+            v[i] = x;
         }
     }
 }
 
+__device__ __forceinline__ float sum16(const float4 *v)
+{
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    return s;
+}
+
+// ---------------------------------------------------------------------------
+// General kernel: M >= 1 token rows in tiles of MT, K streamed through LDS in
+// chunks of KC with a contiguous layout (xs[m*KC + k]).  Used for batched
+// GEMV, rows longer than four wave iterations and the tall F32 logits.
 template <class Dec, int R, int MT, int ACT>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a, uint32_t KC)
 {
@@ -329,21 +345,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a, uint32_t KC)
         __syncthreads();
         for (uint32_t gi = t; gi < (uint32_t)MT * ng; gi += 256) {
             const uint32_t m = gi / ng, gg = gi - m * ng;
-            float v[16];
+            float4 v[4];
             if (m < mt) {
-                stage16<ACT>(a, m0 + m, kc0 + 16 * gg, inv, v);
+                Src16 sv;
+                src_load<ACT>(a, m0 + m, kc0 + 16 * gg, sv);
+                src_xform<ACT>(sv, inv, v);
             } else {
 #pragma unroll
-                for (int i = 0; i < 16; i++) v[i] = 0.0f;
+                for (int i = 0; i < 4; i++) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
-            float s = 0.0f;
             float4 *dst = (float4 *)(xs + m * KC + 16 * gg);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                dst[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-                s += (v[4 * i] + v[4 * i + 1]) + (v[4 * i + 2] + v[4 * i + 3]);
-            }
-            gs[m * (KC / 16) + gg] = s;
+            for (int i = 0; i < 4; i++) dst[i] = v[i];
+            gs[m * (KC / 16) + gg] = sum16(v);
         }
         __syncthreads();
 
@@ -356,10 +370,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a, uint32_t KC)
                 for (int r = 0; r < R; r++)
                     if (row0 + r < a.N)
                         dec.load(raw[r], rs, (uint32_t)((uint64_t)(wave * R + r) * row_bytes + (uint64_t)(bg0 + bl) * Dec::BS));
+                float xr[MT][Dec::NS * Dec::SPAN], gr[MT][Dec::NS];
+#pragma unroll
+                for (int m = 0; m < MT; m++)
+#pragma unroll
+                    for (int j = 0; j < Dec::NS; j++) {
+                        const uint32_t o = bl * 256 + dec.span_off(j);
+#pragma unroll
+                        for (int i = 0; i < Dec::SPAN / 4; i++) {
+                            const float4 f = *(const float4 *)(xs + m * KC + o + 4 * i);
+                            xr[m][j * Dec::SPAN + 4 * i] = f.x; xr[m][j * Dec::SPAN + 4 * i + 1] = f.y;
+                            xr[m][j * Dec::SPAN + 4 * i + 2] = f.z; xr[m][j * Dec::SPAN + 4 * i + 3] = f.w;
+                        }
+                        gr[m][j] = gs[m * (KC / 16) + o / 16];
+                    }
 #pragma unroll
                 for (int r = 0; r < R; r++)
-                    if (row0 + r < a.N)
-                        dec.template accum<MT>(raw[r], xs + bl * 256, KC, gs + bl * 16, KC / 16, acc[r]);
+                    if (row0 + r < a.N) dec.template accum<MT>(raw[r], xr, gr, acc[r]);
             }
         }
     }
@@ -373,6 +400,129 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a, uint32_t KC)
                 float *yp = a.y + (uint64_t)(m0 + m) * a.N + row0 + r;
                 *yp = a.residual ? *yp + v : v;
             }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Batch-1 kernel for rows of at most IT wave iterations (every decode-path
+// GEMV).  Order of work per workgroup:
+//   1. thread t fetches the raw inputs of activation float4s t, t + 256, ...
+//      (coalesced; L2 hits after the first workgroup of an XCD);
+//   2. every wave issues ALL of its weight loads, so HBM latency overlaps the
+//      staging (vmcnt retires in order, which is why the activation loads go
+//      first);
+//   3. the fused RMSNorm reduces the sum of squares of those registers in the
+//      canonical float4 order of thread_sumsq; activations are transformed,
+//      written to LDS, and their 16-element sums formed with two lane
+//      shuffles ((f0 + f1) + (f2 + f3) over the four float4s of a group);
+//   4. per iteration each lane reads its spans from LDS once and runs the dot
+//      products for its R rows as the weight loads land.
+// LDS layout: activations interleaved by block at float4 granularity,
+//   xs4[(I * 64 + q) * STR + s]  for block b = I * BPI + s, elements 4q..4q+3,
+// so the lanes of one LDS read (consecutive slots s) touch consecutive
+// float4s; STR pads each row so that the staging writes (consecutive q) and
+// the reads of different parts fall on different banks.
+// Partial sums: gs[(I * 16 + o / 16) * BPI + s].
+
+template <class Dec, int R, int IT, int ACT>
+__global__ __launch_bounds__(256) void gemv_pf_kernel(GemvArgs a)
+{
+    extern __shared__ float smem[];
+    constexpr uint32_t BPI = Dec::BPI, STR = Dec::STR;
+    constexpr int JF = IT * BPI / 4;  // activation float4s per thread: K <= IT * BPI * 256
+    const uint32_t K = a.K;
+    float4 *xs4 = (float4 *)smem;                               // IT * 64 * STR float4
+    float *gs = smem + 4 * IT * 64 * STR;                       // IT * 16 * BPI
+    float *red = gs + IT * 16 * BPI;                            // 4
+
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t wg_row0 = blockIdx.x * (4 * R);
+    const uint32_t row0 = wg_row0 + wave * R;
+    const uint32_t B = K / 256, NF = K / 4;
+    const uint64_t row_bytes = (uint64_t)B * Dec::BS;
+    const uint64_t wg_off = (uint64_t)wg_row0 * row_bytes;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.W + wg_off, a.w_bytes > wg_off ? a.w_bytes - wg_off : 0);
+    const Dec dec(lane);
+    const uint32_t slot = Dec::slot(lane);
+
+    // 1. activation inputs (NF is a multiple of 64, so each guard is wave-uniform)
+    float4 xa[JF], xb[JF];
+#pragma unroll
+    for (int j = 0; j < JF; j++)
+        if (t + 256u * j < NF) src_load4<ACT>(a, 4 * (t + 256u * j), xa[j], xb[j]);
+
+    // 2. all weight loads of this wave
+    typename Dec::Raw raw[IT][R];
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const uint32_t bl = it * BPI + slot;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (bl < B && row0 + r < a.N)
+                dec.load(raw[it][r], rs, (uint32_t)((uint64_t)(wave * R + r) * row_bytes + (uint64_t)bl * Dec::BS));
+    }
+
+    // 3. RMSNorm scale, transform, stage
+    float inv = 1.0f;
+    if constexpr (ACT == ACT_RMSNORM) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < JF; j++)
+            if (t + 256u * j < NF) {
+                acc = __builtin_fmaf(xa[j].x, xa[j].x, acc);
+                acc = __builtin_fmaf(xa[j].y, xa[j].y, acc);
+                acc = __builtin_fmaf(xa[j].z, xa[j].z, acc);
+                acc = __builtin_fmaf(xa[j].w, xa[j].w, acc);
+            }
+        inv = rms_inv(block_sum_256(acc, red), K, a.eps);
+    }
+#pragma unroll
+    for (int j = 0; j < JF; j++) {
+        const uint32_t f = t + 256u * j;
+        if (f < NF) {
+            const float4 v = xform4<ACT>(xa[j], xb[j], inv);
+            const uint32_t b = f / 64, q = f % 64, I = b / BPI, s = b % BPI;
+            xs4[(I * 64 + q) * STR + s] = v;
+            float sv = (v.x + v.y) + (v.z + v.w);
+            sv = sv + __shfl_xor(sv, 1, 64);
+            sv = sv + __shfl_xor(sv, 2, 64);
+            if ((t & 3) == 0) gs[(I * 16 + q / 4) * BPI + s] = sv;
+        }
+    }
+    __syncthreads();
+
+    // 4. dot products
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const uint32_t bl = it * BPI + slot;
+        if (bl < B) {
+            float xr[1][Dec::NS * Dec::SPAN], gr[1][Dec::NS];
+#pragma unroll
+            for (int j = 0; j < Dec::NS; j++) {
+                const uint32_t o = dec.span_off(j);
+#pragma unroll
+                for (int i = 0; i < Dec::SPAN / 4; i++) {
+                    const float4 fv = xs4[(it * 64 + o / 4 + i) * STR + slot];
+                    xr[0][j * Dec::SPAN + 4 * i] = fv.x; xr[0][j * Dec::SPAN + 4 * i + 1] = fv.y;
+                    xr[0][j * Dec::SPAN + 4 * i + 2] = fv.z; xr[0][j * Dec::SPAN + 4 * i + 3] = fv.w;
+                }
+                gr[0][j] = gs[(it * 16 + o / 16) * BPI + slot];
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (row0 + r < a.N) dec.template accum<1>(raw[it][r], xr, gr, &acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float v = wave_sum(acc[r]);
+        if (lane == 0 && row0 + r < a.N) {
+            float *yp = a.y + row0 + r;
+            *yp = a.residual ? *yp + v : v;
         }
     }
 }
@@ -402,10 +552,40 @@ static hipError_t go(const GemvArgs &a, hipStream_t s)
     return hipGetLastError();
 }
 
+template <class Dec, int R, int IT, int ACT>
+static hipError_t go_pf(const GemvArgs &a, hipStream_t s)
+{
+    const size_t lds = ((size_t)4 * IT * 64 * Dec::STR + (size_t)IT * 16 * Dec::BPI + 4) * sizeof(float);
+    const dim3 grid((a.N + 4 * R - 1) / (4 * R));
+    hipLaunchKernelGGL((gemv_pf_kernel<Dec, R, IT, ACT>), grid, dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+template <class Dec, int R, int ACT>
+static hipError_t go_pf_it(const GemvArgs &a, hipStream_t s)
+{
+    const uint32_t it = (a.K / 256 + Dec::BPI - 1) / Dec::BPI;
+    if (it <= 1) return go_pf<Dec, R, 1, ACT>(a, s);
+    if (it <= 2) return go_pf<Dec, R, 2, ACT>(a, s);
+    return go_pf<Dec, R, 4, ACT>(a, s);
+}
+
+// Rows per wave: about two workgroups per CU where N allows.  Batch-1 shapes
+// whose rows fit in at most four wave iterations (every decode-path GEMV)
+// take the load-first kernel; longer rows and very tall F32 matrices (the
+// logits) stream through the chunked loop kernel.
 template <class Dec, int ACT>
 static hipError_t go_rows(const GemvArgs &a, hipStream_t s)
 {
-    // Rows per wave: enough workgroups to cover 256 CUs twice where N allows.
+    const uint32_t it = (a.K / 256 + Dec::BPI - 1) / Dec::BPI;
+    const uint32_t it_inst = it <= 1 ? 1 : it <= 2 ? 2 : 4;
+    const size_t lds = ((size_t)4 * it_inst * 64 * Dec::STR + (size_t)it_inst * 16 * Dec::BPI + 4) * sizeof(float);
+    const bool f32 = Dec::BS == 1024;
+    if (it <= 4 && lds <= 65536 && !(f32 && a.N > 16384)) {
+        if (a.N >= 12288 && !f32) return go_pf_it<Dec, 4, ACT>(a, s);
+        if (a.N >= 2048) return go_pf_it<Dec, 2, ACT>(a, s);
+        return go_pf_it<Dec, 1, ACT>(a, s);
+    }
     if (a.N >= 16384) return go<Dec, 4, 1, ACT>(a, s);
     if (a.N >= 2048) return go<Dec, 2, 1, ACT>(a, s);
     return go<Dec, 1, 1, ACT>(a, s);
@@ -430,6 +610,7 @@ static hipError_t go_type(const GemvArgs &a, uint32_t act, hipStream_t s)
 
 hipError_t launch_gemv(const GemvArgs &a, uint32_t act, hipStream_t s)
 {
+    if (gemv_mfma_supported(a)) return launch_gemv_mfma(a, act, s);
     switch (a.type) {
     case T_Q4_K: return go_type<DecQ4K>(a, act, s);
     case T_Q5_K: return go_type<DecQ5K>(a, act, s);

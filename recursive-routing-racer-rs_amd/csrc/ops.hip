@@ -89,8 +89,37 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     __shared__ float red[4];
     const float *xr = x + (uint64_t)blockIdx.x * d;
     float *yr = y + (uint64_t)blockIdx.x * d;
+    const uint32_t t = threadIdx.x;
+    if (d % 4 == 0 && d <= 8 * 4 * 256) {
+        // the row stays in registers (one pass over x); thread t owns the
+        // float4s t, t + 256, ..., the canonical order of thread_sumsq
+        float4 v[8];
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t f = t + 256u * j;
+            if (f < d / 4) {
+                v[j] = ((const float4 *)xr)[f];
+                acc = __builtin_fmaf(v[j].x, v[j].x, acc);
+                acc = __builtin_fmaf(v[j].y, v[j].y, acc);
+                acc = __builtin_fmaf(v[j].z, v[j].z, acc);
+                acc = __builtin_fmaf(v[j].w, v[j].w, acc);
+            }
+        }
+        const float inv = rms_inv(block_sum_256(acc, red), d, eps);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t f = t + 256u * j;
+            if (f < d / 4) {
+                const float4 w = ((const float4 *)g)[f];
+                ((float4 *)yr)[f] = make_float4(__fmul_rn(__fmul_rn(w.x, v[j].x), inv), __fmul_rn(__fmul_rn(w.y, v[j].y), inv),
+                                                __fmul_rn(__fmul_rn(w.z, v[j].z), inv), __fmul_rn(__fmul_rn(w.w, v[j].w), inv));
+            }
+        }
+        return;
+    }
     const float inv = rms_inv(block_sumsq_256(xr, d, red), d, eps);
-    for (uint32_t i = threadIdx.x; i < d; i += 256) yr[i] = __fmul_rn(__fmul_rn(g[i], xr[i]), inv);
+    for (uint32_t i = t; i < d; i += 256) yr[i] = __fmul_rn(__fmul_rn(g[i], xr[i]), inv);
 }
 
 hipError_t launch_rmsnorm(const float *x, const float *g, float *y, uint32_t rows, uint32_t d, float eps,
