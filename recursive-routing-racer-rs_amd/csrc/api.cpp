@@ -258,7 +258,9 @@ int rrr_buf_alloc(rrr_ctx *ctx, uint64_t bytes, rrr_buf **out)
     void *p = nullptr;
     if (!ctx->nodevice) {
         TRY(device_ready(ctx));
-        hipError_t e = hipMalloc(&p, bytes);
+        // read slack for kernels, rounded to whole 256-byte lines
+        const uint64_t alloc = (bytes + RRR_READ_SLACK + 255) & ~255ull;
+        hipError_t e = hipMalloc(&p, alloc);
         if (e != hipSuccess) return fail(RRR_ERR_HIP, "hipMalloc(%llu): %s", (unsigned long long)bytes, hipGetErrorString(e));
     }
     rrr_buf *b = new rrr_buf{BUF_MAGIC, ctx, p, bytes, nullptr};

@@ -12,28 +12,40 @@
 // below 2^-20 of the group maximum.
 //
 // Weights.  A K-quant super-block stores small integers q (Q4_K 0..15,
-// Q5_K 0..31, Q6_K 0..63 with an offset of 32) and per-sub-block f32 scales.
-// The raw q bytes go straight into the MFMA B operand; the integer dot
+// Q5_K 0..31, Q6_K 0..63 with an offset of 32) and per-sub-block scales.
+// The raw q values go straight into the MFMA B operand; the integer dot
 // products C_t = sum q * d_t (t = 0, 1, 2) are exact, and
 //     sum_k q_k x_k = 2^(E-14) * (C_0 * 2^14 + C_1 * 2^7 + C_2)
 // is recombined in int32 (no overflow: |C_t| < 2^16) and scaled once per
-// 16 elements by (sub-block scale) * 2^(E-14).  The Q4_K / Q5_K min term
-// uses the f32 16-element sums of x; the Q6_K offset uses the digit sums.
+// 16 elements.  The Q6_K offset (q - 32) is folded into the MFMA accumulator
+// input as -32 * (digit sums of the group); the Q4_K / Q5_K min term uses the
+// f32 16-element sums of x.
 //
 // MFMA mapping (16x16x64, lane l: A row l%16, B column l%16, k-group l/16;
-// D rows 4*(l/16)+r of column l%16 in register r):
+// C/D rows 4*(l/16)+r of column l%16 in register r):
 //   B[k][n]  = q of weight row n (16 rows per workgroup) at k-set K_g,
 //   A[m][k]  = digit (m%4) of x at K_g when m/4 == g (and m%4 < 3), else 0,
-// so lane (n, g) receives its own three partial dot products C_0..C_2 for row
-// n and k-set K_g in registers 0..2.  Each lane's k-set is 16 consecutive
-// elements with one scale, so the scale is applied per lane after the MFMA.
+//   C[4g+r][n] = group constants of K_g: r < 3 the offset term, r = 3 the
+//                group factor 2^(E-14) (bit pattern; A row 4g+3 is zero, so
+//                it comes back unchanged in D),
+// so lane (n, g) receives its own three partial dot products for row n and
+// k-set K_g in registers 0..2 and the factor in register 3.  Each lane's
+// k-set is 16 consecutive elements with one scale, applied after the MFMA.
 //
-// Work split: one workgroup per 16-row tile; its W waves take super-blocks
-// b = w, w + W, ... (split K) and issue all their weight loads before the
-// activation staging; the per-wave partials are added in wave order.
+// Work split: one workgroup per 16-row tile; wave w owns super-blocks
+// [w*BPW, w*BPW + BPW) of the 16 rows.  A wave streams its 16 row pieces
+// with 16-byte loads on consecutive lanes (contiguous runs of BPW blocks per
+// row), encodes its own slice of x, stages both in its private LDS region and
+// runs its MFMAs as soon as its own data has landed -- no workgroup barrier
+// until the final cross-wave sum (plus one for the fused RMSNorm scale).
 #include "act.h"
 
 namespace rrr {
+
+__device__ __forceinline__ u32x4 lds16(const uint8_t *L, uint32_t o)
+{
+    return *(const u32x4 *)(L + o);
+}
 
 // Q4_K (phi4.rs:481-510).  Lane group g takes qs pair g (bytes 32g..32g+31):
 // low nibbles = sub-block 2g, high nibbles = sub-block 2g+1.
@@ -41,27 +53,30 @@ namespace rrr {
 //   u = 1: low nibbles of bytes 16..31  (64g + 16..31)
 //   u = 2: high nibbles of bytes 0..15  (64g + 32..47)
 //   u = 3: high nibbles of bytes 16..31 (64g + 48..63)
+// Block value = d * sum_u sc[u] * S_u - dmin * sum_u mn[u] * X_u.
 struct MqQ4K {
     static constexpr uint32_t BS = 144;
     static constexpr bool HAS_MIN = true, OFF32 = false;
     struct Raw { u32x4 hdr, qs0, qs1; };
     __device__ static uint32_t koff(uint32_t g, int u) { return 64 * g + 16 * u; }
-    __device__ static void load(Raw &w, __amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t g)
+    // o: LDS offset of the 16-byte aligned block piece
+    __device__ static void load(Raw &w, const uint8_t *L, uint32_t o, uint32_t g)
     {
-        w.hdr = bload16(rs, boff);
-        w.qs0 = bload16(rs, boff + 16 + 32 * g);
-        w.qs1 = bload16(rs, boff + 32 + 32 * g);
+        w.hdr = lds16(L, o);
+        w.qs0 = lds16(L, o + 16 + 32 * g);
+        w.qs1 = lds16(L, o + 32 + 32 * g);
     }
-    __device__ static void decode(const Raw &w, uint32_t g, i32x4 *bq, float *sc, float *mn)
+    __device__ static void decode(const Raw &w, uint32_t g, i32x4 *bq, float *sc, float *mn, float &d, float &dmin)
     {
-        const float d = h2f(w.hdr.x), dmin = h2f(w.hdr.x >> 16);
+        d = h2f(w.hdr.x);
+        dmin = h2f(w.hdr.x >> 16);
         uint32_t s0, m0, s1, m1;
         scale_min_k4(2 * g, w.hdr.y, w.hdr.z, w.hdr.w, s0, m0);
         scale_min_k4(2 * g + 1, w.hdr.y, w.hdr.z, w.hdr.w, s1, m1);
-        sc[0] = sc[1] = d * (float)s0;
-        sc[2] = sc[3] = d * (float)s1;
-        mn[0] = mn[1] = dmin * (float)m0;
-        mn[2] = mn[3] = dmin * (float)m1;
+        sc[0] = sc[1] = (float)s0;
+        sc[2] = sc[3] = (float)s1;
+        mn[0] = mn[1] = (float)m0;
+        mn[2] = mn[3] = (float)m1;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             bq[0][i] = (int)(w.qs0[i] & 0x0F0F0F0Fu);
@@ -78,24 +93,25 @@ struct MqQ5K {
     static constexpr bool HAS_MIN = true, OFF32 = false;
     struct Raw { u32x4 hdr, qh0, qh1, qs0, qs1; };
     __device__ static uint32_t koff(uint32_t g, int u) { return 64 * g + 16 * u; }
-    __device__ static void load(Raw &w, __amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t g)
+    __device__ static void load(Raw &w, const uint8_t *L, uint32_t o, uint32_t g)
     {
-        w.hdr = bload16(rs, boff);
-        w.qh0 = bload16(rs, boff + 16);
-        w.qh1 = bload16(rs, boff + 32);
-        w.qs0 = bload16(rs, boff + 48 + 32 * g);
-        w.qs1 = bload16(rs, boff + 64 + 32 * g);
+        w.hdr = lds16(L, o);
+        w.qh0 = lds16(L, o + 16);
+        w.qh1 = lds16(L, o + 32);
+        w.qs0 = lds16(L, o + 48 + 32 * g);
+        w.qs1 = lds16(L, o + 64 + 32 * g);
     }
-    __device__ static void decode(const Raw &w, uint32_t g, i32x4 *bq, float *sc, float *mn)
+    __device__ static void decode(const Raw &w, uint32_t g, i32x4 *bq, float *sc, float *mn, float &d, float &dmin)
     {
-        const float d = h2f(w.hdr.x), dmin = h2f(w.hdr.x >> 16);
+        d = h2f(w.hdr.x);
+        dmin = h2f(w.hdr.x >> 16);
         uint32_t s0, m0, s1, m1;
         scale_min_k4(2 * g, w.hdr.y, w.hdr.z, w.hdr.w, s0, m0);
         scale_min_k4(2 * g + 1, w.hdr.y, w.hdr.z, w.hdr.w, s1, m1);
-        sc[0] = sc[1] = d * (float)s0;
-        sc[2] = sc[3] = d * (float)s1;
-        mn[0] = mn[1] = dmin * (float)m0;
-        mn[2] = mn[3] = dmin * (float)m1;
+        sc[0] = sc[1] = (float)s0;
+        sc[2] = sc[3] = (float)s1;
+        mn[0] = mn[1] = (float)m0;
+        mn[2] = mn[3] = (float)m1;
         const uint32_t lo = 2 * g, hi = 2 * g + 1;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -111,29 +127,30 @@ struct MqQ5K {
 // l0 = 16 (g&1) .. l0+15; quad u of those positions (elements
 // 128 g6 + 32 u + l) is MFMA u and uses scale sc[8 g6 + l0/16 + 2u], the
 // is = g*8 + l/16 rule of phi4.rs:463.  Stored values q + 32 (0..63) enter the
-// MFMA unsigned; the offset is removed with the digit sums.
+// MFMA unsigned; the offset comes in through the accumulator input.
 struct MqQ6K {
     static constexpr uint32_t BS = 210;
     static constexpr bool HAS_MIN = false, OFF32 = true;
     struct Raw { u32x4 qa, qb, qh; u32x2 sc; uint32_t d; };
     __device__ static uint32_t koff(uint32_t g, int u) { return 128 * (g >> 1) + 32 * u + 16 * (g & 1); }
-    __device__ static void load(Raw &w, __amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t g)
+    // o: LDS offset of the block piece, staged 16-byte aligned
+    __device__ static void load(Raw &w, const uint8_t *L, uint32_t o, uint32_t g)
     {
         const uint32_t g6 = g >> 1, l0 = 16 * (g & 1);
-        w.qa = bload16(rs, boff + 64 * g6 + l0);
-        w.qb = bload16(rs, boff + 64 * g6 + 32 + l0);
-        w.qh = bload16(rs, boff + 128 + 32 * g6 + l0);
-        w.sc = __builtin_amdgcn_raw_buffer_load_b64(rs, boff + 192 + 8 * g6, 0, 0);
-        w.d = bload2(rs, boff + 208);
+        w.qa = lds16(L, o + 64 * g6 + l0);
+        w.qb = lds16(L, o + 64 * g6 + 32 + l0);
+        w.qh = lds16(L, o + 128 + 32 * g6 + l0);
+        w.sc = *(const u32x2 *)(L + o + 192 + 8 * g6);
+        w.d = *(const uint16_t *)(L + o + 208);
     }
-    __device__ static void decode(const Raw &w, uint32_t g, i32x4 *bq, float *sc, float *)
+    __device__ static void decode(const Raw &w, uint32_t g, i32x4 *bq, float *sc, float *, float &d, float &)
     {
-        const float d = h2f(w.d);
+        d = h2f(w.d);
         const uint32_t h = g & 1;
-        sc[0] = d * (float)(int8_t)byte_of(w.sc.x, h);
-        sc[1] = d * (float)(int8_t)byte_of(w.sc.x, h + 2);
-        sc[2] = d * (float)(int8_t)byte_of(w.sc.y, h);
-        sc[3] = d * (float)(int8_t)byte_of(w.sc.y, h + 2);
+        sc[0] = (float)(int8_t)byte_of(w.sc.x, h);
+        sc[1] = (float)(int8_t)byte_of(w.sc.x, h + 2);
+        sc[2] = (float)(int8_t)byte_of(w.sc.y, h);
+        sc[3] = (float)(int8_t)byte_of(w.sc.y, h + 2);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t a = w.qa[i], b = w.qb[i], hh = w.qh[i];
@@ -145,13 +162,14 @@ struct MqQ6K {
     }
 };
 
-// Digits of one float4 of activations: returns the three digit planes packed
-// four int8 per dword, and the integer sum of d0*2^14 + d1*2^7 + d2.
-__device__ __forceinline__ void encode4(const float4 &v, int e, uint32_t &p0, uint32_t &p1, uint32_t &p2, int &dsum)
+// Digits of one float4 of activations: the three digit planes packed four
+// int8 per dword, and the per-plane digit sums.
+__device__ __forceinline__ void encode4(const float4 &v, int e, uint32_t &p0, uint32_t &p1, uint32_t &p2, int &s0,
+                                        int &s1, int &s2)
 {
     const float c[4] = {v.x, v.y, v.z, v.w};
     p0 = p1 = p2 = 0u;
-    dsum = 0;
+    s0 = s1 = s2 = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float xs = ldexpf(c[i], -e);
@@ -164,121 +182,201 @@ __device__ __forceinline__ void encode4(const float4 &v, int e, uint32_t &p0, ui
         p0 |= ((uint32_t)i0 & 255u) << (8 * i);
         p1 |= ((uint32_t)i1 & 255u) << (8 * i);
         p2 |= ((uint32_t)i2 & 255u) << (8 * i);
-        dsum += i0 * 16384 + i1 * 128 + i2;
+        s0 += i0;
+        s1 += i1;
+        s2 += i2;
     }
 }
 
-template <class Q, int W, int NBW, int ACT>
-__global__ __launch_bounds__(64 * W) void gemv_mq_kernel(GemvArgs a)
+// Wave-private LDS layout of one wave (BPW super-blocks of 16 rows):
+//   weights: 16 rows x RS bytes, block j of row r at r*RS + j*LB (16-byte
+//            aligned pieces of UPB units; Q6_K pieces carry 14 bytes of the
+//            next block in their last unit)
+//   digits:  3 planes x DG bytes (plane p, local element e at p*DG + e)
+//   aux:     per 16-element group 16 bytes = MFMA accumulator input
+//            {-32*S0, -32*S1, -32*S2 (Q6_K only, else 0), bits of 2^(E-14)}
+//   gsum:    per group the f32 sum of x (Q4_K / Q5_K min term)
+template <class Q, int BPW>
+struct MwGeom {
+    static constexpr uint32_t UPB = (Q::BS + 15) / 16;            // 16-byte units per block piece
+    static constexpr uint32_t LB = 16 * UPB;
+    static constexpr uint32_t RS = (BPW * LB) % 32 == 0 ? BPW * LB + 16 : BPW * LB;  // odd multiple of 16
+    static constexpr uint32_t NU = 16 * BPW * UPB;                 // units per wave
+    static constexpr int S = (NU + 63) / 64;                       // unit slots per lane
+    static constexpr uint32_t DG = BPW * 256;
+    static constexpr uint32_t NGW = BPW * 16;
+    static constexpr uint32_t D_OFF = 16 * RS;
+    static constexpr uint32_t A_OFF = D_OFF + 3 * DG;
+    static constexpr uint32_t G_OFF = A_OFF + 16 * NGW;
+    static constexpr uint32_t BYTES = G_OFF + 4 * NGW;            // multiple of 16
+};
+
+// Sum of squares of x[0..K) in the order of the standalone RMSNorm kernel
+// (thread t < 256 owns float4s t, t + 256, ...; wave butterfly; waves 0..3
+// added in order), so the fused scale is bitwise that kernel's.  cx[j] holds
+// float4 t + 256 j (loaded earlier, index clamped).  Needs at least 4 waves;
+// every thread must call it (one barrier).
+template <int NSQ>
+__device__ __forceinline__ float canonical_sumsq(const float4 *cx, uint32_t K, float *red)
+{
+    const uint32_t t = threadIdx.x;
+    float acc = 0.0f;
+    if (t < 256) {
+#pragma unroll
+        for (int j = 0; j < NSQ; j++)
+            if (t + 256 * j < K / 4) {
+                acc = __builtin_fmaf(cx[j].x, cx[j].x, acc);
+                acc = __builtin_fmaf(cx[j].y, cx[j].y, acc);
+                acc = __builtin_fmaf(cx[j].z, cx[j].z, acc);
+                acc = __builtin_fmaf(cx[j].w, cx[j].w, acc);
+            }
+    }
+    acc = wave_sum(acc);
+    if (t < 256 && (t & 63) == 0) red[t >> 6] = acc;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <class Q, int BPW, int ACT>
+__global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a)
 {
     extern __shared__ float smem[];
-    const uint32_t K = a.K, B = K / 256, NF = K / 4, NG = K / 16;
-    constexpr uint32_t NT = 64 * W;                 // threads per workgroup
-    constexpr int JF = (NBW * W * 64 + NT - 1) / NT; // activation float4s per thread: K <= W * NBW * 256
-    uint8_t *dg = (uint8_t *)smem;                       // 3 digit planes of K bytes + 16 zero bytes
-    float *fac = (float *)(dg + 3 * K + 16);             // NG: 2^(E-14) per group
-    float *gsum = fac + NG;                              // NG: f32 sums (Q4_K/Q5_K) or int digit sums (Q6_K)
-    float *red = gsum + NG;                              // W
-    float *part = red + W;                               // W x 16 per-wave row partials
-
+    using G = MwGeom<Q, BPW>;
+    const uint32_t K = a.K, B = K / 256;
+    const uint32_t W = blockDim.x >> 6;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t n = lane & 15, g = lane >> 4;
+    uint8_t *L = (uint8_t *)smem + wave * G::BYTES;              // this wave's region
+    float *red = (float *)((uint8_t *)smem + W * G::BYTES);      // 4
+    float *part = red + 4;                                       // W x 16
+
     const uint32_t row0 = blockIdx.x * 16;
     const uint64_t row_bytes = (uint64_t)B * Q::BS;
     const uint64_t wg_off = (uint64_t)row0 * row_bytes;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.W + wg_off, a.w_bytes > wg_off ? a.w_bytes - wg_off : 0);
+    // every buffer has RRR_READ_SLACK readable bytes past its end: a Q6_K
+    // piece's last unit runs 14 bytes past its block
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(a.W + wg_off, a.w_bytes > wg_off ? a.w_bytes - wg_off + RRR_READ_SLACK : 0);
+    const uint32_t b0 = wave * BPW;                              // first super-block of this wave
+    const uint32_t nb = b0 < B ? min((uint32_t)BPW, B - b0) : 0u;
 
-    // 1. activation inputs (NF is a multiple of 64: each guard is wave-uniform)
-    float4 xa[JF], xb[JF];
-#pragma unroll
-    for (int j = 0; j < JF; j++)
-        if (t + NT * j < NF) src_load4<ACT>(a, 4 * (t + NT * j), xa[j], xb[j]);
-
-    // 2. all weight loads of this wave: blocks wave, wave + W, ...
-    typename Q::Raw raw[NBW];
-#pragma unroll
-    for (int i = 0; i < NBW; i++) {
-        const uint32_t b = wave + W * i;
-        if (b < B) Q::load(raw[i], rs, (uint32_t)(n * row_bytes + (uint64_t)b * Q::BS), g);
-    }
-
-    // 3. activation staging: RMSNorm scale, transform, int8 digits
-    float inv = 1.0f;
+    // The loads below are unconditional (clamped indices): loads under a
+    // branch make the compiler wait for every outstanding load at the join.
+    // 0. fused RMSNorm: the whole of x in the canonical order (K <= 1024 NSQ)
+    constexpr int NSQ = ACT == ACT_RMSNORM ? 4 * BPW : 1;
+    float4 cx[NSQ];
     if constexpr (ACT == ACT_RMSNORM) {
-        float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < JF; j++)
-            if (t + NT * j < NF) {
-                acc = __builtin_fmaf(xa[j].x, xa[j].x, acc);
-                acc = __builtin_fmaf(xa[j].y, xa[j].y, acc);
-                acc = __builtin_fmaf(xa[j].z, xa[j].z, acc);
-                acc = __builtin_fmaf(xa[j].w, xa[j].w, acc);
-            }
-        inv = rms_inv(block_sum_w<W>(acc, red), K, a.eps);
+        for (int j = 0; j < NSQ; j++) cx[j] = ((const float4 *)a.x)[min(t + 256 * j, K / 4 - 1)];
     }
-    if (t < 4) ((uint32_t *)(dg + 3 * K))[t] = 0u;
+    // 1. this wave's activation inputs: float4 lane + 64 j of its slice
+    float4 xa[BPW], xb[BPW];
 #pragma unroll
-    for (int j = 0; j < JF; j++) {
-        const uint32_t f = t + NT * j;
-        if (f < NF) {
-            const float4 v = xform4<ACT>(xa[j], xb[j], inv);
-            float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-            int e = 0;
-            if (mx > 0.0f && __builtin_isfinite(mx)) {
-                int ex;
-                (void)frexpf(mx, &ex);
-                e = ex - 6;  // mx / 2^e in [32, 64)
-            }
-            uint32_t p0, p1, p2;
-            int ds;
-            encode4(v, e, p0, p1, p2, ds);
-            ((uint32_t *)dg)[f] = p0;
-            ((uint32_t *)(dg + K))[f] = p1;
-            ((uint32_t *)(dg + 2 * K))[f] = p2;
-            if constexpr (Q::OFF32) {
-                ds = ds + __shfl_xor(ds, 1, 64);
-                ds = ds + __shfl_xor(ds, 2, 64);
-                if ((t & 3) == 0) ((int *)gsum)[f / 4] = ds;
-            } else {
-                float sv = (v.x + v.y) + (v.z + v.w);
-                sv = sv + __shfl_xor(sv, 1, 64);
-                sv = sv + __shfl_xor(sv, 2, 64);
-                if ((t & 3) == 0) gsum[f / 4] = sv;
-            }
-            if ((t & 3) == 0)
-                fac[f / 4] = __builtin_isfinite(mx) ? ldexpf(1.0f, e - 14) : __builtin_nanf("");
+    for (int j = 0; j < BPW; j++) src_load4<ACT>(a, min(b0 * 256 + 4 * (lane + 64 * j), K - 4), xa[j], xb[j]);
+
+    // 2. this wave's weight units: unit i = (piece r*BPW + j) * UPB + v
+    u32x4 wr[G::S];
+    uint32_t wd[G::S];
+    {
+        const uint32_t jmax = nb ? nb - 1 : 0u;
+#pragma unroll
+        for (int s = 0; s < G::S; s++) {
+            const uint32_t i = lane + 64 * s, ic = min(i, G::NU - 1);
+            const uint32_t pc = ic / G::UPB, v = ic - pc * G::UPB;
+            const uint32_t r = pc / BPW, j = pc - r * BPW, jc = min(j, jmax);
+            wr[s] = bload16(rs, (uint32_t)(r * row_bytes) + (b0 + jc) * Q::BS + 16 * v);
+            wd[s] = (i < G::NU && j < nb) ? r * G::RS + j * G::LB + 16 * v : ~0u;
         }
     }
-    __syncthreads();
 
-    // 4. MFMAs: lane (n, g) supplies B = q of row n at k-set K_g and A = its
-    // digit row (m = n: plane n%4 of group n/4) when n/4 == g
-    const uint32_t m = n;
-    const bool a_live = (m >> 2) == g && (m & 3) < 3;
-    const uint32_t a_plane = (m & 3) * K;
+    // 3. activation staging of this wave's slice
+    float inv = 1.0f;
+    if constexpr (ACT == ACT_RMSNORM) inv = rms_inv(canonical_sumsq<NSQ>(cx, K, red), K, a.eps);
+#pragma unroll
+    for (int j = 0; j < BPW; j++) {
+        const uint32_t f = lane + 64 * j;                        // local float4 index
+        const float4 v = xform4<ACT>(xa[j], xb[j], inv);
+        float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        int e = 0;
+        if (mx > 0.0f && __builtin_isfinite(mx)) {
+            int ex;
+            (void)frexpf(mx, &ex);
+            e = ex - 6;  // mx / 2^e in [32, 64)
+        }
+        uint32_t p0, p1, p2;
+        int s0, s1, s2;
+        encode4(v, e, p0, p1, p2, s0, s1, s2);
+        *(uint32_t *)(L + G::D_OFF + 4 * f) = p0;
+        *(uint32_t *)(L + G::D_OFF + G::DG + 4 * f) = p1;
+        *(uint32_t *)(L + G::D_OFF + 2 * G::DG + 4 * f) = p2;
+        i32x4 ax = {0, 0, 0, 0};
+        if constexpr (Q::OFF32) {
+            s0 += __shfl_xor(s0, 1, 64);
+            s0 += __shfl_xor(s0, 2, 64);
+            s1 += __shfl_xor(s1, 1, 64);
+            s1 += __shfl_xor(s1, 2, 64);
+            s2 += __shfl_xor(s2, 1, 64);
+            s2 += __shfl_xor(s2, 2, 64);
+            ax[0] = -32 * s0;
+            ax[1] = -32 * s1;
+            ax[2] = -32 * s2;
+        } else {
+            float sv = (v.x + v.y) + (v.z + v.w);
+            sv = sv + __shfl_xor(sv, 1, 64);
+            sv = sv + __shfl_xor(sv, 2, 64);
+            if ((lane & 3) == 0) *(float *)(L + G::G_OFF + f) = sv;  // group f / 4
+        }
+        ax[3] = __float_as_int(__builtin_isfinite(mx) ? ldexpf(1.0f, e - 14) : __builtin_nanf(""));
+        if ((lane & 3) == 0) *(i32x4 *)(L + G::A_OFF + 4 * f) = ax;
+    }
+
+    // 4. weight units to this wave's LDS, then its MFMAs.  Lane (n, g)
+    // supplies B = q of row n at k-set K_g and A = its digit row (m = n:
+    // plane n%4 of group n/4) when n/4 == g.
+#pragma unroll
+    for (int s = 0; s < G::S; s++)
+        if (wd[s] != ~0u) *(u32x4 *)(L + wd[s]) = wr[s];
+    wave_lds_sync();
+
+    const bool a_live = (n >> 2) == g && (n & 3) < 3;
+    const uint32_t a_base = G::D_OFF + (n & 3) * G::DG;
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NBW; i++) {
-        const uint32_t b = wave + W * i;
-        if (b < B) {
-            i32x4 bq[4];
-            float sc[4], mn[4];
-            Q::decode(raw[i], g, bq, sc, mn);
+    for (int j = 0; j < BPW; j++) {
+        if (j < (int)nb) {
+            typename Q::Raw raw;
+            Q::load(raw, L, n * G::RS + j * G::LB, g);
+            i32x4 bq[4], av[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) av[u] = i32x4{0, 0, 0, 0};
+            if (a_live) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) av[u] = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
+            }
+            float sc[4], mn[4], d, dmin;
+            Q::decode(raw, g, bq, sc, mn, d, dmin);
+            float acc_s = 0.0f, acc_m = 0.0f;
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const uint32_t k0 = b * 256 + Q::koff(g, u);
-                const uint32_t aoff = a_live ? a_plane + k0 : 3 * K;
-                const i32x4 av = *(const i32x4 *)(dg + aoff);
-                i32x4 c = {0, 0, 0, 0};
-                c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, av), __builtin_bit_cast(i8x16, bq[u]), c,
-                                                          0, 0, 0);
-                int T = c[0] * 16384 + c[1] * 128 + c[2];
-                if constexpr (Q::OFF32) T -= 32 * ((const int *)gsum)[k0 / 16];
-                acc = fmaf(sc[u] * fac[k0 / 16], (float)T, acc);
-                if constexpr (Q::HAS_MIN) acc = fmaf(-mn[u], gsum[k0 / 16], acc);
+                const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
+                i32x4 cc = *(const i32x4 *)(L + G::A_OFF + 16 * grp);
+                cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, av[u]),
+                                                           __builtin_bit_cast(i8x16, bq[u]), cc, 0, 0, 0);
+                const int T = cc[0] * 16384 + cc[1] * 128 + cc[2];
+                acc_s = fmaf(sc[u], __int_as_float(cc[3]) * (float)T, acc_s);
+                if constexpr (Q::HAS_MIN) acc_m = fmaf(mn[u], *(const float *)(L + G::G_OFF + 4 * grp), acc_m);
             }
+            acc = fmaf(d, acc_s, acc);
+            if constexpr (Q::HAS_MIN) acc = fmaf(-dmin, acc_m, acc);
         }
     }
 
@@ -290,32 +388,31 @@ __global__ __launch_bounds__(64 * W) void gemv_mq_kernel(GemvArgs a)
     __syncthreads();
     if (t < 16 && row0 + t < a.N) {
         float v = part[t];
-#pragma unroll
-        for (int w = 1; w < W; w++) v += part[16 * w + t];
+        for (uint32_t w = 1; w < W; w++) v += part[16 * w + t];
         float *yp = a.y + row0 + t;
-        *yp = a.residual ? *yp + v : v;
+        if (a.residual) v = *yp + v;
+        *yp = v;
     }
 }
 
-template <class Q, int W, int NBW, int ACT>
+// Super-blocks per wave and waves per workgroup (at least 4, the canonical
+// RMSNorm order needs them; waves past the last super-block only encode).
+template <class Q, int BPW, int ACT>
 static hipError_t go_mq(const GemvArgs &a, hipStream_t s)
 {
-    const size_t lds = 3 * (size_t)a.K + 16 + 2 * (size_t)(a.K / 16) * 4 + 17 * W * 4;
-    hipLaunchKernelGGL((gemv_mq_kernel<Q, W, NBW, ACT>), dim3((a.N + 15) / 16), dim3(64 * W), lds, s, a);
+    using G = MwGeom<Q, BPW>;
+    const uint32_t B = a.K / 256;
+    const uint32_t W = max(4u, (B + BPW - 1) / BPW);
+    const size_t lds = W * G::BYTES + (4 + 16 * W) * 4;
+    static_assert(16 * MwGeom<Q, BPW>::BYTES + (4 + 16 * 16) * 4 <= 160 * 1024, "LDS per workgroup");
+    hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT>), dim3((a.N + 15) / 16), dim3(64 * W), lds, s, a);
     return hipGetLastError();
 }
 
-// Waves per 16-row tile: K is split across W waves (super-blocks w, w + W,
-// ...), up to 16 waves so that small matrices still fill the SIMDs.
 template <class Q, int ACT>
 static hipError_t go_mq_k(const GemvArgs &a, hipStream_t s)
 {
-    const uint32_t B = a.K / 256;
-    if (B <= 4) return go_mq<Q, 4, 1, ACT>(a, s);
-    if (B <= 8) return go_mq<Q, 8, 1, ACT>(a, s);
-    if (B <= 12) return go_mq<Q, 12, 1, ACT>(a, s);
-    if (B <= 16) return go_mq<Q, 16, 1, ACT>(a, s);
-    return go_mq<Q, 16, 2, ACT>(a, s);
+    return a.K <= 16 * 256 ? go_mq<Q, 1, ACT>(a, s) : go_mq<Q, 2, ACT>(a, s);
 }
 
 template <class Q>

@@ -29,6 +29,12 @@ struct GemvArgs {
     uint32_t residual;    // y += result instead of y = result
 };
 
+// Every device buffer is allocated with at least this many bytes past its
+// requested size.  Kernels may READ (never write) up to this far past the end
+// of a tensor, e.g. a whole 16-byte unit that straddles the end of a Q6_K
+// matrix (210-byte blocks).  A view ends inside its parent, so it inherits it.
+constexpr uint64_t RRR_READ_SLACK = 16;
+
 uint64_t block_bytes(uint32_t type);  // 144/176/210 per 256 elements, 1024 for F32
 
 hipError_t launch_gemv(const GemvArgs &a, uint32_t act, hipStream_t s);
