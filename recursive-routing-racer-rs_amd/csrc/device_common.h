@@ -30,6 +30,18 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
+// Streaming (non-temporal) variant for data read exactly once, such as
+// weight matrices: keeps activations and outputs resident in the caches.
+constexpr int RRR_CPOL_NT = 2;
+__device__ __forceinline__ u32x4 bload16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, RRR_CPOL_NT);
+}
+// ... with a wave-uniform part of the offset in the scalar offset operand
+__device__ __forceinline__ u32x4 bload16_nt_so(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, RRR_CPOL_NT);
+}
 __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);

@@ -4,28 +4,28 @@
 // with the multiply-accumulate on v_mfma_i32_16x16x64_i8 instead of VALU FMAs.
 //
 // Activation encoding.  Each 16-element group of x is written in block
-// floating point with three signed int8 digits per element:
-//     x ~= 2^E * (d0 + d1 / 128 + d2 / 16384),  |d_t| <= 64,
-// where 2^E is chosen from the group maximum M so that M / 2^E lies in
-// [32, 64).  Every step (scale by 2^-E, round, subtract, scale by 128) is
-// exact in f32, so the encoding error is at most 2^(E-15) per element, i.e.
-// below 2^-20 of the group maximum.
+// floating point: the fixed-point value Q = rint(x * 2^(14-E)), with 2^E
+// chosen from the group maximum M so that M / 2^E lies in [32, 64)
+// (|Q| < 2^20), split into three signed int8 radix-256 digits
+//     Q = d0 + 2^8 d1 + 2^16 d2.
+// The encoding error is at most 2^(E-15) per element, i.e. below 2^-20 of
+// the group maximum.
 //
 // Weights.  A K-quant super-block stores small integers q (Q4_K 0..15,
 // Q5_K 0..31, Q6_K 0..63 with an offset of 32) and per-sub-block scales.
 // The raw q values go straight into the MFMA B operand; the integer dot
 // products C_t = sum q * d_t (t = 0, 1, 2) are exact, and
-//     sum_k q_k x_k = 2^(E-14) * (C_0 * 2^14 + C_1 * 2^7 + C_2)
-// is recombined in int32 (no overflow: |C_t| < 2^16) and scaled once per
-// 16 elements.  The Q6_K offset (q - 32) is folded into the MFMA accumulator
-// input as -32 * (digit sums of the group); the Q4_K / Q5_K min term uses the
-// f32 16-element sums of x.
+//     sum_k q_k x_k = 2^(E-14) * (C_0 + C_1 * 2^8 + C_2 * 2^16)
+// is recombined in int32 (|C_2| < 2^14, |C_0|, |C_1| < 2^17) and scaled once
+// per 16 elements.  The Q6_K offset (q - 32) is folded into the MFMA
+// accumulator input as -32 * (sum of Q over the group); the Q4_K / Q5_K min
+// term uses the f32 16-element sums of x.
 //
 // MFMA mapping (16x16x64, lane l: A row l%16, B column l%16, k-group l/16;
 // C/D rows 4*(l/16)+r of column l%16 in register r):
 //   B[k][n]  = q of weight row n (16 rows per workgroup) at k-set K_g,
 //   A[m][k]  = digit (m%4) of x at K_g when m/4 == g (and m%4 < 3), else 0,
-//   C[4g+r][n] = group constants of K_g: r < 3 the offset term, r = 3 the
+//   C[4g+r][n] = group constants of K_g: r = 0 the offset term, r = 3 the
 //                group factor 2^(E-14) (bit pattern; A row 4g+3 is zero, so
 //                it comes back unchanged in D),
 // so lane (n, g) receives its own three partial dot products for row n and
@@ -162,47 +162,66 @@ struct MqQ6K {
     }
 };
 
-// Digits of one float4 of activations: the three digit planes packed four
-// int8 per dword, and the per-plane digit sums.
-__device__ __forceinline__ void encode4(const float4 &v, int e, uint32_t &p0, uint32_t &p1, uint32_t &p2, int &s0,
-                                        int &s1, int &s2)
+// Fixed-point form of one float4 of activations: Q = rint(x * 2^(14-E))
+// (|Q| < 2^20) as three signed radix-256 digits Q = d0 + 2^8 d1 + 2^16 d2.
+// fma(x, 2^(14-E), 1.5 * 2^23) lands in [2^23, 2^24), where the f32 spacing
+// is 1, so it is the exactly rounded 1.5 * 2^23 + Q and its bit pattern is
+// 0x4B400000 + Q.  Adding the bias 0x808080 makes every byte c_t of
+// Qb = Q + 0x808080 (< 2^24) the digit d_t = c_t - 128, i.e. the int8 byte
+// c_t ^ 0x80.  Returns the digit planes (four int8 per dword, plane t = byte
+// t) and the sum of the four biased values.
+__device__ __forceinline__ void encode4(const float4 &v, float scale, uint32_t &p0, uint32_t &p1, uint32_t &p2,
+                                        uint32_t &qbsum)
 {
-    const float c[4] = {v.x, v.y, v.z, v.w};
-    p0 = p1 = p2 = 0u;
-    s0 = s1 = s2 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float xs = ldexpf(c[i], -e);
-        const float d0 = rintf(xs);
-        float r = (xs - d0) * 128.0f;
-        const float d1 = rintf(r);
-        r = (r - d1) * 128.0f;
-        const float d2 = rintf(r);
-        const int i0 = (int)d0, i1 = (int)d1, i2 = (int)d2;
-        p0 |= ((uint32_t)i0 & 255u) << (8 * i);
-        p1 |= ((uint32_t)i1 & 255u) << (8 * i);
-        p2 |= ((uint32_t)i2 & 255u) << (8 * i);
-        s0 += i0;
-        s1 += i1;
-        s2 += i2;
-    }
+    constexpr float MAGIC = 12582912.0f;                       // 1.5 * 2^23
+    constexpr uint32_t REBIAS = 0x00808080u - 0x4B400000u;     // mod 2^32
+    const uint32_t q0 = __float_as_uint(__builtin_fmaf(v.x, scale, MAGIC)) + REBIAS;
+    const uint32_t q1 = __float_as_uint(__builtin_fmaf(v.y, scale, MAGIC)) + REBIAS;
+    const uint32_t q2 = __float_as_uint(__builtin_fmaf(v.z, scale, MAGIC)) + REBIAS;
+    const uint32_t q3 = __float_as_uint(__builtin_fmaf(v.w, scale, MAGIC)) + REBIAS;
+    qbsum = (q0 + q1) + (q2 + q3);
+    // v_perm: selector bytes 0..3 take bytes of the second operand, 4..7 of
+    // the first, 0x0c gives 0
+    p0 = (__builtin_amdgcn_perm(q1, q0, 0x0c0c0400u) | __builtin_amdgcn_perm(q3, q2, 0x04000c0cu)) ^ 0x80808080u;
+    p1 = (__builtin_amdgcn_perm(q1, q0, 0x0c0c0501u) | __builtin_amdgcn_perm(q3, q2, 0x05010c0cu)) ^ 0x80808080u;
+    p2 = (__builtin_amdgcn_perm(q1, q0, 0x0c0c0602u) | __builtin_amdgcn_perm(q3, q2, 0x06020c0cu)) ^ 0x80808080u;
+}
+
+// Butterflies within a quad of lanes (DPP quad_perm, no LDS traffic).
+__device__ __forceinline__ float quad_max(float v)
+{
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ float quad_sum(float v)
+{
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t quad_sum_u32(uint32_t v)
+{
+    v = v + (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+    return v + (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
 }
 
 // Wave-private LDS layout of one wave (BPW super-blocks of 16 rows):
 //   weights: 16 rows x RS bytes, block j of row r at r*RS + j*LB (16-byte
 //            aligned pieces of UPB units; Q6_K pieces carry 14 bytes of the
-//            next block in their last unit)
+//            next block in their last unit).  Load slot s covers rows
+//            s*RPS .. s*RPS + RPS-1, lane l unit l % UPR of row l / UPR, so a
+//            lane's offsets are fixed and only a uniform per-slot offset moves.
 //   digits:  3 planes x DG bytes (plane p, local element e at p*DG + e)
 //   aux:     per 16-element group 16 bytes = MFMA accumulator input
-//            {-32*S0, -32*S1, -32*S2 (Q6_K only, else 0), bits of 2^(E-14)}
+//            {-32 * sum Q (Q6_K only, else 0), 0, 0, bits of 2^(E-14)}
 //   gsum:    per group the f32 sum of x (Q4_K / Q5_K min term)
 template <class Q, int BPW>
 struct MwGeom {
     static constexpr uint32_t UPB = (Q::BS + 15) / 16;            // 16-byte units per block piece
     static constexpr uint32_t LB = 16 * UPB;
     static constexpr uint32_t RS = (BPW * LB) % 32 == 0 ? BPW * LB + 16 : BPW * LB;  // odd multiple of 16
-    static constexpr uint32_t NU = 16 * BPW * UPB;                 // units per wave
-    static constexpr int S = (NU + 63) / 64;                       // unit slots per lane
+    static constexpr uint32_t UPR = BPW * UPB;                     // units per row
+    static constexpr uint32_t RPS = 64 / UPR;                      // rows per load slot
+    static constexpr int S = (16 + RPS - 1) / RPS;                 // load slots
     static constexpr uint32_t DG = BPW * 256;
     static constexpr uint32_t NGW = BPW * 16;
     static constexpr uint32_t D_OFF = 16 * RS;
@@ -281,20 +300,23 @@ __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a)
 #pragma unroll
     for (int j = 0; j < BPW; j++) src_load4<ACT>(a, min(b0 * 256 + 4 * (lane + 64 * j), K - 4), xa[j], xb[j]);
 
-    // 2. this wave's weight units: unit i = (piece r*BPW + j) * UPB + v
+    // every wave's activation loads enter the memory pipeline before any
+    // weight load of the workgroup (a bare barrier: no wait on the loads)
+    __builtin_amdgcn_s_barrier();
+
+    // 2. this wave's weight units (layout above); lanes past RPS rows and
+    // blocks past nb reload a valid unit and are not stored
     u32x4 wr[G::S];
-    uint32_t wd[G::S];
+    const uint32_t rsel = min(lane / G::UPR, G::RPS - 1), wl = lane - (lane / G::UPR) * G::UPR;
+    const uint32_t jl = wl / G::UPB, vl = wl - jl * G::UPB;
+    const bool lane_ok = lane < G::RPS * G::UPR && jl < nb;
     {
-        const uint32_t jmax = nb ? nb - 1 : 0u;
+        const uint32_t voff = rsel * (uint32_t)row_bytes + (b0 + min(jl, nb ? nb - 1 : 0u)) * Q::BS + 16 * vl;
 #pragma unroll
-        for (int s = 0; s < G::S; s++) {
-            const uint32_t i = lane + 64 * s, ic = min(i, G::NU - 1);
-            const uint32_t pc = ic / G::UPB, v = ic - pc * G::UPB;
-            const uint32_t r = pc / BPW, j = pc - r * BPW, jc = min(j, jmax);
-            wr[s] = bload16(rs, (uint32_t)(r * row_bytes) + (b0 + jc) * Q::BS + 16 * v);
-            wd[s] = (i < G::NU && j < nb) ? r * G::RS + j * G::LB + 16 * v : ~0u;
-        }
+        for (int s = 0; s < G::S; s++)
+            wr[s] = bload16_nt_so(rs, voff, (uint32_t)(s * G::RPS) * (uint32_t)row_bytes);
     }
+    const uint32_t loff = rsel * G::RS + jl * G::LB + 16 * vl;
 
     // 3. activation staging of this wave's slice
     float inv = 1.0f;
@@ -303,36 +325,26 @@ __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a)
     for (int j = 0; j < BPW; j++) {
         const uint32_t f = lane + 64 * j;                        // local float4 index
         const float4 v = xform4<ACT>(xa[j], xb[j], inv);
-        float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const float mx = quad_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         int e = 0;
         if (mx > 0.0f && __builtin_isfinite(mx)) {
             int ex;
             (void)frexpf(mx, &ex);
             e = ex - 6;  // mx / 2^e in [32, 64)
         }
-        uint32_t p0, p1, p2;
-        int s0, s1, s2;
-        encode4(v, e, p0, p1, p2, s0, s1, s2);
+        uint32_t p0, p1, p2, qb;
+        encode4(v, ldexpf(1.0f, 14 - e), p0, p1, p2, qb);
         *(uint32_t *)(L + G::D_OFF + 4 * f) = p0;
         *(uint32_t *)(L + G::D_OFF + G::DG + 4 * f) = p1;
         *(uint32_t *)(L + G::D_OFF + 2 * G::DG + 4 * f) = p2;
         i32x4 ax = {0, 0, 0, 0};
         if constexpr (Q::OFF32) {
-            s0 += __shfl_xor(s0, 1, 64);
-            s0 += __shfl_xor(s0, 2, 64);
-            s1 += __shfl_xor(s1, 1, 64);
-            s1 += __shfl_xor(s1, 2, 64);
-            s2 += __shfl_xor(s2, 1, 64);
-            s2 += __shfl_xor(s2, 2, 64);
-            ax[0] = -32 * s0;
-            ax[1] = -32 * s1;
-            ax[2] = -32 * s2;
+            // sum (q - 32) Q = sum q Q - 32 sum Q: the second term enters the
+            // weight-1 plane's accumulator (int32 wrap-around is harmless, the
+            // recombined value is within +-2^29)
+            ax[0] = -32 * (int)(quad_sum_u32(qb) - 16u * 0x00808080u);
         } else {
-            float sv = (v.x + v.y) + (v.z + v.w);
-            sv = sv + __shfl_xor(sv, 1, 64);
-            sv = sv + __shfl_xor(sv, 2, 64);
+            const float sv = quad_sum((v.x + v.y) + (v.z + v.w));
             if ((lane & 3) == 0) *(float *)(L + G::G_OFF + f) = sv;  // group f / 4
         }
         ax[3] = __float_as_int(__builtin_isfinite(mx) ? ldexpf(1.0f, e - 14) : __builtin_nanf(""));
@@ -344,20 +356,23 @@ __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a)
     // plane n%4 of group n/4) when n/4 == g.
 #pragma unroll
     for (int s = 0; s < G::S; s++)
-        if (wd[s] != ~0u) *(u32x4 *)(L + wd[s]) = wr[s];
+        if (lane_ok && s * G::RPS + rsel < 16)
+            *(u32x4 *)(L + loff + s * G::RPS * G::RS) = wr[s];
     wave_lds_sync();
 
     const bool a_live = (n >> 2) == g && (n & 3) < 3;
     const uint32_t a_base = G::D_OFF + (n & 3) * G::DG;
     float acc = 0.0f;
+    // A operands: zero in the non-live lanes for every block (set once)
+    i32x4 av[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) av[u] = i32x4{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < BPW; j++) {
         if (j < (int)nb) {
             typename Q::Raw raw;
             Q::load(raw, L, n * G::RS + j * G::LB, g);
-            i32x4 bq[4], av[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) av[u] = i32x4{0, 0, 0, 0};
+            i32x4 bq[4];
             if (a_live) {
 #pragma unroll
                 for (int u = 0; u < 4; u++) av[u] = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
@@ -371,7 +386,7 @@ __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a)
                 i32x4 cc = *(const i32x4 *)(L + G::A_OFF + 16 * grp);
                 cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, av[u]),
                                                            __builtin_bit_cast(i8x16, bq[u]), cc, 0, 0, 0);
-                const int T = cc[0] * 16384 + cc[1] * 128 + cc[2];
+                const int T = cc[0] + cc[1] * 256 + cc[2] * 65536;
                 acc_s = fmaf(sc[u], __int_as_float(cc[3]) * (float)T, acc_s);
                 if constexpr (Q::HAS_MIN) acc_m = fmaf(mn[u], *(const float *)(L + G::G_OFF + 4 * grp), acc_m);
             }
