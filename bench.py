@@ -11,9 +11,10 @@ the library's stream.
 Printed: one JSON line with value = algorithmic bytes / time in GB/s, the
 roofline of the dominant kernel (the Q6_K GEMV, timed alone the same way),
 a CPU baseline (the oracle's composed dequant+dot path on the host cores,
-bounded sample) and the other workloads under "extra".
+bounded sample) and the other workloads under "extra", among them the full
+32-layer decode sweep in ms/token.
 
-    python bench.py [--gpus 1] [--steps 1280] [--warmup 128] [--no-cpu] [--no-sweep]
+    python bench.py [--gpus 1] [--steps 1280] [--warmup 128] [--no-cpu] [--no-decode] [--tokens 20]
 """
 import argparse
 import json
@@ -30,7 +31,7 @@ for _p in (REPO, PKG):
 import numpy as np  # noqa: E402
 
 import rrr_hip  # noqa: E402
-from rrr_hip import synth  # noqa: E402
+from rrr_hip import decode, synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 D, QKV, FFN = 3072, 5120, 8192
@@ -95,6 +96,37 @@ class Config2:
         self.ctx.rmsnorm(self.x, self.g, self.normed, 1, D, 1e-5)
 
 
+def decode_sweep(ctx, tokens):
+    """Full Phi-4-mini-shaped decode sweep (32 layers + final RMSNorm + F32
+    logits over 200,064 entries + argmax), one HIP graph per token; the
+    4.45 GB per token stream far past the Infinity Cache by itself."""
+    shape = decode.Phi4Shape()
+    log("[bench] decode sweep: generating and uploading 32 layers + logits matrix")
+    t0 = time.perf_counter()
+    sw = decode.DecodeSweep(ctx, shape, seed=3)
+    ctx.sync()
+    log(f"[bench] decode sweep ready in {time.perf_counter() - t0:.1f} s")
+    g = sw.graph()
+    for _ in range(3):
+        g.launch()
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(tokens):
+        g.launch()
+    ms = ctx.timer_stop() / tokens
+    ctx.sync()
+    g.destroy()
+    logits, tok, _ = sw.results()
+    b = shape.bytes_per_token()
+    log(f"[bench] decode sweep: {ms:.4f} ms/token ({b / (ms * 1e-3) / 1e9:.0f} GB/s), argmax {tok}")
+    return {"ms_per_token": round(ms, 5), "tokens": tokens, "bytes_per_token": b,
+            "GBs": round(b / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "argmax": tok, "logits_finite": bool(np.all(np.isfinite(logits))),
+            "workload": "32 layers (RMSNorm+QKV Q5_K 5120x3072, O Q4_K 3072x3072 +res, RMSNorm+gate/up Q4_K "
+                        "16384x3072, silu+down Q6_K/Q4_K 3072x8192 +res) + RMSNorm + F32 logits 200064x3072 "
+                        "(transposed 8192-entry chunks) + argmax, seed 3"}
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's composed dequant+dot path (restated phi4.rs formulas,
     rows split over threads like rayon par_chunks) on this host, one config-2
@@ -140,7 +172,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--tokens", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -193,6 +226,9 @@ def main():
                                "frac_hbm": round(B_QKV / (ms_q5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": B_QKV},
         "rmsnorm_3072": {"us": round(ms_nm * 1e3, 3), "bytes": B_NORM},
     }
+
+    if not args.no_decode:
+        extra["decode_sweep"] = decode_sweep(ctx, args.tokens)
 
     cpu = None
     if not args.no_cpu:

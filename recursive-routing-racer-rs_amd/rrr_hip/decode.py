@@ -1,0 +1,172 @@
+"""Phi-4-mini-shaped decode weight sweep, batch 1.
+
+One token of the dispatch table that the reference builds once
+(phi4.rs:972-1064) and replays per token (forward_gpu, phi4.rs:1099-1168),
+issued through the C ABI and normally recorded as one graph.
+
+Per layer (phi4.rs:1006-1033), with the reference's separate dispatches
+fused where the numerics allow it:
+
+    rmsnorm(attn_norm) -> QKV GEMV            rrr_gemv_rmsnorm          Q5_K 5120x3072
+    rope_kv_store + attention                 (position 0: RoPE is the identity and
+                                               softmax over one key is 1, so the
+                                               attention output is V gathered per
+                                               GQA head)
+    O-proj GEMV -> residual_add               rrr_gemv_residual(GQA_V)  Q4_K 3072x3072
+    rmsnorm(ffn_norm) -> gate+up GEMV         rrr_gemv_rmsnorm          Q4_K 16384x3072
+    silu_gate -> down GEMV -> residual_add    rrr_gemv_residual(SILU)   Q6_K (even layers) /
+                                                                        Q4_K (odd) 3072x8192
+
+then rmsnorm(output_norm) -> F32 logits over the transposed 8192-entry vocab
+chunks (phi4.rs:874-893, 1049-1064) as rrr_logits_rmsnorm, and the argmax
+that the reference does on the host (phi4.rs:1172-1195) as rrr_argmax_f32.
+The fused entry points are bitwise equal to their unfused sequences.
+
+Weights are seeded synthetic tensors (the recipes of synth.py); each tensor
+has its own stream id, so any subset can be regenerated on the host.
+"""
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import engine as E
+from . import synth
+
+
+@dataclass(frozen=True)
+class Phi4Shape:
+    d_model: int = 3072
+    n_layers: int = 32
+    n_heads: int = 24
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    ffn_dim: int = 8192
+    vocab: int = 200064
+    eps: float = 1e-5
+    chunk: int = 8192            # logits vocab chunk (phi4.rs:877)
+
+    @property
+    def qkv_dim(self):
+        return self.d_model + 2 * self.n_kv_heads * self.head_dim
+
+    @property
+    def heads_per_kv(self):
+        return self.n_heads // self.n_kv_heads
+
+    def down_type(self, layer):
+        return E.Q6_K if layer % 2 == 0 else E.Q4_K
+
+    def layer_tensors(self, layer):
+        """(name, qtype, K, N) of the layer's four weight matrices."""
+        d, f = self.d_model, self.ffn_dim
+        return [("attn_qkv", E.Q5_K, d, self.qkv_dim), ("attn_output", E.Q4_K, d, d),
+                ("ffn_up", E.Q4_K, d, 2 * f), ("ffn_down", self.down_type(layer), f, d)]
+
+    def bytes_per_token(self):
+        """Algorithmic HBM bytes of one token: raw weight bytes plus every
+        activation read or written once."""
+        d, f = self.d_model, self.ffn_dim
+        total = 0
+        for i in range(self.n_layers):
+            total += 2 * 3 * d * 4                                     # two RMSNorms (x, gamma, y)
+            for _, qt, K, N in self.layer_tensors(i):
+                total += E.tensor_bytes(qt, K, N) + K * 4 + N * 4
+        total += 3 * d * 4                                             # output norm
+        total += self.vocab * d * 4 + d * 4 + self.vocab * 4           # logits
+        return total
+
+
+# stream ids of the synthetic tensors
+def _stream(layer, slot):
+    return 1000 + 16 * layer + slot
+
+
+S_ATTN_NORM, S_QKV, S_O, S_FFN_NORM, S_UP, S_DOWN = range(6)
+S_OUT_NORM, S_EMB, S_X = 10, 11, 12
+
+
+def gamma_host(seed, stream, d):
+    return synth.normal_f32(seed, stream, d, 1.0, 0.1)
+
+
+def layer_host(seed, shape, layer):
+    """Host copies of one layer: dict of raw weight bytes and norm gammas."""
+    out = {"attn_norm": gamma_host(seed, _stream(layer, S_ATTN_NORM), shape.d_model),
+           "ffn_norm": gamma_host(seed, _stream(layer, S_FFN_NORM), shape.d_model)}
+    slots = {"attn_qkv": S_QKV, "attn_output": S_O, "ffn_up": S_UP, "ffn_down": S_DOWN}
+    for name, qt, K, N in shape.layer_tensors(layer):
+        out[name] = synth.weight(seed, _stream(layer, slots[name]), qt, K, N)
+    return out
+
+
+def embedding_chunks_host(seed, shape):
+    """The logits matrix E ~ N(0, 0.02) in the reference's transposed chunk
+    layout, generated directly in storage order: chunk c (n entries) holds
+    B_c[d * n + v] = E[c * chunk + v][d] (phi4.rs:886)."""
+    return synth.normal_f32(seed, S_EMB, shape.vocab * shape.d_model, 0.0, 0.02)
+
+
+def x_host(seed, shape):
+    """The token's input hidden state (stands in for the embedding row)."""
+    return synth.normal_f32(seed, S_X, shape.d_model)
+
+
+class DecodeSweep:
+    """Device weights and activations of the sweep; record_token() issues one
+    token's operations on the context's stream."""
+
+    def __init__(self, ctx, shape=Phi4Shape(), seed=3, keep_host=False):
+        self.ctx, self.shape, self.seed = ctx, shape, seed
+        self.host = {} if keep_host else None
+        d = shape.d_model
+        self.layers = []
+        for i in range(shape.n_layers):
+            h = layer_host(seed, shape, i)
+            dev = {"attn_norm": ctx.to_device(h["attn_norm"]), "ffn_norm": ctx.to_device(h["ffn_norm"])}
+            for name, qt, K, N in shape.layer_tensors(i):
+                dev[name] = ctx.weight_upload(qt, K, N, h[name])
+            self.layers.append(dev)
+            if keep_host:
+                self.host[i] = h
+        out_norm = gamma_host(seed, S_OUT_NORM, d)
+        emb = embedding_chunks_host(seed, shape)
+        x = x_host(seed, shape)
+        self.out_norm = ctx.to_device(out_norm)
+        self.emb = ctx.to_device(emb)
+        self.x_in = ctx.to_device(x)
+        if keep_host:
+            self.host.update(out_norm=out_norm, emb=emb, x=x)
+        del emb
+        self.zero = ctx.to_device(np.zeros(d, np.float32))
+        self.hidden = ctx.alloc(d * 4)
+        self.qkv = ctx.alloc(shape.qkv_dim * 4)
+        self.gate_up = ctx.alloc(2 * shape.ffn_dim * 4)
+        self.logits = ctx.alloc(shape.vocab * 4)
+        self.token = ctx.alloc(4)
+
+    def record_token(self):
+        c, s = self.ctx, self.shape
+        d = s.d_model
+        gqa = s.head_dim | (s.heads_per_kv << 16)
+        c.residual_add(self.x_in, self.zero, self.hidden, d)       # hidden = embedding row
+        for i, L in enumerate(self.layers):
+            c.gemv_rmsnorm(self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], E.Q5_K, self.qkv, d, s.qkv_dim)
+            c.gemv_residual(self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], E.Q4_K, self.hidden, d, d)
+            c.gemv_rmsnorm(self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], E.Q4_K, self.gate_up, d, 2 * s.ffn_dim)
+            c.gemv_residual(self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], s.down_type(i), self.hidden,
+                            s.ffn_dim, d)
+        c.logits_rmsnorm(self.hidden, self.out_norm, s.eps, self.emb, self.logits, d, s.vocab,
+                         E.LOGITS_CHUNKED, s.chunk)
+        c.argmax_f32(self.logits, s.vocab, self.token)
+
+    def graph(self):
+        self.ctx.graph_begin()
+        self.record_token()
+        return self.ctx.graph_end()
+
+    def results(self):
+        """(logits f32[vocab], argmax index, final hidden state f32[d])."""
+        c = self.ctx
+        return (c.download(self.logits, np.float32, self.shape.vocab),
+                int(c.download(self.token, np.uint32, 1)[0]),
+                c.download(self.hidden, np.float32, self.shape.d_model))

@@ -248,3 +248,32 @@ def test_compute_engine_mirror_requires_registration(monkeypatch):
         eng.dispatch_batch_persistent_v2([("matmul_q4k", h, b"", [1, 1, 1], True)])
     assert ei.value.code == ERR_INVALID_ARG
     eng.close()
+
+
+def test_decode_sweep_shape_and_bytes():
+    # Phi-4-mini shape of the sweep and its per-token byte count, summed here
+    # from the per-op algorithmic bytes (raw weights + activations once).
+    from rrr_hip import decode
+    s = decode.Phi4Shape()
+    assert (s.qkv_dim, s.heads_per_kv, s.vocab % s.chunk) == (5120, 3, 3456)
+    assert [s.down_type(i) for i in range(4)] == [rrr_hip.Q6_K, rrr_hip.Q4_K, rrr_hip.Q6_K, rrr_hip.Q4_K]
+    norm2, qkv, o, up = 73_728, 10_846_208, 5_332_992, 28_389_376
+    down_q6, down_q4 = 20_688_896, 14_200_832
+    layers = 16 * (norm2 + qkv + o + up + down_q6) + 16 * (norm2 + qkv + o + up + down_q4)
+    logits = 2_458_386_432 + 12_288 + 800_256
+    assert s.bytes_per_token() == layers + 36_864 + logits == 4_446_025_216
+
+
+def test_decode_host_tensors_are_reproducible():
+    import dataclasses
+    from rrr_hip import decode
+    s = dataclasses.replace(decode.Phi4Shape(), n_layers=2, vocab=300, d_model=512, ffn_dim=1024,
+                            n_heads=4, n_kv_heads=2, head_dim=128)
+    a, b = decode.layer_host(3, s, 1), decode.layer_host(3, s, 1)
+    for k in a:
+        assert np.array_equal(a[k], b[k])
+    assert a["ffn_down"].size == rrr_hip.tensor_bytes(rrr_hip.Q4_K, 1024, 512)
+    assert decode.layer_host(3, s, 0)["ffn_down"].size == rrr_hip.tensor_bytes(rrr_hip.Q6_K, 1024, 512)
+    assert not np.array_equal(decode.layer_host(3, s, 0)["attn_qkv"], a["attn_qkv"])
+    emb = decode.embedding_chunks_host(3, s)
+    assert emb.size == 300 * 512 and abs(float(emb.std()) - 0.02) < 0.002
