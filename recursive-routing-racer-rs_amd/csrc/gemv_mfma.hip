@@ -263,31 +263,44 @@ __device__ __forceinline__ void wave_lds_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <class Q, int BPW, int ACT>
-__global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a)
+// Scalar offset of a load past every weight byte (the path requires
+// w_bytes + RRR_READ_SLACK < MQ_OOB): such loads return zeros and move no data.
+constexpr uint32_t MQ_OOB = 0x80000000u;
+
+// Persistent form (MULTI): workgroup b takes the 16-row tiles b, b + G, ...
+// (G = gridDim.x) with the same wave <-> K-slice split for every tile, so the
+// activation slice is encoded once per workgroup and, with one super-block per
+// wave, the MFMA A operands and accumulator inputs stay in registers.  The
+// loads of tile i+1 are issued before tile i is staged and multiplied.  The
+// single-tile form (one tile per workgroup) issues no prefetch: even loads
+// past the buffer end cost texture-addresser time.  Row sums are added over
+// the waves in wave order, so results depend on neither form nor G.
+template <class Q, int BPW, int ACT, bool MULTI>
+__global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntiles)
 {
     extern __shared__ float smem[];
     using G = MwGeom<Q, BPW>;
+    constexpr bool AREG = BPW == 1;
     const uint32_t K = a.K, B = K / 256;
-    const uint32_t W = blockDim.x >> 6;
+    const uint32_t W = blockDim.x >> 6, NT = blockDim.x;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t n = lane & 15, g = lane >> 4;
+    const uint32_t GR = gridDim.x, tile0 = blockIdx.x;
+    const uint32_t ntl = MULTI ? (tile0 < ntiles ? (ntiles - tile0 + GR - 1) / GR : 0u) : 1u;  // tiles of this workgroup
     uint8_t *L = (uint8_t *)smem + wave * G::BYTES;              // this wave's region
     float *red = (float *)((uint8_t *)smem + W * G::BYTES);      // 4
-    float *part = red + 4;                                       // W x 16
+    float *part = red + 4;                                       // ntl x W x 16 per-wave row partials
 
-    const uint32_t row0 = blockIdx.x * 16;
-    const uint64_t row_bytes = (uint64_t)B * Q::BS;
-    const uint64_t wg_off = (uint64_t)row0 * row_bytes;
+    const uint32_t row_bytes = B * Q::BS, tile_bytes = 16 * row_bytes;
     // every buffer has RRR_READ_SLACK readable bytes past its end: a Q6_K
     // piece's last unit runs 14 bytes past its block
-    const __amdgpu_buffer_rsrc_t rs =
-        make_rsrc(a.W + wg_off, a.w_bytes > wg_off ? a.w_bytes - wg_off + RRR_READ_SLACK : 0);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.W, a.w_bytes + RRR_READ_SLACK);
     const uint32_t b0 = wave * BPW;                              // first super-block of this wave
     const uint32_t nb = b0 < B ? min((uint32_t)BPW, B - b0) : 0u;
 
-    // The loads below are unconditional (clamped indices): loads under a
-    // branch make the compiler wait for every outstanding load at the join.
+    // The loads below are unconditional (clamped indices, out-of-range scalar
+    // offsets): loads under a branch make the compiler wait for every
+    // outstanding load at the join.
     // 0. fused RMSNorm: the whole of x in the canonical order (K <= 1024 NSQ)
     constexpr int NSQ = ACT == ACT_RMSNORM ? 4 * BPW : 1;
     float4 cx[NSQ];
@@ -304,19 +317,20 @@ __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a)
     // weight load of the workgroup (a bare barrier: no wait on the loads)
     __builtin_amdgcn_s_barrier();
 
-    // 2. this wave's weight units (layout above); lanes past RPS rows and
-    // blocks past nb reload a valid unit and are not stored
-    u32x4 wr[G::S];
+    // 2. weight units of this wave's slice of a tile (layout above); lanes
+    // past RPS rows and blocks past nb reload a valid unit and are not stored
     const uint32_t rsel = min(lane / G::UPR, G::RPS - 1), wl = lane - (lane / G::UPR) * G::UPR;
     const uint32_t jl = wl / G::UPB, vl = wl - jl * G::UPB;
     const bool lane_ok = lane < G::RPS * G::UPR && jl < nb;
-    {
-        const uint32_t voff = rsel * (uint32_t)row_bytes + (b0 + min(jl, nb ? nb - 1 : 0u)) * Q::BS + 16 * vl;
-#pragma unroll
-        for (int s = 0; s < G::S; s++)
-            wr[s] = bload16_nt_so(rs, voff, (uint32_t)(s * G::RPS) * (uint32_t)row_bytes);
-    }
+    const uint32_t voff = rsel * row_bytes + (b0 + min(jl, nb ? nb - 1 : 0u)) * Q::BS + 16 * vl;
     const uint32_t loff = rsel * G::RS + jl * G::LB + 16 * vl;
+    u32x4 wa[G::S], wb[MULTI ? G::S : 1];
+    auto issue = [&](u32x4 *w, uint32_t tl) {
+        const uint32_t tb = tl < ntl ? (tile0 + tl * GR) * tile_bytes : MQ_OOB;
+#pragma unroll
+        for (int s = 0; s < G::S; s++) w[s] = bload16_nt_so(rs, voff, tb + s * G::RPS * row_bytes);
+    };
+    issue(wa, 0);
 
     // 3. activation staging of this wave's slice
     float inv = 1.0f;
@@ -350,77 +364,148 @@ __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a)
         ax[3] = __float_as_int(__builtin_isfinite(mx) ? ldexpf(1.0f, e - 14) : __builtin_nanf(""));
         if ((lane & 3) == 0) *(i32x4 *)(L + G::A_OFF + 4 * f) = ax;
     }
-
-    // 4. weight units to this wave's LDS, then its MFMAs.  Lane (n, g)
-    // supplies B = q of row n at k-set K_g and A = its digit row (m = n:
-    // plane n%4 of group n/4) when n/4 == g.
-#pragma unroll
-    for (int s = 0; s < G::S; s++)
-        if (lane_ok && s * G::RPS + rsel < 16)
-            *(u32x4 *)(L + loff + s * G::RPS * G::RS) = wr[s];
     wave_lds_sync();
 
+    // A operands (zero in the non-live lanes), accumulator inputs and group
+    // sums of the slice; lane (n, g) supplies A = its digit row (m = n: plane
+    // n%4 of group n/4) when n/4 == g
     const bool a_live = (n >> 2) == g && (n & 3) < 3;
     const uint32_t a_base = G::D_OFF + (n & 3) * G::DG;
-    float acc = 0.0f;
-    // A operands: zero in the non-live lanes for every block (set once)
-    i32x4 av[4];
+    i32x4 av[AREG ? 4 : 1], aux[AREG ? 4 : 1];
+    float gs[AREG ? 4 : 1];
+    if constexpr (AREG) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) av[u] = i32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int j = 0; j < BPW; j++) {
-        if (j < (int)nb) {
-            typename Q::Raw raw;
-            Q::load(raw, L, n * G::RS + j * G::LB, g);
-            i32x4 bq[4];
-            if (a_live) {
-#pragma unroll
-                for (int u = 0; u < 4; u++) av[u] = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
-            }
-            float sc[4], mn[4], d, dmin;
-            Q::decode(raw, g, bq, sc, mn, d, dmin);
-            float acc_s = 0.0f, acc_m = 0.0f;
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
-                i32x4 cc = *(const i32x4 *)(L + G::A_OFF + 16 * grp);
-                cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, av[u]),
-                                                           __builtin_bit_cast(i8x16, bq[u]), cc, 0, 0, 0);
-                const int T = cc[0] + cc[1] * 256 + cc[2] * 65536;
-                acc_s = fmaf(sc[u], __int_as_float(cc[3]) * (float)T, acc_s);
-                if constexpr (Q::HAS_MIN) acc_m = fmaf(mn[u], *(const float *)(L + G::G_OFF + 4 * grp), acc_m);
-            }
-            acc = fmaf(d, acc_s, acc);
-            if constexpr (Q::HAS_MIN) acc = fmaf(-dmin, acc_m, acc);
+        for (int u = 0; u < 4; u++) {
+            av[u] = i32x4{0, 0, 0, 0};
+            aux[u] = *(const i32x4 *)(L + G::A_OFF + Q::koff(g, u));
+            gs[u] = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + Q::koff(g, u) / 4) : 0.0f;
         }
+        if (a_live) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) av[u] = *(const i32x4 *)(L + a_base + Q::koff(g, u));
+        }
+    } else {
+        av[0] = i32x4{0, 0, 0, 0};
     }
 
-    // 5. reduce the 4 k-groups of a row (lanes n, n+16, n+32, n+48), then the
-    // W waves in order
-    acc = acc + __shfl_xor(acc, 16, 64);
-    acc = acc + __shfl_xor(acc, 32, 64);
-    if (lane < 16) part[wave * 16 + lane] = acc;
-    __syncthreads();
-    if (t < 16 && row0 + t < a.N) {
-        float v = part[t];
-        for (uint32_t w = 1; w < W; w++) v += part[16 * w + t];
-        float *yp = a.y + row0 + t;
-        if (a.residual) v = *yp + v;
-        *yp = v;
+    // 4. per tile: this tile's units to LDS, MFMAs, row partials to part[]
+    auto process = [&](const u32x4 *w, uint32_t tl) {
+        wave_lds_sync();
+#pragma unroll
+        for (int s = 0; s < G::S; s++)
+            if (lane_ok && s * G::RPS + rsel < 16) *(u32x4 *)(L + loff + s * G::RPS * G::RS) = w[s];
+        wave_lds_sync();
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < BPW; j++) {
+            if (j < (int)nb) {
+                typename Q::Raw raw;
+                Q::load(raw, L, n * G::RS + j * G::LB, g);
+                i32x4 bq[4];
+                float sc[4], mn[4], d, dmin;
+                Q::decode(raw, g, bq, sc, mn, d, dmin);
+                float acc_s = 0.0f, acc_m = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
+                    i32x4 A, C;
+                    float gsum;
+                    if constexpr (AREG) {
+                        A = av[u];
+                        C = aux[u];
+                        gsum = gs[u];
+                    } else {
+                        A = av[0];
+                        if (a_live) A = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
+                        C = *(const i32x4 *)(L + G::A_OFF + 16 * grp);
+                        gsum = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + 4 * grp) : 0.0f;
+                    }
+                    const i32x4 cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, A),
+                                                                           __builtin_bit_cast(i8x16, bq[u]), C, 0, 0, 0);
+                    const int T = cc[0] + cc[1] * 256 + cc[2] * 65536;
+                    acc_s = fmaf(sc[u], __int_as_float(cc[3]) * (float)T, acc_s);
+                    if constexpr (Q::HAS_MIN) acc_m = fmaf(mn[u], gsum, acc_m);
+                }
+                acc = fmaf(d, acc_s, acc);
+                if constexpr (Q::HAS_MIN) acc = fmaf(-dmin, acc_m, acc);
+            }
+        }
+        // the 4 k-groups of a row (lanes n, n+16, n+32, n+48)
+        acc = acc + __shfl_xor(acc, 16, 64);
+        acc = acc + __shfl_xor(acc, 32, 64);
+        if (lane < 16) part[(tl * W + wave) * 16 + lane] = acc;
+    };
+    if constexpr (MULTI) {
+        // two register sets in alternation (a copy between them would wait
+        // for the prefetch); the loads stay on straight-line paths
+        for (uint32_t tl = 0; tl < ntl; tl += 2) {
+            issue(wb, tl + 1);
+            process(wa, tl);
+            if (tl + 1 >= ntl) break;
+            issue(wa, tl + 2);
+            process(wb, tl + 1);
+        }
+    } else {
+        process(wa, 0);
     }
+
+    // 5. rows of every tile of this workgroup: the W waves' partials in order
+    __syncthreads();
+    for (uint32_t i = t; i < ntl * 16; i += NT) {
+        const uint32_t tl = i >> 4, r = i & 15, row = (tile0 + tl * GR) * 16 + r;
+        if (row < a.N) {
+            float v = part[tl * W * 16 + r];
+            for (uint32_t w = 1; w < W; w++) v += part[(tl * W + w) * 16 + r];
+            float *yp = a.y + row;
+            if (a.residual) v = *yp + v;
+            *yp = v;
+        }
+    }
+}
+
+static uint32_t device_cus()
+{
+    static uint32_t cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev] = (uint32_t)v;
+    }
+    return cus[dev];
 }
 
 // Super-blocks per wave and waves per workgroup (at least 4, the canonical
 // RMSNorm order needs them; waves past the last super-block only encode).
-template <class Q, int BPW, int ACT>
-static hipError_t go_mq(const GemvArgs &a, hipStream_t s)
+// Up to one workgroup per CU, each taking ceil(tiles / workgroups) tiles as
+// far as its row partials fit in LDS.
+template <class Q, int BPW>
+static void mq_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds)
 {
     using G = MwGeom<Q, BPW>;
     const uint32_t B = a.K / 256;
-    const uint32_t W = max(4u, (B + BPW - 1) / BPW);
-    const size_t lds = W * G::BYTES + (4 + 16 * W) * 4;
-    static_assert(16 * MwGeom<Q, BPW>::BYTES + (4 + 16 * 16) * 4 <= 160 * 1024, "LDS per workgroup");
-    hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT>), dim3((a.N + 15) / 16), dim3(64 * W), lds, s, a);
+    W = max(4u, (B + BPW - 1) / BPW);
+    const uint32_t ntiles = (a.N + 15) / 16;
+    const size_t fixed = W * G::BYTES + 16;
+    const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64));
+    const uint32_t per = min((ntiles + device_cus() - 1) / device_cus(), per_max);
+    grid = (ntiles + per - 1) / per;
+    lds = fixed + (size_t)per * W * 64;
+}
+
+template <class Q, int BPW, int ACT>
+static hipError_t go_mq(const GemvArgs &a, hipStream_t s)
+{
+    static_assert(16 * MwGeom<Q, BPW>::BYTES + 16 + 16 * 64 <= 160 * 1024, "LDS per workgroup");
+    uint32_t W, grid;
+    size_t lds;
+    mq_plan<Q, BPW>(a, W, grid, lds);
+    const uint32_t ntiles = (a.N + 15) / 16;
+    if (grid == ntiles)
+        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, false>), dim3(grid), dim3(64 * W), lds, s, a, ntiles);
+    else
+        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, true>), dim3(grid), dim3(64 * W), lds, s, a, ntiles);
     return hipGetLastError();
 }
 
@@ -444,7 +529,8 @@ static hipError_t go_mq_act(const GemvArgs &a, uint32_t act, hipStream_t s)
 
 bool gemv_mfma_supported(const GemvArgs &a)
 {
-    return a.M == 1 && (a.type == T_Q4_K || a.type == T_Q5_K || a.type == T_Q6_K) && a.K <= 8192;
+    if (a.M != 1 || (a.type != T_Q4_K && a.type != T_Q5_K && a.type != T_Q6_K) || a.K > 8192) return false;
+    return a.w_bytes + RRR_READ_SLACK < MQ_OOB;
 }
 
 hipError_t launch_gemv_mfma(const GemvArgs &a, uint32_t act, hipStream_t s)
