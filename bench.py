@@ -2,7 +2,8 @@
 
 One "step" is the RMSNorm(3072) + Q5_K QKV GEMV (5120x3072) + Q6_K FFN-down
 GEMV (3072x8192) workload at batch 1, over seeded synthetic inputs resident
-in HBM.  Consecutive steps rotate through `--copies` distinct copies of the
+in HBM.  The RMSNorm runs inside the QKV GEMV (rrr_gemv_rmsnorm, bitwise equal
+to rrr_rmsnorm followed by rrr_gemv); the three-kernel form is reported too.  Consecutive steps rotate through `--copies` distinct copies of the
 two weight matrices (32 x 31.5 MB by default), so every step streams its
 weights from HBM rather than from the 256 MB Infinity Cache.  The timed
 steps are one HIP graph replay bracketed by a device sync and HIP events on
@@ -15,6 +16,11 @@ bounded sample) and the other workloads under "extra", among them the full
 32-layer decode sweep in ms/token.
 
     python bench.py [--gpus 1] [--steps 1280] [--warmup 128] [--no-cpu] [--no-decode] [--tokens 20]
+
+`--decode-only` runs just the decode sweep.  `--traffic` only runs the dominant kernel (64 launches over the rotating
+copies) and a calibration kernel of known traffic, for rocprofv3 --pmc
+FETCH_SIZE / WRITE_SIZE passes; profiles/gemv_q6k_3072x8192_traffic.md holds
+the result that fills roofline.traffic.
 """
 import argparse
 import json
@@ -34,6 +40,8 @@ import rrr_hip  # noqa: E402
 from rrr_hip import decode, synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_q6k_3072x8192_traffic.md")
+CAL_N = 16 << 20  # calibration residual_add: reads 2 x 64 MiB, writes 64 MiB
 D, QKV, FFN = 3072, 5120, 8192
 SEED = 2  # configs are seeded 1..5; this is the second one
 
@@ -82,6 +90,11 @@ class Config2:
 
     def step(self, i):
         c = self.ctx
+        c.gemv_rmsnorm(self.x, self.g, 1e-5, self.wq[i % self.copies], rrr_hip.Q5_K, self.qkv, D, QKV)
+        c.gemv(self.x2, self.wd[i % self.copies], rrr_hip.Q6_K, self.down, FFN, D)
+
+    def step_unfused(self, i):
+        c = self.ctx
         c.rmsnorm(self.x, self.g, self.normed, 1, D, 1e-5)
         c.gemv(self.normed, self.wq[i % self.copies], rrr_hip.Q5_K, self.qkv, D, QKV)
         c.gemv(self.x2, self.wd[i % self.copies], rrr_hip.Q6_K, self.down, FFN, D)
@@ -94,6 +107,34 @@ class Config2:
 
     def norm_only(self, i):
         self.ctx.rmsnorm(self.x, self.g, self.normed, 1, D, 1e-5)
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 summary (line `traffic_bytes_per_launch: N`), else None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def traffic_run(ctx, copies):
+    """The kernels of the --pmc passes, each launch synchronised."""
+    cfg = Config2(ctx, copies)
+    for i in range(64):
+        cfg.q6k_only(i)
+        ctx.sync()
+    a = ctx.to_device(np.ones(CAL_N, np.float32))
+    b = ctx.to_device(np.ones(CAL_N, np.float32))
+    o = ctx.alloc(CAL_N * 4)
+    for _ in range(4):
+        ctx.residual_add(a, b, o, CAL_N)
+        ctx.sync()
+    log(f"[bench] traffic run: 64 x q6k gemv 3072x8192, 4 x residual_add {CAL_N} floats")
 
 
 def decode_sweep(ctx, tokens):
@@ -174,6 +215,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--tokens", type=int, default=20)
+    ap.add_argument("--traffic", action="store_true")
+    ap.add_argument("--decode-only", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -182,6 +225,14 @@ def main():
 
     ctx = rrr_hip.Context(0)
     ctx.set_async(True)
+    if args.traffic:
+        traffic_run(ctx, args.copies)
+        ctx.close()
+        return
+    if args.decode_only:  # profiling aid: the sweep alone, its figures as JSON
+        print(json.dumps({"decode_sweep": decode_sweep(ctx, args.tokens)}), flush=True)
+        ctx.close()
+        return
     log(f"[bench] generating config-2 inputs, {args.copies} weight copies")
     cfg = Config2(ctx, args.copies)
     ctx.sync()
@@ -210,6 +261,9 @@ def main():
     value = B_STEP / (ms_step * 1e-3) / 1e9
     log(f"[bench] config 2: {ms_step * 1e3:.2f} us/step, {value:.1f} GB/s")
 
+    ms_unf = timed_graph(ctx, cfg.step_unfused, args.steps) / args.steps
+    log(f"[bench] config 2 as three kernels (rmsnorm, gemv, gemv): {ms_unf * 1e3:.2f} us/step")
+
     # dominant kernel alone, same rotation: average launch duration
     n_k = args.steps
     ms_q6 = timed_graph(ctx, cfg.q6k_only, n_k) / n_k
@@ -225,6 +279,8 @@ def main():
         "q5k_gemv_5120x3072": {"us": round(ms_q5 * 1e3, 3), "GBs": round(B_QKV / (ms_q5 * 1e-3) / 1e9, 1),
                                "frac_hbm": round(B_QKV / (ms_q5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": B_QKV},
         "rmsnorm_3072": {"us": round(ms_nm * 1e3, 3), "bytes": B_NORM},
+        "config2_three_kernels": {"us_per_step": round(ms_unf * 1e3, 3),
+                                  "GBs": round(B_STEP / (ms_unf * 1e-3) / 1e9, 1)},
     }
 
     if not args.no_decode:
@@ -248,11 +304,12 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded splitmix64: K-quant blocks per the config recipe, N(0,1) activations)",
-        "config": {"workload": "rmsnorm_3072 + q5k_gemv_5120x3072 + q6k_gemv_3072x8192, batch 1",
+        "config": {"workload": "rmsnorm_3072 + q5k_gemv_5120x3072 + q6k_gemv_3072x8192, batch 1 "
+                               "(RMSNorm fused into the QKV GEMV)",
                    "weight_copies": args.copies, "bytes_per_step": B_STEP, "seed": SEED},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_kernel<DecQ6K> 3072x8192", "bytes_per_launch": B_DOWN},
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "gemv_mq_kernel<MqQ6K> (int8 MFMA) 3072x8192", "bytes_per_launch": B_DOWN},
         "cpu_baseline": cpu,
         "extra": extra,
     }
