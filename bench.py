@@ -137,6 +137,24 @@ def traffic_run(ctx, copies):
     log(f"[bench] traffic run: 64 x q6k gemv 3072x8192, 4 x residual_add {CAL_N} floats")
 
 
+def host_roundtrip(ctx, cfg, n=200):
+    """The boundary's host-buffer call (rrr_matmul_kquant, mirror of
+    gpu_matmul_kquant): x uploaded from host memory, the Q6_K GEMV, y
+    downloaded, each call synchronous; host wall clock, median of n."""
+    ctx.set_async(False)
+    x = synth.normal_f32(SEED, 3, FFN)
+    times = []
+    for i in range(n + 10):
+        t0 = time.perf_counter()
+        ctx.matmul_kquant(cfg.x2, cfg.wd[i % cfg.copies], cfg.down, rrr_hip.Q6_K, x, FFN, D)
+        times.append(time.perf_counter() - t0)
+    ctx.set_async(True)
+    us = float(np.median(times[10:])) * 1e6
+    log(f"[bench] q6k gemv with host x / y (PCIe round trip, synchronous): {us:.1f} us")
+    return {"us": round(us, 2), "GBs": round(B_DOWN / (us * 1e-6) / 1e9, 1),
+            "note": "rrr_matmul_kquant: upload x (32 KiB), GEMV, download y (12 KiB), host clock"}
+
+
 def decode_sweep(ctx, tokens):
     """Full Phi-4-mini-shaped decode sweep (32 layers + final RMSNorm + F32
     logits over 200,064 entries + argmax), one HIP graph per token; the
@@ -282,6 +300,8 @@ def main():
         "config2_three_kernels": {"us_per_step": round(ms_unf * 1e3, 3),
                                   "GBs": round(B_STEP / (ms_unf * 1e-3) / 1e9, 1)},
     }
+
+    extra["q6k_gemv_host_roundtrip"] = host_roundtrip(ctx, cfg)
 
     if not args.no_decode:
         extra["decode_sweep"] = decode_sweep(ctx, args.tokens)
