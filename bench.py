@@ -155,6 +155,29 @@ def host_roundtrip(ctx, cfg, n=200):
             "note": "rrr_matmul_kquant: upload x (32 KiB), GEMV, download y (12 KiB), host clock"}
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
+
+
+def prefill(ctx, reps=20):
+    """Prefill dequant-GEMM, M = 512 tokens: X bf16 512x3072 . gate/up Q4_K
+    16384x3072 and X 512x8192 . down Q6_K 3072x8192 (fp16 MFMA, fp32
+    accumulate); graph of `reps` launches per shape, HIP events."""
+    out = {}
+    for name, qt, K, N in (("prefill_gateup_q4k_512x16384x3072", rrr_hip.Q4_K, 3072, 16384),
+                           ("prefill_down_q6k_512x3072x8192", rrr_hip.Q6_K, 8192, 3072)):
+        M = 512
+        W = ctx.weight_upload(qt, K, N, synth.weight(5, 1 + qt, qt, K, N))
+        X = ctx.to_device(synth.normal_bf16(5, 20 + qt, M * K))
+        Y = ctx.alloc(M * N * 4)
+        ms = timed_graph(ctx, lambda i: ctx.gemm_bf16(X, W, qt, Y, K, N, M), reps) / reps
+        tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        log(f"[bench] {name}: {ms * 1e3:.2f} us, {tf:.0f} TFLOP/s ({100 * tf / MFMA_PEAK_TFLOPS:.1f} % of fp16 peak)")
+        out[name] = {"us": round(ms * 1e3, 3), "TFLOPs": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4),
+                     "flops": 2 * M * N * K}
+        W.free(); X.free(); Y.free()
+    return out
+
+
 def decode_sweep(ctx, tokens):
     """Full Phi-4-mini-shaped decode sweep (32 layers + final RMSNorm + F32
     logits over 200,064 entries + argmax), one HIP graph per token; the
@@ -232,6 +255,7 @@ def main():
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--tokens", type=int, default=20)
     ap.add_argument("--traffic", action="store_true")
     ap.add_argument("--decode-only", action="store_true")
@@ -302,6 +326,8 @@ def main():
     }
 
     extra["q6k_gemv_host_roundtrip"] = host_roundtrip(ctx, cfg)
+    if not args.no_prefill:
+        extra.update(prefill(ctx))
 
     if not args.no_decode:
         extra["decode_sweep"] = decode_sweep(ctx, args.tokens)

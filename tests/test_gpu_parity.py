@@ -339,3 +339,39 @@ def test_graph_replay_matches_eager(ctx):
     graph.destroy()
     for t in (W, xb, gb, yb, ob):
         t.free()
+
+
+# ---- prefill dequant-GEMM (fp16 MFMA, fp32 accumulate): 2e-3 ------------------
+
+GEMM_TOL = 2e-3
+
+
+def bf16_to_f32(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("qtype,K,N,M", [(12, 3072, 16384, 128), (14, 8192, 192, 128), (13, 3072, 256, 256),
+                                         (12, 512, 128, 384), (14, 256, 64, 128)])
+def test_gemm_bf16_parity(ctx, qtype, K, N, M):
+    raw = weights(qtype, K, N, seed=11, stream=qtype)
+    xb = synth.normal_bf16(11, 50 + qtype, M * K)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    Xd, Yd = ctx.to_device(xb), ctx.alloc(M * N * 4)
+    ctx.gemm_bf16(Xd, W, qtype, Yd, K, N, M)
+    got = ctx.download(Yd, np.float32, M * N).reshape(M, N)
+    ref = orc.gemv(qtype, raw, bf16_to_f32(xb), K, N, M, THREADS, f64=True).reshape(M, N)
+    assert np.all(np.isfinite(got))
+    assert err(got, ref) < GEMM_TOL
+    # every row meets the bar on its own, so no tile is silently wrong
+    row_err = np.max(np.abs(got - ref), axis=1) / np.max(np.abs(ref), axis=1)
+    assert np.max(row_err) < 4 * GEMM_TOL
+    W.free(); Xd.free(); Yd.free()
+
+
+def test_gemm_bf16_unsupported_shapes(ctx):
+    W = ctx.weight_upload(12, 256, 64, weights(12, 256, 64))
+    X, Y = ctx.alloc(100 * 256 * 2), ctx.alloc(100 * 64 * 4)
+    with pytest.raises(rrr_hip.RrrError) as ei:
+        ctx.gemm_bf16(X, W, 12, Y, 256, 64, 100)      # M not a multiple of 128
+    assert ei.value.code == rrr_hip.engine.ERR_UNSUPPORTED
+    W.free(); X.free(); Y.free()
