@@ -212,7 +212,7 @@ __global__ __launch_bounds__(256) void gemm_dq_kernel(const uint16_t *X, const u
         Q::load(raw, wrs, wrow, 2 * (s & 1) + up, so_w);
 #pragma unroll
         for (int i = 0; i < XPT; i++)
-            xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xrow + 16 * i, so_x, RRR_CPOL_NT);
+            xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xrow + 16 * i, so_x, 0);  // reused by every N tile: cached
     };
     auto stage = [&](uint32_t s, int buf) {
         if (u_ok) {
