@@ -7,15 +7,18 @@
 // accumulators (lane l: A row l%16 and B column l%16 at k-group l/16, 8 f16
 // each; D rows 4*(l/16)+r of column l%16 in register r).
 //
-// K steps of BK = 128 (half a super-block).  Per step every weight row of the
-// tile contributes two 64-element units ("pairs": elements 64g..64g+63 of a
-// super-block, one scale pair for Q4_K/Q5_K, four scales for Q6_K); a thread
-// dequantizes one unit with the reference's formulas (phi4.rs:444-542) in f32
-// and rounds to f16 into LDS.  X rows are converted bf16 -> f16, exact for
-// |x| in f16's normal range.  LDS is double-buffered: the MFMAs of step s read
-// one buffer while the raw data of step s+1, loaded into registers during
-// step s-1, is dequantized into the other.  fp16 weights keep the product
-// error at 2^-12 per weight (bf16 weights would be 2^-9).
+// K steps of BK = 64 (a quarter super-block).  Per step each thread
+// dequantizes UE = BN/4 consecutive elements of one weight row into an fp16 LDS
+// tile and converts 64 * BM / 256 elements of X from bf16 to fp16 (exact for
+// |x| in f16's normal range).  The dequant runs in packed fp16: v_perm places
+// each quant byte q under the exponent of 1024 (f16 0x64qq = 1024 + q), an
+// exact v_pk_add removes the 1024 (1056 for Q6_K's offset), and one
+// v_pk_fma / v_pk_mul applies the sub-block scale and min (phi4.rs:444-542:
+// w = d*sc*q - dmin*m, w = d*sc*(q - 32)) with one rounding to fp16; fp16
+// weights keep the product error near 2^-11 per weight (bf16 would be 2^-8).
+// LDS is double-buffered: step s+1 is staged between the two MFMA halves of
+// step s so its VALU work overlaps the matrix core, and step s+2's loads are
+// issued behind it.
 //
 // Tile order: the M/BM tiles of one N tile get workgroup ids congruent mod 8,
 // so they run on the same XCD and the weight tile is fetched from HBM once.
@@ -42,139 +45,135 @@ __device__ __forceinline__ uint32_t pk_f16_rn(float a, float b)
     return __builtin_bit_cast(uint32_t, h);
 }
 
-// Raw bytes of one 64-element unit (pair g of a super-block) and its dequant.
-// Q4_K (phi4.rs:481-510): qs bytes 32g..32g+31, low nibbles = sub-block 2g,
-// high nibbles = 2g+1; w = (d*sc)*q - (dmin*m).
+__device__ __forceinline__ f16x2v f16x2_bits(uint32_t v) { return __builtin_bit_cast(f16x2v, v); }
+__device__ __forceinline__ uint32_t bits_f16x2(f16x2v v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Four quant bytes (each < 1024) of one dword -> two fp16 pairs (1024 + q)
+__device__ __forceinline__ void q4_to_f16(uint32_t v, f16x2v &p01, f16x2v &p23)
+{
+    p01 = f16x2_bits(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u));
+    p23 = f16x2_bits(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u));
+}
+
+// Units of UE consecutive elements e0 .. e0+UE-1 of one super-block row
+// (e0 % UE == 0, UE in {16, 32}).  Load offsets split into a per-lane part
+// (voff: row start + position inside the chunk) and the step's uniform part
+// (soff: block start + chunk position), so the loads need no VALU per step.
+// dequant() writes UE/2 dwords of fp16 pairs in element order.
+
+// Q4_K (phi4.rs:481-510): element 64g + 32h + l is the h-th nibble of qs[32g + l]
+// of sub-block 2g + h; w = (d*sc)*q - dmin*m.
+template <int UE>
 struct GqQ4K {
     static constexpr uint32_t BS = 144;
-    struct Raw { u32x4 hdr, q0, q1; };
-    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t g, uint32_t so)
+    struct Raw { u32x4 hdr, q[UE / 16]; };
+    // chunk c (64 elements, = pair g), lane part lp = UE * p inside the chunk
+    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t lp)
     {
-        r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, boff, so, RRR_CPOL_NT);
-        r.q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 16 + 32 * g, so, RRR_CPOL_NT);
-        r.q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 32 + 32 * g, so, RRR_CPOL_NT);
+        r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, blk, 0);
+#pragma unroll
+        for (int i = 0; i < UE / 16; i++)
+            r.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 + (lp & 31) + 16 * i, blk + 32 * c, 0);
     }
-    // out[j] packs elements 2j, 2j+1 of the unit (32 dwords)
-    __device__ static void dequant(const Raw &r, uint32_t g, uint32_t *out)
+    __device__ static void dequant(const Raw &r, uint32_t c, uint32_t lp, uint32_t *out)
     {
-        const float d = h2f(r.hdr.x), dmin = h2f(r.hdr.x >> 16);
-        uint32_t s0, m0, s1, m1;
-        scale_min_k4(2 * g, r.hdr.y, r.hdr.z, r.hdr.w, s0, m0);
-        scale_min_k4(2 * g + 1, r.hdr.y, r.hdr.z, r.hdr.w, s1, m1);
-        const float a0 = __fmul_rn(d, (float)s0), b0 = __fmul_rn(dmin, (float)m0);
-        const float a1 = __fmul_rn(d, (float)s1), b1 = __fmul_rn(dmin, (float)m1);
-        const u32x4 q[2] = {r.q0, r.q1};
+        const uint32_t sb = 2 * c + (lp >> 5), h = lp >> 5;
+        uint32_t sc, mn;
+        scale_min_k4(sb, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
+        const _Float16 A = (_Float16)__fmul_rn(h2f(r.hdr.x), (float)sc);
+        const _Float16 Bn = (_Float16)(-__fmul_rn(h2f(r.hdr.x >> 16), (float)mn));
+        const f16x2v A2 = {A, A}, B2 = {Bn, Bn}, K2 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t w = q[i >> 2][i & 3];  // bytes 4i..4i+3 of the 32
-#pragma unroll
-            for (int h = 0; h < 2; h++) {        // h=0: low nibbles (sub-block 2g), h=1: high (2g+1)
-                const uint32_t v = (w >> (4 * h)) & 0x0F0F0F0Fu;
-                const float A = h ? a1 : a0, B = h ? b1 : b0;
-                const float e0 = __fsub_rn(__fmul_rn(A, (float)(v & 255u)), B);
-                const float e1 = __fsub_rn(__fmul_rn(A, (float)((v >> 8) & 255u)), B);
-                const float e2 = __fsub_rn(__fmul_rn(A, (float)((v >> 16) & 255u)), B);
-                const float e3 = __fsub_rn(__fmul_rn(A, (float)(v >> 24)), B);
-                out[16 * h + 2 * i] = pk_f16_rn(e0, e1);
-                out[16 * h + 2 * i + 1] = pk_f16_rn(e2, e3);
-            }
+        for (int i = 0; i < UE / 4; i++) {
+            const uint32_t v = (r.q[i >> 2][i & 3] >> (4 * h)) & 0x0F0F0F0Fu;
+            f16x2v p01, p23;
+            q4_to_f16(v, p01, p23);
+            out[2 * i] = bits_f16x2(__builtin_elementwise_fma(A2, p01 - K2, B2));
+            out[2 * i + 1] = bits_f16x2(__builtin_elementwise_fma(A2, p23 - K2, B2));
         }
     }
 };
 
-// Q5_K (phi4.rs:512-542): Q4_K plus bit (2g / 2g+1) of qh[l] as bit 4.
+// Q5_K (phi4.rs:512-542): Q4_K plus bit sb of qh[l] as bit 4.
+template <int UE>
 struct GqQ5K {
     static constexpr uint32_t BS = 176;
-    struct Raw { u32x4 hdr, h0, h1, q0, q1; };
-    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t g, uint32_t so)
+    struct Raw { u32x4 hdr, qh[UE / 16], q[UE / 16]; };
+    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t lp)
     {
-        r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, boff, so, RRR_CPOL_NT);
-        r.h0 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 16, so, RRR_CPOL_NT);
-        r.h1 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 32, so, RRR_CPOL_NT);
-        r.q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 48 + 32 * g, so, RRR_CPOL_NT);
-        r.q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 64 + 32 * g, so, RRR_CPOL_NT);
+        r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, blk, 0);
+#pragma unroll
+        for (int i = 0; i < UE / 16; i++) {
+            r.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 + (lp & 31) + 16 * i, blk, 0);
+            r.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 48 + (lp & 31) + 16 * i, blk + 32 * c, 0);
+        }
     }
-    __device__ static void dequant(const Raw &r, uint32_t g, uint32_t *out)
+    __device__ static void dequant(const Raw &r, uint32_t c, uint32_t lp, uint32_t *out)
     {
-        const float d = h2f(r.hdr.x), dmin = h2f(r.hdr.x >> 16);
-        uint32_t s0, m0, s1, m1;
-        scale_min_k4(2 * g, r.hdr.y, r.hdr.z, r.hdr.w, s0, m0);
-        scale_min_k4(2 * g + 1, r.hdr.y, r.hdr.z, r.hdr.w, s1, m1);
-        const float a0 = __fmul_rn(d, (float)s0), b0 = __fmul_rn(dmin, (float)m0);
-        const float a1 = __fmul_rn(d, (float)s1), b1 = __fmul_rn(dmin, (float)m1);
-        const u32x4 q[2] = {r.q0, r.q1}, qh[2] = {r.h0, r.h1};
+        const uint32_t sb = 2 * c + (lp >> 5), h = lp >> 5;
+        uint32_t sc, mn;
+        scale_min_k4(sb, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
+        const _Float16 A = (_Float16)__fmul_rn(h2f(r.hdr.x), (float)sc);
+        const _Float16 Bn = (_Float16)(-__fmul_rn(h2f(r.hdr.x >> 16), (float)mn));
+        const f16x2v A2 = {A, A}, B2 = {Bn, Bn}, K2 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t w = q[i >> 2][i & 3], hb = qh[i >> 2][i & 3];
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint32_t v = ((w >> (4 * h)) & 0x0F0F0F0Fu) | (((hb >> (2 * g + h)) & 0x01010101u) << 4);
-                const float A = h ? a1 : a0, B = h ? b1 : b0;
-                const float e0 = __fsub_rn(__fmul_rn(A, (float)(v & 255u)), B);
-                const float e1 = __fsub_rn(__fmul_rn(A, (float)((v >> 8) & 255u)), B);
-                const float e2 = __fsub_rn(__fmul_rn(A, (float)((v >> 16) & 255u)), B);
-                const float e3 = __fsub_rn(__fmul_rn(A, (float)(v >> 24)), B);
-                out[16 * h + 2 * i] = pk_f16_rn(e0, e1);
-                out[16 * h + 2 * i + 1] = pk_f16_rn(e2, e3);
-            }
+        for (int i = 0; i < UE / 4; i++) {
+            const uint32_t v = ((r.q[i >> 2][i & 3] >> (4 * h)) & 0x0F0F0F0Fu) |
+                               (((r.qh[i >> 2][i & 3] >> sb) & 0x01010101u) << 4);
+            f16x2v p01, p23;
+            q4_to_f16(v, p01, p23);
+            out[2 * i] = bits_f16x2(__builtin_elementwise_fma(A2, p01 - K2, B2));
+            out[2 * i + 1] = bits_f16x2(__builtin_elementwise_fma(A2, p23 - K2, B2));
         }
     }
 };
 
-// Q6_K (phi4.rs:444-479): pair g = quadrants 2(g&1), 2(g&1)+1 of half g/2:
-// element 64g + 32u + l (u = 0, 1) is ql[64(g/2) + 32u + l] (low nibble for even
-// g, high for odd) with qh[32(g/2) + l] bits 2(2(g&1)+u); scale index
-// is = (64g + 32u + l) / 16; w = (d*sc[is]) * (q - 32).
+// Q6_K (phi4.rs:444-479): element 128h6 + 32Qd + l is ql[64h6 + 32(Qd&1) + l]
+// (high nibble when Qd >= 2) with qh[32h6 + l] bits 2Qd; scale sc[e/16] (the
+// is = g*8 + l/16 rule, phi4.rs:463); w = (d*sc)*(q - 32).
+template <int UE>
 struct GqQ6K {
     static constexpr uint32_t BS = 210;
-    struct Raw { u32x4 l0, l1, l2, l3, h0, h1; uint32_t sc, d; };
-    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t boff, uint32_t g, uint32_t so)
+    struct Raw { u32x4 ql[UE / 16], qh[UE / 16]; uint32_t sc, d; };
+    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t lp)
     {
-        const uint32_t g6 = g >> 1;
-        r.l0 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 64 * g6, so, RRR_CPOL_NT);
-        r.l1 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 64 * g6 + 16, so, RRR_CPOL_NT);
-        r.l2 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 64 * g6 + 32, so, RRR_CPOL_NT);
-        r.l3 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 64 * g6 + 48, so, RRR_CPOL_NT);
-        r.h0 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 128 + 32 * g6, so, RRR_CPOL_NT);
-        r.h1 = __builtin_amdgcn_raw_buffer_load_b128(rs, boff + 128 + 32 * g6 + 16, so, RRR_CPOL_NT);
-        r.sc = __builtin_amdgcn_raw_buffer_load_b32(rs, boff + 192 + 4 * g, so, RRR_CPOL_NT);
-        r.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, boff + 208, so, RRR_CPOL_NT);
+        const uint32_t h6 = c >> 1, l0 = lp & 31, qd1 = (lp >> 5) & 1;
+#pragma unroll
+        for (int i = 0; i < UE / 16; i++) {
+            r.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 32 * qd1 + l0 + 16 * i, blk + 64 * h6, 0);
+            r.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 128 + l0 + 16 * i, blk + 32 * h6, 0);
+        }
+        r.sc = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 192, blk + 4 * c, 0);
+        r.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, voff + 208, blk, 0);
     }
-    __device__ static void dequant(const Raw &r, uint32_t g, uint32_t *out)
+    __device__ static void dequant(const Raw &r, uint32_t c, uint32_t lp, uint32_t *out)
     {
+        const uint32_t qd = 2 * (c & 1) + (lp >> 5), hi = c & 1, is0 = lp >> 4;   // is = 4c + lp/16 (+1)
         const float d = h2f(r.d);
-        const uint32_t hi = g & 1;
-        float ds[4];
+        const f16x2v K2 = {(_Float16)1056.0f, (_Float16)1056.0f};
 #pragma unroll
-        for (int s = 0; s < 4; s++) ds[s] = __fmul_rn(d, (float)(int8_t)byte_of(r.sc, s));
-        const u32x4 ql[4] = {r.l0, r.l1, r.l2, r.l3}, qh[2] = {r.h0, r.h1};
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) {                          // positions l = 4i..4i+3
-                const uint32_t w = ql[2 * u + (i >> 2)][i & 3], hb = qh[i >> 2][i & 3];
-                const uint32_t shift = 2 * (2 * hi + u);
-                const uint32_t v = ((w >> (4 * hi)) & 0x0F0F0F0Fu) | (((hb >> shift) & 0x03030303u) << 4);
-                const float A = ds[2 * u + (i >= 4)];              // is = 4g + 2u + l/16
-                const float e0 = __fmul_rn(A, (float)((int)(v & 255u) - 32));
-                const float e1 = __fmul_rn(A, (float)((int)((v >> 8) & 255u) - 32));
-                const float e2 = __fmul_rn(A, (float)((int)((v >> 16) & 255u) - 32));
-                const float e3 = __fmul_rn(A, (float)((int)(v >> 24) - 32));
-                out[16 * u + 2 * i] = pk_f16_rn(e0, e1);
-                out[16 * u + 2 * i + 1] = pk_f16_rn(e2, e3);
-            }
+        for (int i = 0; i < UE / 4; i++) {
+            const _Float16 A = (_Float16)__fmul_rn(d, (float)(int8_t)byte_of(r.sc, is0 + (i >> 2)));
+            const f16x2v A2 = {A, A};
+            const uint32_t v = ((r.ql[i >> 2][i & 3] >> (4 * hi)) & 0x0F0F0F0Fu) |
+                               (((r.qh[i >> 2][i & 3] >> (2 * qd)) & 0x03030303u) << 4);
+            f16x2v p01, p23;
+            q4_to_f16(v, p01, p23);
+            out[2 * i] = bits_f16x2(A2 * (p01 - K2));
+            out[2 * i + 1] = bits_f16x2(A2 * (p23 - K2));
         }
     }
 };
 
-template <class Q, int BM, int BN>
+template <template <int> class QT, int BM, int BN>
 __global__ __launch_bounds__(256) void gemm_dq_kernel(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K,
                                                       uint32_t N, uint32_t M, uint32_t tiles_n)
 {
-    constexpr int BK = 128, LDK = BK + 8;                  // f16 per LDS row (16-byte pad)
+    constexpr int BK = 64, LDK = BK + 8;                   // f16 per LDS row (16-byte pad)
     constexpr int TI = BM / 32, TJ = BN / 32;              // 16x16 tiles per wave
-    constexpr int UNITS = BN * 2;                          // weight units per step
-    constexpr int XPT = BM * BK / 256 / 8;                 // X 16-byte loads per thread
+    constexpr int TPW = 256 / BN, UE = 64 / TPW;           // threads per weight row, elements per thread
+    constexpr int TPX = 256 / BM, XE = 64 / TPX;           // threads per X row, elements per thread
+    using Q = QT<UE>;
     extern __shared__ float smem[];
     _Float16 *As = (_Float16 *)smem;                       // [2][BM][LDK]
     _Float16 *Bs = As + 2 * BM * LDK;                      // [2][BN][LDK]
@@ -194,37 +193,33 @@ __global__ __launch_bounds__(256) void gemm_dq_kernel(const uint16_t *X, const u
     const uint32_t m0 = mt * BM, n0 = nt * BN;
     const uint32_t nsteps = K / BK, B = K / 256;
 
-    // weight unit of this thread: row n0 + ur, pair 2*(step%2) + up
-    const bool u_ok = t < UNITS;
-    const uint32_t ur = (t >> 1) % BN, up = t & 1;
+    // weight unit of this thread: row n0 + ur, elements UE*up .. of each 64-chunk
+    const uint32_t ur = t / TPW, lp = UE * (t % TPW);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, (uint64_t)N * B * Q::BS);
-    const uint32_t wrow = (n0 + ur) * B * Q::BS;
-    // X: thread covers row m0 + xr, 8 * XPT consecutive k of the step
-    const uint32_t xr = t / (256 / BM), xk = (t % (256 / BM)) * 8 * XPT;
+    const uint32_t wvoff = (n0 + ur) * B * Q::BS;
+    // X: thread covers row m0 + xr, XE consecutive k of each step
+    const uint32_t xr = t / TPX, xk = XE * (t % TPX);
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X, (uint64_t)M * K * 2);
-    const uint32_t xrow = ((m0 + xr) * K + xk) * 2;
+    const uint32_t xvoff = ((m0 + xr) * K + xk) * 2;
 
     typename Q::Raw raw;
-    u32x4 xv[XPT];
+    u32x4 xv[XE / 8];
     auto issue = [&](uint32_t s) {
-        const uint32_t so_w = s < nsteps ? (s >> 1) * Q::BS : GM_OOB;
-        const uint32_t so_x = s < nsteps ? s * BK * 2 : GM_OOB;
-        Q::load(raw, wrs, wrow, 2 * (s & 1) + up, so_w);
+        const bool ok = s < nsteps;
+        Q::load(raw, wrs, wvoff, ok ? (s >> 2) * Q::BS : GM_OOB, s & 3, lp);
+        const uint32_t so = ok ? s * BK * 2 : GM_OOB;
 #pragma unroll
-        for (int i = 0; i < XPT; i++)
-            xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xrow + 16 * i, so_x, 0);  // reused by every N tile: cached
+        for (int i = 0; i < XE / 8; i++) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvoff + 16 * i, so, 0);
     };
     auto stage = [&](uint32_t s, int buf) {
-        if (u_ok) {
-            uint32_t o[32];
-            Q::dequant(raw, 2 * (s & 1) + up, o);
-            _Float16 *dst = Bs + (buf * BN + ur) * LDK + 64 * up;
+        uint32_t o[UE / 2];
+        Q::dequant(raw, s & 3, lp, o);
+        _Float16 *dst = Bs + (buf * BN + ur) * LDK + lp;
 #pragma unroll
-            for (int i = 0; i < 8; i++) *(u32x4 *)(dst + 8 * i) = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
-        }
+        for (int i = 0; i < UE / 8; i++) *(u32x4 *)(dst + 8 * i) = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
         _Float16 *xd = As + (buf * BM + xr) * LDK + xk;
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
+        for (int i = 0; i < XE / 8; i++) {
             const u32x4 v = xv[i];
             u32x4 h;
 #pragma unroll
@@ -239,31 +234,32 @@ __global__ __launch_bounds__(256) void gemm_dq_kernel(const uint16_t *X, const u
 #pragma unroll
         for (int j = 0; j < TJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    const uint32_t fr = lane & 15, fk = 8 * (lane >> 4);
+    auto mfma_half = [&](int cur, int kk) {
+        const _Float16 *Ab = As + (cur * BM + wm * (BM / 2) + fr) * LDK + fk + 32 * kk;
+        const _Float16 *Bb = Bs + (cur * BN + wn * (BN / 2) + fr) * LDK + fk + 32 * kk;
+        f16x8v a[TI], b[TJ];
+#pragma unroll
+        for (int i = 0; i < TI; i++) a[i] = *(const f16x8v *)(Ab + 16 * i * LDK);
+#pragma unroll
+        for (int j = 0; j < TJ; j++) b[j] = *(const f16x8v *)(Bb + 16 * j * LDK);
+#pragma unroll
+        for (int i = 0; i < TI; i++)
+#pragma unroll
+            for (int j = 0; j < TJ; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    };
+
     issue(0);
     stage(0, 0);
     issue(1);
     __syncthreads();
-    const uint32_t fr = lane & 15, fk = 8 * (lane >> 4);
     for (uint32_t s = 0; s < nsteps; s++) {
         const int cur = s & 1;
-        const _Float16 *Ab = As + (cur * BM + wm * (BM / 2) + fr) * LDK + fk;
-        const _Float16 *Bb = Bs + (cur * BN + wn * (BN / 2) + fr) * LDK + fk;
-#pragma unroll
-        for (int kk = 0; kk < BK / 32; kk++) {
-            f16x8v a[TI], b[TJ];
-#pragma unroll
-            for (int i = 0; i < TI; i++) a[i] = *(const f16x8v *)(Ab + 16 * i * LDK + 32 * kk);
-#pragma unroll
-            for (int j = 0; j < TJ; j++) b[j] = *(const f16x8v *)(Bb + 16 * j * LDK + 32 * kk);
-#pragma unroll
-            for (int i = 0; i < TI; i++)
-#pragma unroll
-                for (int j = 0; j < TJ; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-        // next step's data into the other buffer, then the loads two steps ahead
-        stage(s + 1, cur ^ 1);
+        mfma_half(cur, 0);
+        stage(s + 1, cur ^ 1);   // overlaps the matrix core's work on the first half
         issue(s + 2);
+        mfma_half(cur, 1);
         __syncthreads();
     }
 
@@ -281,24 +277,24 @@ __global__ __launch_bounds__(256) void gemm_dq_kernel(const uint16_t *X, const u
         }
 }
 
-template <class Q, int BM, int BN>
+template <template <int> class QT, int BM, int BN>
 static hipError_t go_gemm(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K, uint32_t N, uint32_t M,
                           hipStream_t s)
 {
-    constexpr size_t lds = 2 * (size_t)(BM + BN) * (128 + 8) * 2;
+    constexpr size_t lds = 2 * (size_t)(BM + BN) * (64 + 8) * 2;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
     const uint32_t tiles_n = N / BN, tiles = tiles_n * (M / BM);
-    hipLaunchKernelGGL((gemm_dq_kernel<Q, BM, BN>), dim3(tiles), dim3(256), lds, s, X, W, Y, K, N, M, tiles_n);
+    hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN>), dim3(tiles), dim3(256), lds, s, X, W, Y, K, N, M, tiles_n);
     return hipGetLastError();
 }
 
-template <class Q>
+template <template <int> class QT>
 static hipError_t go_gemm_t(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K, uint32_t N, uint32_t M,
                             hipStream_t s)
 {
-    // 128 x 128 tiles when they fill the CUs, else 128 x 64
-    if (N % 128 == 0 && (N / 128) * (M / 128) >= 256) return go_gemm<Q, 128, 128>(X, W, Y, K, N, M, s);
-    return go_gemm<Q, 128, 64>(X, W, Y, K, N, M, s);
+    // 256 x 128 tiles when they cover at least half of the CUs, else 128 x 64
+    if (M % 256 == 0 && N % 128 == 0 && (N / 128) * (M / 256) >= 128) return go_gemm<QT, 256, 128>(X, W, Y, K, N, M, s);
+    return go_gemm<QT, 128, 64>(X, W, Y, K, N, M, s);
 }
 
 bool gemm_bf16_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t w_bytes, uint64_t x_bytes)

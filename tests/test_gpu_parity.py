@@ -351,7 +351,9 @@ def bf16_to_f32(bits):
 
 
 @pytest.mark.parametrize("qtype,K,N,M", [(12, 3072, 16384, 128), (14, 8192, 192, 128), (13, 3072, 256, 256),
-                                         (12, 512, 128, 384), (14, 256, 64, 128)])
+                                         (12, 512, 128, 384), (14, 256, 64, 128),
+                                         # 256 x 128 workgroup tiles
+                                         (12, 512, 16384, 256), (14, 768, 16384, 256), (13, 256, 16384, 256)])
 def test_gemm_bf16_parity(ctx, qtype, K, N, M):
     raw = weights(qtype, K, N, seed=11, stream=qtype)
     xb = synth.normal_bf16(11, 50 + qtype, M * K)
