@@ -2,23 +2,23 @@
 // in raw Q4_K / Q5_K / Q6_K super-blocks (the batched shape of phi4.rs:1257-1268
 // at prompt length; the reference has no MFMA kernel for it).
 //
-// Workgroup: 256 threads = 2 x 2 waves over a BM x BN output tile, each wave a
-// (BM/2) x (BN/2) block of 16x16 v_mfma_f32_16x16x32_f16 tiles with fp32
-// accumulators (lane l: A row l%16 and B column l%16 at k-group l/16, 8 f16
-// each; D rows 4*(l/16)+r of column l%16 in register r).
+// Workgroup: 512 threads.  Waves 0-3 (2 x 2) each own a (BM/2) x (BN/2)
+// block of 16x16 v_mfma_f32_16x16x32_f16 tiles with fp32 accumulators (lane
+// l: A row l%16 and B column l%16 at k-group l/16, 8 f16 each; D rows
+// 4*(l/16)+r of column l%16 in register r).  Waves 4-7 stage the operands.
 //
-// K steps of BK = 64 (a quarter super-block).  Per step each thread
-// dequantizes UE = BN/4 consecutive elements of one weight row into an fp16 LDS
-// tile and converts 64 * BM / 256 elements of X from bf16 to fp16 (exact for
-// |x| in f16's normal range).  The dequant runs in packed fp16: v_perm places
+// K steps of BK elements.  Per step each staging thread dequantizes
+// UE = BN*BK/256 consecutive elements of one weight row into an fp16 LDS tile
+// and converts BM*BK/256 elements of X from bf16 to fp16 (exact for |x| in
+// f16's normal range).  The dequant runs in packed fp16: v_perm places
 // each quant byte q under the exponent of 1024 (f16 0x64qq = 1024 + q), an
 // exact v_pk_add removes the 1024 (1056 for Q6_K's offset), and one
 // v_pk_fma / v_pk_mul applies the sub-block scale and min (phi4.rs:444-542:
 // w = d*sc*q - dmin*m, w = d*sc*(q - 32)) with one rounding to fp16; fp16
 // weights keep the product error near 2^-11 per weight (bf16 would be 2^-8).
-// LDS is double-buffered: step s+1 is staged between the two MFMA halves of
-// step s so its VALU work overlaps the matrix core, and step s+2's loads are
-// issued behind it.
+// LDS is double-buffered: step s+1 is staged while the MFMA waves work on
+// step s; a ring of three register sets keeps the loads of steps s+2 .. s+4
+// in flight.
 //
 // Tile order: the M/BM tiles of one N tile get workgroup ids congruent mod 8,
 // so they run on the same XCD and the weight tile is fetched from HBM once.
@@ -56,9 +56,8 @@ __device__ __forceinline__ void q4_to_f16(uint32_t v, f16x2v &p01, f16x2v &p23)
 }
 
 // Units of UE consecutive elements e0 .. e0+UE-1 of one super-block row
-// (e0 % UE == 0, UE in {16, 32}).  Load offsets split into a per-lane part
-// (voff: row start + position inside the chunk) and the step's uniform part
-// (soff: block start + chunk position), so the loads need no VALU per step.
+// (e0 = 64c + lp, lp % UE == 0, lp < 64, UE in {16, 32}).  Loads take the row
+// and in-block offset in voff and the block start in the scalar offset blk.
 // dequant() writes UE/2 dwords of fp16 pairs in element order.
 
 // Q4_K (phi4.rs:481-510): element 64g + 32h + l is the h-th nibble of qs[32g + l]
@@ -73,7 +72,7 @@ struct GqQ4K {
         r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, blk, 0);
 #pragma unroll
         for (int i = 0; i < UE / 16; i++)
-            r.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 + (lp & 31) + 16 * i, blk + 32 * c, 0);
+            r.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 + 32 * c + (lp & 31) + 16 * i, blk, 0);
     }
     __device__ static void dequant(const Raw &r, uint32_t c, uint32_t lp, uint32_t *out)
     {
@@ -105,7 +104,7 @@ struct GqQ5K {
 #pragma unroll
         for (int i = 0; i < UE / 16; i++) {
             r.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 + (lp & 31) + 16 * i, blk, 0);
-            r.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 48 + (lp & 31) + 16 * i, blk + 32 * c, 0);
+            r.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 48 + 32 * c + (lp & 31) + 16 * i, blk, 0);
         }
     }
     __device__ static void dequant(const Raw &r, uint32_t c, uint32_t lp, uint32_t *out)
@@ -140,10 +139,10 @@ struct GqQ6K {
         const uint32_t h6 = c >> 1, l0 = lp & 31, qd1 = (lp >> 5) & 1;
 #pragma unroll
         for (int i = 0; i < UE / 16; i++) {
-            r.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 32 * qd1 + l0 + 16 * i, blk + 64 * h6, 0);
-            r.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 128 + l0 + 16 * i, blk + 32 * h6, 0);
+            r.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * h6 + 32 * qd1 + l0 + 16 * i, blk, 0);
+            r.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 128 + 32 * h6 + l0 + 16 * i, blk, 0);
         }
-        r.sc = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 192, blk + 4 * c, 0);
+        r.sc = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 192 + 4 * c, blk, 0);
         r.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, voff + 208, blk, 0);
     }
     __device__ static void dequant(const Raw &r, uint32_t c, uint32_t lp, uint32_t *out)
@@ -165,21 +164,26 @@ struct GqQ6K {
     }
 };
 
-template <template <int> class QT, int BM, int BN>
-__global__ __launch_bounds__(256) void gemm_dq_kernel(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K,
+// Warp-specialised form: waves 0-3 run the MFMAs of a BM x BN tile (2 x 2,
+// each (BM/2) x (BN/2)), waves 4-7 load, dequantize and convert the next step
+// into the other LDS buffer, so every SIMD holds one wave of each kind and the
+// staging VALU fills the matrix core's gaps.  Both roles pass one barrier per
+// step (plus one after the prologue) on separate straight-line paths.
+template <template <int> class QT, int BM, int BN, int BK>
+__global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K,
                                                       uint32_t N, uint32_t M, uint32_t tiles_n)
 {
-    constexpr int BK = 64, LDK = BK + 8;                   // f16 per LDS row (16-byte pad)
-    constexpr int TI = BM / 32, TJ = BN / 32;              // 16x16 tiles per wave
-    constexpr int TPW = 256 / BN, UE = 64 / TPW;           // threads per weight row, elements per thread
-    constexpr int TPX = 256 / BM, XE = 64 / TPX;           // threads per X row, elements per thread
+    constexpr int LDK = BK + 8;                            // f16 per LDS row (16-byte pad)
+    constexpr int TI = BM / 32, TJ = BN / 32;              // 16x16 tiles per MFMA wave
+    constexpr int UE = BN * BK / 256, TPW = BK / UE;       // weight elements per producer thread, threads per row
+    constexpr int XE = BM * BK / 256, TPX = BK / XE;       // X elements per producer thread, threads per row
+    static_assert((UE == 16 || UE == 32) && XE % 8 == 0 && BK % 64 == 0, "tile shape");
     using Q = QT<UE>;
     extern __shared__ float smem[];
     _Float16 *As = (_Float16 *)smem;                       // [2][BM][LDK]
     _Float16 *Bs = As + 2 * BM * LDK;                      // [2][BN][LDK]
 
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const uint32_t wm = wave >> 1, wn = wave & 1;
     // tile of this workgroup (same XCD for the M tiles of one N tile)
     const uint32_t id = blockIdx.x, tiles_m = M / BM;
     uint32_t nt, mt;
@@ -193,73 +197,101 @@ __global__ __launch_bounds__(256) void gemm_dq_kernel(const uint16_t *X, const u
     const uint32_t m0 = mt * BM, n0 = nt * BN;
     const uint32_t nsteps = K / BK, B = K / 256;
 
-    // weight unit of this thread: row n0 + ur, elements UE*up .. of each 64-chunk
-    const uint32_t ur = t / TPW, lp = UE * (t % TPW);
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, (uint64_t)N * B * Q::BS);
-    const uint32_t wvoff = (n0 + ur) * B * Q::BS;
-    // X: thread covers row m0 + xr, XE consecutive k of each step
-    const uint32_t xr = t / TPX, xk = XE * (t % TPX);
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X, (uint64_t)M * K * 2);
-    const uint32_t xvoff = ((m0 + xr) * K + xk) * 2;
-
-    typename Q::Raw raw;
-    u32x4 xv[XE / 8];
-    auto issue = [&](uint32_t s) {
-        const bool ok = s < nsteps;
-        Q::load(raw, wrs, wvoff, ok ? (s >> 2) * Q::BS : GM_OOB, s & 3, lp);
-        const uint32_t so = ok ? s * BK * 2 : GM_OOB;
+    if (wave >= 4) {
+        // ---- producer: loads, dequant, conversion --------------------------
+        const uint32_t tp = t - 256;
+        const uint32_t ur = tp / TPW, lb = UE * (tp % TPW);   // row, first element inside the step
+        const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, (uint64_t)N * B * Q::BS);
+        const uint32_t wvoff = (n0 + ur) * B * Q::BS;
+        const uint32_t xr = tp / TPX, xk = XE * (tp % TPX);
+        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X, (uint64_t)M * K * 2);
+        const uint32_t xvoff = ((m0 + xr) * K + xk) * 2;
+        struct Set {
+            typename Q::Raw raw;
+            u32x4 xv[XE / 8];
+        };
+        Set S0, S1, S2;
+        // element e0 of the step's unit inside its super-block: chunk e0/64, lane part e0%64
+        auto issue = [&](Set &st, uint32_t s) {
+            const bool ok = s < nsteps;   // past the end: out-of-range offsets, zeros
+            const uint32_t e0 = (s * BK) % 256 + lb;
+            Q::load(st.raw, wrs, wvoff, ok ? (s * BK / 256) * Q::BS : GM_OOB, e0 >> 6, e0 & 63);
+            const uint32_t so = ok ? s * BK * 2 : GM_OOB;
 #pragma unroll
-        for (int i = 0; i < XE / 8; i++) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvoff + 16 * i, so, 0);
-    };
-    auto stage = [&](uint32_t s, int buf) {
-        uint32_t o[UE / 2];
-        Q::dequant(raw, s & 3, lp, o);
-        _Float16 *dst = Bs + (buf * BN + ur) * LDK + lp;
+            for (int i = 0; i < XE / 8; i++) st.xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvoff + 16 * i, so, 0);
+        };
+        auto stage = [&](const Set &st, uint32_t s) {
+            const uint32_t buf = s & 1, e0 = (s * BK) % 256 + lb;
+            uint32_t o[UE / 2];
+            Q::dequant(st.raw, e0 >> 6, e0 & 63, o);
+            _Float16 *dst = Bs + (buf * BN + ur) * LDK + lb;
 #pragma unroll
-        for (int i = 0; i < UE / 8; i++) *(u32x4 *)(dst + 8 * i) = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
-        _Float16 *xd = As + (buf * BM + xr) * LDK + xk;
+            for (int i = 0; i < UE / 8; i++) *(u32x4 *)(dst + 8 * i) = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+            _Float16 *xd = As + (buf * BM + xr) * LDK + xk;
 #pragma unroll
-        for (int i = 0; i < XE / 8; i++) {
-            const u32x4 v = xv[i];
-            u32x4 h;
+            for (int i = 0; i < XE / 8; i++) {
+                const u32x4 v = st.xv[i];
+                u32x4 h;
 #pragma unroll
-            for (int c = 0; c < 4; c++) h[c] = pk_f16(__uint_as_float(v[c] << 16), __uint_as_float(v[c] & 0xFFFF0000u));
-            *(u32x4 *)(xd + 8 * i) = h;
+                for (int c = 0; c < 4; c++) h[c] = pk_f16(__uint_as_float(v[c] << 16), __uint_as_float(v[c] & 0xFFFF0000u));
+                *(u32x4 *)(xd + 8 * i) = h;
+            }
+        };
+        issue(S0, 0);
+        issue(S1, 1);
+        issue(S2, 2);
+        stage(S0, 0);
+        issue(S0, 3);
+        __syncthreads();
+        // step s: stage s+1 (its set then takes the loads of s+4); steps past
+        // the end (nsteps rounded up to 3) stage zeros
+        for (uint32_t s = 0; s < nsteps; s += 3) {
+            stage(S1, s + 1);
+            issue(S1, s + 4);
+            __syncthreads();
+            stage(S2, s + 2);
+            issue(S2, s + 5);
+            __syncthreads();
+            stage(S0, s + 3);
+            issue(S0, s + 6);
+            __syncthreads();
         }
-    };
+        return;
+    }
 
+    // ---- consumer: MFMAs on LDS buffer s&1 ----------------------------------
+    const uint32_t wm = wave >> 1, wn = wave & 1;
     f32x4 acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; i++)
 #pragma unroll
         for (int j = 0; j < TJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
     const uint32_t fr = lane & 15, fk = 8 * (lane >> 4);
-    auto mfma_half = [&](int cur, int kk) {
-        const _Float16 *Ab = As + (cur * BM + wm * (BM / 2) + fr) * LDK + fk + 32 * kk;
-        const _Float16 *Bb = Bs + (cur * BN + wn * (BN / 2) + fr) * LDK + fk + 32 * kk;
-        f16x8v a[TI], b[TJ];
+    auto mfma_step = [&](uint32_t s) {
+        const uint32_t cur = s & 1;
+        const _Float16 *Ab = As + (cur * BM + wm * (BM / 2) + fr) * LDK + fk;
+        const _Float16 *Bb = Bs + (cur * BN + wn * (BN / 2) + fr) * LDK + fk;
 #pragma unroll
-        for (int i = 0; i < TI; i++) a[i] = *(const f16x8v *)(Ab + 16 * i * LDK);
+        for (int kk = 0; kk < BK / 32; kk++) {
+            f16x8v a[TI], b[TJ];
 #pragma unroll
-        for (int j = 0; j < TJ; j++) b[j] = *(const f16x8v *)(Bb + 16 * j * LDK);
+            for (int i = 0; i < TI; i++) a[i] = *(const f16x8v *)(Ab + 16 * i * LDK + 32 * kk);
 #pragma unroll
-        for (int i = 0; i < TI; i++)
+            for (int j = 0; j < TJ; j++) b[j] = *(const f16x8v *)(Bb + 16 * j * LDK + 32 * kk);
 #pragma unroll
-            for (int j = 0; j < TJ; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < TJ; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
     };
-
-    issue(0);
-    stage(0, 0);
-    issue(1);
     __syncthreads();
-    for (uint32_t s = 0; s < nsteps; s++) {
-        const int cur = s & 1;
-        mfma_half(cur, 0);
-        stage(s + 1, cur ^ 1);   // overlaps the matrix core's work on the first half
-        issue(s + 2);
-        mfma_half(cur, 1);
+    for (uint32_t s = 0; s < nsteps; s += 3) {
+        mfma_step(s);
+        __syncthreads();
+        mfma_step(s + 1);
+        __syncthreads();
+        mfma_step(s + 2);
         __syncthreads();
     }
 
@@ -277,14 +309,14 @@ __global__ __launch_bounds__(256) void gemm_dq_kernel(const uint16_t *X, const u
         }
 }
 
-template <template <int> class QT, int BM, int BN>
+template <template <int> class QT, int BM, int BN, int BK>
 static hipError_t go_gemm(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K, uint32_t N, uint32_t M,
                           hipStream_t s)
 {
-    constexpr size_t lds = 2 * (size_t)(BM + BN) * (64 + 8) * 2;
+    constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * 2;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
     const uint32_t tiles_n = N / BN, tiles = tiles_n * (M / BM);
-    hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN>), dim3(tiles), dim3(256), lds, s, X, W, Y, K, N, M, tiles_n);
+    hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK>), dim3(tiles), dim3(512), lds, s, X, W, Y, K, N, M, tiles_n);
     return hipGetLastError();
 }
 
@@ -293,8 +325,10 @@ static hipError_t go_gemm_t(const uint16_t *X, const uint8_t *W, float *Y, uint3
                             hipStream_t s)
 {
     // 256 x 128 tiles when they cover at least half of the CUs, else 128 x 64
-    if (M % 256 == 0 && N % 128 == 0 && (N / 128) * (M / 256) >= 128) return go_gemm<QT, 256, 128>(X, W, Y, K, N, M, s);
-    return go_gemm<QT, 128, 64>(X, W, Y, K, N, M, s);
+    // (with K steps of 128 so each barrier covers as much MFMA work)
+    if (M % 256 == 0 && N % 128 == 0 && (N / 128) * (M / 256) >= 128)
+        return go_gemm<QT, 256, 128, 64>(X, W, Y, K, N, M, s);
+    return go_gemm<QT, 128, 64, 128>(X, W, Y, K, N, M, s);
 }
 
 bool gemm_bf16_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t w_bytes, uint64_t x_bytes)
