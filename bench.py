@@ -178,6 +178,46 @@ def prefill(ctx, reps=20):
     return out
 
 
+def gemv_q4k_config1(ctx, reps=256, copies=64):
+    """Single Q4_K GEMV 3072x3072, batch 1, rotating `copies` weight copies
+    (64 x 5.3 MB: one pass exceeds the 256 MB Infinity Cache)."""
+    K = N = 3072
+    ws = [ctx.weight_upload(rrr_hip.Q4_K, K, N, synth.weight(1, 200 + c, rrr_hip.Q4_K, K, N)) for c in range(copies)]
+    x, y = ctx.to_device(synth.normal_f32(1, 1, K)), ctx.alloc(N * 4)
+    ms = timed_graph(ctx, lambda i: ctx.gemv(x, ws[i % copies], rrr_hip.Q4_K, y, K, N), reps) / reps
+    b = rrr_hip.tensor_bytes(rrr_hip.Q4_K, K, N) + 4 * K + 4 * N
+    gbs = b / (ms * 1e-3) / 1e9
+    log(f"[bench] q4k gemv 3072x3072 (config 1): {ms * 1e3:.2f} us ({gbs:.0f} GB/s)")
+    for w in ws:
+        w.free()
+    x.free(); y.free()
+    return {"us": round(ms * 1e3, 3), "GBs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": b}
+
+
+def skinny(ctx, reps=64):
+    """Batched GEMV / skinny GEMM, M in {4, 8, 32} token rows of f32 X:
+    gate+up Q4_K 16384x3072 (10 copies, 283 MB) and QKV Q5_K 5120x3072
+    (26 copies, 281 MB), rotated so the weights stream from HBM."""
+    out = {}
+    for name, qt, K, N, copies in (("gateup_q4k_16384x3072", rrr_hip.Q4_K, 3072, 16384, 10),
+                                   ("qkv_q5k_5120x3072", rrr_hip.Q5_K, 3072, 5120, 26)):
+        ws = [ctx.weight_upload(qt, K, N, synth.weight(4, 300 + c, qt, K, N)) for c in range(copies)]
+        for M in (4, 8, 32):
+            x, y = ctx.to_device(synth.normal_f32(4, 40 + M, M * K)), ctx.alloc(M * N * 4)
+            ms = timed_graph(ctx, lambda i: ctx.gemv(x, ws[i % copies], qt, y, K, N, M), reps) / reps
+            b = rrr_hip.tensor_bytes(qt, K, N) + 4 * M * K + 4 * M * N
+            gbs = b / (ms * 1e-3) / 1e9
+            tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+            log(f"[bench] skinny {name} M={M}: {ms * 1e3:.2f} us ({gbs:.0f} GB/s, {tf:.1f} TFLOP/s)")
+            out[f"skinny_{name}_m{M}"] = {"us": round(ms * 1e3, 3), "GBs": round(gbs, 1),
+                                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": b,
+                                          "TFLOPs": round(tf, 2)}
+            x.free(); y.free()
+        for w in ws:
+            w.free()
+    return out
+
+
 def decode_sweep(ctx, tokens):
     """Full Phi-4-mini-shaped decode sweep (32 layers + final RMSNorm + F32
     logits over 200,064 entries + argmax), one HIP graph per token; the
@@ -259,6 +299,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=20)
     ap.add_argument("--traffic", action="store_true")
     ap.add_argument("--decode-only", action="store_true")
+    ap.add_argument("--no-skinny", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -326,6 +367,9 @@ def main():
     }
 
     extra["q6k_gemv_host_roundtrip"] = host_roundtrip(ctx, cfg)
+    extra["q4k_gemv_3072x3072"] = gemv_q4k_config1(ctx)
+    if not args.no_skinny:
+        extra.update(skinny(ctx))
     if not args.no_prefill:
         extra.update(prefill(ctx))
 

@@ -611,6 +611,7 @@ static hipError_t go_type(const GemvArgs &a, uint32_t act, hipStream_t s)
 hipError_t launch_gemv(const GemvArgs &a, uint32_t act, hipStream_t s)
 {
     if (gemv_mfma_supported(a)) return launch_gemv_mfma(a, act, s);
+    if (a.M > 1 && act == ACT_PLAIN && skinny_supported(a)) return launch_skinny(a, s);
     switch (a.type) {
     case T_Q4_K: return go_type<DecQ4K>(a, act, s);
     case T_Q5_K: return go_type<DecQ5K>(a, act, s);

@@ -41,6 +41,9 @@ hipError_t launch_gemv(const GemvArgs &a, uint32_t act, hipStream_t s);
 // int8-MFMA batch-1 K-quant GEMV (gemv_mfma.hip)
 bool gemv_mfma_supported(const GemvArgs &a);
 hipError_t launch_gemv_mfma(const GemvArgs &a, uint32_t act, hipStream_t s);
+// fp16-MFMA batched GEMV for 2 <= M <= 32, Q4_K / Q5_K (skinny.hip)
+bool skinny_supported(const GemvArgs &a);
+hipError_t launch_skinny(const GemvArgs &a, hipStream_t s);
 hipError_t launch_dequant(uint32_t type, const uint8_t *W, uint64_t w_bytes, float *out,
                           uint64_t n_elements, hipStream_t s);
 hipError_t launch_rmsnorm(const float *x, const float *g, float *y, uint32_t rows, uint32_t d,

@@ -2,8 +2,9 @@
 
 Bars: dequantized weights bit-exact; GEMV / batched GEMV / RMSNorm / logits
 within 1e-4 normwise relative error max|got - ref| / max|ref| against the
-oracle evaluated in fp64 (TOL below); fused kernels bit-identical to the
-unfused sequence they replace.
+oracle evaluated in fp64 (TOL below), MFMA shapes (prefill GEMM, batched
+GEMV above 16 rows) within 2e-3; fused kernels bit-identical to the unfused
+sequence they replace.
 """
 import os
 
@@ -134,9 +135,18 @@ def test_matmul_kquant_helper_and_dispatch_names(ctx):
 
 # ---- batched GEMV / skinny ----------------------------------------------------------
 
+# Q4_K / Q5_K at 2 <= M <= 32 run on the fp16 matrix cores: up to 16 rows
+# with hi/lo-split activations (the GEMV bar), above that hi only (the MFMA bar)
+MFMA_TOL = 2e-3
+
+
+def batched_tol(qtype, K, M):
+    return MFMA_TOL if qtype in (12, 13) and 16 < M <= 32 and K <= 3072 else TOL
+
+
 @pytest.mark.parametrize("qtype,K,N", [(12, 3072, 16384), (13, 3072, 5120), (14, 8192, 3072), (0, 3072, 2048),
-                                       (12, 512, 37)])
-@pytest.mark.parametrize("M", [2, 3, 4, 8, 32])
+                                       (12, 512, 37), (13, 4096, 300)])
+@pytest.mark.parametrize("M", [2, 3, 4, 8, 13, 16, 17, 32])
 def test_batched_gemv_parity(ctx, qtype, K, N, M):
     raw = weights(qtype, K, N, seed=6, stream=qtype)
     X = synth.normal_f32(6, 50 + M, M * K)
@@ -145,8 +155,9 @@ def test_batched_gemv_parity(ctx, qtype, K, N, M):
     ctx.gemv(Xb, W, qtype, Yb, K, N, M)
     Y = ctx.download(Yb).reshape(M, N)
     ref = orc.gemv(qtype, raw, X, K, N, M, THREADS, f64=True)
+    tol = batched_tol(qtype, K, M)
     for m in range(M):
-        assert err(Y[m], ref[m]) < TOL, m
+        assert err(Y[m], ref[m]) < tol, m
     if qtype:
         name = {12: "matmul_gpuq4_batch", 13: "matmul_gpuq5_batch", 14: "matmul_gpuq6_batch"}[qtype]
         ctx.fill_u32(Yb, 0)
