@@ -67,6 +67,7 @@ typedef enum rrr_logits_layout {
 typedef struct rrr_ctx rrr_ctx;
 typedef struct rrr_buf rrr_buf;
 typedef struct rrr_graph rrr_graph;
+typedef struct rrr_sweep rrr_sweep;
 
 /* ---- engine lifetime ------------------------------------------------- */
 
@@ -243,6 +244,45 @@ int rrr_graph_begin(rrr_ctx *ctx);
 int rrr_graph_end(rrr_ctx *ctx, rrr_graph **out);
 int rrr_graph_launch(rrr_ctx *ctx, rrr_graph *g);
 int rrr_graph_destroy(rrr_ctx *ctx, rrr_graph *g);
+
+/* ---- persistent decode sweep -------------------------------------------- */
+
+/* One op of a sweep: exactly the arguments of rrr_gemv_rmsnorm (kind
+ * RRR_SWEEP_GEMV_RMSNORM; act_kind / act_param unused) or of
+ * rrr_gemv_residual (kind RRR_SWEEP_GEMV_RESIDUAL; gamma / eps unused). */
+enum { RRR_SWEEP_GEMV_RMSNORM = 0, RRR_SWEEP_GEMV_RESIDUAL = 1 };
+typedef struct rrr_sweep_op {
+    uint32_t kind;
+    const rrr_buf *x;
+    const rrr_buf *gamma;
+    float eps;
+    uint32_t act_kind;
+    uint32_t act_param;
+    const rrr_buf *W;
+    uint32_t type;
+    rrr_buf *y;
+    uint32_t K;
+    uint32_t N;
+} rrr_sweep_op;
+
+/* A list of fused decode GEMVs run in order by ONE persistent launch (one
+ * workgroup per CU): the MI355X counterpart of replaying the layer dispatches
+ * through dispatch_batch_persistent_v2 with a barrier between dependent
+ * dispatches (engine.rs:317-370, phi4.rs:1163-1168).  Each op starts once
+ * every row of the previous op is written; its weights start streaming
+ * before that.  Results are bit-identical to issuing the ops one by one.
+ * Supported: the decode layer's forms -- RMSNorm + Q5_K or Q4_K with
+ * K <= 4096, GQA-V + Q4_K with K <= 4096, SiLU-gate + Q6_K or Q4_K with
+ * 4096 < K <= 8192; RRR_ERR_UNSUPPORTED otherwise.  The buffers are referenced, not copied: they must outlive the
+ * sweep and stay at their size. */
+int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_sweep **out);
+/* Runs the sweep on the context stream (not inside rrr_graph_begin/end). */
+int rrr_sweep_run(rrr_ctx *ctx, rrr_sweep *sw);
+/* Waits for the stream; RRR_ERR_HIP if a run gave up waiting for an op (a
+ * bounded wait of about 2 s expired: its outputs are invalid), else RRR_OK.
+ * Clears the condition. */
+int rrr_sweep_check(rrr_ctx *ctx, rrr_sweep *sw);
+int rrr_sweep_destroy(rrr_ctx *ctx, rrr_sweep *sw);
 
 /* ---- synchronisation and timing -------------------------------------- */
 

@@ -14,6 +14,9 @@
 #include <mutex>
 #include <string>
 #include <unordered_set>
+#include <algorithm>
+#include <vector>
+#include <algorithm>
 
 #include "internal.h"
 
@@ -54,6 +57,16 @@ struct rrr_buf {
     rrr_buf *parent;  // non-null for views
 };
 
+struct rrr_sweep {
+    uint32_t magic;
+    void *ops;          // device SweepOpDev[nops]
+    uint32_t *flags;    // device: progress flags, error word, go words
+    uint32_t *err;      // device, inside the flag area
+    uint32_t nops, grid;
+    size_t lds;
+    uint64_t runs;
+};
+
 struct rrr_graph {
     uint32_t magic;
     rrr_ctx *ctx;
@@ -73,6 +86,7 @@ struct rrr_ctx {
     void *scratch;  // argmax partial candidates
     std::unordered_set<rrr_buf *> bufs;
     std::unordered_set<rrr_graph *> graphs;
+    std::unordered_set<rrr_sweep *> sweeps;
 };
 
 namespace {
@@ -224,6 +238,12 @@ int rrr_destroy(rrr_ctx *ctx)
             g->magic = 0;
             delete g;
         }
+        for (rrr_sweep *sw : ctx->sweeps) {
+            (void)hipFree(sw->ops);
+            (void)hipFree(sw->flags);
+            sw->magic = 0;
+            delete sw;
+        }
         for (rrr_buf *b : ctx->bufs)
             if (!b->parent && b->ptr) (void)hipFree(b->ptr);
         (void)hipFree(ctx->scratch);
@@ -232,6 +252,7 @@ int rrr_destroy(rrr_ctx *ctx)
         (void)hipStreamDestroy(ctx->stream);
     } else {
         for (rrr_graph *g : ctx->graphs) delete g;
+        for (rrr_sweep *sw : ctx->sweeps) delete sw;
     }
     for (rrr_buf *b : ctx->bufs) {
         b->magic = 0;
@@ -399,9 +420,10 @@ int rrr_dequant(rrr_ctx *ctx, uint32_t type, const rrr_buf *W, rrr_buf *out, uin
                   "rrr_dequant");
 }
 
-static int gemv_common(rrr_ctx *ctx, const rrr_buf *X, uint64_t x_floats, const rrr_buf *gamma, float eps,
-                       uint32_t act, uint32_t hd, uint32_t hpk, const rrr_buf *W, uint32_t type, rrr_buf *Y,
-                       uint32_t K, uint32_t N, uint32_t M, uint32_t residual, const char *what)
+// Checks of one GEMV-family call and its launch arguments.
+static int gemv_prepare(rrr_ctx *ctx, const rrr_buf *X, uint64_t x_floats, const rrr_buf *gamma, float eps,
+                        uint32_t act, uint32_t hd, uint32_t hpk, const rrr_buf *W, uint32_t type, rrr_buf *Y,
+                        uint32_t K, uint32_t N, uint32_t M, uint32_t residual, const char *what, GemvArgs &a)
 {
     TRY(check_buf(ctx, X, what));
     TRY(check_buf(ctx, W, what));
@@ -415,8 +437,7 @@ static int gemv_common(rrr_ctx *ctx, const rrr_buf *X, uint64_t x_floats, const 
     TRY(need_f32(Y, (uint64_t)M * N, what));
     if (gamma) TRY(need_f32(gamma, K, what));
     if (act == ACT_RMSNORM && !(std::isfinite(eps) && eps >= 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: eps", what);
-    TRY(device_ready(ctx));
-    GemvArgs a{};
+    a = GemvArgs{};
     a.type = type;
     a.x = (const float *)X->ptr;
     a.gamma = gamma ? (const float *)gamma->ptr : nullptr;
@@ -430,7 +451,39 @@ static int gemv_common(rrr_ctx *ctx, const rrr_buf *X, uint64_t x_floats, const 
     a.N = N;
     a.M = M;
     a.residual = residual;
+    return RRR_OK;
+}
+
+static int gemv_common(rrr_ctx *ctx, const rrr_buf *X, uint64_t x_floats, const rrr_buf *gamma, float eps,
+                       uint32_t act, uint32_t hd, uint32_t hpk, const rrr_buf *W, uint32_t type, rrr_buf *Y,
+                       uint32_t K, uint32_t N, uint32_t M, uint32_t residual, const char *what)
+{
+    GemvArgs a;
+    TRY(gemv_prepare(ctx, X, x_floats, gamma, eps, act, hd, hpk, W, type, Y, K, N, M, residual, what, a));
+    TRY(device_ready(ctx));
     return finish(ctx, launch_gemv(a, act, ctx->stream), what);
+}
+
+// The operand set of rrr_gemv_residual's activation kinds (x floats, act).
+static int residual_act(uint32_t act_kind, uint32_t act_param, uint32_t K, uint64_t &x_floats, uint32_t &act,
+                        uint32_t &hd, uint32_t &hpk, const char *what)
+{
+    hd = hpk = 0;
+    switch (act_kind) {
+    case RRR_ACT_IDENTITY: x_floats = K; act = ACT_PLAIN; return RRR_OK;
+    case RRR_ACT_SILU_GATE: x_floats = 2ull * K; act = ACT_SILU; return RRR_OK;
+    case RRR_ACT_GQA_V:
+        hd = act_param & 0xFFFFu;
+        hpk = act_param >> 16;
+        if (hd == 0 || hpk == 0 || hd % 16 || K % (hd * hpk) || (K / hpk) % 16)
+            return fail(RRR_ERR_INVALID_ARG, "%s: GQA params head_dim=%u heads_per_kv=%u do not tile K=%u", what, hd,
+                        hpk, K);
+        x_floats = (uint64_t)K + 2ull * (K / hpk);
+        act = ACT_GQA_V;
+        return RRR_OK;
+    default:
+        return fail(RRR_ERR_INVALID_ARG, "%s: act_kind %u", what, act_kind);
+    }
 }
 
 int rrr_gemv(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t type, rrr_buf *Y, uint32_t K, uint32_t N,
@@ -453,22 +506,10 @@ int rrr_gemv_residual(rrr_ctx *ctx, const rrr_buf *x, uint32_t act_kind, uint32_
 {
     TRY(check_ctx(ctx));
     const char *what = "rrr_gemv_residual";
-    switch (act_kind) {
-    case RRR_ACT_IDENTITY:
-        return gemv_common(ctx, x, K, nullptr, 0.0f, ACT_PLAIN, 0, 0, W, type, hidden, K, N, 1, 1, what);
-    case RRR_ACT_SILU_GATE:
-        return gemv_common(ctx, x, 2ull * K, nullptr, 0.0f, ACT_SILU, 0, 0, W, type, hidden, K, N, 1, 1, what);
-    case RRR_ACT_GQA_V: {
-        const uint32_t hd = act_param & 0xFFFFu, hpk = act_param >> 16;
-        if (hd == 0 || hpk == 0 || hd % 16 || K % (hd * hpk) || (K / hpk) % 16)
-            return fail(RRR_ERR_INVALID_ARG, "%s: GQA params head_dim=%u heads_per_kv=%u do not tile K=%u", what, hd,
-                        hpk, K);
-        return gemv_common(ctx, x, (uint64_t)K + 2ull * (K / hpk), nullptr, 0.0f, ACT_GQA_V, hd, hpk, W, type, hidden,
-                           K, N, 1, 1, what);
-    }
-    default:
-        return fail(RRR_ERR_INVALID_ARG, "%s: act_kind %u", what, act_kind);
-    }
+    uint64_t x_floats;
+    uint32_t act, hd, hpk;
+    TRY(residual_act(act_kind, act_param, K, x_floats, act, hd, hpk, what));
+    return gemv_common(ctx, x, x_floats, nullptr, 0.0f, act, hd, hpk, W, type, hidden, K, N, 1, 1, what);
 }
 
 int rrr_gemm_bf16(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t type, rrr_buf *Y, uint32_t K, uint32_t N,
@@ -797,6 +838,138 @@ int rrr_graph_destroy(rrr_ctx *ctx, rrr_graph *g)
 }
 
 // ---- sync and timing ----------------------------------------------------------
+
+// ---- persistent decode sweep --------------------------------------------
+
+static constexpr uint32_t SWEEP_MAGIC = 0x53574550u;
+
+static int check_sweep(rrr_ctx *ctx, rrr_sweep *sw, const char *what)
+{
+    if (!sw) return fail(RRR_ERR_NULL, "%s: null sweep", what);
+    if (!ctx->sweeps.count(sw) || sw->magic != SWEEP_MAGIC)
+        return fail(RRR_ERR_STALE, "%s: sweep already destroyed or not owned by this context", what);
+    return RRR_OK;
+}
+
+int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_sweep **out)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_sweep_create";
+    if (!out || (!ops && n)) return fail(RRR_ERR_NULL, "%s: null argument", what);
+    *out = nullptr;
+    if (n == 0) return fail(RRR_ERR_INVALID_ARG, "%s: no ops", what);
+    if (ctx->capturing) return fail(RRR_ERR_INVALID_ARG, "%s: not inside rrr_graph_begin/end", what);
+    TRY(device_ready(ctx));
+    const uint32_t cus = sweep_cus();
+    std::vector<GemvArgs> args(n);
+    std::vector<uint32_t> acts(n), variants(n), ntiles(n);
+    size_t lds = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        const rrr_sweep_op &o = ops[i];
+        GemvArgs &a = args[i];
+        if (o.kind == RRR_SWEEP_GEMV_RMSNORM) {
+            if (!o.gamma) return fail(RRR_ERR_NULL, "%s: op %u: null gamma", what, i);
+            TRY(gemv_prepare(ctx, o.x, o.K, o.gamma, o.eps, ACT_RMSNORM, 0, 0, o.W, o.type, o.y, o.K, o.N, 1, 0,
+                             what, a));
+            acts[i] = ACT_RMSNORM;
+        } else if (o.kind == RRR_SWEEP_GEMV_RESIDUAL) {
+            uint64_t x_floats;
+            uint32_t act, hd, hpk;
+            TRY(residual_act(o.act_kind, o.act_param, o.K, x_floats, act, hd, hpk, what));
+            TRY(gemv_prepare(ctx, o.x, x_floats, nullptr, 0.0f, act, hd, hpk, o.W, o.type, o.y, o.K, o.N, 1, 1,
+                             what, a));
+            acts[i] = act;
+        } else {
+            return fail(RRR_ERR_INVALID_ARG, "%s: op %u: kind %u", what, i, o.kind);
+        }
+        size_t l;
+        if (!sweep_plan_op(a, acts[i], cus, variants[i], ntiles[i], l))
+            return fail(RRR_ERR_UNSUPPORTED, "%s: op %u (type %u, K=%u, N=%u) is not a sweep shape", what, i, o.type,
+                        o.K, o.N);
+        lds = std::max(lds, l);
+    }
+    const uint32_t grid = sweep_grid(lds);
+    if (grid == 0) return fail(RRR_ERR_UNSUPPORTED, "%s: a 1024-thread workgroup with %zu B of LDS does not fit", what, lds);
+    std::vector<uint8_t> packed((size_t)n * sweep_op_bytes());
+    for (uint32_t i = 0; i < n; i++) sweep_pack_op(packed.data() + (size_t)i * sweep_op_bytes(), args[i], variants[i], ntiles[i]);
+    rrr_sweep *sw = new rrr_sweep{};
+    sw->magic = SWEEP_MAGIC;
+    sw->nops = n;
+    sw->grid = grid;
+    sw->lds = lds;
+    hipError_t e = hipMalloc(&sw->ops, packed.size());
+    const size_t fbytes = 4 * sweep_flag_words(grid);
+    if (e == hipSuccess) e = hipMalloc((void **)&sw->flags, fbytes);
+    if (e == hipSuccess) {
+        sw->err = sw->flags + sweep_err_word(grid);
+        e = hipMemcpyAsync(sw->ops, packed.data(), packed.size(), hipMemcpyHostToDevice, ctx->stream);
+    }
+    if (e == hipSuccess) e = hipMemsetAsync(sw->flags, 0, fbytes, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(sw->ops);
+        (void)hipFree(sw->flags);
+        delete sw;
+        return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    }
+    ctx->sweeps.insert(sw);
+    *out = sw;
+    return ok();
+}
+
+int rrr_sweep_run(rrr_ctx *ctx, rrr_sweep *sw)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_sweep_run";
+    TRY(check_sweep(ctx, sw, what));
+    if (ctx->capturing) return fail(RRR_ERR_UNSUPPORTED, "%s: a sweep cannot be recorded into a graph", what);
+    TRY(device_ready(ctx));
+    // flags only grow: run r waits for values above everything run r-1 wrote
+    uint64_t epoch = sw->runs * (sw->nops + 1ull);
+    if (epoch + sw->nops >= (1ull << 30)) {
+        hipError_t e = hipMemsetAsync(sw->flags, 0, 4 * sweep_flag_words(sw->grid), ctx->stream);
+        if (e != hipSuccess) return finish(ctx, e, what);
+        sw->runs = 0;
+        epoch = 0;
+    }
+    sw->runs++;
+    return finish(ctx, launch_sweep(sw->ops, sw->nops, sw->flags, (uint32_t)epoch, sw->grid, sw->lds, ctx->stream),
+                  what);
+}
+
+int rrr_sweep_check(rrr_ctx *ctx, rrr_sweep *sw)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_sweep_check";
+    TRY(check_sweep(ctx, sw, what));
+    TRY(device_ready(ctx));
+    uint32_t err = 0;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = hipMemcpy(&err, sw->err, 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    if (err) {
+        // start over: flags and the error word back to zero
+        e = hipMemset(sw->flags, 0, 4 * sweep_flag_words(sw->grid));
+        sw->runs = 0;
+        if (e != hipSuccess) return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+        return fail(RRR_ERR_HIP, "%s: a sweep run gave up waiting for an op; its outputs are invalid", what);
+    }
+    return ok();
+}
+
+int rrr_sweep_destroy(rrr_ctx *ctx, rrr_sweep *sw)
+{
+    TRY(check_ctx(ctx));
+    TRY(check_sweep(ctx, sw, "rrr_sweep_destroy"));
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(sw->ops);
+    (void)hipFree(sw->flags);
+    ctx->sweeps.erase(sw);
+    sw->magic = 0;
+    delete sw;
+    return ok();
+}
 
 int rrr_set_async(rrr_ctx *ctx, int async)
 {

@@ -1,0 +1,608 @@
+// gemv_mq.h -- batch-1 K-quant GEMV on the int8 matrix cores: quant unit
+// decoders, activation encoding and the per-workgroup body shared by the
+// standalone launch (gemv_mfma.hip) and the persistent decode sweep
+// (sweep.hip).
+//
+// y[n] = sum_k x[k] * W[n][k] for Q4_K / Q5_K / Q6_K rows (phi4.rs:628-630),
+// with the multiply-accumulate on v_mfma_i32_16x16x64_i8 instead of VALU FMAs.
+//
+// Activation encoding.  Each 16-element group of x is written in block
+// floating point: the fixed-point value Q = rint(x * 2^(14-E)), with 2^E
+// chosen from the group maximum M so that M / 2^E lies in [32, 64)
+// (|Q| < 2^20), split into three signed int8 radix-256 digits
+//     Q = d0 + 2^8 d1 + 2^16 d2.
+// The encoding error is at most 2^(E-15) per element, i.e. below 2^-20 of
+// the group maximum.
+//
+// Weights.  A K-quant super-block stores small integers q (Q4_K 0..15,
+// Q5_K 0..31, Q6_K 0..63 with an offset of 32) and per-sub-block scales.
+// The raw q values go straight into the MFMA B operand; the integer dot
+// products C_t = sum q * d_t (t = 0, 1, 2) are exact, and
+//     sum_k q_k x_k = 2^(E-14) * (C_0 + C_1 * 2^8 + C_2 * 2^16)
+// is recombined in int32 (|C_2| < 2^14, |C_0|, |C_1| < 2^17) and scaled once
+// per 16 elements.  The Q6_K offset (q - 32) is folded into the MFMA
+// accumulator input as -32 * (sum of Q over the group); the Q4_K / Q5_K min
+// term uses the f32 16-element sums of x.
+//
+// MFMA mapping (16x16x64, lane l: A row l%16, B column l%16, k-group l/16;
+// C/D rows 4*(l/16)+r of column l%16 in register r):
+//   B[k][n]  = q of weight row n (16 rows per workgroup) at k-set K_g,
+//   A[m][k]  = digit (m%4) of x at K_g when m/4 == g (and m%4 < 3), else 0,
+//   C[4g+r][n] = group constants of K_g: r = 0 the offset term, r = 3 the
+//                group factor 2^(E-14) (bit pattern; A row 4g+3 is zero, so
+//                it comes back unchanged in D),
+// so lane (n, g) receives its own three partial dot products for row n and
+// k-set K_g in registers 0..2 and the factor in register 3.  Each lane's
+// k-set is 16 consecutive elements with one scale, applied after the MFMA.
+//
+// Work split: one workgroup per 16-row tile; wave w owns super-blocks
+// [w*BPW, w*BPW + BPW) of the 16 rows.  A wave streams its 16 row pieces
+// with 16-byte loads on consecutive lanes (contiguous runs of BPW blocks per
+// row), encodes its own slice of x, stages both in its private LDS region and
+// runs its MFMAs as soon as its own data has landed -- no workgroup barrier
+// until the final cross-wave sum (plus one for the fused RMSNorm scale).
+#pragma once
+
+#include "act.h"
+
+namespace rrr {
+
+__device__ __forceinline__ u32x4 lds16(const uint8_t *L, uint32_t o)
+{
+    return *(const u32x4 *)(L + o);
+}
+
+// Q4_K (phi4.rs:481-510).  Lane group g takes qs pair g (bytes 32g..32g+31):
+// low nibbles = sub-block 2g, high nibbles = sub-block 2g+1.
+//   u = 0: low nibbles of bytes 0..15   (k-set 64g + 0..15)
+//   u = 1: low nibbles of bytes 16..31  (64g + 16..31)
+//   u = 2: high nibbles of bytes 0..15  (64g + 32..47)
+//   u = 3: high nibbles of bytes 16..31 (64g + 48..63)
+// Block value = d * sum_u sc[u] * S_u - dmin * sum_u mn[u] * X_u.
+struct MqQ4K {
+    static constexpr uint32_t BS = 144;
+    static constexpr bool HAS_MIN = true, OFF32 = false;
+    struct Raw { u32x4 hdr, qs0, qs1; };
+    __device__ static uint32_t koff(uint32_t g, int u) { return 64 * g + 16 * u; }
+    // o: LDS offset of the 16-byte aligned block piece
+    __device__ static void load(Raw &w, const uint8_t *L, uint32_t o, uint32_t g)
+    {
+        w.hdr = lds16(L, o);
+        w.qs0 = lds16(L, o + 16 + 32 * g);
+        w.qs1 = lds16(L, o + 32 + 32 * g);
+    }
+    __device__ static void decode(const Raw &w, uint32_t g, i32x4 *bq, float *sc, float *mn, float &d, float &dmin)
+    {
+        d = h2f(w.hdr.x);
+        dmin = h2f(w.hdr.x >> 16);
+        uint32_t s0, m0, s1, m1;
+        scale_min_k4(2 * g, w.hdr.y, w.hdr.z, w.hdr.w, s0, m0);
+        scale_min_k4(2 * g + 1, w.hdr.y, w.hdr.z, w.hdr.w, s1, m1);
+        sc[0] = sc[1] = (float)s0;
+        sc[2] = sc[3] = (float)s1;
+        mn[0] = mn[1] = (float)m0;
+        mn[2] = mn[3] = (float)m1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            bq[0][i] = (int)(w.qs0[i] & 0x0F0F0F0Fu);
+            bq[1][i] = (int)(w.qs1[i] & 0x0F0F0F0Fu);
+            bq[2][i] = (int)((w.qs0[i] >> 4) & 0x0F0F0F0Fu);
+            bq[3][i] = (int)((w.qs1[i] >> 4) & 0x0F0F0F0Fu);
+        }
+    }
+};
+
+// Q5_K (phi4.rs:512-542): Q4_K's nibbles plus bit s of qh[j] as bit 4.
+struct MqQ5K {
+    static constexpr uint32_t BS = 176;
+    static constexpr bool HAS_MIN = true, OFF32 = false;
+    struct Raw { u32x4 hdr, qh0, qh1, qs0, qs1; };
+    __device__ static uint32_t koff(uint32_t g, int u) { return 64 * g + 16 * u; }
+    __device__ static void load(Raw &w, const uint8_t *L, uint32_t o, uint32_t g)
+    {
+        w.hdr = lds16(L, o);
+        w.qh0 = lds16(L, o + 16);
+        w.qh1 = lds16(L, o + 32);
+        w.qs0 = lds16(L, o + 48 + 32 * g);
+        w.qs1 = lds16(L, o + 64 + 32 * g);
+    }
+    __device__ static void decode(const Raw &w, uint32_t g, i32x4 *bq, float *sc, float *mn, float &d, float &dmin)
+    {
+        d = h2f(w.hdr.x);
+        dmin = h2f(w.hdr.x >> 16);
+        uint32_t s0, m0, s1, m1;
+        scale_min_k4(2 * g, w.hdr.y, w.hdr.z, w.hdr.w, s0, m0);
+        scale_min_k4(2 * g + 1, w.hdr.y, w.hdr.z, w.hdr.w, s1, m1);
+        sc[0] = sc[1] = (float)s0;
+        sc[2] = sc[3] = (float)s1;
+        mn[0] = mn[1] = (float)m0;
+        mn[2] = mn[3] = (float)m1;
+        const uint32_t lo = 2 * g, hi = 2 * g + 1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            bq[0][i] = (int)((w.qs0[i] & 0x0F0F0F0Fu) | (((w.qh0[i] >> lo) & 0x01010101u) << 4));
+            bq[1][i] = (int)((w.qs1[i] & 0x0F0F0F0Fu) | (((w.qh1[i] >> lo) & 0x01010101u) << 4));
+            bq[2][i] = (int)(((w.qs0[i] >> 4) & 0x0F0F0F0Fu) | (((w.qh0[i] >> hi) & 0x01010101u) << 4));
+            bq[3][i] = (int)(((w.qs1[i] >> 4) & 0x0F0F0F0Fu) | (((w.qh1[i] >> hi) & 0x01010101u) << 4));
+        }
+    }
+};
+
+// Q6_K (phi4.rs:444-479).  Lane group g takes half g6 = g/2 and positions
+// l0 = 16 (g&1) .. l0+15; quad u of those positions (elements
+// 128 g6 + 32 u + l) is MFMA u and uses scale sc[8 g6 + l0/16 + 2u], the
+// is = g*8 + l/16 rule of phi4.rs:463.  Stored values q + 32 (0..63) enter the
+// MFMA unsigned; the offset comes in through the accumulator input.
+struct MqQ6K {
+    static constexpr uint32_t BS = 210;
+    static constexpr bool HAS_MIN = false, OFF32 = true;
+    struct Raw { u32x4 qa, qb, qh; u32x2 sc; uint32_t d; };
+    __device__ static uint32_t koff(uint32_t g, int u) { return 128 * (g >> 1) + 32 * u + 16 * (g & 1); }
+    // o: LDS offset of the block piece, staged 16-byte aligned
+    __device__ static void load(Raw &w, const uint8_t *L, uint32_t o, uint32_t g)
+    {
+        const uint32_t g6 = g >> 1, l0 = 16 * (g & 1);
+        w.qa = lds16(L, o + 64 * g6 + l0);
+        w.qb = lds16(L, o + 64 * g6 + 32 + l0);
+        w.qh = lds16(L, o + 128 + 32 * g6 + l0);
+        w.sc = *(const u32x2 *)(L + o + 192 + 8 * g6);
+        w.d = *(const uint16_t *)(L + o + 208);
+    }
+    __device__ static void decode(const Raw &w, uint32_t g, i32x4 *bq, float *sc, float *, float &d, float &)
+    {
+        d = h2f(w.d);
+        const uint32_t h = g & 1;
+        sc[0] = (float)(int8_t)byte_of(w.sc.x, h);
+        sc[1] = (float)(int8_t)byte_of(w.sc.x, h + 2);
+        sc[2] = (float)(int8_t)byte_of(w.sc.y, h);
+        sc[3] = (float)(int8_t)byte_of(w.sc.y, h + 2);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t a = w.qa[i], b = w.qb[i], hh = w.qh[i];
+            bq[0][i] = (int)((a & 0x0F0F0F0Fu) | ((hh & 0x03030303u) << 4));
+            bq[1][i] = (int)((b & 0x0F0F0F0Fu) | ((hh & 0x0C0C0C0Cu) << 2));
+            bq[2][i] = (int)(((a >> 4) & 0x0F0F0F0Fu) | (hh & 0x30303030u));
+            bq[3][i] = (int)(((b >> 4) & 0x0F0F0F0Fu) | ((hh >> 2) & 0x30303030u));
+        }
+    }
+};
+
+// Fixed-point form of one float4 of activations: Q = rint(x * 2^(14-E))
+// (|Q| < 2^20) as three signed radix-256 digits Q = d0 + 2^8 d1 + 2^16 d2.
+// fma(x, 2^(14-E), 1.5 * 2^23) lands in [2^23, 2^24), where the f32 spacing
+// is 1, so it is the exactly rounded 1.5 * 2^23 + Q and its bit pattern is
+// 0x4B400000 + Q.  Adding the bias 0x808080 makes every byte c_t of
+// Qb = Q + 0x808080 (< 2^24) the digit d_t = c_t - 128, i.e. the int8 byte
+// c_t ^ 0x80.  Returns the digit planes (four int8 per dword, plane t = byte
+// t) and the sum of the four biased values.
+__device__ __forceinline__ void encode4(const float4 &v, float scale, uint32_t &p0, uint32_t &p1, uint32_t &p2,
+                                        uint32_t &qbsum)
+{
+    constexpr float MAGIC = 12582912.0f;                       // 1.5 * 2^23
+    constexpr uint32_t REBIAS = 0x00808080u - 0x4B400000u;     // mod 2^32
+    const uint32_t q0 = __float_as_uint(__builtin_fmaf(v.x, scale, MAGIC)) + REBIAS;
+    const uint32_t q1 = __float_as_uint(__builtin_fmaf(v.y, scale, MAGIC)) + REBIAS;
+    const uint32_t q2 = __float_as_uint(__builtin_fmaf(v.z, scale, MAGIC)) + REBIAS;
+    const uint32_t q3 = __float_as_uint(__builtin_fmaf(v.w, scale, MAGIC)) + REBIAS;
+    qbsum = (q0 + q1) + (q2 + q3);
+    // v_perm: selector bytes 0..3 take bytes of the second operand, 4..7 of
+    // the first, 0x0c gives 0
+    p0 = (__builtin_amdgcn_perm(q1, q0, 0x0c0c0400u) | __builtin_amdgcn_perm(q3, q2, 0x04000c0cu)) ^ 0x80808080u;
+    p1 = (__builtin_amdgcn_perm(q1, q0, 0x0c0c0501u) | __builtin_amdgcn_perm(q3, q2, 0x05010c0cu)) ^ 0x80808080u;
+    p2 = (__builtin_amdgcn_perm(q1, q0, 0x0c0c0602u) | __builtin_amdgcn_perm(q3, q2, 0x06020c0cu)) ^ 0x80808080u;
+}
+
+// Butterflies within a quad of lanes (DPP quad_perm, no LDS traffic).
+__device__ __forceinline__ float quad_max(float v)
+{
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+}
+__device__ __forceinline__ float quad_sum(float v)
+{
+    v = v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t quad_sum_u32(uint32_t v)
+{
+    v = v + (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+    return v + (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+}
+
+// Wave-private LDS layout of one wave (BPW super-blocks of 16 rows):
+//   weights: 16 rows x RS bytes, block j of row r at r*RS + j*LB (16-byte
+//            aligned pieces of UPB units; Q6_K pieces carry 14 bytes of the
+//            next block in their last unit).  Load slot s covers rows
+//            s*RPS .. s*RPS + RPS-1, lane l unit l % UPR of row l / UPR, so a
+//            lane's offsets are fixed and only a uniform per-slot offset moves.
+//   digits:  3 planes x DG bytes (plane p, local element e at p*DG + e)
+//   aux:     per 16-element group 16 bytes = MFMA accumulator input
+//            {-32 * sum Q (Q6_K only, else 0), 0, 0, bits of 2^(E-14)}
+//   gsum:    per group the f32 sum of x (Q4_K / Q5_K min term)
+template <class Q, int BPW>
+struct MwGeom {
+    static constexpr uint32_t UPB = (Q::BS + 15) / 16;            // 16-byte units per block piece
+    static constexpr uint32_t LB = 16 * UPB;
+    static constexpr uint32_t RS = (BPW * LB) % 32 == 0 ? BPW * LB + 16 : BPW * LB;  // odd multiple of 16
+    static constexpr uint32_t UPR = BPW * UPB;                     // units per row
+    static constexpr uint32_t RPS = 64 / UPR;                      // rows per load slot
+    static constexpr int S = (16 + RPS - 1) / RPS;                 // load slots
+    static constexpr uint32_t DG = BPW * 256;
+    static constexpr uint32_t NGW = BPW * 16;
+    static constexpr uint32_t D_OFF = 16 * RS;
+    static constexpr uint32_t A_OFF = D_OFF + 3 * DG;
+    static constexpr uint32_t G_OFF = A_OFF + 16 * NGW;
+    static constexpr uint32_t BYTES = G_OFF + 4 * NGW;            // multiple of 16
+};
+
+// Sum of squares of x[0..K) in the order of the standalone RMSNorm kernel
+// (thread t < 256 owns float4s t, t + 256, ...; wave butterfly; waves 0..3
+// added in order), so the fused scale is bitwise that kernel's.  cx[j] holds
+// float4 t + 256 j (loaded earlier, index clamped).  Needs at least 4 waves;
+// every thread must call it (one barrier).
+template <int NSQ>
+__device__ __forceinline__ float canonical_sumsq(const float4 *cx, uint32_t K, float *red)
+{
+    const uint32_t t = threadIdx.x;
+    float acc = 0.0f;
+    if (t < 256) {
+#pragma unroll
+        for (int j = 0; j < NSQ; j++)
+            if (t + 256 * j < K / 4) {
+                acc = __builtin_fmaf(cx[j].x, cx[j].x, acc);
+                acc = __builtin_fmaf(cx[j].y, cx[j].y, acc);
+                acc = __builtin_fmaf(cx[j].z, cx[j].z, acc);
+                acc = __builtin_fmaf(cx[j].w, cx[j].w, acc);
+            }
+    }
+    acc = wave_sum(acc);
+    if (t < 256 && (t & 63) == 0) red[t >> 6] = acc;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Scalar offset of a load past every weight byte (the path requires
+// w_bytes + RRR_READ_SLACK < MQ_OOB): such loads return zeros and move no data.
+constexpr uint32_t MQ_OOB = 0x80000000u;
+
+
+// ---------------------------------------------------------------------------
+// Sweep form (SW): the body runs once per op inside the persistent decode
+// sweep.  Its activations and outputs are written by other workgroups of the
+// same launch, on other XCDs whose L2s are not coherent with this one: they
+// are read and written with agent-scope (sc1) buffer operations, which go
+// through to the coherent level.  The weights of the workgroup's first tile
+// are requested before the wait for the previous op, so HBM keeps streaming
+// through the hand-off.
+constexpr int RRR_CPOL_SC1 = 16;
+
+// Wait of one op for the previous one: every workgroup's progress flag has
+// reached `target` (flags only grow; 0 = no wait).  Workgroup 0 gathers the
+// flags (one wave, 16 bytes a lane) and publishes `target` in SWEEP_GO_COPIES
+// go words, 128 bytes apart; every other workgroup polls one go word with a
+// single lane, so the coherent level sees a few hundred loads per round
+// instead of one per workgroup and flag.  The spins are bounded (about 2 s of
+// the 100 MHz real-time clock): on expiry the error word is set and the
+// workgroup abandons the sweep instead of hanging.
+constexpr uint32_t SWEEP_GO_COPIES = 8, SWEEP_GO_STRIDE = 32;   // u32 words
+struct SweepWait {
+    const uint32_t *flags;   // one per workgroup, 16-byte padded to a multiple of 4
+    uint32_t *go;            // SWEEP_GO_COPIES x SWEEP_GO_STRIDE words
+    uint32_t target;
+    uint32_t *err;
+    uint32_t *bail;          // LDS word shared by the workgroup
+};
+
+__device__ __forceinline__ uint32_t coh_load_u32(const uint32_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool sweep_reached(uint32_t v, uint32_t target) { return (int)(v - target) >= 0; }
+
+// every thread of the workgroup calls it; the result is uniform
+__device__ __forceinline__ bool sweep_wait(SweepWait &sw)
+{
+    if (sw.target == 0) return true;
+    const uint32_t t = threadIdx.x;
+    if (t == 0) *sw.bail = 0u;
+    if (t < 64) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        bool expired = false;
+        if (blockIdx.x == 0) {
+            // gather: lane l covers flags 4l .. 4l+3 (padding flags read as done)
+            const uint32_t G = gridDim.x;
+            for (;;) {
+                bool ok = true;
+                if (4 * t < G) {
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(sw.flags, 16ull * ((G + 3) / 4)),
+                                                                          16 * t, 0, RRR_CPOL_SC1);
+                    ok = sweep_reached(v.x, sw.target) && (4 * t + 1 >= G || sweep_reached(v.y, sw.target)) &&
+                         (4 * t + 2 >= G || sweep_reached(v.z, sw.target)) &&
+                         (4 * t + 3 >= G || sweep_reached(v.w, sw.target));
+                }
+                if (__all(ok)) break;
+                if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) { expired = true; break; }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (!expired && t < SWEEP_GO_COPIES)
+                __hip_atomic_store(sw.go + t * SWEEP_GO_STRIDE, sw.target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else if (t == 0) {
+            const uint32_t *g = sw.go + (blockIdx.x % SWEEP_GO_COPIES) * SWEEP_GO_STRIDE;
+            while (!sweep_reached(coh_load_u32(g), sw.target)) {
+                if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) { expired = true; break; }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        if (expired) {
+            *sw.bail = 1u;
+            __hip_atomic_store(sw.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+    return *sw.bail == 0u;
+}
+
+// Activation inputs of 4 consecutive elements at k (k % 4 == 0), as
+// src_load4 (act.h); SW reads them through the coherent level.
+template <int ACT, bool SW>
+__device__ __forceinline__ void mq_src_load4(const GemvArgs &a, __amdgpu_buffer_rsrc_t rx, uint32_t k, float4 &xa,
+                                             float4 &xb)
+{
+    if constexpr (!SW) {
+        src_load4<ACT>(a, k, xa, xb);
+    } else {
+        uint32_t i = k;
+        if constexpr (ACT == ACT_GQA_V) {
+            const uint32_t hd = a.head_dim, hpk = a.heads_per_kv;
+            i = a.K + a.K / hpk + (k / (hd * hpk)) * hd + k % hd;
+        }
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, 4 * i, 0, RRR_CPOL_SC1);
+        xa = make_float4(u2f(v.x), u2f(v.y), u2f(v.z), u2f(v.w));
+        if constexpr (ACT == ACT_RMSNORM) xb = *(const float4 *)(a.gamma + k);   // weights: read-only
+        if constexpr (ACT == ACT_SILU) {
+            const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rx, 4 * (a.K + k), 0, RRR_CPOL_SC1);
+            xb = make_float4(u2f(u.x), u2f(u.y), u2f(u.z), u2f(u.w));
+        }
+    }
+}
+
+// Persistent form (MULTI): workgroup b takes the 16-row tiles b, b + G, ...
+// (G = gridDim.x) with the same wave <-> K-slice split for every tile, so the
+// activation slice is encoded once per workgroup and, with one super-block per
+// wave, the MFMA A operands and accumulator inputs stay in registers.  The
+// loads of tile i+1 are issued as soon as tile i is staged in LDS, before it
+// is multiplied.  The
+// single-tile form (one tile per workgroup) issues no prefetch: even loads
+// past the buffer end cost texture-addresser time.  Row sums are added over
+// the waves in wave order, so results depend on neither form, G nor the
+// number of waves.  Returns false when a sweep wait was abandoned.
+template <class Q, int BPW, int ACT, bool MULTI, bool SW>
+__device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, SweepWait &sw)
+{
+    extern __shared__ float smem[];
+    using G = MwGeom<Q, BPW>;
+    constexpr bool AREG = BPW == 1;
+    const uint32_t K = a.K, B = K / 256;
+    const uint32_t W = blockDim.x >> 6, NT = blockDim.x;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t n = lane & 15, g = lane >> 4;
+    const uint32_t GR = gridDim.x, tile0 = blockIdx.x;
+    const uint32_t ntl = MULTI ? (tile0 < ntiles ? (ntiles - tile0 + GR - 1) / GR : 0u) : 1u;  // tiles of this workgroup
+    uint8_t *L = (uint8_t *)smem + wave * G::BYTES;              // this wave's region
+    float *red = (float *)((uint8_t *)smem + W * G::BYTES);      // 4
+    float *part = red + 4;                                       // ntl x W x 16 per-wave row partials
+
+    const uint32_t row_bytes = B * Q::BS, tile_bytes = 16 * row_bytes;
+    // every buffer has RRR_READ_SLACK readable bytes past its end: a Q6_K
+    // piece's last unit runs 14 bytes past its block
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.W, a.w_bytes + RRR_READ_SLACK);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, 0xFFFFFFFFull);
+    const uint32_t b0 = wave * BPW;                              // first super-block of this wave
+    const uint32_t nb = b0 < B ? min((uint32_t)BPW, B - b0) : 0u;
+
+    // weight units of this wave's slice of a tile (layout above); lanes past
+    // RPS rows and blocks past nb reload a valid unit and are not stored, and
+    // rows past 16 in the last slot read nothing
+    const uint32_t rsel = min(lane / G::UPR, G::RPS - 1), wl = lane - (lane / G::UPR) * G::UPR;
+    const uint32_t jl = wl / G::UPB, vl = wl - jl * G::UPB;
+    const bool lane_ok = lane < G::RPS * G::UPR && jl < nb;
+    const uint32_t voff = rsel * row_bytes + (b0 + min(jl, nb ? nb - 1 : 0u)) * Q::BS + 16 * vl;
+    const uint32_t voff_last = (G::S - 1) * G::RPS + rsel < 16 ? voff : MQ_OOB;
+    const uint32_t loff = rsel * G::RS + jl * G::LB + 16 * vl;
+    u32x4 wa[G::S];
+    auto issue = [&](u32x4 *w, uint32_t tl) {
+        const uint32_t tb = tl < ntl ? (tile0 + tl * GR) * tile_bytes : MQ_OOB;
+#pragma unroll
+        for (int s = 0; s < G::S; s++)
+            w[s] = bload16_nt_so(rs, s == G::S - 1 ? voff_last : voff, tb + s * G::RPS * row_bytes);
+    };
+
+    // The loads below are unconditional (clamped indices, out-of-range scalar
+    // offsets): loads under a branch make the compiler wait for every
+    // outstanding load at the join.
+    // 0. in the sweep: this op's first tile, then the wait for the previous op
+    if constexpr (SW) {
+        issue(wa, 0);
+        if (!sweep_wait(sw)) return false;
+    }
+    // 1. fused RMSNorm: the whole of x in the canonical order (K <= 1024 NSQ)
+    constexpr int NSQ = ACT == ACT_RMSNORM ? 4 * BPW : 1;
+    float4 cx[NSQ];
+    if constexpr (ACT == ACT_RMSNORM) {
+#pragma unroll
+        for (int j = 0; j < NSQ; j++) {
+            const uint32_t f = min(t + 256 * j, K / 4 - 1);
+            if constexpr (SW) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, 16 * f, 0, RRR_CPOL_SC1);
+                cx[j] = make_float4(u2f(v.x), u2f(v.y), u2f(v.z), u2f(v.w));
+            } else {
+                cx[j] = ((const float4 *)a.x)[f];
+            }
+        }
+    }
+    // 2. this wave's activation inputs: float4 lane + 64 j of its slice
+    float4 xa[BPW], xb[BPW];
+#pragma unroll
+    for (int j = 0; j < BPW; j++) mq_src_load4<ACT, SW>(a, rx, min(b0 * 256 + 4 * (lane + 64 * j), K - 4), xa[j], xb[j]);
+
+    if constexpr (!SW) {
+        // every wave's activation loads enter the memory pipeline before any
+        // weight load of the workgroup (a bare barrier: no wait on the loads)
+        __builtin_amdgcn_s_barrier();
+        issue(wa, 0);
+    }
+
+    // 3. activation staging of this wave's slice
+    float inv = 1.0f;
+    if constexpr (ACT == ACT_RMSNORM) inv = rms_inv(canonical_sumsq<NSQ>(cx, K, red), K, a.eps);
+#pragma unroll
+    for (int j = 0; j < BPW; j++) {
+        const uint32_t f = lane + 64 * j;                        // local float4 index
+        const float4 v = xform4<ACT>(xa[j], xb[j], inv);
+        const float mx = quad_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        int e = 0;
+        if (mx > 0.0f && __builtin_isfinite(mx)) {
+            int ex;
+            (void)frexpf(mx, &ex);
+            e = ex - 6;  // mx / 2^e in [32, 64)
+        }
+        uint32_t p0, p1, p2, qb;
+        encode4(v, ldexpf(1.0f, 14 - e), p0, p1, p2, qb);
+        *(uint32_t *)(L + G::D_OFF + 4 * f) = p0;
+        *(uint32_t *)(L + G::D_OFF + G::DG + 4 * f) = p1;
+        *(uint32_t *)(L + G::D_OFF + 2 * G::DG + 4 * f) = p2;
+        i32x4 ax = {0, 0, 0, 0};
+        if constexpr (Q::OFF32) {
+            // sum (q - 32) Q = sum q Q - 32 sum Q: the second term enters the
+            // weight-1 plane's accumulator (int32 wrap-around is harmless, the
+            // recombined value is within +-2^29)
+            ax[0] = -32 * (int)(quad_sum_u32(qb) - 16u * 0x00808080u);
+        } else {
+            const float sv = quad_sum((v.x + v.y) + (v.z + v.w));
+            if ((lane & 3) == 0) *(float *)(L + G::G_OFF + f) = sv;  // group f / 4
+        }
+        ax[3] = __float_as_int(__builtin_isfinite(mx) ? ldexpf(1.0f, e - 14) : __builtin_nanf(""));
+        if ((lane & 3) == 0) *(i32x4 *)(L + G::A_OFF + 4 * f) = ax;
+    }
+    wave_lds_sync();
+
+    // A operands (zero in the non-live lanes), accumulator inputs and group
+    // sums of the slice; lane (n, g) supplies A = its digit row (m = n: plane
+    // n%4 of group n/4) when n/4 == g
+    const bool a_live = (n >> 2) == g && (n & 3) < 3;
+    const uint32_t a_base = G::D_OFF + (n & 3) * G::DG;
+    i32x4 av[AREG ? 4 : 1], aux[AREG ? 4 : 1];
+    float gs[AREG ? 4 : 1];
+    if constexpr (AREG) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            av[u] = i32x4{0, 0, 0, 0};
+            aux[u] = *(const i32x4 *)(L + G::A_OFF + Q::koff(g, u));
+            gs[u] = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + Q::koff(g, u) / 4) : 0.0f;
+        }
+        if (a_live) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) av[u] = *(const i32x4 *)(L + a_base + Q::koff(g, u));
+        }
+    } else {
+        av[0] = i32x4{0, 0, 0, 0};
+    }
+
+    // 4. per tile: this tile's units to LDS (the registers then take the
+    // next tile's loads), MFMAs, row partials to part[]
+    auto process = [&](uint32_t tl) {
+        wave_lds_sync();
+#pragma unroll
+        for (int s = 0; s < G::S; s++)
+            if (lane_ok && s * G::RPS + rsel < 16) *(u32x4 *)(L + loff + s * G::RPS * G::RS) = wa[s];
+        if constexpr (MULTI) issue(wa, tl + 1);
+        wave_lds_sync();
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < BPW; j++) {
+            if (j < (int)nb) {
+                typename Q::Raw raw;
+                Q::load(raw, L, n * G::RS + j * G::LB, g);
+                i32x4 bq[4];
+                float sc[4], mn[4], d, dmin;
+                Q::decode(raw, g, bq, sc, mn, d, dmin);
+                float acc_s = 0.0f, acc_m = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
+                    i32x4 A, C;
+                    float gsum;
+                    if constexpr (AREG) {
+                        A = av[u];
+                        C = aux[u];
+                        gsum = gs[u];
+                    } else {
+                        A = av[0];
+                        if (a_live) A = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
+                        C = *(const i32x4 *)(L + G::A_OFF + 16 * grp);
+                        gsum = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + 4 * grp) : 0.0f;
+                    }
+                    const i32x4 cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, A),
+                                                                           __builtin_bit_cast(i8x16, bq[u]), C, 0, 0, 0);
+                    const int T = cc[0] + cc[1] * 256 + cc[2] * 65536;
+                    acc_s = fmaf(sc[u], __int_as_float(cc[3]) * (float)T, acc_s);
+                    if constexpr (Q::HAS_MIN) acc_m = fmaf(mn[u], gsum, acc_m);
+                }
+                acc = fmaf(d, acc_s, acc);
+                if constexpr (Q::HAS_MIN) acc = fmaf(-dmin, acc_m, acc);
+            }
+        }
+        // the 4 k-groups of a row (lanes n, n+16, n+32, n+48)
+        acc = acc + __shfl_xor(acc, 16, 64);
+        acc = acc + __shfl_xor(acc, 32, 64);
+        if (lane < 16) part[(tl * W + wave) * 16 + lane] = acc;
+    };
+    if constexpr (MULTI) {
+        for (uint32_t tl = 0; tl < ntl; tl++) process(tl);
+    } else {
+        process(0);
+    }
+
+    // 5. rows of every tile of this workgroup: the W waves' partials in order
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, 4ull * a.N);
+    for (uint32_t i = t; i < ntl * 16; i += NT) {
+        const uint32_t tl = i >> 4, r = i & 15, row = (tile0 + tl * GR) * 16 + r;
+        if (row < a.N) {
+            float v = part[tl * W * 16 + r];
+            for (uint32_t w = 1; w < W; w++) v += part[(tl * W + w) * 16 + r];
+            if constexpr (SW) {
+                if (a.residual) v = u2f(__builtin_amdgcn_raw_buffer_load_b32(ry, 4 * row, 0, RRR_CPOL_SC1)) + v;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, 4 * row, 0, RRR_CPOL_SC1);
+            } else {
+                float *yp = a.y + row;
+                if (a.residual) v = *yp + v;
+                *yp = v;
+            }
+        }
+    }
+    return true;
+}
+
+inline uint32_t device_cus()
+{
+    static uint32_t cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev] = (uint32_t)v;
+    }
+    return cus[dev];
+}
+
+}  // namespace rrr

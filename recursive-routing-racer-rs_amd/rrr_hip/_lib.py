@@ -33,6 +33,23 @@ class DispatchDesc(ctypes.Structure):
     ]
 
 
+class SweepOp(ctypes.Structure):
+    """rrr_sweep_op (include/rrr_hip.h)."""
+    _fields_ = [
+        ("kind", u32),
+        ("x", c_buf_p),
+        ("gamma", c_buf_p),
+        ("eps", f32),
+        ("act_kind", u32),
+        ("act_param", u32),
+        ("W", c_buf_p),
+        ("type", u32),
+        ("y", c_buf_p),
+        ("K", u32),
+        ("N", u32),
+    ]
+
+
 # name -> (restype, argtypes); every symbol include/rrr_hip.h declares.
 SIGNATURES = {
     "rrr_init": (i32, [i32, ctypes.POINTER(c_ctx_p)]),
@@ -67,6 +84,10 @@ SIGNATURES = {
     "rrr_graph_end": (i32, [c_ctx_p, ctypes.POINTER(vp)]),
     "rrr_graph_launch": (i32, [c_ctx_p, vp]),
     "rrr_graph_destroy": (i32, [c_ctx_p, vp]),
+    "rrr_sweep_create": (i32, [c_ctx_p, ctypes.POINTER(SweepOp), u32, ctypes.POINTER(vp)]),
+    "rrr_sweep_run": (i32, [c_ctx_p, vp]),
+    "rrr_sweep_check": (i32, [c_ctx_p, vp]),
+    "rrr_sweep_destroy": (i32, [c_ctx_p, vp]),
     "rrr_set_async": (i32, [c_ctx_p, i32]),
     "rrr_sync": (i32, [c_ctx_p]),
     "rrr_timer_start": (i32, [c_ctx_p]),

@@ -159,6 +159,32 @@ class DecodeSweep:
                          E.LOGITS_CHUNKED, s.chunk)
         c.argmax_f32(self.logits, s.vocab, self.token)
 
+    def sweep_ops(self):
+        """The 4 fused GEMVs of every layer as one persistent sweep's op list
+        (the same calls record_token issues one by one)."""
+        s = self.shape
+        d = s.d_model
+        gqa = s.head_dim | (s.heads_per_kv << 16)
+        ops = []
+        for i, L in enumerate(self.layers):
+            ops += [("rmsnorm", self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], E.Q5_K, self.qkv, d, s.qkv_dim),
+                    ("residual", self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], E.Q4_K, self.hidden, d, d),
+                    ("rmsnorm", self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], E.Q4_K, self.gate_up, d,
+                     2 * s.ffn_dim),
+                    ("residual", self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], s.down_type(i), self.hidden,
+                     s.ffn_dim, d)]
+        return ops
+
+    def run_token_sweep(self, sweep):
+        """One token with the layers as one persistent launch (`sweep` from
+        ctx.sweep(self.sweep_ops())), the logits and argmax as before."""
+        c, s = self.ctx, self.shape
+        c.residual_add(self.x_in, self.zero, self.hidden, s.d_model)
+        sweep.run()
+        c.logits_rmsnorm(self.hidden, self.out_norm, s.eps, self.emb, self.logits, s.d_model, s.vocab,
+                         E.LOGITS_CHUNKED, s.chunk)
+        c.argmax_f32(self.logits, s.vocab, self.token)
+
     def graph(self):
         self.ctx.graph_begin()
         self.record_token()

@@ -31,6 +31,7 @@ ERR_STALE = -10
 F32, Q4_K, Q5_K, Q6_K = 0, 12, 13, 14
 LOGITS_ROWS, LOGITS_CHUNKED = 0, 1
 ACT_IDENTITY, ACT_SILU_GATE, ACT_GQA_V = 0, 1, 2
+SWEEP_GEMV_RMSNORM, SWEEP_GEMV_RESIDUAL = 0, 1
 DEVICE_NONE = -1
 BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, F32: 1024}
 
@@ -89,6 +90,41 @@ class Graph:
     def destroy(self):
         if self.handle:
             _check(_lib.hip().rrr_graph_destroy(self.ctx._h, ctypes.c_void_p(self.handle)))
+            self.handle = None
+
+
+class Sweep:
+    """A list of fused decode GEMVs run by one persistent launch
+    (rrr_sweep_*).  Ops are ("rmsnorm", x, gamma, eps, W, qtype, y, K, N) or
+    ("residual", x, act_kind, act_param, W, qtype, hidden, K, N)."""
+
+    def __init__(self, ctx, ops):
+        self.ctx = ctx
+        self._keep = ops
+        arr = (_lib.SweepOp * len(ops))()
+        for o, op in zip(arr, ops):
+            if op[0] == "rmsnorm":
+                _, x, gamma, eps, W, qt, y, K, N = op
+                o.kind, o.gamma, o.eps = SWEEP_GEMV_RMSNORM, gamma._h, eps
+            elif op[0] == "residual":
+                _, x, act_kind, act_param, W, qt, y, K, N = op
+                o.kind, o.act_kind, o.act_param = SWEEP_GEMV_RESIDUAL, act_kind, act_param
+            else:
+                raise ValueError(f"sweep op kind {op[0]!r}")
+            o.x, o.W, o.type, o.y, o.K, o.N = x._h, W._h, qt, y._h, K, N
+        h = ctypes.c_void_p()
+        _check(_lib.hip().rrr_sweep_create(ctx._h, arr, len(ops), ctypes.byref(h)))
+        self.handle = h.value
+
+    def run(self):
+        _check(_lib.hip().rrr_sweep_run(self.ctx._h, ctypes.c_void_p(self.handle)))
+
+    def check(self):
+        _check(_lib.hip().rrr_sweep_check(self.ctx._h, ctypes.c_void_p(self.handle)))
+
+    def destroy(self):
+        if self.handle:
+            _check(_lib.hip().rrr_sweep_destroy(self.ctx._h, ctypes.c_void_p(self.handle)))
             self.handle = None
 
 
@@ -222,6 +258,9 @@ class Context:
         h = ctypes.c_void_p()
         _check(self.lib.rrr_graph_end(self._h, ctypes.byref(h)))
         return Graph(self, h.value)
+
+    def sweep(self, ops):
+        return Sweep(self, ops)
 
     def set_async(self, flag):
         _check(self.lib.rrr_set_async(self._h, 1 if flag else 0))

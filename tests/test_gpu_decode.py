@@ -16,7 +16,7 @@ import pytest
 
 import oracle.oracle as orc
 import rrr_hip
-from rrr_hip import decode
+from rrr_hip import decode, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -81,3 +81,50 @@ def test_decode_graph_replay_matches_eager(ctx, sweep):
         assert np.array_equal(logits.view(np.uint32), logits0.view(np.uint32))
         assert np.array_equal(hidden.view(np.uint32), hidden0.view(np.uint32))
     g.destroy()
+
+
+def test_decode_sweep_persistent_matches_per_op(ctx, sweep):
+    """The layers as one persistent launch give the same bits as the per-op
+    launches, on repeated runs (its progress flags carry over)."""
+    logits0, tok0, hidden0 = sweep.results()
+    sw = ctx.sweep(sweep.sweep_ops())
+    try:
+        for _ in range(3):
+            sweep.run_token_sweep(sw)
+            sw.check()
+            logits, tok, hidden = sweep.results()
+            assert np.array_equal(hidden.view(np.uint32), hidden0.view(np.uint32))
+            assert np.array_equal(logits.view(np.uint32), logits0.view(np.uint32))
+            assert tok == tok0
+    finally:
+        sw.destroy()
+
+
+
+def test_sweep_rejects_other_forms_and_graph_capture(ctx):
+    K, N = 3072, 64
+    W = ctx.weight_upload(rrr_hip.Q6_K, K, N, synth.weight(1, 1, rrr_hip.Q6_K, K, N))
+    W4 = ctx.weight_upload(rrr_hip.Q4_K, K, N, synth.weight(1, 2, rrr_hip.Q4_K, K, N))
+    x, g, y = ctx.to_device(synth.normal_f32(1, 3, K)), ctx.to_device(synth.normal_f32(1, 4, K)), ctx.alloc(N * 4)
+    try:
+        # RMSNorm + Q6_K is not one of the decode layer's forms
+        with pytest.raises(rrr_hip.RrrError) as e:
+            ctx.sweep([("rmsnorm", x, g, 1e-5, W, rrr_hip.Q6_K, y, K, N)])
+        assert e.value.code == rrr_hip.engine.ERR_UNSUPPORTED
+        sw = ctx.sweep([("rmsnorm", x, g, 1e-5, W4, rrr_hip.Q4_K, y, K, N)])
+        ctx.graph_begin()
+        ctx.fill_u32(y, 0)
+        with pytest.raises(rrr_hip.RrrError) as e:
+            sw.run()
+        assert e.value.code == rrr_hip.engine.ERR_UNSUPPORTED
+        ctx.graph_end().destroy()
+        sw.run()
+        sw.check()
+        ref = orc.gemv(rrr_hip.Q4_K, synth.weight(1, 2, rrr_hip.Q4_K, K, N),
+                       orc.rms_norm(synth.normal_f32(1, 3, K), synth.normal_f32(1, 4, K), 1e-5), K, N, 1, THREADS,
+                       f64=True)[0]
+        assert orc.normwise_err(ctx.download(y), ref) < TOL
+        sw.destroy()
+    finally:
+        for b in (W, W4, x, g, y):
+            b.free()
