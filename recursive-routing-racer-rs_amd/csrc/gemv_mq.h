@@ -235,6 +235,20 @@ struct MwGeom {
     static constexpr uint32_t BYTES = G_OFF + 4 * NGW;            // multiple of 16
 };
 
+// Odd Q6_K blocks (210 bytes) start 2 bytes past a 4-byte boundary, and
+// 16-byte loads that are only 2-byte aligned take a slow path (~1.5 us more
+// per 20 MB).  Such a block's units are loaded from 2 bytes earlier and moved
+// down by 2 bytes in registers, the top 2 bytes coming from the next lane
+// (the block's next unit; for the last unit they fall past byte 222 of the
+// block, which is never read).  `sh` is 0 or 2; every lane of the wave
+// calls it.
+__device__ __forceinline__ u32x4 q6_realign(const u32x4 &v, uint32_t sh)
+{
+    const uint32_t nx = (uint32_t)__builtin_amdgcn_mov_dpp((int)v.x, 0x130, 0xF, 0xF, false);   // wave_shl:1
+    return u32x4{__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh),
+                 __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(nx, v.w, sh)};
+}
+
 // Sum of squares of x[0..K) in the order of the standalone RMSNorm kernel
 // (thread t < 256 owns float4s t, t + 256, ...; wave butterfly; waves 0..3
 // added in order), so the fused scale is bitwise that kernel's.  cx[j] holds
@@ -414,9 +428,12 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, Swee
     const uint32_t rsel = min(lane / G::UPR, G::RPS - 1), wl = lane - (lane / G::UPR) * G::UPR;
     const uint32_t jl = wl / G::UPB, vl = wl - jl * G::UPB;
     const bool lane_ok = lane < G::RPS * G::UPR && jl < nb;
-    const uint32_t voff = rsel * row_bytes + (b0 + min(jl, nb ? nb - 1 : 0u)) * Q::BS + 16 * vl;
-    const uint32_t voff_last = (G::S - 1) * G::RPS + rsel < 16 ? voff : MQ_OOB;
+    const uint32_t blk = b0 + min(jl, nb ? nb - 1 : 0u);
+    constexpr bool REALIGN = Q::BS % 4 != 0;
+    const uint32_t sh = REALIGN ? (blk * Q::BS) & 3u : 0u;     // 0 or 2 bytes
+    const uint32_t voff = rsel * row_bytes + blk * Q::BS - sh + 16 * vl;
     const uint32_t loff = rsel * G::RS + jl * G::LB + 16 * vl;
+    const uint32_t voff_last = (G::S - 1) * G::RPS + rsel < 16 ? voff : MQ_OOB;
     u32x4 wa[G::S];
     auto issue = [&](u32x4 *w, uint32_t tl) {
         const uint32_t tb = tl < ntl ? (tile0 + tl * GR) * tile_bytes : MQ_OOB;
@@ -521,8 +538,11 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, Swee
     auto process = [&](uint32_t tl) {
         wave_lds_sync();
 #pragma unroll
-        for (int s = 0; s < G::S; s++)
-            if (lane_ok && s * G::RPS + rsel < 16) *(u32x4 *)(L + loff + s * G::RPS * G::RS) = wa[s];
+        for (int s = 0; s < G::S; s++) {
+            u32x4 v = wa[s];
+            if constexpr (REALIGN) v = q6_realign(v, sh);
+            if (lane_ok && s * G::RPS + rsel < 16) *(u32x4 *)(L + loff + s * G::RPS * G::RS) = v;
+        }
         if constexpr (MULTI) issue(wa, tl + 1);
         wave_lds_sync();
         float acc = 0.0f;
