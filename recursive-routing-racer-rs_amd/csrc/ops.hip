@@ -177,10 +177,13 @@ hipError_t launch_fill_u32(uint32_t *p, uint64_t n, uint32_t v, hipStream_t s)
 // ---------------------------------------------------------------------------
 // Logits over the reference's transposed chunks (phi4.rs:874-893):
 // chunk c holds n_c = min(chunk, V - c*chunk) vocab rows as B_c[d*n_c + v].
-// A workgroup owns 256 consecutive vocab entries of one chunk (lane = 4
-// entries, one 16-byte load per d), wave w sums d in [w*K/4, (w+1)*K/4), and
-// the four partials are added in wave order through LDS.  The activation
-// (optionally RMS-normalised in place) sits in LDS.
+// A workgroup owns 64 consecutive vocab entries of one chunk, so the ~3,100
+// workgroups of the 200,064-entry vocabulary spread evenly over the CUs
+// (with 256 entries, 782 workgroups left 14 CUs a fourth 3 MB workgroup at
+// the end).  Wave w sums d in [w*K/4, (w+1)*K/4) as four interleaved row
+// streams (a lane: 4 entries of every 4th row, one 16-byte load per row), the
+// streams are added by a fixed butterfly and the waves in order through LDS.
+// The activation (optionally RMS-normalised in place) sits in LDS.
 __global__ __launch_bounds__(256) void logits_chunked_kernel(const float *__restrict__ x, const float *__restrict__ gamma,
                                                              float eps, const float *__restrict__ E,
                                                              float *__restrict__ y, uint32_t K, uint32_t V,
@@ -188,33 +191,37 @@ __global__ __launch_bounds__(256) void logits_chunked_kernel(const float *__rest
 {
     extern __shared__ float sm[];
     float *xs = sm;             // K
-    float *part = xs + K;       // 4 * 256
-    float *red = part + 1024;   // 4
+    float *part = xs + K;       // 4 waves x 64 entries
+    float *red = part + 256;    // 4
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     float inv = 1.0f;
     if (gamma) inv = rms_inv(block_sumsq_256(x, K, red), K, eps);
     for (uint32_t i = t; i < K; i += 256) xs[i] = gamma ? __fmul_rn(__fmul_rn(gamma[i], x[i]), inv) : x[i];
     __syncthreads();
 
-    const uint32_t v0 = blockIdx.x * 256;
+    // 64 vocab entries per workgroup (chunks are multiples of 64 entries when
+    // there are several): lane (q, g) = (lane % 16, lane / 16) reads entries
+    // 4q .. 4q+3 of the rows d = d0 + 4i + g of its wave's quarter of K
+    const uint32_t v0 = blockIdx.x * 64;
     const uint32_t c = v0 / chunk, cstart = c * chunk;
     const uint32_t n = (V - cstart) < chunk ? (V - cstart) : chunk;
-    const uint32_t vin = v0 - cstart + 4 * lane;  // index inside the chunk
+    const uint32_t q = lane & 15, g = lane >> 4;
+    const uint32_t vin = v0 - cstart + 4 * q;     // index inside the chunk
     const uint64_t cbase = (uint64_t)cstart * K;  // chunk c starts after c full chunks
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(E + cbase, (uint64_t)n * K * 4);
     const uint32_t dq = K / 4, d0 = wave * dq;
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
     if (vin < n) {
-        uint32_t off = (d0 * n + vin) * 4;
-        const uint32_t step = n * 4;
+        const uint32_t step = 4 * n * 4;          // 4 rows
+        uint32_t off = ((d0 + g) * n + vin) * 4;
         uint32_t dd = 0;
-        for (; dd + 8 <= dq; dd += 8) {
+        for (; dd + 32 <= dq; dd += 32) {
             u32x4 w[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) w[u] = bload16(rs, off + u * step);
+            for (int u = 0; u < 8; u++) w[u] = bload16_nt(rs, off + u * step);
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                const float xv = xs[d0 + dd + u];
+                const float xv = xs[d0 + dd + 4 * u + g];
                 a0 = fmaf(xv, u2f(w[u].x), a0);
                 a1 = fmaf(xv, u2f(w[u].y), a1);
                 a2 = fmaf(xv, u2f(w[u].z), a2);
@@ -222,9 +229,9 @@ __global__ __launch_bounds__(256) void logits_chunked_kernel(const float *__rest
             }
             off += 8 * step;
         }
-        for (; dd < dq; dd++) {
-            const u32x4 w = bload16(rs, off);
-            const float xv = xs[d0 + dd];
+        for (; dd + g < dq; dd += 4) {
+            const u32x4 w = bload16_nt(rs, off);
+            const float xv = xs[d0 + dd + g];
             a0 = fmaf(xv, u2f(w.x), a0);
             a1 = fmaf(xv, u2f(w.y), a1);
             a2 = fmaf(xv, u2f(w.z), a2);
@@ -232,24 +239,28 @@ __global__ __launch_bounds__(256) void logits_chunked_kernel(const float *__rest
             off += step;
         }
     }
-    float4 *p4 = (float4 *)part;
-    p4[wave * 64 + lane] = make_float4(a0, a1, a2, a3);
+    // the 4 row streams of a wave (lanes q, q+16, q+32, q+48), then the waves
+    // in order
+    a0 = a0 + __shfl_xor(a0, 16, 64); a0 = a0 + __shfl_xor(a0, 32, 64);
+    a1 = a1 + __shfl_xor(a1, 16, 64); a1 = a1 + __shfl_xor(a1, 32, 64);
+    a2 = a2 + __shfl_xor(a2, 16, 64); a2 = a2 + __shfl_xor(a2, 32, 64);
+    a3 = a3 + __shfl_xor(a3, 16, 64); a3 = a3 + __shfl_xor(a3, 32, 64);
+    if (g == 0) ((float4 *)part)[wave * 16 + q] = make_float4(a0, a1, a2, a3);
     __syncthreads();
-    if (wave == 0 && vin < n) {
-        float r[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            r[e] = ((part[4 * lane + e] + part[256 + 4 * lane + e]) + part[512 + 4 * lane + e]) + part[768 + 4 * lane + e];
-        for (int e = 0; e < 4; e++)
-            if (vin + e < n) y[cstart + vin + e] = r[e];
+    if (t < 64 && v0 - cstart + t < n) {
+        const float r = ((part[t] + part[64 + t]) + part[128 + t]) + part[192 + t];
+        y[cstart + (v0 - cstart) + t] = r;
     }
 }
 
 hipError_t launch_logits_chunked(const float *x, const float *gamma, float eps, const float *E, float *y,
                                  uint32_t K, uint32_t V, uint32_t chunk, hipStream_t s)
 {
-    const size_t lds = ((size_t)K + 1024 + 4) * sizeof(float);
-    const uint32_t nwg = (V + 255) / 256;
+    const size_t lds = ((size_t)K + 256 + 4) * sizeof(float);
+    // 64-entry groups of each chunk (a partial last chunk may leave a
+    // partial group)
+    uint32_t nwg = 0;
+    for (uint32_t c0 = 0; c0 < V; c0 += chunk) nwg += ((V - c0 < chunk ? V - c0 : chunk) + 63) / 64;
     hipLaunchKernelGGL(logits_chunked_kernel, dim3(nwg), dim3(256), lds, s, x, gamma, eps, E, y, K, V, chunk);
     return hipGetLastError();
 }
