@@ -862,7 +862,7 @@ int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_swee
     TRY(device_ready(ctx));
     const uint32_t cus = sweep_cus();
     std::vector<GemvArgs> args(n);
-    std::vector<uint32_t> acts(n), variants(n), ntiles(n);
+    std::vector<uint32_t> acts(n), variants(n), ntiles(n), trs(n);
     size_t lds = 0;
     for (uint32_t i = 0; i < n; i++) {
         const rrr_sweep_op &o = ops[i];
@@ -883,7 +883,7 @@ int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_swee
             return fail(RRR_ERR_INVALID_ARG, "%s: op %u: kind %u", what, i, o.kind);
         }
         size_t l;
-        if (!sweep_plan_op(a, acts[i], cus, variants[i], ntiles[i], l))
+        if (!sweep_plan_op(a, acts[i], cus, variants[i], ntiles[i], trs[i], l))
             return fail(RRR_ERR_UNSUPPORTED, "%s: op %u (type %u, K=%u, N=%u) is not a sweep shape", what, i, o.type,
                         o.K, o.N);
         lds = std::max(lds, l);
@@ -891,7 +891,7 @@ int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_swee
     const uint32_t grid = sweep_grid(lds);
     if (grid == 0) return fail(RRR_ERR_UNSUPPORTED, "%s: a 1024-thread workgroup with %zu B of LDS does not fit", what, lds);
     std::vector<uint8_t> packed((size_t)n * sweep_op_bytes());
-    for (uint32_t i = 0; i < n; i++) sweep_pack_op(packed.data() + (size_t)i * sweep_op_bytes(), args[i], variants[i], ntiles[i]);
+    for (uint32_t i = 0; i < n; i++) sweep_pack_op(packed.data() + (size_t)i * sweep_op_bytes(), args[i], variants[i], ntiles[i], trs[i]);
     rrr_sweep *sw = new rrr_sweep{};
     sw->magic = SWEEP_MAGIC;
     sw->nops = n;

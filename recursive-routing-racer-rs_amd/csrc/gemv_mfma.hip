@@ -6,26 +6,28 @@
 namespace rrr {
 
 template <class Q, int BPW, int ACT, bool MULTI>
-__global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntiles)
+__global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntiles, uint32_t tr)
 {
     SweepWait none{nullptr, nullptr, 0u, nullptr, nullptr};
-    (void)mq_body<Q, BPW, ACT, MULTI, false>(a, ntiles, none);
+    (void)mq_body<Q, BPW, ACT, MULTI, false>(a, ntiles, tr, none);
 }
 
 // Super-blocks per wave and waves per workgroup (at least 4, the canonical
 // RMSNorm order needs them; waves past the last super-block only encode).
-// Up to one workgroup per CU, each taking ceil(tiles / workgroups) tiles as
-// far as its row partials fit in LDS.
+// Up to one workgroup per CU, each taking its tiles as far as its row
+// partials fit in LDS.
 template <class Q, int BPW>
-static void mq_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds)
+static void mq_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds, uint32_t &tr, uint32_t &ntiles)
 {
     using G = MwGeom<Q, BPW>;
     const uint32_t B = a.K / 256;
     W = max(4u, (B + BPW - 1) / BPW);
-    const uint32_t ntiles = (a.N + 15) / 16;
     const size_t fixed = W * G::BYTES + 16;
     const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64));
-    const uint32_t per = min((ntiles + device_cus() - 1) / device_cus(), per_max);
+    uint32_t per;
+    // even tiles pay off with one super-block per wave; with two (K > 4096)
+    // the empty load slots of a short tile cost more than the CUs it adds
+    mq_tiles(a.N, device_cus(), per_max, BPW == 1 ? 1u : 16u, tr, ntiles, per);
     grid = (ntiles + per - 1) / per;
     lds = fixed + (size_t)per * W * 64;
 }
@@ -34,14 +36,13 @@ template <class Q, int BPW, int ACT>
 static hipError_t go_mq(const GemvArgs &a, hipStream_t s)
 {
     static_assert(16 * MwGeom<Q, BPW>::BYTES + 16 + 16 * 64 <= 160 * 1024, "LDS per workgroup");
-    uint32_t W, grid;
+    uint32_t W, grid, tr, ntiles;
     size_t lds;
-    mq_plan<Q, BPW>(a, W, grid, lds);
-    const uint32_t ntiles = (a.N + 15) / 16;
+    mq_plan<Q, BPW>(a, W, grid, lds, tr, ntiles);
     if (grid == ntiles)
-        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, false>), dim3(grid), dim3(64 * W), lds, s, a, ntiles);
+        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, false>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
     else
-        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, true>), dim3(grid), dim3(64 * W), lds, s, a, ntiles);
+        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, true>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
     return hipGetLastError();
 }
 

@@ -388,7 +388,10 @@ __device__ __forceinline__ void mq_src_load4(const GemvArgs &a, __amdgpu_buffer_
     }
 }
 
-// Persistent form (MULTI): workgroup b takes the 16-row tiles b, b + G, ...
+// A tile is tr <= 16 rows (the MFMA's 16 columns, the rest idle), chosen by
+// the launcher so that the tiles spread evenly over the CUs (K <= 4096,
+// N = 3072: 256 tiles of 12 rows rather than 192 of 16).
+// Persistent form (MULTI): workgroup b takes the tiles b, b + G, ...
 // (G = gridDim.x) with the same wave <-> K-slice split for every tile, so the
 // activation slice is encoded once per workgroup and, with one super-block per
 // wave, the MFMA A operands and accumulator inputs stay in registers.  The
@@ -399,7 +402,7 @@ __device__ __forceinline__ void mq_src_load4(const GemvArgs &a, __amdgpu_buffer_
 // the waves in wave order, so results depend on neither form, G nor the
 // number of waves.  Returns false when a sweep wait was abandoned.
 template <class Q, int BPW, int ACT, bool MULTI, bool SW>
-__device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, SweepWait &sw)
+__device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr, SweepWait &sw)
 {
     extern __shared__ float smem[];
     using G = MwGeom<Q, BPW>;
@@ -414,7 +417,7 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, Swee
     float *red = (float *)((uint8_t *)smem + W * G::BYTES);      // 4
     float *part = red + 4;                                       // ntl x W x 16 per-wave row partials
 
-    const uint32_t row_bytes = B * Q::BS, tile_bytes = 16 * row_bytes;
+    const uint32_t row_bytes = B * Q::BS, tile_bytes = tr * row_bytes;
     // every buffer has RRR_READ_SLACK readable bytes past its end: a Q6_K
     // piece's last unit runs 14 bytes past its block
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.W, a.w_bytes + RRR_READ_SLACK);
@@ -424,7 +427,7 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, Swee
 
     // weight units of this wave's slice of a tile (layout above); lanes past
     // RPS rows and blocks past nb reload a valid unit and are not stored, and
-    // rows past 16 in the last slot read nothing
+    // rows past the tile's tr rows read nothing
     const uint32_t rsel = min(lane / G::UPR, G::RPS - 1), wl = lane - (lane / G::UPR) * G::UPR;
     const uint32_t jl = wl / G::UPB, vl = wl - jl * G::UPB;
     const bool lane_ok = lane < G::RPS * G::UPR && jl < nb;
@@ -433,13 +436,12 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, Swee
     const uint32_t sh = REALIGN ? (blk * Q::BS) & 3u : 0u;     // 0 or 2 bytes
     const uint32_t voff = rsel * row_bytes + blk * Q::BS - sh + 16 * vl;
     const uint32_t loff = rsel * G::RS + jl * G::LB + 16 * vl;
-    const uint32_t voff_last = (G::S - 1) * G::RPS + rsel < 16 ? voff : MQ_OOB;
     u32x4 wa[G::S];
     auto issue = [&](u32x4 *w, uint32_t tl) {
         const uint32_t tb = tl < ntl ? (tile0 + tl * GR) * tile_bytes : MQ_OOB;
 #pragma unroll
         for (int s = 0; s < G::S; s++)
-            w[s] = bload16_nt_so(rs, s == G::S - 1 ? voff_last : voff, tb + s * G::RPS * row_bytes);
+            w[s] = bload16_nt_so(rs, s * G::RPS + rsel < tr ? voff : MQ_OOB, tb + s * G::RPS * row_bytes);
     };
 
     // The loads below are unconditional (clamped indices, out-of-range scalar
@@ -541,7 +543,7 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, Swee
         for (int s = 0; s < G::S; s++) {
             u32x4 v = wa[s];
             if constexpr (REALIGN) v = q6_realign(v, sh);
-            if (lane_ok && s * G::RPS + rsel < 16) *(u32x4 *)(L + loff + s * G::RPS * G::RS) = v;
+            if (lane_ok && s * G::RPS + rsel < tr) *(u32x4 *)(L + loff + s * G::RPS * G::RS) = v;
         }
         if constexpr (MULTI) issue(wa, tl + 1);
         wave_lds_sync();
@@ -595,8 +597,8 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, Swee
     __syncthreads();
     const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, 4ull * a.N);
     for (uint32_t i = t; i < ntl * 16; i += NT) {
-        const uint32_t tl = i >> 4, r = i & 15, row = (tile0 + tl * GR) * 16 + r;
-        if (row < a.N) {
+        const uint32_t tl = i >> 4, r = i & 15, row = (tile0 + tl * GR) * tr + r;
+        if (r < tr && row < a.N) {
             float v = part[tl * W * 16 + r];
             for (uint32_t w = 1; w < W; w++) v += part[(tl * W + w) * 16 + r];
             if constexpr (SW) {
@@ -610,6 +612,20 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, Swee
         }
     }
     return true;
+}
+
+// Rows per tile and tiles per workgroup for `wgs` workgroups: the fewest
+// tiles per workgroup (k, at most per_max) that cover N with tiles of at most
+// 16 rows, then the smallest tile (tr rows, at least min_tr) that still does,
+// so that the tiles split evenly.
+inline void mq_tiles(uint32_t N, uint32_t wgs, uint32_t per_max, uint32_t min_tr, uint32_t &tr, uint32_t &ntiles,
+                     uint32_t &per)
+{
+    uint32_t k = (N + 16 * wgs - 1) / (16 * wgs);
+    k = max(1u, min(k, per_max));
+    tr = max(min_tr, min(16u, (N + k * wgs - 1) / (k * wgs)));
+    ntiles = (N + tr - 1) / tr;
+    per = min((ntiles + wgs - 1) / wgs, per_max);
 }
 
 inline uint32_t device_cus()

@@ -45,9 +45,10 @@ hipError_t launch_gemv_mfma(const GemvArgs &a, uint32_t act, hipStream_t s);
 bool skinny_supported(const GemvArgs &a);
 hipError_t launch_skinny(const GemvArgs &a, hipStream_t s);
 // Persistent decode sweep (sweep.hip): per-op plan, packing and the launch
-bool sweep_plan_op(const GemvArgs &a, uint32_t act, uint32_t grid, uint32_t &variant, uint32_t &ntiles, size_t &lds);
+bool sweep_plan_op(const GemvArgs &a, uint32_t act, uint32_t grid, uint32_t &variant, uint32_t &ntiles, uint32_t &tr,
+                   size_t &lds);
 size_t sweep_op_bytes();
-void sweep_pack_op(void *dst, const GemvArgs &a, uint32_t variant, uint32_t ntiles);
+void sweep_pack_op(void *dst, const GemvArgs &a, uint32_t variant, uint32_t ntiles, uint32_t tr);
 uint32_t sweep_cus();
 uint32_t sweep_grid(size_t lds);
 // words of the flag area (progress flags, error word, go words), and the

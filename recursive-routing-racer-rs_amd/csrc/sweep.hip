@@ -18,6 +18,8 @@ struct SweepOpDev {
     GemvArgs a;
     uint32_t variant;
     uint32_t ntiles;
+    uint32_t tr;        // rows per tile
+    uint32_t pad;
 };
 
 // variant = 8 * type index (Q4_K 0, Q5_K 1, Q6_K 2) + 4 * (BPW - 1) + activation
@@ -43,13 +45,13 @@ __global__ __launch_bounds__(1024) void sweep_kernel(const SweepOpDev *ops, uint
         const SweepOpDev o = ops[op];
         SweepWait sw{flags, go, op ? epoch + op : 0u, err, &bail};
         bool ok;
-        const uint32_t v = o.variant, act = v & 3;
+        const uint32_t v = o.variant;
         switch (v) {
-        case sweep_variant_of(1, 1, ACT_RMSNORM): ok = mq_body<MqQ5K, 1, ACT_RMSNORM, true, true>(o.a, o.ntiles, sw); break;
-        case sweep_variant_of(0, 1, ACT_GQA_V): ok = mq_body<MqQ4K, 1, ACT_GQA_V, true, true>(o.a, o.ntiles, sw); break;
-        case sweep_variant_of(0, 1, ACT_RMSNORM): ok = mq_body<MqQ4K, 1, ACT_RMSNORM, true, true>(o.a, o.ntiles, sw); break;
-        case sweep_variant_of(2, 2, ACT_SILU): ok = mq_body<MqQ6K, 2, ACT_SILU, true, true>(o.a, o.ntiles, sw); break;
-        default: ok = mq_body<MqQ4K, 2, ACT_SILU, true, true>(o.a, o.ntiles, sw); break;
+        case sweep_variant_of(1, 1, ACT_RMSNORM): ok = mq_body<MqQ5K, 1, ACT_RMSNORM, true, true>(o.a, o.ntiles, o.tr, sw); break;
+        case sweep_variant_of(0, 1, ACT_GQA_V): ok = mq_body<MqQ4K, 1, ACT_GQA_V, true, true>(o.a, o.ntiles, o.tr, sw); break;
+        case sweep_variant_of(0, 1, ACT_RMSNORM): ok = mq_body<MqQ4K, 1, ACT_RMSNORM, true, true>(o.a, o.ntiles, o.tr, sw); break;
+        case sweep_variant_of(2, 2, ACT_SILU): ok = mq_body<MqQ6K, 2, ACT_SILU, true, true>(o.a, o.ntiles, o.tr, sw); break;
+        default: ok = mq_body<MqQ4K, 2, ACT_SILU, true, true>(o.a, o.ntiles, o.tr, sw); break;
         }
         if (!ok) return;
         // this workgroup's rows of the op have been written through: publish
@@ -61,7 +63,8 @@ __global__ __launch_bounds__(1024) void sweep_kernel(const SweepOpDev *ops, uint
 
 // Per-op set-up: the variant, the tile count and the LDS the op needs with
 // `grid` workgroups of 16 waves; false if the sweep cannot run it.
-bool sweep_plan_op(const GemvArgs &a, uint32_t act, uint32_t grid, uint32_t &variant, uint32_t &ntiles, size_t &lds)
+bool sweep_plan_op(const GemvArgs &a, uint32_t act, uint32_t grid, uint32_t &variant, uint32_t &ntiles, uint32_t &tr,
+                   size_t &lds)
 {
     if (a.M != 1 || a.K % 256 || a.K == 0 || a.K > 8192 || a.w_bytes + RRR_READ_SLACK >= MQ_OOB) return false;
     const uint32_t ti = a.type == T_Q4_K ? 0 : a.type == T_Q5_K ? 1 : a.type == T_Q6_K ? 2 : 3;
@@ -83,17 +86,17 @@ bool sweep_plan_op(const GemvArgs &a, uint32_t act, uint32_t grid, uint32_t &var
         variant != sweep_variant_of(0, 1, ACT_RMSNORM) && variant != sweep_variant_of(2, 2, ACT_SILU) &&
         variant != sweep_variant_of(0, 2, ACT_SILU))
         return false;
-    ntiles = (a.N + 15) / 16;
-    const uint32_t per = (ntiles + grid - 1) / grid;
+    uint32_t per;
+    mq_tiles(a.N, grid, 64, bpw == 1 ? 1u : 16u, tr, ntiles, per);
     lds = 16 * bytes + 16 + (size_t)per * 16 * 64;
     return lds <= 160 * 1024;
 }
 
 size_t sweep_op_bytes() { return sizeof(SweepOpDev); }
 
-void sweep_pack_op(void *dst, const GemvArgs &a, uint32_t variant, uint32_t ntiles)
+void sweep_pack_op(void *dst, const GemvArgs &a, uint32_t variant, uint32_t ntiles, uint32_t tr)
 {
-    SweepOpDev o{a, variant, ntiles};
+    SweepOpDev o{a, variant, ntiles, tr, 0u};
     *(SweepOpDev *)dst = o;
 }
 
