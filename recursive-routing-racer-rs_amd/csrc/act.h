@@ -29,7 +29,7 @@ __device__ __forceinline__ float4 xform4(const float4 &x, const float4 &y, float
         return make_float4(__fmul_rn(__fmul_rn(y.x, x.x), inv), __fmul_rn(__fmul_rn(y.y, x.y), inv),
                            __fmul_rn(__fmul_rn(y.z, x.z), inv), __fmul_rn(__fmul_rn(y.w, x.w), inv));
     else if constexpr (ACT == ACT_SILU)
-        return make_float4(silu_f(x.x) * y.x, silu_f(x.y) * y.y, silu_f(x.z) * y.z, silu_f(x.w) * y.w);
+        return make_float4(silu_fast(x.x) * y.x, silu_fast(x.y) * y.y, silu_fast(x.z) * y.z, silu_fast(x.w) * y.w);
     else
         return x;
 }

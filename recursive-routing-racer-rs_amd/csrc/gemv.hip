@@ -287,7 +287,7 @@ __device__ __forceinline__ void src_xform(const Src16 &s, float inv, float4 *v)
                                __fmul_rn(__fmul_rn(w.z, x.z), inv), __fmul_rn(__fmul_rn(w.w, x.w), inv));
         } else if constexpr (ACT == ACT_SILU) {
             const float4 u = s.b[i];
-            v[i] = make_float4(silu_f(x.x) * u.x, silu_f(x.y) * u.y, silu_f(x.z) * u.z, silu_f(x.w) * u.w);
+            v[i] = make_float4(silu_fast(x.x) * u.x, silu_fast(x.y) * u.y, silu_fast(x.z) * u.z, silu_fast(x.w) * u.w);
         } else {
             v[i] = x;
         }

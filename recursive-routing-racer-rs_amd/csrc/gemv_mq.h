@@ -452,6 +452,12 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint
         issue(wa, 0);
         if (!sweep_wait(sw)) return false;
     }
+    // the residual of this thread's first output row, read now rather than
+    // on the kernel's tail (a clamped row when there is none)
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, 4ull * a.N);
+    const uint32_t row_first = min((tile0 + (t >> 4) * GR) * tr + (t & 15), a.N - 1);
+    const float yres = SW ? u2f(__builtin_amdgcn_raw_buffer_load_b32(ry, 4 * row_first, 0, RRR_CPOL_SC1))
+                          : a.y[row_first];
     // 1. fused RMSNorm: the whole of x in the canonical order (K <= 1024 NSQ)
     constexpr int NSQ = ACT == ACT_RMSNORM ? 4 * BPW : 1;
     float4 cx[NSQ];
@@ -595,20 +601,21 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint
 
     // 5. rows of every tile of this workgroup: the W waves' partials in order
     __syncthreads();
-    const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, 4ull * a.N);
     for (uint32_t i = t; i < ntl * 16; i += NT) {
         const uint32_t tl = i >> 4, r = i & 15, row = (tile0 + tl * GR) * tr + r;
         if (r < tr && row < a.N) {
             float v = part[tl * W * 16 + r];
             for (uint32_t w = 1; w < W; w++) v += part[(tl * W + w) * 16 + r];
-            if constexpr (SW) {
-                if (a.residual) v = u2f(__builtin_amdgcn_raw_buffer_load_b32(ry, 4 * row, 0, RRR_CPOL_SC1)) + v;
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, 4 * row, 0, RRR_CPOL_SC1);
-            } else {
-                float *yp = a.y + row;
-                if (a.residual) v = *yp + v;
-                *yp = v;
+            if (a.residual) {
+                const float h = i == t ? yres
+                                : SW ? u2f(__builtin_amdgcn_raw_buffer_load_b32(ry, 4 * row, 0, RRR_CPOL_SC1))
+                                     : a.y[row];
+                v = h + v;
             }
+            if constexpr (SW)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, 4 * row, 0, RRR_CPOL_SC1);
+            else
+                a.y[row] = v;
         }
     }
     return true;
