@@ -172,6 +172,35 @@ int rrr_logits_f32(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *E, rrr_buf *lo
  * (phi4.rs:1172-1183). */
 int rrr_argmax_f32(rrr_ctx *ctx, const rrr_buf *logits, uint32_t V, rrr_buf *out_index);
 
+/* ---- decode glue: RoPE + f16 KV cache, decode attention -------------- */
+
+/* The rope_kv_store pipeline (phi4.rs:1016-1017; push [pos, n_heads,
+ * n_kv_heads, head_dim, rope_dim, q_dim, kv_stride], :1115-1117).  qkv holds
+ * [q(q_dim) | k(kv_stride) | v(kv_stride)] f32.  RoPE as apply_rope_cfg
+ * (phi4.rs:238-256) rotates pairs (2i, 2i+1), i < rope_dim/2, of every Q
+ * head and every K head in place: freq_i = theta^(-2i/rope_dim) / f_i
+ * (f_i = rope_factors[i] for i < n_factors, else 1), angle = pos * freq_i,
+ * cos and sin scaled by attn_factor.  Then K and V are stored as f16 (round
+ * to nearest even) into row pos of k_cache / v_cache (rows of kv_stride f16,
+ * the MAX_SEQ x kv_stride caches of phi4.rs:894-903).  rope_dim = 0 skips the
+ * rotation: the kv_store pipeline (phi4.rs:1666-1677).  Phi-4-mini:
+ * theta 10000, attn_factor 1.190238, rope_dim 96 (phi4.rs:114-116). */
+int rrr_rope_kv_store(rrr_ctx *ctx, rrr_buf *qkv, const rrr_buf *rope_factors, uint32_t n_factors,
+                      rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos, uint32_t n_heads,
+                      uint32_t n_kv_heads, uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim,
+                      uint32_t kv_stride, float theta, float attn_factor);
+
+/* The attention pipeline (phi4.rs:1018, :1304-1312; push [seq_len,
+ * n_kv_heads, heads_per_kv, head_dim], one workgroup per query head in the
+ * reference): for query head h (h < n_kv_heads * heads_per_kv) and KV head
+ * g = h / heads_per_kv, out[h] = sum_t softmax_t(q_h . k_t / sqrt(head_dim))
+ * v_t over cache rows t < seq_len (f16 K and V, f32 arithmetic).  q and out
+ * are n_heads * head_dim f32 (16-byte aligned), the caches 16-byte aligned.
+ * head_dim must be 128 and heads_per_kv at most 8. */
+int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const rrr_buf *v_cache,
+                  rrr_buf *out, uint32_t seq_len, uint32_t n_kv_heads, uint32_t heads_per_kv,
+                  uint32_t head_dim);
+
 /* ---- fused decode-sweep ops (the four launches per layer) ------------ */
 
 /* Y = W . rmsnorm(x, gamma, eps): RMSNorm folded into the GEMV's activation
@@ -209,12 +238,20 @@ int rrr_logits_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, flo
  *   rmsnorm                               bufs [x, g, y],  push [rows, d]
  *   silu_gate                             bufs [gu, mid],  push [F]
  *   residual_add                          bufs [a, b, out], push [d]
+ *   rope_kv_store   bufs [qkv, rope_factors, k_cache, v_cache],
+ *                   push [pos, n_heads, n_kv_heads, head_dim, rope_dim, q_dim, kv_stride]
+ *   kv_store        bufs [qkv, k_cache, v_cache], push [pos, q_dim, kv_stride]
+ *   attention       bufs [q, k_cache, v_cache, out],
+ *                   push [seq_len, n_kv_heads, heads_per_kv, head_dim]
  * The matmul_gpuq* names take RAW GGUF bytes here (the repack is gone) with
  * the type implied by the name.  The grid argument is accepted for call-shape
  * compatibility and checked against the push constants; launch geometry is
  * chosen by the library.  Unknown names and the out-of-scope pipelines
- * (rope, rope_kv_store, kv_store, attention) return RRR_ERR_UNSUPPORTED.
- * rmsnorm uses eps = 1e-5, baked in as the reference's shader does. */
+ * (rope, fused_norm_matmul_q*k) return RRR_ERR_UNSUPPORTED.  rmsnorm uses
+ * eps = 1e-5 and rope_kv_store theta 10000 / attention factor 1.190238, baked
+ * in as the reference's shaders do; rope_kv_store takes the first
+ * min(size / 4, rope_dim / 2) floats of rope_factors as the LongRoPE
+ * factors. */
 int rrr_dispatch(rrr_ctx *ctx, const char *name, rrr_buf *const *bufs, uint32_t n_bufs,
                  const void *push, uint32_t push_bytes, const uint32_t groups[3]);
 

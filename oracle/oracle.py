@@ -17,6 +17,7 @@ LIB = os.path.join(HERE, "liboracle.so")
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _f64p = ctypes.POINTER(ctypes.c_double)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
 _u32 = ctypes.c_uint32
 _sz = ctypes.c_size_t
 
@@ -40,6 +41,11 @@ _SIG = {
     "rrr_o_logits_f32": (ctypes.c_int, [_f32p, _f32p, _f32p, _u32, _u32, _u32, _u32, ctypes.c_int]),
     "rrr_o_logits_f64": (ctypes.c_int, [_f32p, _f32p, _f64p, _u32, _u32, _u32, _u32, ctypes.c_int]),
     "rrr_o_logits_chunk_build": (None, [_f32p, _u32, _u32, _u32, _f32p]),
+    "rrr_o_f32_to_f16_n": (None, [_f32p, _u16p, _sz]),
+    "rrr_o_rope": (None, [_f32p, _u32, _u32, _u32, _u32, ctypes.c_float, ctypes.c_float, _f32p, _u32]),
+    "rrr_o_rope_kv_store": (None, [_f32p, _f32p, _u32, _u16p, _u16p, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                   ctypes.c_float, ctypes.c_float]),
+    "rrr_o_attention_f64": (None, [_f32p, _u16p, _u16p, _f64p, _u32, _u32, _u32, _u32]),
 }
 
 _lib = None
@@ -173,3 +179,55 @@ def normwise_err(got, ref):
     ref = np.asarray(ref, dtype=np.float64)
     den = np.max(np.abs(ref))
     return float(np.max(np.abs(got - ref)) / (den if den > 0 else 1.0))
+
+
+# ---- decode glue: RoPE, the f16 KV-cache store, decode attention ----
+
+# the reference's legacy Phi-4-mini constants (phi4.rs:114-116)
+ROPE_DIM, ROPE_THETA, ROPE_ATTN_FACTOR = 96, 10000.0, 1.190238
+
+
+def f32_to_f16_bits(x):
+    """binary32 -> binary16 bit patterns, round to nearest even."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.size, dtype=np.uint16)
+    lib().rrr_o_f32_to_f16_n(_p(x, _f32p), _p(out, _u16p), x.size)
+    return out.reshape(x.shape)
+
+
+def rope(x, pos, n_heads, head_dim, rope_dim=ROPE_DIM, theta=ROPE_THETA, attn_factor=ROPE_ATTN_FACTOR,
+         factors=None):
+    """apply_rope_cfg (phi4.rs:238-256) on a copy of x (n_heads x head_dim)."""
+    x = np.array(x, dtype=np.float32, copy=True).ravel()
+    f = np.ascontiguousarray(factors if factors is not None else np.ones(1, np.float32), dtype=np.float32)
+    nf = 0 if factors is None else f.size
+    lib().rrr_o_rope(_p(x, _f32p), pos, n_heads, head_dim, rope_dim, theta, attn_factor, _p(f, _f32p), nf)
+    return x
+
+
+def rope_kv_store(qkv, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim, rope_dim=ROPE_DIM, factors=None,
+                  theta=ROPE_THETA, attn_factor=ROPE_ATTN_FACTOR):
+    """The rope_kv_store pipeline: returns (qkv after RoPE, k_cache, v_cache)
+    with row pos of the (uint16) caches written; the inputs are not changed."""
+    qkv = np.array(qkv, dtype=np.float32, copy=True).ravel()
+    kc = np.array(k_cache, dtype=np.uint16, copy=True).ravel()
+    vc = np.array(v_cache, dtype=np.uint16, copy=True).ravel()
+    f = np.ascontiguousarray(factors if factors is not None else np.ones(1, np.float32), dtype=np.float32)
+    nf = 0 if factors is None else f.size
+    q_dim, kv_stride = n_heads * head_dim, n_kv_heads * head_dim
+    assert qkv.size >= q_dim + 2 * kv_stride and kc.size >= (pos + 1) * kv_stride and vc.size == kc.size
+    lib().rrr_o_rope_kv_store(_p(qkv, _f32p), _p(f, _f32p), nf, _p(kc, _u16p), _p(vc, _u16p), pos, n_heads,
+                              n_kv_heads, head_dim, rope_dim, q_dim, kv_stride, theta, attn_factor)
+    return qkv, kc, vc
+
+
+def attention_f64(q, k_cache, v_cache, seq_len, n_kv_heads, heads_per_kv, head_dim):
+    """Decode attention over cache rows [0, seq_len) in double."""
+    q = np.ascontiguousarray(q, dtype=np.float32).ravel()
+    kc = np.ascontiguousarray(k_cache, dtype=np.uint16).ravel()
+    vc = np.ascontiguousarray(v_cache, dtype=np.uint16).ravel()
+    assert q.size >= n_kv_heads * heads_per_kv * head_dim and kc.size >= seq_len * n_kv_heads * head_dim
+    out = np.empty(n_kv_heads * heads_per_kv * head_dim, dtype=np.float64)
+    lib().rrr_o_attention_f64(_p(q, _f32p), _p(kc, _u16p), _p(vc, _u16p), _p(out, _f64p), seq_len, n_kv_heads,
+                              heads_per_kv, head_dim)
+    return out

@@ -487,3 +487,123 @@ int rrr_o_logits_f64(const float *x, const float *E, double *y, uint32_t K, uint
 {
     return logits_common(x, E, NULL, y, K, V, layout, chunk, threads);
 }
+
+/* ---- decode glue: RoPE, the f16 KV-cache store, decode attention ---- */
+
+/* IEEE binary32 -> binary16, round to nearest, ties to even; overflow gives
+ * +-inf, NaNs stay NaN (quiet).  The reference keeps K and V in f16 caches
+ * (kv_size = MAX_SEQ * kv_stride * 2 bytes, phi4.rs:898) written by its
+ * kv_store / rope_kv_store shaders (dispatched at :1016-1017 and :1676; the
+ * SPIR-V is not in the tree), whose conversion is the default round-to-
+ * nearest-even of a float -> half conversion. */
+uint16_t rrr_o_f32_to_f16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, e = (x >> 23) & 0xFFu;
+    uint32_t m = x & 0x7FFFFFu;
+    if (e == 0xFFu) return (uint16_t)(sign | 0x7C00u | (m ? 0x200u | (m >> 13) : 0u));
+    const int32_t E = (int32_t)e - 127 + 15;
+    if (E >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (E <= 0) {
+        if (E < -10) return (uint16_t)sign;
+        m |= 0x800000u;                            /* 24-bit significand */
+        const uint32_t shift = (uint32_t)(14 - E); /* value / 2^-24 = m >> shift */
+        const uint32_t half = 1u << (shift - 1), rest = m & ((1u << shift) - 1u);
+        uint32_t r = m >> shift;
+        if (rest > half || (rest == half && (r & 1u))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((uint32_t)E << 10) | (m >> 13);
+    const uint32_t rest = m & 0x1FFFu;
+    if (rest > 0x1000u || (rest == 0x1000u && (r & 1u))) r++;  /* a carry may reach the exponent / inf */
+    return (uint16_t)(sign | r);
+}
+
+void rrr_o_f32_to_f16_n(const float *x, uint16_t *out, size_t n)
+{
+    for (size_t i = 0; i < n; i++) out[i] = rrr_o_f32_to_f16(x[i]);
+}
+
+/* phi4.rs:238-256 (apply_rope_cfg), step for step in f32: pairs (2i, 2i+1)
+ * of the first rope_dim dims of each head, base_freq = 1 / theta^(2i /
+ * rope_dim) (powf), divided by the LongRoPE factor (1 past the factor list),
+ * angle = pos * freq, sin/cos scaled by the attention factor.  Rust's f32
+ * powf / sin_cos call the platform libm powf / sinf / cosf, as this does. */
+void rrr_o_rope(float *x, uint32_t pos, uint32_t n_heads, uint32_t head_dim, uint32_t rope_dim, float theta,
+                float attn_factor, const float *factors, uint32_t n_factors)
+{
+    for (uint32_t h = 0; h < n_heads; h++) {
+        const size_t base = (size_t)h * head_dim;
+        for (uint32_t i = 0; i < rope_dim / 2; i++) {
+            const float base_freq = 1.0f / powf(theta, 2.0f * (float)i / (float)rope_dim);
+            const float factor = i < n_factors ? factors[i] : 1.0f;
+            const float freq = base_freq / factor;
+            const float angle = (float)pos * freq;
+            const float sin_t = sinf(angle), cos_t = cosf(angle);
+            const float cos_scaled = cos_t * attn_factor;
+            const float sin_scaled = sin_t * attn_factor;
+            const float x0 = x[base + 2 * i], x1 = x[base + 2 * i + 1];
+            x[base + 2 * i] = x0 * cos_scaled - x1 * sin_scaled;
+            x[base + 2 * i + 1] = x0 * sin_scaled + x1 * cos_scaled;
+        }
+    }
+}
+
+/* The rope_kv_store pipeline (phi4.rs:1016-1017; push [pos, n_heads,
+ * n_kv_heads, head_dim, rope_dim, q_dim, kv_stride], :1115-1117): RoPE on the
+ * Q heads (qkv[0, q_dim)) and the K heads (qkv[q_dim, q_dim + kv_stride)) in
+ * place, as the CPU path does before its store (:1656-1657), then K and V as
+ * f16 into row pos of the caches (row stride kv_stride).  rope_dim = 0 skips
+ * the rotation: the kv_store pipeline (:1666-1677). */
+void rrr_o_rope_kv_store(float *qkv, const float *factors, uint32_t n_factors, uint16_t *k_cache, uint16_t *v_cache,
+                         uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t rope_dim,
+                         uint32_t q_dim, uint32_t kv_stride, float theta, float attn_factor)
+{
+    if (rope_dim) {
+        rrr_o_rope(qkv, pos, n_heads, head_dim, rope_dim, theta, attn_factor, factors, n_factors);
+        rrr_o_rope(qkv + q_dim, pos, n_kv_heads, head_dim, rope_dim, theta, attn_factor, factors, n_factors);
+    }
+    for (uint32_t i = 0; i < kv_stride; i++) {
+        k_cache[(size_t)pos * kv_stride + i] = rrr_o_f32_to_f16(qkv[q_dim + i]);
+        v_cache[(size_t)pos * kv_stride + i] = rrr_o_f32_to_f16(qkv[q_dim + kv_stride + i]);
+    }
+}
+
+/* Decode attention of the attention pipeline (phi4.rs:1018, :1304-1312;
+ * push [seq_len, n_kv_heads, heads_per_kv, head_dim], one workgroup per
+ * query head; the shader is not in the tree).  The textbook definition, in
+ * double: query head h reads kv head g = h / heads_per_kv;
+ * s_t = (q_h . k_t) / sqrt(head_dim) over the f16 cache rows t < seq_len,
+ * p = softmax(s), out_h = sum_t p_t v_t. */
+void rrr_o_attention_f64(const float *q, const uint16_t *k_cache, const uint16_t *v_cache, double *out,
+                         uint32_t seq_len, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t head_dim)
+{
+    const size_t kv_stride = (size_t)n_kv_heads * head_dim;
+    const double scale = 1.0 / sqrt((double)head_dim);
+    double *s = (double *)malloc(sizeof(double) * (seq_len ? seq_len : 1));
+    for (uint32_t h = 0; h < n_kv_heads * heads_per_kv; h++) {
+        const size_t g = h / heads_per_kv;
+        double mx = -INFINITY;
+        for (uint32_t t = 0; t < seq_len; t++) {
+            double acc = 0.0;
+            for (uint32_t d = 0; d < head_dim; d++)
+                acc += (double)q[(size_t)h * head_dim + d] *
+                       (double)rrr_o_f16_to_f32(k_cache[t * kv_stride + g * head_dim + d]);
+            s[t] = acc * scale;
+            if (s[t] > mx) mx = s[t];
+        }
+        double den = 0.0;
+        for (uint32_t t = 0; t < seq_len; t++) {
+            s[t] = exp(s[t] - mx);
+            den += s[t];
+        }
+        for (uint32_t d = 0; d < head_dim; d++) {
+            double acc = 0.0;
+            for (uint32_t t = 0; t < seq_len; t++)
+                acc += s[t] * (double)rrr_o_f16_to_f32(v_cache[t * kv_stride + g * head_dim + d]);
+            out[(size_t)h * head_dim + d] = acc / den;
+        }
+    }
+    free(s);
+}

@@ -23,6 +23,16 @@
  *                         all-ones x gives row sums; fp64 evaluation bound
  *   rrr_o_logits_*        chunk layout round trip (phi4.rs:877-893) and
  *                         row-major == chunked on the same data
+ *   rrr_o_f32_to_f16      numpy's IEEE round-to-nearest-even binary16 cast on
+ *                         every binary16 value, every tie between neighbours,
+ *                         overflow / subnormal / NaN edges and 2^20 randoms
+ *   rrr_o_rope            pos 0 = exact scaling by the attention factor,
+ *                         dims past rope_dim untouched, pair norms scaled by
+ *                         the factor, rotations compose (pos a then b = a + b),
+ *                         and an fp64 complex-rotation evaluation
+ *   rrr_o_attention_f64   closed forms: one position gives V, equal keys give
+ *                         the mean of V, one dominant key gives its V; heads
+ *                         of one KV group with equal queries agree
  */
 #ifndef RRR_ORACLE_H
 #define RRR_ORACLE_H
@@ -101,6 +111,25 @@ void rrr_o_logits_chunk_build(const float *E, uint32_t K, uint32_t V,
 
 /* bf16 -> f32 widening (exact) used for the prefill activations. */
 float rrr_o_bf16_to_f32(uint16_t bits);
+
+/* ---- decode glue (the rows after the weight sweep) ---- */
+
+/* binary32 -> binary16, round to nearest even (the f16 KV caches, phi4.rs:898). */
+uint16_t rrr_o_f32_to_f16(float f);
+void rrr_o_f32_to_f16_n(const float *x, uint16_t *out, size_t n);
+
+/* phi4.rs:238-256 (apply_rope_cfg) in f32, in place over n_heads heads. */
+void rrr_o_rope(float *x, uint32_t pos, uint32_t n_heads, uint32_t head_dim, uint32_t rope_dim, float theta,
+                float attn_factor, const float *factors, uint32_t n_factors);
+
+/* The rope_kv_store / kv_store pipelines (phi4.rs:1016-1017, :1666-1677). */
+void rrr_o_rope_kv_store(float *qkv, const float *factors, uint32_t n_factors, uint16_t *k_cache, uint16_t *v_cache,
+                         uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t rope_dim,
+                         uint32_t q_dim, uint32_t kv_stride, float theta, float attn_factor);
+
+/* The attention pipeline (phi4.rs:1018, :1304-1312) in double. */
+void rrr_o_attention_f64(const float *q, const uint16_t *k_cache, const uint16_t *v_cache, double *out,
+                         uint32_t seq_len, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t head_dim);
 
 #ifdef __cplusplus
 }

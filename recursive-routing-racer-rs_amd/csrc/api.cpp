@@ -14,9 +14,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_set>
-#include <algorithm>
 #include <vector>
-#include <algorithm>
 
 #include "internal.h"
 
@@ -83,7 +81,7 @@ struct rrr_ctx {
     bool timer_started;
     hipStream_t stream;
     hipEvent_t ev0, ev1;
-    void *scratch;  // argmax partial candidates
+    void *scratch;  // argmax partial candidates / attention split partials
     std::unordered_set<rrr_buf *> bufs;
     std::unordered_set<rrr_graph *> graphs;
     std::unordered_set<rrr_sweep *> sweeps;
@@ -203,7 +201,8 @@ int rrr_init(int device, rrr_ctx **out)
         if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
         if (e == hipSuccess) e = hipEventCreate(&ctx->ev0);
         if (e == hipSuccess) e = hipEventCreate(&ctx->ev1);
-        if (e == hipSuccess) e = hipMalloc(&ctx->scratch, argmax_partials_bytes());
+        // argmax candidates and attention split partials (ops ordered on the stream share it)
+        if (e == hipSuccess) e = hipMalloc(&ctx->scratch, std::max(argmax_partials_bytes(), attention_partials_bytes()));
         if (e != hipSuccess) {
             if (ctx->scratch) (void)hipFree(ctx->scratch);
             if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
@@ -651,6 +650,71 @@ int rrr_argmax_f32(rrr_ctx *ctx, const rrr_buf *logits, uint32_t V, rrr_buf *out
                   what);
 }
 
+// ---- decode glue: RoPE + f16 KV store, decode attention --------------------
+
+int rrr_rope_kv_store(rrr_ctx *ctx, rrr_buf *qkv, const rrr_buf *rope_factors, uint32_t n_factors, rrr_buf *k_cache,
+                      rrr_buf *v_cache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                      uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride, float theta, float attn_factor)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_rope_kv_store";
+    TRY(check_buf(ctx, qkv, what));
+    TRY(check_buf(ctx, k_cache, what));
+    TRY(check_buf(ctx, v_cache, what));
+    if (n_factors) TRY(check_buf(ctx, rope_factors, what));
+    if (kv_stride == 0 || kv_stride % 2) return fail(RRR_ERR_BAD_SHAPE, "%s: kv_stride=%u must be even and positive", what, kv_stride);
+    if (rope_dim) {
+        if (head_dim == 0 || head_dim % 2 || rope_dim % 2 || rope_dim > head_dim)
+            return fail(RRR_ERR_BAD_SHAPE, "%s: need even head_dim >= even rope_dim (head_dim=%u rope_dim=%u)", what,
+                        head_dim, rope_dim);
+        if ((uint64_t)n_heads * head_dim > q_dim)
+            return fail(RRR_ERR_BAD_SHAPE, "%s: %u Q heads of %u do not fit q_dim=%u", what, n_heads, head_dim, q_dim);
+        if ((uint64_t)n_kv_heads * head_dim != kv_stride)
+            return fail(RRR_ERR_BAD_SHAPE, "%s: kv_stride=%u is not n_kv_heads * head_dim", what, kv_stride);
+        if (!(theta > 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: theta must be positive", what);
+    }
+    TRY(need(qkv, 4 * ((uint64_t)q_dim + 2ull * kv_stride), what));
+    TRY(need(k_cache, 2 * ((uint64_t)pos + 1) * kv_stride, what));
+    TRY(need(v_cache, 2 * ((uint64_t)pos + 1) * kv_stride, what));
+    if (n_factors) TRY(need(rope_factors, 4ull * n_factors, what));
+    if (((uintptr_t)qkv->ptr | (uintptr_t)k_cache->ptr | (uintptr_t)v_cache->ptr) & 3)
+        return fail(RRR_ERR_INVALID_ARG, "%s: buffers must be 4-byte aligned", what);
+    TRY(device_ready(ctx));
+    RopeArgs r{n_factors ? (const float *)rope_factors->ptr : nullptr, n_factors, pos, rope_dim ? n_heads : 0u,
+               head_dim, rope_dim, q_dim, kv_stride, theta, attn_factor};
+    return finish(ctx, launch_rope_kv_store((float *)qkv->ptr, r, (uint16_t *)k_cache->ptr, (uint16_t *)v_cache->ptr,
+                                            ctx->stream),
+                  what);
+}
+
+int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const rrr_buf *v_cache, rrr_buf *out,
+                  uint32_t seq_len, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t head_dim)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_attention";
+    TRY(check_buf(ctx, q, what));
+    TRY(check_buf(ctx, k_cache, what));
+    TRY(check_buf(ctx, v_cache, what));
+    TRY(check_buf(ctx, out, what));
+    if (head_dim != ATT_HD) return fail(RRR_ERR_UNSUPPORTED, "%s: head_dim=%u (the kernels take %u)", what, head_dim, ATT_HD);
+    if (seq_len == 0 || n_kv_heads == 0 || heads_per_kv == 0)
+        return fail(RRR_ERR_BAD_SHAPE, "%s: seq_len, n_kv_heads and heads_per_kv must be positive", what);
+    if (heads_per_kv > 8 || (uint64_t)n_kv_heads * heads_per_kv > ATT_HEADS_MAX)
+        return fail(RRR_ERR_UNSUPPORTED, "%s: at most 8 query heads per KV head and %u query heads", what, ATT_HEADS_MAX);
+    const uint64_t nq = (uint64_t)n_kv_heads * heads_per_kv * head_dim, kv = (uint64_t)seq_len * n_kv_heads * head_dim;
+    TRY(need_f32(q, nq, what));
+    TRY(need_f32(out, nq, what));
+    TRY(need(k_cache, 2 * kv, what));
+    TRY(need(v_cache, 2 * kv, what));
+    if (((uintptr_t)k_cache->ptr | (uintptr_t)v_cache->ptr) & 15)
+        return fail(RRR_ERR_INVALID_ARG, "%s: caches must be 16-byte aligned", what);
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_attention((const float *)q->ptr, (const uint16_t *)k_cache->ptr,
+                                        (const uint16_t *)v_cache->ptr, (float *)out->ptr, ctx->scratch, seq_len,
+                                        n_kv_heads, heads_per_kv, sweep_cus(), ctx->stream),
+                  what);
+}
+
 // ---- name-keyed dispatch shim ----------------------------------------------
 
 static int push_u32(const void *push, uint32_t push_bytes, uint32_t n, uint32_t *out, const char *name)
@@ -733,8 +797,37 @@ static int dispatch_one(rrr_ctx *ctx, const char *name, rrr_buf *const *bufs, ui
         TRY(want_grid(groups, (pc[0] + 255) / 256, 1, 1, name));
         return rrr_residual_add(ctx, bufs[0], bufs[1], bufs[2], pc[0]);
     }
-    static const char *out_of_scope[] = {"rope", "rope_kv_store", "kv_store", "attention", "fused_norm_matmul_q4k",
-                                         "fused_norm_matmul_q5k", "fused_norm_matmul_q6k"};
+    if (!strcmp(name, "rope_kv_store")) {
+        // bufs [qkv, rope_factors, k_cache, v_cache], push [pos, n_heads, n_kv_heads, head_dim, rope_dim, q_dim,
+        // kv_stride] (phi4.rs:1016-1017, :1115-1117); theta and the attention factor are baked in, as in the
+        // reference's shader (the legacy constants, phi4.rs:114-116)
+        uint32_t p7[7];
+        TRY(want_bufs(n_bufs, 4, bufs, name));
+        TRY(push_u32(push, push_bytes, 7, p7, name));
+        const uint32_t rp = (p7[1] + p7[2]) * (p7[4] / 2), hkv = p7[6] / 2;
+        TRY(want_grid(groups, (std::max(rp, hkv) + 63) / 64, 1, 1, name));
+        const uint32_t nf = bufs[1] ? (uint32_t)std::min<uint64_t>(bufs[1]->bytes / 4, p7[4] / 2) : 0u;
+        return rrr_rope_kv_store(ctx, bufs[0], bufs[1], nf, bufs[2], bufs[3], p7[0], p7[1], p7[2], p7[3], p7[4], p7[5],
+                                 p7[6], 10000.0f, 1.190238f);
+    }
+    if (!strcmp(name, "kv_store")) {
+        // bufs [qkv, k_cache, v_cache], push [pos, q_dim, kv_stride] (phi4.rs:1670-1677)
+        TRY(want_bufs(n_bufs, 3, bufs, name));
+        TRY(push_u32(push, push_bytes, 3, pc, name));
+        TRY(want_grid(groups, (pc[2] / 2 + 255) / 256, 1, 1, name));
+        return rrr_rope_kv_store(ctx, bufs[0], nullptr, 0, bufs[1], bufs[2], pc[0], 0, 0, 0, 0, pc[1], pc[2], 0.0f, 0.0f);
+    }
+    if (!strcmp(name, "attention")) {
+        // bufs [q, k_cache, v_cache, out], push [seq_len, n_kv_heads, heads_per_kv, head_dim], grid [n_heads, 1, 1]
+        // (phi4.rs:1018, :1304-1312)
+        uint32_t p4[4];
+        TRY(want_bufs(n_bufs, 4, bufs, name));
+        TRY(push_u32(push, push_bytes, 4, p4, name));
+        TRY(want_grid(groups, p4[1] * p4[2], 1, 1, name));
+        return rrr_attention(ctx, bufs[0], bufs[1], bufs[2], bufs[3], p4[0], p4[1], p4[2], p4[3]);
+    }
+    static const char *out_of_scope[] = {"rope", "fused_norm_matmul_q4k", "fused_norm_matmul_q5k",
+                                         "fused_norm_matmul_q6k"};
     for (const char *o : out_of_scope)
         if (!strcmp(name, o))
             return fail(RRR_ERR_UNSUPPORTED, "rrr_dispatch: pipeline '%s' is outside the weight-heavy decode path", name);

@@ -70,6 +70,21 @@ hipError_t launch_logits_chunked(const float *x, const float *gamma, float eps, 
 // Argmax: `partials` holds at least argmax_partials_bytes() bytes.
 uint64_t argmax_partials_bytes();
 hipError_t launch_argmax(const float *v, uint32_t n, void *partials, uint32_t *out, hipStream_t s);
+// RoPE + f16 KV store (attn.hip): the rope_kv_store / kv_store pipelines.
+struct RopeArgs {
+    const float *factors;   // LongRoPE divisors of the first n_factors pairs
+    uint32_t n_factors;
+    uint32_t pos, n_heads, head_dim, rope_dim, q_dim, kv_stride;
+    float theta, attn_factor;
+};
+hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uint16_t *vc, hipStream_t s);
+// Decode attention (attn.hip): head_dim ATT_HD, up to ATT_HEADS_MAX query
+// heads, `partials` of attention_partials_bytes().
+constexpr uint32_t ATT_HD = 128, ATT_HEADS_MAX = 64, ATT_SPLITS_MAX = 64;
+uint64_t attention_partials_bytes();
+void attention_plan(uint32_t seq, uint32_t n_kv_heads, uint32_t cus, uint32_t &splits, uint32_t &per);
+hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out, void *partials,
+                            uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t cus, hipStream_t s);
 hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint64_t w_bytes, uint32_t type,
                             float *Y, uint32_t K, uint32_t N, uint32_t M, hipStream_t s);
 

@@ -77,6 +77,9 @@ SIGNATURES = {
     "rrr_gemv_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, u32, c_buf_p, u32, u32]),
     "rrr_gemv_residual": (i32, [c_ctx_p, c_buf_p, u32, u32, c_buf_p, u32, c_buf_p, u32, u32]),
     "rrr_logits_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, c_buf_p, u32, u32, u32, u32]),
+    "rrr_rope_kv_store": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, c_buf_p, c_buf_p, u32, u32, u32, u32, u32, u32, u32,
+                                f32, f32]),
+    "rrr_attention": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, c_buf_p, u32, u32, u32, u32]),
     "rrr_dispatch": (i32, [c_ctx_p, ctypes.c_char_p, ctypes.POINTER(c_buf_p), u32, vp, u32,
                            ctypes.POINTER(u32)]),
     "rrr_dispatch_batch": (i32, [c_ctx_p, ctypes.POINTER(DispatchDesc), u32]),

@@ -226,6 +226,16 @@ class Context:
     def logits_rmsnorm(self, x, gamma, eps, E, y, K, V, layout=LOGITS_ROWS, chunk=8192):
         _check(self.lib.rrr_logits_rmsnorm(self._h, x._h, gamma._h, eps, E._h, y._h, K, V, layout, chunk))
 
+    def rope_kv_store(self, qkv, rope_factors, n_factors, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim,
+                      rope_dim, q_dim, kv_stride, theta=10000.0, attn_factor=1.190238):
+        _check(self.lib.rrr_rope_kv_store(self._h, qkv._h, rope_factors._h if rope_factors is not None else None,
+                                          n_factors, k_cache._h, v_cache._h, pos, n_heads, n_kv_heads, head_dim,
+                                          rope_dim, q_dim, kv_stride, theta, attn_factor))
+
+    def attention(self, q, k_cache, v_cache, out, seq_len, n_kv_heads, heads_per_kv, head_dim):
+        _check(self.lib.rrr_attention(self._h, q._h, k_cache._h, v_cache._h, out._h, seq_len, n_kv_heads,
+                                      heads_per_kv, head_dim))
+
     def dispatch(self, name, bufs, push_u32, groups):
         arr = (ctypes.c_void_p * max(len(bufs), 1))(*[b.handle for b in bufs])
         pb = struct.pack("<%dI" % len(push_u32), *push_u32)

@@ -213,7 +213,10 @@ def test_dispatch_shim_validation(vctx):
     assert code_of(vctx.dispatch, "matmul_q5k", [x, W, y], [K, N], [N + 1, 1, 1]) == ERR_INVALID_ARG
     assert code_of(vctx.dispatch, "matmul_q5k", [x, W], [K, N], [N, 1, 1]) == ERR_INVALID_ARG
     assert code_of(vctx.dispatch, "matmul_q5k", [x, W, y], [K], [N, 1, 1]) == ERR_INVALID_ARG
-    assert code_of(vctx.dispatch, "attention", [x, W, y, x], [1, 8, 3, 128], [24, 1, 1]) == ERR_UNSUPPORTED
+    assert code_of(vctx.dispatch, "attention", [x, W, y, x], [1, 8, 3, 128], [24, 1, 1]) == ERR_SHORT_BUFFER
+    assert code_of(vctx.dispatch, "attention", [x, W, W, x], [1, 8, 3, 128], [24, 1, 1]) == ERR_NO_DEVICE
+    assert code_of(vctx.dispatch, "attention", [x, W, W, x], [1, 8, 3, 128], [8, 1, 1]) == ERR_INVALID_ARG
+    assert code_of(vctx.dispatch, "rope", [x, x], [0] * 5, [1, 1, 1]) == ERR_UNSUPPORTED
     assert code_of(vctx.dispatch, "no_such_shader", [x], [1], [1, 1, 1]) == ERR_UNSUPPORTED
     assert code_of(vctx.dispatch, "rmsnorm", [x, x, x], [1, K], [1, 1, 1]) == ERR_NO_DEVICE
     # batch: failing entry is named
@@ -221,6 +224,31 @@ def test_dispatch_shim_validation(vctx):
         vctx.dispatch_batch([("matmul_q5k", [x, W, y], [K, N], [N, 1, 1], True),
                              ("rope", [x, x], [0] * 5, [1, 1, 1], True)])
     assert "entry 0" in ei.value.msg or ei.value.code == ERR_NO_DEVICE
+
+
+def test_rope_kv_store_and_attention_validation(vctx):
+    nh, nkv, hd, rd = 24, 8, 128, 96
+    qd, kvs = nh * hd, nkv * hd
+    qkv = vctx.alloc((qd + 2 * kvs) * 4)
+    fac = vctx.alloc(48 * 4)
+    kc, vc = vctx.alloc(16 * kvs * 2), vctx.alloc(16 * kvs * 2)
+    rk = vctx.rope_kv_store
+    assert code_of(rk, qkv, fac, 48, kc, vc, 15, nh, nkv, hd, rd, qd, kvs) == ERR_NO_DEVICE
+    assert code_of(rk, qkv, fac, 48, kc, vc, 16, nh, nkv, hd, rd, qd, kvs) == ERR_SHORT_BUFFER   # row 16 of 16
+    assert code_of(rk, qkv, fac, 49, kc, vc, 0, nh, nkv, hd, rd, qd, kvs) == ERR_SHORT_BUFFER    # factors
+    assert code_of(rk, qkv, fac, 48, kc, vc, 0, nh, nkv, hd, 130, qd, kvs) == ERR_BAD_SHAPE      # rope_dim > hd
+    assert code_of(rk, qkv, fac, 48, kc, vc, 0, nh, nkv, hd, 95, qd, kvs) == ERR_BAD_SHAPE       # odd rope_dim
+    assert code_of(rk, qkv, fac, 48, kc, vc, 0, nh, nkv, hd, rd, qd, kvs + 2) == ERR_BAD_SHAPE   # kv_stride
+    assert code_of(rk, qkv, fac, 48, kc, vc, 0, nh + 1, nkv, hd, rd, qd, kvs) == ERR_BAD_SHAPE   # q heads
+    assert code_of(rk, qkv, None, 0, kc, vc, 0, 0, 0, 0, 0, qd, kvs) == ERR_NO_DEVICE           # kv_store form
+    at = vctx.attention
+    q, out = vctx.alloc(qd * 4), vctx.alloc(qd * 4)
+    assert code_of(at, q, kc, vc, out, 16, nkv, 3, hd) == ERR_NO_DEVICE
+    assert code_of(at, q, kc, vc, out, 17, nkv, 3, hd) == ERR_SHORT_BUFFER
+    assert code_of(at, q, kc, vc, out, 0, nkv, 3, hd) == ERR_BAD_SHAPE
+    assert code_of(at, q, kc, vc, out, 4, nkv, 3, 64) == ERR_UNSUPPORTED
+    assert code_of(at, q, kc, vc, out, 4, 8, 9, hd) == ERR_UNSUPPORTED
+    assert code_of(at, q, kc, vc, out, 4, 16, 4, hd) in (ERR_UNSUPPORTED, ERR_SHORT_BUFFER)
 
 
 def test_graph_state_rules(vctx):

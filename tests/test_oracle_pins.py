@@ -230,3 +230,130 @@ def test_seeded_fixture_regression():
     assert np.array_equal(orc.rms_norm(z["norm_x"], z["norm_g"]), z["norm_y"])
     assert np.array_equal(orc.silu_gate(z["silu_gu"], 512), z["silu_mid"])
     assert np.array_equal(orc.logits(z["lg_x"], z["lg_E"], 256, 120), z["lg_y"])
+
+
+# ---- decode glue: f16 store, RoPE, attention ------------------------------------
+
+def test_f32_to_f16_matches_ieee_rne():
+    # every binary16 value (as f32), every midpoint between neighbours (ties to
+    # even), the overflow / subnormal edges, NaN and 2^20 random floats
+    h = np.arange(0x10000, dtype=np.uint32).astype(np.uint16)
+    f = h.view(np.float16).astype(np.float32)
+    finite = np.isfinite(f)
+    got = orc.f32_to_f16_bits(f[finite])
+    assert np.array_equal(got, f[finite].astype(np.float16).view(np.uint16))
+    pos = np.arange(0x7BFF, dtype=np.uint32).astype(np.uint16)
+    lo = pos.view(np.float16).astype(np.float64)
+    hi = (pos + 1).view(np.float16).astype(np.float64)
+    mid = ((lo + hi) / 2).astype(np.float32)               # exact in f32
+    assert np.array_equal(orc.f32_to_f16_bits(mid), mid.astype(np.float16).view(np.uint16))
+    assert np.array_equal(orc.f32_to_f16_bits(-mid), (-mid).astype(np.float16).view(np.uint16))
+    rng = np.random.default_rng(5)
+    r = (rng.standard_normal(1 << 20) * np.exp2(rng.uniform(-30, 20, 1 << 20))).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = r.astype(np.float16).view(np.uint16)
+    assert np.array_equal(orc.f32_to_f16_bits(r), want)
+    edge = np.array([65504.0, 65519.99, 65520.0, 1e9, 2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0001, 2.0 ** -26,
+                     6.1e-5, np.inf, -np.inf, 0.0, -0.0], np.float32)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(orc.f32_to_f16_bits(edge), edge.astype(np.float16).view(np.uint16))
+    nan = orc.f32_to_f16_bits(np.array([np.nan], np.float32))[0]
+    assert (nan & 0x7C00) == 0x7C00 and (nan & 0x3FF) != 0
+
+
+def _rope_f64(x, pos, n_heads, hd, rd, theta, attn, factors):
+    """apply_rope_cfg's rotation as a complex product in double."""
+    y = np.array(x, np.float64).reshape(n_heads, hd)
+    i = np.arange(rd // 2)
+    f = np.ones(rd // 2) if factors is None else np.concatenate([factors, np.ones(max(0, rd // 2 - len(factors)))])[:rd // 2]
+    ang = pos * (theta ** (-2.0 * i / rd)) / f
+    z = (y[:, 0:rd:2] + 1j * y[:, 1:rd:2]) * np.exp(1j * ang) * attn
+    y[:, 0:rd:2], y[:, 1:rd:2] = z.real, z.imag
+    return y.ravel()
+
+
+def test_rope_pins():
+    rng = np.random.default_rng(11)
+    nh, hd, rd = 3, 128, 96
+    x = rng.standard_normal(nh * hd).astype(np.float32)
+    fac = (1.0 + rng.uniform(0, 3, rd // 2)).astype(np.float32)
+    # pos 0: cos 0 = 1 and sin 0 = 0 exactly, so the rotated dims are scaled
+    # by the attention factor (one f32 product each) and the rest untouched
+    y0 = orc.rope(x, 0, nh, hd, rd, factors=fac).reshape(nh, hd)
+    xs = x.reshape(nh, hd)
+    a = np.float32(orc.ROPE_ATTN_FACTOR)
+    assert np.array_equal(y0[:, :rd], xs[:, :rd] * a)
+    assert np.array_equal(y0[:, rd:], xs[:, rd:])
+    for pos in (1, 7, 300, 2047):
+        y = orc.rope(x, pos, nh, hd, rd, factors=fac)
+        ref = _rope_f64(x, pos, nh, hd, rd, orc.ROPE_THETA, orc.ROPE_ATTN_FACTOR, fac)
+        # f32 angle = pos * freq carries a relative error ~2^-24: |angle| <= 2047
+        assert np.max(np.abs(y - ref)) < 2e-4 * np.max(np.abs(ref))
+        yy = y.reshape(nh, hd)
+        # each pair's norm is scaled by the attention factor
+        n0 = np.hypot(xs[:, 0:rd:2].astype(np.float64), xs[:, 1:rd:2])
+        n1 = np.hypot(yy[:, 0:rd:2].astype(np.float64), yy[:, 1:rd:2])
+        assert np.allclose(n1, n0 * orc.ROPE_ATTN_FACTOR, rtol=1e-5, atol=1e-6)
+        assert np.array_equal(yy[:, rd:], xs[:, rd:])
+    # rotations compose: pos a then pos b equals pos a + b (with attn^2)
+    ab = orc.rope(orc.rope(x, 5, nh, hd, rd, attn_factor=1.0), 9, nh, hd, rd, attn_factor=1.0)
+    c = orc.rope(x, 14, nh, hd, rd, attn_factor=1.0)
+    assert np.max(np.abs(ab - c)) < 1e-5 * np.max(np.abs(c))
+    # factors past the list are 1 (no factors at all = plain RoPE)
+    p1 = orc.rope(x, 33, nh, hd, rd, factors=np.ones(1, np.float32))
+    p0 = orc.rope(x, 33, nh, hd, rd)
+    assert np.array_equal(p1, p0)
+
+
+def test_rope_kv_store_layout():
+    rng = np.random.default_rng(12)
+    nh, nkv, hd, rd = 6, 2, 128, 96
+    qd, kvs = nh * hd, nkv * hd
+    qkv = rng.standard_normal(qd + 2 * kvs).astype(np.float32)
+    kc = np.zeros(4 * kvs, np.uint16)
+    vc = np.zeros(4 * kvs, np.uint16)
+    out, k2, v2 = orc.rope_kv_store(qkv, kc, vc, 2, nh, nkv, hd, rd)
+    assert np.array_equal(out[:qd], orc.rope(qkv[:qd], 2, nh, hd, rd))
+    assert np.array_equal(out[qd:qd + kvs], orc.rope(qkv[qd:qd + kvs], 2, nkv, hd, rd))
+    assert np.array_equal(out[qd + kvs:], qkv[qd + kvs:])                     # V is not rotated
+    assert np.array_equal(k2[2 * kvs:3 * kvs], orc.f32_to_f16_bits(out[qd:qd + kvs]))
+    assert np.array_equal(v2[2 * kvs:3 * kvs], orc.f32_to_f16_bits(qkv[qd + kvs:]))
+    assert not k2[:2 * kvs].any() and not k2[3 * kvs:].any() and not v2[3 * kvs:].any()
+    # rope_dim = 0 (kv_store): no rotation
+    out0, k0, _ = orc.rope_kv_store(qkv, kc, vc, 1, nh, nkv, hd, 0)
+    assert np.array_equal(out0, qkv)
+    assert np.array_equal(k0[kvs:2 * kvs], orc.f32_to_f16_bits(qkv[qd:qd + kvs]))
+
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(13)
+    nkv, hpk, hd = 2, 3, 128
+    nh, kvs = nkv * hpk, nkv * hd
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    S = 9
+    kc = orc.f32_to_f16_bits(rng.standard_normal(S * kvs).astype(np.float32))
+    vc = orc.f32_to_f16_bits(rng.standard_normal(S * kvs).astype(np.float32))
+    vf = vc.view(np.float16).astype(np.float64).reshape(S, nkv, hd)   # exact widening (pinned above)
+    # one position: the softmax is 1, the output is that V row
+    o1 = orc.attention_f64(q, kc, vc, 1, nkv, hpk, hd).reshape(nh, hd)
+    for h in range(nh):
+        assert np.array_equal(o1[h], vf[0, h // hpk])
+    # equal keys: uniform weights, the mean of V
+    keq = np.tile(kc[:kvs], S)
+    om = orc.attention_f64(q, keq, vc, S, nkv, hpk, hd).reshape(nh, hd)
+    for h in range(nh):
+        assert np.allclose(om[h], vf[:, h // hpk].mean(axis=0), rtol=0, atol=1e-12)
+    # one dominant key: its V
+    kd = np.zeros(S * kvs, np.uint16)
+    qd = np.zeros(nh * hd, np.float32)
+    qd[:] = 1.0
+    big = orc.f32_to_f16_bits(np.full(hd, 30.0, np.float32))
+    for g in range(nkv):
+        kd[4 * kvs + g * hd:4 * kvs + (g + 1) * hd] = big
+    od = orc.attention_f64(qd, kd, vc, S, nkv, hpk, hd).reshape(nh, hd)
+    for h in range(nh):
+        assert np.allclose(od[h], vf[4, h // hpk], rtol=0, atol=1e-9)
+    # query heads of one KV group with the same query agree
+    qs = np.tile(q[:hd], nh)
+    os_ = orc.attention_f64(qs, kc, vc, S, nkv, hpk, hd).reshape(nh, hd)
+    assert np.array_equal(os_[0], os_[1]) and np.array_equal(os_[0], os_[2])
