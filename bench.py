@@ -225,7 +225,7 @@ def decode_sweep(ctx, tokens):
     shape = decode.Phi4Shape()
     log("[bench] decode sweep: generating and uploading 32 layers + logits matrix")
     t0 = time.perf_counter()
-    sw = decode.DecodeSweep(ctx, shape, seed=3)
+    sw = decode.DecodeSweep(ctx, shape, seed=3, attention=True)
     ctx.sync()
     log(f"[bench] decode sweep ready in {time.perf_counter() - t0:.1f} s")
     g = sw.graph()
@@ -257,8 +257,31 @@ def decode_sweep(ctx, tokens):
     same = bool(np.array_equal(logits_p.view(np.uint32), logits.view(np.uint32)))
     log(f"[bench] decode sweep (persistent layer sweep): {ms_p:.4f} ms/token ({b / (ms_p * 1e-3) / 1e9:.0f} GB/s), "
         f"argmax {tok_p}, logits identical to the per-op run: {same}")
+    # the full decode step at the last cache position: RoPE + f16 KV store and
+    # attention over 2048 rows per layer on top of the sweep
+    pos = shape.max_seq - 1
+    ga = sw.graph(pos)
+    ga.launch()
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(tokens):
+        ga.launch()
+    ms_a = ctx.timer_stop() / tokens
+    ga.destroy()
+    # attention alone at 2048 rows, rotating over the 32 layers' caches
+    n_att = 4 * shape.n_layers
+    kv_bytes = 2 * shape.max_seq * shape.kv_stride * 2
+    us_att = timed_graph(ctx, lambda i: ctx.attention(sw.qkv, *sw.kv[i % shape.n_layers], sw.attn_out, shape.max_seq,
+                                                       shape.n_kv_heads, shape.heads_per_kv, shape.head_dim),
+                         n_att) * 1e3 / n_att
+    log(f"[bench] decode step at position {pos} (RoPE + KV store + attention over {shape.max_seq} rows): "
+        f"{ms_a:.4f} ms/token; attention alone {us_att:.2f} us/layer ({kv_bytes / (us_att * 1e-6) / 1e9:.0f} GB/s)")
     best = min(ms, ms_p)
     return {"ms_per_token": round(best, 5), "tokens": tokens, "bytes_per_token": b,
+            "ms_per_token_at_pos_2047_with_attention": round(ms_a, 5),
+            "attention_2048_rows": {"us_per_layer": round(us_att, 3), "kv_bytes": kv_bytes,
+                                    "GBs": round(kv_bytes / (us_att * 1e-6) / 1e9, 1),
+                                    "frac_hbm": round(kv_bytes / (us_att * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
             "GBs": round(b / (best * 1e-3) / 1e9, 1), "frac_hbm": round(b / (best * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "ms_per_token_per_op_graph": round(ms, 5), "ms_per_token_persistent": round(ms_p, 5),
             "persistent_logits_identical": same,

@@ -196,7 +196,8 @@ int rrr_rope_kv_store(rrr_ctx *ctx, rrr_buf *qkv, const rrr_buf *rope_factors, u
  * g = h / heads_per_kv, out[h] = sum_t softmax_t(q_h . k_t / sqrt(head_dim))
  * v_t over cache rows t < seq_len (f16 K and V, f32 arithmetic).  q and out
  * are n_heads * head_dim f32 (16-byte aligned), the caches 16-byte aligned.
- * head_dim must be 128 and heads_per_kv at most 8. */
+ * head_dim must be 128, heads_per_kv at most 8 and seq_len at most 2048
+ * (the reference's MAX_SEQ, phi4.rs:181). */
 int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const rrr_buf *v_cache,
                   rrr_buf *out, uint32_t seq_len, uint32_t n_kv_heads, uint32_t heads_per_kv,
                   uint32_t head_dim);

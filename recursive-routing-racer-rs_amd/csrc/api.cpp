@@ -81,7 +81,8 @@ struct rrr_ctx {
     bool timer_started;
     hipStream_t stream;
     hipEvent_t ev0, ev1;
-    void *scratch;  // argmax partial candidates / attention split partials
+    void *scratch;      // argmax partial candidates
+    void *att_scratch;  // attention: per-KV-head counters (zero between calls) and split partials
     std::unordered_set<rrr_buf *> bufs;
     std::unordered_set<rrr_graph *> graphs;
     std::unordered_set<rrr_sweep *> sweeps;
@@ -190,7 +191,7 @@ int rrr_init(int device, rrr_ctx **out)
     ctx->async = ctx->capturing = ctx->timer_started = false;
     ctx->stream = nullptr;
     ctx->ev0 = ctx->ev1 = nullptr;
-    ctx->scratch = nullptr;
+    ctx->scratch = ctx->att_scratch = nullptr;
     if (!ctx->nodevice) {
         int n = rrr_device_count();
         if (device >= n) {
@@ -201,9 +202,12 @@ int rrr_init(int device, rrr_ctx **out)
         if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
         if (e == hipSuccess) e = hipEventCreate(&ctx->ev0);
         if (e == hipSuccess) e = hipEventCreate(&ctx->ev1);
-        // argmax candidates and attention split partials (ops ordered on the stream share it)
-        if (e == hipSuccess) e = hipMalloc(&ctx->scratch, std::max(argmax_partials_bytes(), attention_partials_bytes()));
+        if (e == hipSuccess) e = hipMalloc(&ctx->scratch, argmax_partials_bytes());
+        if (e == hipSuccess) e = hipMalloc(&ctx->att_scratch, attention_scratch_bytes());
+        if (e == hipSuccess) e = hipMemset(ctx->att_scratch, 0, attention_scratch_bytes());
+        if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) {
+            if (ctx->att_scratch) (void)hipFree(ctx->att_scratch);
             if (ctx->scratch) (void)hipFree(ctx->scratch);
             if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
             if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
@@ -246,6 +250,7 @@ int rrr_destroy(rrr_ctx *ctx)
         for (rrr_buf *b : ctx->bufs)
             if (!b->parent && b->ptr) (void)hipFree(b->ptr);
         (void)hipFree(ctx->scratch);
+        (void)hipFree(ctx->att_scratch);
         (void)hipEventDestroy(ctx->ev0);
         (void)hipEventDestroy(ctx->ev1);
         (void)hipStreamDestroy(ctx->stream);
@@ -699,6 +704,7 @@ int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const 
     if (head_dim != ATT_HD) return fail(RRR_ERR_UNSUPPORTED, "%s: head_dim=%u (the kernels take %u)", what, head_dim, ATT_HD);
     if (seq_len == 0 || n_kv_heads == 0 || heads_per_kv == 0)
         return fail(RRR_ERR_BAD_SHAPE, "%s: seq_len, n_kv_heads and heads_per_kv must be positive", what);
+    if (seq_len > ATT_SEQ_MAX) return fail(RRR_ERR_UNSUPPORTED, "%s: seq_len=%u exceeds %u", what, seq_len, ATT_SEQ_MAX);
     if (heads_per_kv > 8 || (uint64_t)n_kv_heads * heads_per_kv > ATT_HEADS_MAX)
         return fail(RRR_ERR_UNSUPPORTED, "%s: at most 8 query heads per KV head and %u query heads", what, ATT_HEADS_MAX);
     const uint64_t nq = (uint64_t)n_kv_heads * heads_per_kv * head_dim, kv = (uint64_t)seq_len * n_kv_heads * head_dim;
@@ -710,7 +716,7 @@ int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const 
         return fail(RRR_ERR_INVALID_ARG, "%s: caches must be 16-byte aligned", what);
     TRY(device_ready(ctx));
     return finish(ctx, launch_attention((const float *)q->ptr, (const uint16_t *)k_cache->ptr,
-                                        (const uint16_t *)v_cache->ptr, (float *)out->ptr, ctx->scratch, seq_len,
+                                        (const uint16_t *)v_cache->ptr, (float *)out->ptr, ctx->att_scratch, seq_len,
                                         n_kv_heads, heads_per_kv, sweep_cus(), ctx->stream),
                   what);
 }

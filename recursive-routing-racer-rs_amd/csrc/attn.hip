@@ -68,29 +68,63 @@ hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uin
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention, split over the sequence (flash-decoding).  Workgroup
-// (g, sp) takes KV head g and cache rows [sp * per, sp * per + per): its 16
-// lane groups of 16 lanes each take every 16th row, lane li owning dims
-// 8 li .. 8 li + 7 of the row (one 16-byte f16 load of K and one of V).  The
-// HPK query heads of the KV group share every K/V load.  Scores go through
-// exp2 with the queries pre-scaled by log2(e) / sqrt(head_dim); each lane
-// group keeps a running max, sum and output (online softmax), the 16 groups
-// are merged in LDS, and the workgroup writes {output, max, sum} per query
-// head; attn_merge_kernel combines the splits.  The row -> lane group and
-// split assignment depend on seq_len only, so results are reproducible.
-constexpr uint32_t ATT_PART = ATT_HD + 2;   // floats of one split's partial: output, max, sum
+// Decode attention, split over the sequence (flash-decoding), one launch.
+// Workgroup (g, sp) takes KV head g and cache rows [sp * per, sp * per + per),
+// at most 16 * ATT_ROWS_PER_GROUP of them: its 16 lane groups of 16 lanes each
+// take every 16th row (all of their K and V loads in flight at once), lane li
+// owning dims 8 li .. 8 li + 7 of a row (one 16-byte f16 load of K and one of
+// V; a score is one DPP row sum).  The HPK query heads of the KV group share
+// every K/V load.  Scores go through exp2 with the queries pre-scaled by
+// log2(e) / sqrt(head_dim); each lane group keeps a running max, sum and
+// output (online softmax).  The 16 lane groups are merged in LDS, and the
+// workgroup's {output, max, sum} per query head is written through
+// the coherent level; the last workgroup of KV head g to arrive (an
+// agent-scope counter) merges the splits and writes the output, then resets
+// the counter for the next call.  Every merge runs in a fixed order, so the
+// result depends on seq_len only.
+constexpr uint32_t ATT_PART = ATT_HD + 4;   // floats of one split's partial: output, max, sum (16-byte rows)
+constexpr uint32_t ATT_COUNTER_STRIDE = 64;  // u32 words between two KV heads' counters
+
+__device__ __forceinline__ float safe_scale(float m, float M) { return m == -__builtin_inff() ? 0.0f : exp2f(m - M); }
+
+// Sum over the 16 lanes of a DPP row (butterfly: xor 1, xor 2, then the
+// half-row and row mirrors); every lane of the row gets the sum.
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));  // row_mirror
+    return v;
+}
 
 template <int HPK>
-__global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ q, const uint16_t *__restrict__ kc,
-                                                         const uint16_t *__restrict__ vc, float *__restrict__ part,
-                                                         uint32_t seq, uint32_t per, uint32_t kv_stride, float qscale)
+__global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, const uint16_t *__restrict__ kc,
+                                                   const uint16_t *__restrict__ vc, float *part, uint32_t *counters,
+                                                   float *__restrict__ out, uint32_t seq, uint32_t per,
+                                                   uint32_t kv_stride, float qscale)
 {
-    __shared__ float sm[16][HPK][2];
-    __shared__ float so[16][HPK][ATT_HD];
+    __shared__ float gml[16][HPK][2];
+    __shared__ __attribute__((aligned(16))) float go[16][HPK][ATT_HD];
+    __shared__ float sw[HPK][ATT_SPLITS_MAX];      // split weights exp2(m_s - M), then the merged sums
+    __shared__ float sL[HPK];
+    __shared__ __attribute__((aligned(16))) float so[HPK][8][ATT_HD];   // sums over split subsets
+    __shared__ uint32_t last;
     const uint32_t g = blockIdx.x, sp = blockIdx.y, splits = gridDim.y;
     const uint32_t t = threadIdx.x, grp = t >> 4, li = t & 15;
     const uint32_t r0 = sp * per, r1 = min(seq, r0 + per);
 
+    // this lane group's rows r0 + grp + 16 k (k < ATT_ROWS_PER_GROUP), all
+    // requested first; a row past the split repeats the split's last row
+    // (already fetched by another lane group: no extra memory traffic)
+    u32x4 kr[ATT_ROWS_PER_GROUP], vr[ATT_ROWS_PER_GROUP];
+#pragma unroll
+    for (int k = 0; k < (int)ATT_ROWS_PER_GROUP; k++) {
+        const uint32_t row = min(r0 + grp + 16 * k, r1 - 1);
+        const size_t off = (size_t)row * kv_stride + (size_t)g * ATT_HD + 8 * li;
+        kr[k] = *(const u32x4 *)(kc + off);
+        vr[k] = *(const u32x4 *)(vc + off);
+    }
     float qv[HPK][8];
 #pragma unroll
     for (int h = 0; h < HPK; h++) {
@@ -107,122 +141,193 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
 #pragma unroll
         for (int d = 0; d < 8; d++) o[h][d] = 0.0f;
     }
-    for (uint32_t row = r0 + grp; row < r1; row += 16) {
-        const size_t off = (size_t)row * kv_stride + (size_t)g * ATT_HD + 8 * li;
-        const u32x4 kr = *(const u32x4 *)(kc + off);
-        const u32x4 vr = *(const u32x4 *)(vc + off);
-        float k[8], v[8];
+#pragma unroll
+    for (int k = 0; k < (int)ATT_ROWS_PER_GROUP; k++) {
+        // rows past the split leave the state as it is (uniform in the row of 16 lanes)
+        const bool live = r0 + grp + 16 * k < r1;
+        float kf[8], v[8];
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            k[2 * w] = h2f(kr[w] & 0xFFFFu);
-            k[2 * w + 1] = h2f(kr[w] >> 16);
-            v[2 * w] = h2f(vr[w] & 0xFFFFu);
-            v[2 * w + 1] = h2f(vr[w] >> 16);
+            kf[2 * w] = h2f(kr[k][w] & 0xFFFFu);
+            kf[2 * w + 1] = h2f(kr[k][w] >> 16);
+            v[2 * w] = h2f(vr[k][w] & 0xFFFFu);
+            v[2 * w + 1] = h2f(vr[k][w] >> 16);
         }
 #pragma unroll
         for (int h = 0; h < HPK; h++) {
             float s = 0.0f;
 #pragma unroll
-            for (int d = 0; d < 8; d++) s = fmaf(qv[h][d], k[d], s);
-            s += __shfl_xor(s, 1, 16);
-            s += __shfl_xor(s, 2, 16);
-            s += __shfl_xor(s, 4, 16);
-            s += __shfl_xor(s, 8, 16);
-            const float mn = fmaxf(m[h], s);
-            const float c = exp2f(m[h] - mn), p = exp2f(s - mn);
-            l[h] = fmaf(l[h], c, p);
+            for (int d = 0; d < 8; d++) s = fmaf(qv[h][d], kf[d], s);
+            s = row16_sum(s);
+            if (live) {
+                const float mn = fmaxf(m[h], s);
+                const float c = exp2f(m[h] - mn), p = exp2f(s - mn);
+                l[h] = fmaf(l[h], c, p);
 #pragma unroll
-            for (int d = 0; d < 8; d++) o[h][d] = fmaf(o[h][d], c, p * v[d]);
-            m[h] = mn;
+                for (int d = 0; d < 8; d++) o[h][d] = fmaf(o[h][d], c, p * v[d]);
+                m[h] = mn;
+            }
         }
     }
+    // the workgroup's 16 lane groups, in LDS
 #pragma unroll
     for (int h = 0; h < HPK; h++) {
         if (li == 0) {
-            sm[grp][h][0] = m[h];
-            sm[grp][h][1] = l[h];
+            gml[grp][h][0] = m[h];
+            gml[grp][h][1] = l[h];
         }
+        float4 *dst = (float4 *)&go[grp][h][8 * li];
+        dst[0] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+        dst[1] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+    }
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, (uint64_t)gridDim.x * HPK * splits * ATT_PART * 4);
+    for (uint32_t i = t; i < HPK * ATT_HD; i += 256) {
+        const uint32_t h = i / ATT_HD, d = i % ATT_HD;
+        float M = -__builtin_inff();
 #pragma unroll
-        for (int d = 0; d < 8; d++) so[grp][h][8 * li + d] = o[h][d];
+        for (int gi = 0; gi < 16; gi++) M = fmaxf(M, gml[gi][h][0]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < 16; gi++) {
+            const float c = safe_scale(gml[gi][h][0], M);   // 0 for a group without rows
+            L = fmaf(gml[gi][h][1], c, L);
+            O = fmaf(go[gi][h][d], c, O);
+        }
+        if (splits == 1) {
+            out[(size_t)(g * HPK + h) * ATT_HD + d] = O / L;
+        } else {
+            // partial of (g, sp, h): [output 128 | max | sum]
+            const uint32_t base = (((g * splits + sp) * HPK + h) * ATT_PART) * 4;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(O), rp, base + 4 * d, 0, RRR_CPOL_SC1);
+            if (d == 0) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M), rp, base + 4 * ATT_HD, 0, RRR_CPOL_SC1);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(L), rp, base + 4 * ATT_HD + 4, 0, RRR_CPOL_SC1);
+            }
+        }
+    }
+    if (splits == 1) return;
+    // publish: this workgroup's partials are at the coherent level, then count
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == 0)
+        last = __hip_atomic_fetch_add(counters + g * ATT_COUNTER_STRIDE, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    __syncthreads();
+    if (!last) return;
+    // the last workgroup of KV head g merges its splits.  Thread t takes dims
+    // 4 (t % 32) .. +3 of split subset ss = t / 32 (splits ss, ss + 8, ...):
+    // all of its output quads and the splits' maxima and sums are requested
+    // at once, then everything is added in a fixed order.
+    const uint32_t dq = t & 31, ss = t >> 5;
+    u32x4 ov[HPK][ATT_SPLITS_MAX / 8];
+#pragma unroll
+    for (int h = 0; h < HPK; h++)
+#pragma unroll
+        for (uint32_t j = 0; j < ATT_SPLITS_MAX / 8; j++) {
+            const uint32_t s = ss + 8 * j;
+            ov[h][j] = s < splits ? __builtin_amdgcn_raw_buffer_load_b128(
+                                        rp, (((g * splits + s) * HPK + h) * ATT_PART + 4 * dq) * 4, 0, RRR_CPOL_SC1)
+                                  : u32x4{0u, 0u, 0u, 0u};
+        }
+    float ms = -__builtin_inff(), ls = 0.0f;
+    const uint32_t sh = t / HPK, hh = t % HPK;   // (split, head) of the max / sum this thread reads
+    if (t < splits * HPK) {
+        const uint32_t base = (((g * splits + sh) * HPK + hh) * ATT_PART) * 4;
+        ms = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, base + 4 * ATT_HD, 0, RRR_CPOL_SC1));
+        ls = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, base + 4 * ATT_HD + 4, 0, RRR_CPOL_SC1));
+        sw[hh][sh] = ms;
+    }
+    __syncthreads();
+    if (t < HPK) {   // the head's max over its splits, then its weights and sum, in split order
+        float M = -__builtin_inff();
+        for (uint32_t s = 0; s < splits; s++) M = fmaxf(M, sw[t][s]);
+        sL[t] = M;
+    }
+    __syncthreads();
+    if (t < splits * HPK) sw[hh][sh] = exp2f(ms - sL[hh]);
+    __syncthreads();
+    if (t < splits * HPK) so[hh][0][sh] = ls * sw[hh][sh];   // staged for the ordered sum below
+    __syncthreads();
+    if (t < HPK) {
+        float L = 0.0f;
+        for (uint32_t s = 0; s < splits; s++) L += so[t][0][s];
+        sL[t] = L;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (uint32_t j = 0; j < ATT_SPLITS_MAX / 8; j++) {
+            const uint32_t s = ss + 8 * j;
+            if (s < splits) {
+                const float c = sw[h][s];
+                acc.x = fmaf(__uint_as_float(ov[h][j].x), c, acc.x);
+                acc.y = fmaf(__uint_as_float(ov[h][j].y), c, acc.y);
+                acc.z = fmaf(__uint_as_float(ov[h][j].z), c, acc.z);
+                acc.w = fmaf(__uint_as_float(ov[h][j].w), c, acc.w);
+            }
+        }
+        *(float4 *)&so[h][ss][4 * dq] = acc;
     }
     __syncthreads();
     for (uint32_t i = t; i < HPK * ATT_HD; i += 256) {
         const uint32_t h = i / ATT_HD, d = i % ATT_HD;
-        float M = -__builtin_inff();
-        for (int gi = 0; gi < 16; gi++) M = fmaxf(M, sm[gi][h][0]);
-        float L = 0.0f, O = 0.0f;
-        for (int gi = 0; gi < 16; gi++) {
-            const float c = exp2f(sm[gi][h][0] - M);   // 0 for a group without rows
-            L = fmaf(sm[gi][h][1], c, L);
-            O = fmaf(so[gi][h][d], c, O);
-        }
-        float *dst = part + ((size_t)(g * HPK + h) * splits + sp) * ATT_PART;
-        dst[d] = O;
-        if (d == 0) {
-            dst[ATT_HD] = M;
-            dst[ATT_HD + 1] = L;
-        }
+        float O = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) O += so[h][k][d];
+        out[(size_t)(g * HPK + h) * ATT_HD + d] = O / sL[h];
     }
+    if (t == 0) __hip_atomic_store(counters + g * ATT_COUNTER_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__global__ __launch_bounds__(ATT_HD) void attn_merge_kernel(const float *__restrict__ part, float *__restrict__ out,
-                                                            uint32_t splits)
-{
-    const uint32_t h = blockIdx.x, d = threadIdx.x;
-    const float *p = part + (size_t)h * splits * ATT_PART;
-    float M = -__builtin_inff();
-    for (uint32_t s = 0; s < splits; s++) M = fmaxf(M, p[s * ATT_PART + ATT_HD]);
-    float L = 0.0f, O = 0.0f;
-    for (uint32_t s = 0; s < splits; s++) {
-        const float c = exp2f(p[s * ATT_PART + ATT_HD] - M);
-        L = fmaf(p[s * ATT_PART + ATT_HD + 1], c, L);
-        O = fmaf(p[s * ATT_PART + d], c, O);
-    }
-    out[(size_t)h * ATT_HD + d] = O / L;
-}
-
-uint64_t attention_partials_bytes() { return (uint64_t)ATT_HEADS_MAX * ATT_SPLITS_MAX * ATT_PART * 4; }
+// counters (one u32 per KV head, each on its own 256-byte line) then the
+// split partials
+constexpr uint64_t ATT_COUNTER_BYTES = (uint64_t)ATT_HEADS_MAX * ATT_COUNTER_STRIDE * 4;
+uint64_t attention_scratch_bytes() { return ATT_COUNTER_BYTES + (uint64_t)ATT_HEADS_MAX * ATT_SPLITS_MAX * ATT_PART * 4; }
 
 // Rows per split: enough splits for about two workgroups per CU, at least 16
-// rows (one per lane group) each, at most ATT_SPLITS_MAX splits.
-void attention_plan(uint32_t seq, uint32_t n_kv_heads, uint32_t cus, uint32_t &splits, uint32_t &per)
+// rows (one per lane group) and at most 16 * ATT_ROWS_PER_GROUP rows each,
+// at most ATT_SPLITS_MAX splits and at most 256 / heads_per_kv (the merge
+// reads one split maximum and sum per thread).
+void attention_plan(uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t cus, uint32_t &splits,
+                    uint32_t &per)
 {
-    const uint32_t want = max(1u, min(ATT_SPLITS_MAX, (2 * cus + n_kv_heads - 1) / n_kv_heads));
-    splits = max(1u, min(want, (seq + 15) / 16));
+    const uint32_t cap = min(ATT_SPLITS_MAX, 256 / heads_per_kv);
+    const uint32_t want = max(1u, min(cap, (2 * cus + n_kv_heads - 1) / n_kv_heads));
+    const uint32_t least = (seq + 16 * ATT_ROWS_PER_GROUP - 1) / (16 * ATT_ROWS_PER_GROUP);
+    splits = max(least, max(1u, min(want, (seq + 15) / 16)));
     per = (seq + splits - 1) / splits;
     splits = (seq + per - 1) / per;   // every split has at least one row
 }
 
 template <int HPK>
-static void go_attn(const float *q, const uint16_t *kc, const uint16_t *vc, float *part, uint32_t seq, uint32_t per,
-                    uint32_t kv_stride, float qscale, uint32_t n_kv_heads, uint32_t splits, hipStream_t s)
+static void go_attn(const float *q, const uint16_t *kc, const uint16_t *vc, float *part, uint32_t *counters, float *out,
+                    uint32_t seq, uint32_t per, uint32_t kv_stride, float qscale, uint32_t n_kv_heads, uint32_t splits,
+                    hipStream_t s)
 {
-    hipLaunchKernelGGL(attn_split_kernel<HPK>, dim3(n_kv_heads, splits), dim3(256), 0, s, q, kc, vc, part, seq, per,
-                       kv_stride, qscale);
+    hipLaunchKernelGGL(attn_kernel<HPK>, dim3(n_kv_heads, splits), dim3(256), 0, s, q, kc, vc, part, counters, out, seq,
+                       per, kv_stride, qscale);
 }
 
-hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out, void *partials,
+hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out, void *scratch,
                             uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t cus, hipStream_t s)
 {
     uint32_t splits, per;
-    attention_plan(seq, n_kv_heads, cus, splits, per);
+    attention_plan(seq, n_kv_heads, heads_per_kv, cus, splits, per);
     const uint32_t kv_stride = n_kv_heads * ATT_HD;
     const float qscale = (float)(1.4426950408889634 / sqrt((double)ATT_HD));   // log2(e) / sqrt(head_dim)
-    float *part = (float *)partials;
+    uint32_t *counters = (uint32_t *)scratch;
+    float *part = (float *)((char *)scratch + ATT_COUNTER_BYTES);
+#define RRR_ATT_CASE(H) \
+    case H: go_attn<H>(q, kc, vc, part, counters, out, seq, per, kv_stride, qscale, n_kv_heads, splits, s); break;
     switch (heads_per_kv) {
-    case 1: go_attn<1>(q, kc, vc, part, seq, per, kv_stride, qscale, n_kv_heads, splits, s); break;
-    case 2: go_attn<2>(q, kc, vc, part, seq, per, kv_stride, qscale, n_kv_heads, splits, s); break;
-    case 3: go_attn<3>(q, kc, vc, part, seq, per, kv_stride, qscale, n_kv_heads, splits, s); break;
-    case 4: go_attn<4>(q, kc, vc, part, seq, per, kv_stride, qscale, n_kv_heads, splits, s); break;
-    case 5: go_attn<5>(q, kc, vc, part, seq, per, kv_stride, qscale, n_kv_heads, splits, s); break;
-    case 6: go_attn<6>(q, kc, vc, part, seq, per, kv_stride, qscale, n_kv_heads, splits, s); break;
-    case 7: go_attn<7>(q, kc, vc, part, seq, per, kv_stride, qscale, n_kv_heads, splits, s); break;
-    case 8: go_attn<8>(q, kc, vc, part, seq, per, kv_stride, qscale, n_kv_heads, splits, s); break;
+        RRR_ATT_CASE(1) RRR_ATT_CASE(2) RRR_ATT_CASE(3) RRR_ATT_CASE(4)
+        RRR_ATT_CASE(5) RRR_ATT_CASE(6) RRR_ATT_CASE(7) RRR_ATT_CASE(8)
     default: return hipErrorInvalidValue;
     }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(n_kv_heads * heads_per_kv), dim3(ATT_HD), 0, s, part, out, splits);
+#undef RRR_ATT_CASE
     return hipGetLastError();
 }
 

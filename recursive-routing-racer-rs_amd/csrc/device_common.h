@@ -33,6 +33,9 @@ __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // Streaming (non-temporal) variant for data read exactly once, such as
 // weight matrices: keeps activations and outputs resident in the caches.
 constexpr int RRR_CPOL_NT = 2;
+// agent-scope coherent access (sc1): goes through to the level shared by
+// every XCD, for data exchanged between workgroups of one launch
+constexpr int RRR_CPOL_SC1 = 16;
 __device__ __forceinline__ u32x4 bload16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, RRR_CPOL_NT);

@@ -295,7 +295,6 @@ constexpr uint32_t MQ_OOB = 0x80000000u;
 // through to the coherent level.  The weights of the workgroup's first tile
 // are requested before the wait for the previous op, so HBM keeps streaming
 // through the hand-off.
-constexpr int RRR_CPOL_SC1 = 16;
 
 // Wait of one op for the previous one: every workgroup's progress flag has
 // reached `target` (flags only grow; 0 = no wait).  Workgroup 0 gathers the

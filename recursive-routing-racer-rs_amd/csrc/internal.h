@@ -79,11 +79,15 @@ struct RopeArgs {
 };
 hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uint16_t *vc, hipStream_t s);
 // Decode attention (attn.hip): head_dim ATT_HD, up to ATT_HEADS_MAX query
-// heads, `partials` of attention_partials_bytes().
-constexpr uint32_t ATT_HD = 128, ATT_HEADS_MAX = 64, ATT_SPLITS_MAX = 64;
-uint64_t attention_partials_bytes();
-void attention_plan(uint32_t seq, uint32_t n_kv_heads, uint32_t cus, uint32_t &splits, uint32_t &per);
-hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out, void *partials,
+// heads (ATT_HEADS_MAX KV heads), `scratch` of attention_scratch_bytes()
+// zeroed once before the first call (its counters return to zero after
+// every call; calls on one scratch area must not overlap).
+constexpr uint32_t ATT_HD = 128, ATT_HEADS_MAX = 64, ATT_SPLITS_MAX = 32, ATT_ROWS_PER_GROUP = 4;
+constexpr uint32_t ATT_SEQ_MAX = ATT_SPLITS_MAX * 16 * ATT_ROWS_PER_GROUP;   // 2048 cache rows (MAX_SEQ)
+uint64_t attention_scratch_bytes();
+void attention_plan(uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t cus, uint32_t &splits,
+                    uint32_t &per);
+hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out, void *scratch,
                             uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t cus, hipStream_t s);
 hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint64_t w_bytes, uint32_t type,
                             float *Y, uint32_t K, uint32_t N, uint32_t M, hipStream_t s);

@@ -22,6 +22,12 @@ chunks (phi4.rs:874-893, 1049-1064) as rrr_logits_rmsnorm, and the argmax
 that the reference does on the host (phi4.rs:1172-1195) as rrr_argmax_f32.
 The fused entry points are bitwise equal to their unfused sequences.
 
+With attention=True the sweep also owns per-layer f16 KV caches and
+record_token(pos) runs the full decode step at position pos (phi4.rs:1006-1033
+with the attention rows in): rope_kv_store (RoPE on Q and K, K and V stored
+in row pos) and attention over rows 0..pos replace the position-0 gather,
+and the O-proj GEMV takes the attention output.
+
 Weights are seeded synthetic tensors (the recipes of synth.py); each tensor
 has its own stream id, so any subset can be regenerated on the host.
 """
@@ -44,6 +50,10 @@ class Phi4Shape:
     vocab: int = 200064
     eps: float = 1e-5
     chunk: int = 8192            # logits vocab chunk (phi4.rs:877)
+    rope_dim: int = 96           # phi4.rs:114-116
+    rope_theta: float = 10000.0
+    rope_attn_factor: float = 1.190238
+    max_seq: int = 2048          # KV-cache rows (MAX_SEQ, phi4.rs:181)
 
     @property
     def qkv_dim(self):
@@ -52,6 +62,10 @@ class Phi4Shape:
     @property
     def heads_per_kv(self):
         return self.n_heads // self.n_kv_heads
+
+    @property
+    def kv_stride(self):
+        return self.n_kv_heads * self.head_dim
 
     def down_type(self, layer):
         return E.Q6_K if layer % 2 == 0 else E.Q4_K
@@ -82,7 +96,7 @@ def _stream(layer, slot):
 
 
 S_ATTN_NORM, S_QKV, S_O, S_FFN_NORM, S_UP, S_DOWN = range(6)
-S_OUT_NORM, S_EMB, S_X = 10, 11, 12
+S_OUT_NORM, S_EMB, S_X, S_ROPE = 10, 11, 12, 13
 
 
 def gamma_host(seed, stream, d):
@@ -106,6 +120,12 @@ def embedding_chunks_host(seed, shape):
     return synth.normal_f32(seed, S_EMB, shape.vocab * shape.d_model, 0.0, 0.02)
 
 
+def rope_factors_host(seed, shape):
+    """LongRoPE divisors of the rope_dim / 2 frequency pairs (the model's
+    rope_factors_short tensor, phi4.rs:711-712), synthetic: 1 + |N(0, 1)|."""
+    return (1.0 + np.abs(synth.normal_f32(seed, S_ROPE, shape.rope_dim // 2))).astype(np.float32)
+
+
 def x_host(seed, shape):
     """The token's input hidden state (stands in for the embedding row)."""
     return synth.normal_f32(seed, S_X, shape.d_model)
@@ -115,7 +135,7 @@ class DecodeSweep:
     """Device weights and activations of the sweep; record_token() issues one
     token's operations on the context's stream."""
 
-    def __init__(self, ctx, shape=Phi4Shape(), seed=3, keep_host=False):
+    def __init__(self, ctx, shape=Phi4Shape(), seed=3, keep_host=False, attention=False):
         self.ctx, self.shape, self.seed = ctx, shape, seed
         self.host = {} if keep_host else None
         d = shape.d_model
@@ -143,15 +163,35 @@ class DecodeSweep:
         self.gate_up = ctx.alloc(2 * shape.ffn_dim * 4)
         self.logits = ctx.alloc(shape.vocab * 4)
         self.token = ctx.alloc(4)
+        self.attention = attention
+        if attention:
+            fac = rope_factors_host(seed, shape)
+            self.rope_factors = ctx.to_device(fac)
+            if keep_host:
+                self.host["rope_factors"] = fac
+            cache_bytes = shape.max_seq * shape.kv_stride * 2
+            self.kv = [(ctx.alloc(cache_bytes), ctx.alloc(cache_bytes)) for _ in range(shape.n_layers)]
+            self.attn_out = ctx.alloc(d * 4)
 
-    def record_token(self):
+    def record_token(self, pos=None):
+        """One token: the position-0 weight sweep (pos None), or with
+        attention=True the full decode step at position pos."""
         c, s = self.ctx, self.shape
         d = s.d_model
         gqa = s.head_dim | (s.heads_per_kv << 16)
+        if pos is not None and not (self.attention and 0 <= pos < s.max_seq):
+            raise ValueError("a position needs attention=True and pos < max_seq")
         c.residual_add(self.x_in, self.zero, self.hidden, d)       # hidden = embedding row
         for i, L in enumerate(self.layers):
             c.gemv_rmsnorm(self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], E.Q5_K, self.qkv, d, s.qkv_dim)
-            c.gemv_residual(self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], E.Q4_K, self.hidden, d, d)
+            if pos is None:
+                c.gemv_residual(self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], E.Q4_K, self.hidden, d, d)
+            else:
+                kc, vc = self.kv[i]
+                c.rope_kv_store(self.qkv, self.rope_factors, s.rope_dim // 2, kc, vc, pos, s.n_heads, s.n_kv_heads,
+                                s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta, s.rope_attn_factor)
+                c.attention(self.qkv, kc, vc, self.attn_out, pos + 1, s.n_kv_heads, s.heads_per_kv, s.head_dim)
+                c.gemv_residual(self.attn_out, E.ACT_IDENTITY, 0, L["attn_output"], E.Q4_K, self.hidden, d, d)
             c.gemv_rmsnorm(self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], E.Q4_K, self.gate_up, d, 2 * s.ffn_dim)
             c.gemv_residual(self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], s.down_type(i), self.hidden,
                             s.ffn_dim, d)
@@ -185,9 +225,9 @@ class DecodeSweep:
                          E.LOGITS_CHUNKED, s.chunk)
         c.argmax_f32(self.logits, s.vocab, self.token)
 
-    def graph(self):
+    def graph(self, pos=None):
         self.ctx.graph_begin()
-        self.record_token()
+        self.record_token(pos)
         return self.ctx.graph_end()
 
     def results(self):

@@ -128,3 +128,75 @@ def test_sweep_rejects_other_forms_and_graph_capture(ctx):
     finally:
         for b in (W, W4, x, g, y):
             b.free()
+
+
+# ---- the full decode step with RoPE, the f16 KV caches and attention ----------
+
+SHAPE_ATT = dataclasses.replace(SHAPE, max_seq=16)
+ATT_POSITIONS = [0, 1, 2, 3, 4]
+
+
+def oracle_step(s, host, caches, pos):
+    """One decode step at position pos in the oracle, layer by layer as
+    phi4.rs:1006-1033: RMSNorm -> QKV -> rope_kv_store -> attention -> O-proj
+    + residual -> RMSNorm -> gate/up -> silu * up -> down + residual.  The
+    GEMVs and attention are fp64; RoPE and the f16 cache store are the f32
+    restatement.  caches[i] = (k, v) uint16 arrays, updated in place."""
+    d, F = s.d_model, s.ffn_dim
+    h = host["x"].astype(np.float64)
+    for i in range(s.n_layers):
+        L = host[i]
+        normed = orc.rms_norm(h.astype(np.float32), L["attn_norm"], s.eps)
+        qkv = orc.gemv(rrr_hip.Q5_K, L["attn_qkv"], normed, d, s.qkv_dim, 1, THREADS, f64=True)[0].astype(np.float32)
+        kc, vc = caches[i]
+        qkv, kc, vc = orc.rope_kv_store(qkv, kc, vc, pos, s.n_heads, s.n_kv_heads, s.head_dim, s.rope_dim,
+                                        factors=host["rope_factors"], theta=s.rope_theta,
+                                        attn_factor=s.rope_attn_factor)
+        caches[i] = (kc, vc)
+        att = orc.attention_f64(qkv[:d], kc, vc, pos + 1, s.n_kv_heads, s.heads_per_kv, s.head_dim)
+        h = h + orc.gemv(rrr_hip.Q4_K, L["attn_output"], att.astype(np.float32), d, d, 1, THREADS, f64=True)[0]
+        normed = orc.rms_norm(h.astype(np.float32), L["ffn_norm"], s.eps)
+        gu = orc.gemv(rrr_hip.Q4_K, L["ffn_up"], normed, d, 2 * F, 1, THREADS, f64=True)[0]
+        mid = orc.silu_gate(gu.astype(np.float32), F)
+        h = h + orc.gemv(s.down_type(i), L["ffn_down"], mid, F, d, 1, THREADS, f64=True)[0]
+    normed = orc.rms_norm(h.astype(np.float32), host["out_norm"], s.eps)
+    logits = orc.logits(normed, host["emb"], d, s.vocab, 1, s.chunk, THREADS, f64=True)
+    return logits, h
+
+
+def test_decode_steps_with_attention_match_oracle(ctx):
+    """Positions 0..4 in order: each step writes its cache row and attends
+    over all rows so far, in the GPU sweep and in the oracle."""
+    s = SHAPE_ATT
+    sw = decode.DecodeSweep(ctx, s, seed=3, keep_host=True, attention=True)
+    caches = [(np.zeros(s.max_seq * s.kv_stride, np.uint16), np.zeros(s.max_seq * s.kv_stride, np.uint16))
+              for _ in range(s.n_layers)]
+    for pos in ATT_POSITIONS:
+        sw.record_token(pos)
+        ctx.sync()
+        logits, tok, hidden = sw.results()
+        ref_logits, ref_h = oracle_step(s, sw.host, caches, pos)
+        assert np.all(np.isfinite(logits))
+        assert orc.normwise_err(hidden, ref_h) < TOL, pos
+        assert orc.normwise_err(logits, ref_logits) < TOL, pos
+        assert tok == int(np.argmax(logits))
+    # the cache rows written so far hold each position's V (from the GEMV, so
+    # equal to the oracle's within the tolerance and one f16 rounding)
+    kc, vc = sw.kv[0]
+    n = len(ATT_POSITIONS) * s.kv_stride
+    vg = ctx.download(vc, np.uint16, n).view(np.float16).astype(np.float64)
+    vo = caches[0][1][:n].view(np.float16).astype(np.float64)
+    assert np.all(np.abs(vg - vo) <= TOL * np.max(np.abs(vo)) + np.abs(vo) * 2.0 ** -10)
+    # a graph of the step at the last position replays bitwise (its cache
+    # row is rewritten with the same values)
+    logits0, tok0, hidden0 = sw.results()
+    g = sw.graph(ATT_POSITIONS[-1])
+    for _ in range(3):
+        g.launch()
+        ctx.sync()
+        logits, tok, hidden = sw.results()
+        assert np.array_equal(logits.view(np.uint32), logits0.view(np.uint32))
+        assert np.array_equal(hidden.view(np.uint32), hidden0.view(np.uint32))
+    g.destroy()
+    with pytest.raises(ValueError):
+        sw.record_token(s.max_seq)

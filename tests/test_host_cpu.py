@@ -247,6 +247,7 @@ def test_rope_kv_store_and_attention_validation(vctx):
     assert code_of(at, q, kc, vc, out, 17, nkv, 3, hd) == ERR_SHORT_BUFFER
     assert code_of(at, q, kc, vc, out, 0, nkv, 3, hd) == ERR_BAD_SHAPE
     assert code_of(at, q, kc, vc, out, 4, nkv, 3, 64) == ERR_UNSUPPORTED
+    assert code_of(at, q, kc, vc, out, 2049, nkv, 3, hd) == ERR_UNSUPPORTED     # beyond 2048 cache rows
     assert code_of(at, q, kc, vc, out, 4, 8, 9, hd) == ERR_UNSUPPORTED
     assert code_of(at, q, kc, vc, out, 4, 16, 4, hd) in (ERR_UNSUPPORTED, ERR_SHORT_BUFFER)
 
