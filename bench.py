@@ -225,7 +225,7 @@ def decode_sweep(ctx, tokens):
     shape = decode.Phi4Shape()
     log("[bench] decode sweep: generating and uploading 32 layers + logits matrix")
     t0 = time.perf_counter()
-    sw = decode.DecodeSweep(ctx, shape, seed=3, attention=True)
+    sw = decode.DecodeSweep(ctx, shape, seed=3, attention=True, logits="both")
     ctx.sync()
     log(f"[bench] decode sweep ready in {time.perf_counter() - t0:.1f} s")
     g = sw.graph()
@@ -276,9 +276,34 @@ def decode_sweep(ctx, tokens):
                          n_att) * 1e3 / n_att
     log(f"[bench] decode step at position {pos} (RoPE + KV store + attention over {shape.max_seq} rows): "
         f"{ms_a:.4f} ms/token; attention alone {us_att:.2f} us/layer ({kv_bytes / (us_att * 1e-6) / 1e9:.0f} GB/s)")
+    # the same weight sweep with the logits read from the raw Q6_K token_embd
+    # (504 MB) instead of its 2.46 GB F32 expansion
+    gq = sw.graph(logits="q6k")
+    gq.launch()
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(tokens):
+        gq.launch()
+    ms_q = ctx.timer_stop() / tokens
+    gq.destroy()
+    lq, tok_q, _ = sw.results()
+    bq = shape.bytes_per_token("q6k")
+    n_lq = 16
+    us_lq = timed_graph(ctx, lambda i: ctx.logits_rmsnorm(sw.hidden, sw.out_norm, shape.eps, sw.emb_q6k, sw.logits,
+                                                          shape.d_model, shape.vocab, rrr_hip.LOGITS_Q6K, 0),
+                        n_lq) * 1e3 / n_lq
+    lq_bytes = rrr_hip.tensor_bytes(rrr_hip.Q6_K, shape.d_model, shape.vocab) + 3 * shape.d_model * 4 + shape.vocab * 4
+    log(f"[bench] decode sweep with Q6_K token_embd logits: {ms_q:.4f} ms/token ({bq / (ms_q * 1e-3) / 1e9:.0f} GB/s), "
+        f"argmax {tok_q}; the Q6_K logits alone {us_lq:.1f} us ({lq_bytes / (us_lq * 1e-6) / 1e9:.0f} GB/s)")
     best = min(ms, ms_p)
     return {"ms_per_token": round(best, 5), "tokens": tokens, "bytes_per_token": b,
             "ms_per_token_at_pos_2047_with_attention": round(ms_a, 5),
+            "q6k_token_embd_logits": {"ms_per_token": round(ms_q, 5), "bytes_per_token": bq,
+                                      "GBs": round(bq / (ms_q * 1e-3) / 1e9, 1),
+                                      "logits_us": round(us_lq, 2), "logits_bytes": lq_bytes,
+                                      "logits_GBs": round(lq_bytes / (us_lq * 1e-6) / 1e9, 1),
+                                      "logits_frac_hbm": round(lq_bytes / (us_lq * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "argmax": tok_q, "logits_finite": bool(np.all(np.isfinite(lq)))},
             "attention_2048_rows": {"us_per_layer": round(us_att, 3), "kv_bytes": kv_bytes,
                                     "GBs": round(kv_bytes / (us_att * 1e-6) / 1e9, 1),
                                     "frac_hbm": round(kv_bytes / (us_att * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},

@@ -60,8 +60,12 @@ typedef enum rrr_ggml_type {
 /* Logits weight layouts. */
 typedef enum rrr_logits_layout {
     RRR_LOGITS_ROWS = 0,    /* E[v][d], V rows of K f32 (token_embd order) */
-    RRR_LOGITS_CHUNKED = 1  /* reference chunks: B_c[d*n + v] = E[(c*chunk+v)*K + d]
+    RRR_LOGITS_CHUNKED = 1, /* reference chunks: B_c[d*n + v] = E[(c*chunk+v)*K + d]
                                (phi4.rs:874-893), chunks back to back */
+    RRR_LOGITS_Q6K = 2      /* the tied token_embd as stored: V rows of K/256 raw
+                               Q6_K super-blocks, the tensor the reference
+                               dequantizes to build its F32 copy (phi4.rs:709,
+                               :866-893); chunk is unused */
 } rrr_logits_layout;
 
 typedef struct rrr_ctx rrr_ctx;
@@ -163,7 +167,9 @@ int rrr_residual_add(rrr_ctx *ctx, const rrr_buf *a, const rrr_buf *b, rrr_buf *
  * chunked matmul_tiled logit dispatches (phi4.rs:1049-1064, :1416-1434):
  * layout RRR_LOGITS_CHUNKED accepts the reference's transposed chunks of
  * `chunk` rows (8192 in the reference) back to back, RRR_LOGITS_ROWS the
- * untransposed E. */
+ * untransposed E.  RRR_LOGITS_Q6K reads the raw Q6_K token_embd instead of
+ * its F32 expansion: E[v][d] = dequant_q6_k (phi4.rs:444-479) of row v, the
+ * same values the F32 layouts hold, from 4.9x fewer bytes (K % 256 == 0). */
 int rrr_logits_f32(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *E, rrr_buf *logits, uint32_t K,
                    uint32_t V, uint32_t layout, uint32_t chunk);
 
@@ -223,7 +229,7 @@ int rrr_gemv_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float
 enum { RRR_ACT_IDENTITY = 0, RRR_ACT_SILU_GATE = 1, RRR_ACT_GQA_V = 2 };
 int rrr_gemv_residual(rrr_ctx *ctx, const rrr_buf *x, uint32_t act_kind, uint32_t act_param,
                       const rrr_buf *W, uint32_t type, rrr_buf *hidden, uint32_t K, uint32_t N);
-/* logits = E . rmsnorm(x, gamma, eps), E in RRR_LOGITS_ROWS or CHUNKED. */
+/* logits = E . rmsnorm(x, gamma, eps), E in any rrr_logits_layout. */
 int rrr_logits_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps,
                        const rrr_buf *E, rrr_buf *logits, uint32_t K, uint32_t V, uint32_t layout,
                        uint32_t chunk);

@@ -592,17 +592,22 @@ static int logits_common(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, f
     TRY(check_buf(ctx, y, what));
     if (gamma) TRY(check_buf(ctx, gamma, what));
     if (K == 0 || V == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: K and V must be positive", what);
-    if (layout > RRR_LOGITS_CHUNKED) return fail(RRR_ERR_INVALID_ARG, "%s: layout %u", what, layout);
+    if (layout > RRR_LOGITS_Q6K) return fail(RRR_ERR_INVALID_ARG, "%s: layout %u", what, layout);
     if (gamma && !(std::isfinite(eps) && eps >= 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: eps", what);
     TRY(need_f32(x, K, what));
     TRY(need_f32(y, V, what));
     if (gamma) TRY(need_f32(gamma, K, what));
-    TRY(need(E, (uint64_t)V * K * 4, what));
-    if (layout == RRR_LOGITS_ROWS) {
+    if (layout == RRR_LOGITS_Q6K) {
+        if (K % 256) return fail(RRR_ERR_BAD_SHAPE, "%s: Q6_K rows need K %% 256 == 0 (K=%u)", what, K);
+        TRY(need(E, rrr_tensor_bytes(RRR_TYPE_Q6_K, K, V), what));
+    } else {
+        TRY(need(E, (uint64_t)V * K * 4, what));
+    }
+    if (layout != RRR_LOGITS_CHUNKED) {
         if (K % 256) return fail(RRR_ERR_BAD_SHAPE, "%s: row layout needs K %% 256 == 0 (K=%u)", what, K);
         TRY(device_ready(ctx));
         GemvArgs a{};
-        a.type = T_F32;
+        a.type = layout == RRR_LOGITS_Q6K ? T_Q6_K : T_F32;
         a.x = (const float *)x->ptr;
         a.gamma = gamma ? (const float *)gamma->ptr : nullptr;
         a.eps = eps;

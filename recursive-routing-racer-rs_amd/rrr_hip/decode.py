@@ -76,9 +76,10 @@ class Phi4Shape:
         return [("attn_qkv", E.Q5_K, d, self.qkv_dim), ("attn_output", E.Q4_K, d, d),
                 ("ffn_up", E.Q4_K, d, 2 * f), ("ffn_down", self.down_type(layer), f, d)]
 
-    def bytes_per_token(self):
+    def bytes_per_token(self, logits="f32"):
         """Algorithmic HBM bytes of one token: raw weight bytes plus every
-        activation read or written once."""
+        activation read or written once; logits from the F32 matrix or, with
+        logits="q6k", from the raw Q6_K token_embd."""
         d, f = self.d_model, self.ffn_dim
         total = 0
         for i in range(self.n_layers):
@@ -86,7 +87,8 @@ class Phi4Shape:
             for _, qt, K, N in self.layer_tensors(i):
                 total += E.tensor_bytes(qt, K, N) + K * 4 + N * 4
         total += 3 * d * 4                                             # output norm
-        total += self.vocab * d * 4 + d * 4 + self.vocab * 4           # logits
+        emb = E.tensor_bytes(E.Q6_K, d, self.vocab) if logits == "q6k" else self.vocab * d * 4
+        total += emb + d * 4 + self.vocab * 4                          # logits
         return total
 
 
@@ -96,7 +98,7 @@ def _stream(layer, slot):
 
 
 S_ATTN_NORM, S_QKV, S_O, S_FFN_NORM, S_UP, S_DOWN = range(6)
-S_OUT_NORM, S_EMB, S_X, S_ROPE = 10, 11, 12, 13
+S_OUT_NORM, S_EMB, S_X, S_ROPE, S_EMB_Q6K = 10, 11, 12, 13, 14
 
 
 def gamma_host(seed, stream, d):
@@ -120,6 +122,13 @@ def embedding_chunks_host(seed, shape):
     return synth.normal_f32(seed, S_EMB, shape.vocab * shape.d_model, 0.0, 0.02)
 
 
+def embedding_q6k_host(seed, shape):
+    """The tied token_embd as raw Q6_K super-blocks (vocab rows of d_model /
+    256 blocks), the tensor the reference dequantizes into its F32 logits
+    matrix (phi4.rs:709, :866-893)."""
+    return synth.weight(seed, S_EMB_Q6K, E.Q6_K, shape.d_model, shape.vocab)
+
+
 def rope_factors_host(seed, shape):
     """LongRoPE divisors of the rope_dim / 2 frequency pairs (the model's
     rope_factors_short tensor, phi4.rs:711-712), synthetic: 1 + |N(0, 1)|."""
@@ -135,7 +144,12 @@ class DecodeSweep:
     """Device weights and activations of the sweep; record_token() issues one
     token's operations on the context's stream."""
 
-    def __init__(self, ctx, shape=Phi4Shape(), seed=3, keep_host=False, attention=False):
+    def __init__(self, ctx, shape=Phi4Shape(), seed=3, keep_host=False, attention=False, logits="f32"):
+        """logits: "f32" (the F32 matrix in the reference's transposed
+        chunks), "q6k" (a raw Q6_K token_embd read as stored) or "both"
+        (both held; `logits_mode` picks the one a token uses)."""
+        if logits not in ("f32", "q6k", "both"):
+            raise ValueError(f"logits={logits!r}")
         self.ctx, self.shape, self.seed = ctx, shape, seed
         self.host = {} if keep_host else None
         d = shape.d_model
@@ -149,14 +163,25 @@ class DecodeSweep:
             if keep_host:
                 self.host[i] = h
         out_norm = gamma_host(seed, S_OUT_NORM, d)
-        emb = embedding_chunks_host(seed, shape)
         x = x_host(seed, shape)
         self.out_norm = ctx.to_device(out_norm)
-        self.emb = ctx.to_device(emb)
         self.x_in = ctx.to_device(x)
         if keep_host:
-            self.host.update(out_norm=out_norm, emb=emb, x=x)
-        del emb
+            self.host.update(out_norm=out_norm, x=x)
+        self.emb = self.emb_q6k = None
+        if logits in ("f32", "both"):
+            emb = embedding_chunks_host(seed, shape)
+            self.emb = ctx.to_device(emb)
+            if keep_host:
+                self.host["emb"] = emb
+            del emb
+        if logits in ("q6k", "both"):
+            raw = embedding_q6k_host(seed, shape)
+            self.emb_q6k = ctx.weight_upload(E.Q6_K, d, shape.vocab, raw)
+            if keep_host:
+                self.host["emb_q6k"] = raw
+            del raw
+        self.logits_mode = "q6k" if logits == "q6k" else "f32"
         self.zero = ctx.to_device(np.zeros(d, np.float32))
         self.hidden = ctx.alloc(d * 4)
         self.qkv = ctx.alloc(shape.qkv_dim * 4)
@@ -195,8 +220,18 @@ class DecodeSweep:
             c.gemv_rmsnorm(self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], E.Q4_K, self.gate_up, d, 2 * s.ffn_dim)
             c.gemv_residual(self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], s.down_type(i), self.hidden,
                             s.ffn_dim, d)
-        c.logits_rmsnorm(self.hidden, self.out_norm, s.eps, self.emb, self.logits, d, s.vocab,
-                         E.LOGITS_CHUNKED, s.chunk)
+        self.record_logits()
+
+    def record_logits(self):
+        """Final RMSNorm + logits (F32 chunks or raw Q6_K rows, by
+        logits_mode) + argmax."""
+        c, s = self.ctx, self.shape
+        if self.logits_mode == "q6k":
+            c.logits_rmsnorm(self.hidden, self.out_norm, s.eps, self.emb_q6k, self.logits, s.d_model, s.vocab,
+                             E.LOGITS_Q6K, 0)
+        else:
+            c.logits_rmsnorm(self.hidden, self.out_norm, s.eps, self.emb, self.logits, s.d_model, s.vocab,
+                             E.LOGITS_CHUNKED, s.chunk)
         c.argmax_f32(self.logits, s.vocab, self.token)
 
     def sweep_ops(self):
@@ -221,14 +256,22 @@ class DecodeSweep:
         c, s = self.ctx, self.shape
         c.residual_add(self.x_in, self.zero, self.hidden, s.d_model)
         sweep.run()
-        c.logits_rmsnorm(self.hidden, self.out_norm, s.eps, self.emb, self.logits, s.d_model, s.vocab,
-                         E.LOGITS_CHUNKED, s.chunk)
-        c.argmax_f32(self.logits, s.vocab, self.token)
+        self.record_logits()
 
-    def graph(self, pos=None):
-        self.ctx.graph_begin()
-        self.record_token(pos)
-        return self.ctx.graph_end()
+    def graph(self, pos=None, logits=None):
+        """One token as a HIP graph; logits ("f32" / "q6k") overrides
+        logits_mode for it."""
+        mode = self.logits_mode
+        if logits is not None:
+            if (self.emb_q6k if logits == "q6k" else self.emb) is None:
+                raise ValueError(f"no {logits} logits matrix was built")
+            self.logits_mode = logits
+        try:
+            self.ctx.graph_begin()
+            self.record_token(pos)
+            return self.ctx.graph_end()
+        finally:
+            self.logits_mode = mode
 
     def results(self):
         """(logits f32[vocab], argmax index, final hidden state f32[d])."""

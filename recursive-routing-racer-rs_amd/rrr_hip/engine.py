@@ -29,7 +29,7 @@ ERR_STATE = -9
 ERR_STALE = -10
 
 F32, Q4_K, Q5_K, Q6_K = 0, 12, 13, 14
-LOGITS_ROWS, LOGITS_CHUNKED = 0, 1
+LOGITS_ROWS, LOGITS_CHUNKED, LOGITS_Q6K = 0, 1, 2
 ACT_IDENTITY, ACT_SILU_GATE, ACT_GQA_V = 0, 1, 2
 SWEEP_GEMV_RMSNORM, SWEEP_GEMV_RESIDUAL = 0, 1
 DEVICE_NONE = -1

@@ -32,7 +32,7 @@ def gqa_gather(qkv, s):
     return np.repeat(v, s.heads_per_kv, axis=0).reshape(-1)
 
 
-def oracle_token(s, host):
+def oracle_token(s, host, logits="f32"):
     d, F = s.d_model, s.ffn_dim
     h = host["x"].astype(np.float64)
     for i in range(s.n_layers):
@@ -46,8 +46,11 @@ def oracle_token(s, host):
         mid = orc.silu_gate(gu.astype(np.float32), F)
         h = h + orc.gemv(s.down_type(i), L["ffn_down"], mid, F, d, 1, THREADS, f64=True)[0]
     normed = orc.rms_norm(h.astype(np.float32), host["out_norm"], s.eps)
-    logits = orc.logits(normed, host["emb"], d, s.vocab, 1, s.chunk, THREADS, f64=True)
-    return logits, h
+    if logits == "q6k":
+        out = orc.gemv(rrr_hip.Q6_K, host["emb_q6k"], normed, d, s.vocab, 1, THREADS, f64=True)[0]
+    else:
+        out = orc.logits(normed, host["emb"], d, s.vocab, 1, s.chunk, THREADS, f64=True)
+    return out, h
 
 
 @pytest.fixture(scope="module")
@@ -68,6 +71,31 @@ def test_decode_token_matches_oracle(sweep):
     top2 = np.sort(ref_logits)[-2:]
     if top2[1] - top2[0] > TOL * np.max(np.abs(ref_logits)):
         assert tok == int(np.argmax(ref_logits))
+
+
+def test_decode_token_q6k_logits_matches_oracle(ctx, sweep):
+    """Logits from the raw Q6_K token_embd: the layers give the same bits as
+    the F32-logits token, the logits match the fp64 dot over dequant_q6_k of
+    the rows, and a graph of the token replays bitwise."""
+    sw = decode.DecodeSweep(ctx, SHAPE, seed=3, keep_host=True, logits="q6k")
+    sw.record_token()
+    ctx.sync()
+    logits, tok, hidden = sw.results()
+    ref_logits, ref_h = oracle_token(SHAPE, sw.host, logits="q6k")
+    assert np.array_equal(hidden.view(np.uint32), sweep.results()[2].view(np.uint32))
+    assert np.all(np.isfinite(logits))
+    assert orc.normwise_err(logits, ref_logits) < TOL
+    assert tok == int(np.argmax(logits))
+    top2 = np.sort(ref_logits)[-2:]
+    if top2[1] - top2[0] > TOL * np.max(np.abs(ref_logits)):
+        assert tok == int(np.argmax(ref_logits))
+    g = sw.graph()
+    for _ in range(2):
+        ctx.fill_u32(sw.logits, 0)
+        g.launch()
+        ctx.sync()
+        assert np.array_equal(sw.results()[0].view(np.uint32), logits.view(np.uint32))
+    g.destroy()
 
 
 def test_decode_graph_replay_matches_eager(ctx, sweep):

@@ -185,8 +185,15 @@ def test_elementwise_and_logits_validation(vctx):
     xk = vctx.alloc(K * 4)
     assert code_of(vctx.logits_f32, xk, E, lg, K, V, rrr_hip.LOGITS_ROWS) == ERR_NO_DEVICE
     assert code_of(vctx.logits_f32, xk, E, lg, K, V, rrr_hip.LOGITS_CHUNKED, 300) == ERR_UNSUPPORTED
-    assert code_of(vctx.logits_f32, xk, E, lg, K, V, 2) == ERR_INVALID_ARG
+    assert code_of(vctx.logits_f32, xk, E, lg, K, V, 3) == ERR_INVALID_ARG
     assert code_of(vctx.logits_f32, xk, E, lg, K, V + 1, rrr_hip.LOGITS_ROWS) == ERR_SHORT_BUFFER
+    # raw Q6_K token_embd rows: K % 256, the Q6_K tensor size
+    E6 = vctx.alloc(rrr_hip.tensor_bytes(rrr_hip.Q6_K, K, V))
+    lg2 = vctx.alloc((V + 16) * 4)
+    assert code_of(vctx.logits_f32, xk, E6, lg, K, V, rrr_hip.LOGITS_Q6K, 0) == ERR_NO_DEVICE
+    assert code_of(vctx.logits_f32, xk, E6, lg, K, V, rrr_hip.LOGITS_ROWS) == ERR_SHORT_BUFFER
+    assert code_of(vctx.logits_f32, xk, E6, lg, 250, V, rrr_hip.LOGITS_Q6K, 0) == ERR_BAD_SHAPE
+    assert code_of(vctx.logits_f32, xk, E6, lg2, K, V + 16, rrr_hip.LOGITS_Q6K, 0) == ERR_SHORT_BUFFER
     out = vctx.alloc(4)
     assert code_of(vctx.argmax_f32, lg, V, out) == ERR_NO_DEVICE
     assert code_of(vctx.argmax_f32, lg, V + 1, out) == ERR_SHORT_BUFFER
