@@ -5,17 +5,18 @@
 
 namespace rrr {
 
-template <class Q, int BPW, int ACT, bool MULTI>
+template <class Q, int BPW, int ACT, bool MULTI, int TR>
 __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntiles, uint32_t tr)
 {
     SweepWait none{nullptr, nullptr, 0u, nullptr, nullptr};
-    (void)mq_body<Q, BPW, ACT, MULTI, false>(a, ntiles, tr, none);
+    (void)mq_body<Q, BPW, ACT, MULTI, false, TR>(a, ntiles, tr, none);
 }
 
 // Super-blocks per wave and waves per workgroup (at least 4, the canonical
 // RMSNorm order needs them; waves past the last super-block only encode).
 // Up to one workgroup per CU, each taking its tiles as far as its row
-// partials fit in LDS.
+// partials fit in LDS.  Tiles split evenly over the CUs (a wave issues only
+// the load slots its tile height needs, so short tiles cost no empty loads).
 template <class Q, int BPW>
 static void mq_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds, uint32_t &tr, uint32_t &ntiles)
 {
@@ -25,11 +26,19 @@ static void mq_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds,
     const size_t fixed = W * G::BYTES + 16;
     const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64));
     uint32_t per;
-    // even tiles pay off with one super-block per wave; with two (K > 4096)
-    // the empty load slots of a short tile cost more than the CUs it adds
-    mq_tiles(a.N, device_cus(), per_max, BPW == 1 ? 1u : 16u, tr, ntiles, per);
+    mq_tiles(a.N, device_cus(), per_max, 1u, tr, ntiles, per);
     grid = (ntiles + per - 1) / per;
     lds = fixed + (size_t)per * W * 64;
+}
+
+template <class Q, int BPW, int ACT, int TR>
+static void launch_mq(const GemvArgs &a, uint32_t W, uint32_t grid, size_t lds, uint32_t tr, uint32_t ntiles,
+                      hipStream_t s)
+{
+    if (grid == ntiles)
+        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, false, TR>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
+    else
+        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, true, TR>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
 }
 
 template <class Q, int BPW, int ACT>
@@ -39,10 +48,14 @@ static hipError_t go_mq(const GemvArgs &a, hipStream_t s)
     uint32_t W, grid, tr, ntiles;
     size_t lds;
     mq_plan<Q, BPW>(a, W, grid, lds, tr, ntiles);
-    if (grid == ntiles)
-        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, false>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
+    // slot sets for the tile heights of the decode shapes (N = 5120: 10 rows,
+    // N = 3072: 12 rows, larger N: 16 rows)
+    if (tr <= 10)
+        launch_mq<Q, BPW, ACT, 10>(a, W, grid, lds, tr, ntiles, s);
+    else if (tr <= 12)
+        launch_mq<Q, BPW, ACT, 12>(a, W, grid, lds, tr, ntiles, s);
     else
-        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, true>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
+        launch_mq<Q, BPW, ACT, 16>(a, W, grid, lds, tr, ntiles, s);
     return hipGetLastError();
 }
 

@@ -226,7 +226,7 @@ struct MwGeom {
     static constexpr uint32_t RS = (BPW * LB) % 32 == 0 ? BPW * LB + 16 : BPW * LB;  // odd multiple of 16
     static constexpr uint32_t UPR = BPW * UPB;                     // units per row
     static constexpr uint32_t RPS = 64 / UPR;                      // rows per load slot
-    static constexpr int S = (16 + RPS - 1) / RPS;                 // load slots
+    static constexpr int S = (16 + RPS - 1) / RPS;                 // load slots of a 16-row tile
     static constexpr uint32_t DG = BPW * 256;
     static constexpr uint32_t NGW = BPW * 16;
     static constexpr uint32_t D_OFF = 16 * RS;
@@ -400,11 +400,16 @@ __device__ __forceinline__ void mq_src_load4(const GemvArgs &a, __amdgpu_buffer_
 // past the buffer end cost texture-addresser time.  Row sums are added over
 // the waves in wave order, so results depend on neither form, G nor the
 // number of waves.  Returns false when a sweep wait was abandoned.
-template <class Q, int BPW, int ACT, bool MULTI, bool SW>
+// TR: the most rows a tile of the launch has (tr <= TR <= 16); a wave issues
+// the load slots that cover TR rows, so a launch of shorter tiles issues no
+// empty slots.
+template <class Q, int BPW, int ACT, bool MULTI, bool SW, int TR = 16>
 __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr, SweepWait &sw)
 {
     extern __shared__ float smem[];
     using G = MwGeom<Q, BPW>;
+    static_assert(TR >= 1 && TR <= 16, "tile rows");
+    constexpr int S = (TR + (int)G::RPS - 1) / (int)G::RPS;     // load slots
     constexpr bool AREG = BPW == 1;
     const uint32_t K = a.K, B = K / 256;
     const uint32_t W = blockDim.x >> 6, NT = blockDim.x;
@@ -435,11 +440,11 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint
     const uint32_t sh = REALIGN ? (blk * Q::BS) & 3u : 0u;     // 0 or 2 bytes
     const uint32_t voff = rsel * row_bytes + blk * Q::BS - sh + 16 * vl;
     const uint32_t loff = rsel * G::RS + jl * G::LB + 16 * vl;
-    u32x4 wa[G::S];
+    u32x4 wa[S];
     auto issue = [&](u32x4 *w, uint32_t tl) {
         const uint32_t tb = tl < ntl ? (tile0 + tl * GR) * tile_bytes : MQ_OOB;
 #pragma unroll
-        for (int s = 0; s < G::S; s++)
+        for (int s = 0; s < S; s++)
             w[s] = bload16_nt_so(rs, s * G::RPS + rsel < tr ? voff : MQ_OOB, tb + s * G::RPS * row_bytes);
     };
 
@@ -545,7 +550,7 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint
     auto process = [&](uint32_t tl) {
         wave_lds_sync();
 #pragma unroll
-        for (int s = 0; s < G::S; s++) {
+        for (int s = 0; s < S; s++) {
             u32x4 v = wa[s];
             if constexpr (REALIGN) v = q6_realign(v, sh);
             if (lane_ok && s * G::RPS + rsel < tr) *(u32x4 *)(L + loff + s * G::RPS * G::RS) = v;
