@@ -295,8 +295,35 @@ def decode_sweep(ctx, tokens):
     lq_bytes = rrr_hip.tensor_bytes(rrr_hip.Q6_K, shape.d_model, shape.vocab) + 3 * shape.d_model * 4 + shape.vocab * 4
     log(f"[bench] decode sweep with Q6_K token_embd logits: {ms_q:.4f} ms/token ({bq / (ms_q * 1e-3) / 1e9:.0f} GB/s), "
         f"argmax {tok_q}; the Q6_K logits alone {us_lq:.1f} us ({lq_bytes / (us_lq * 1e-6) / 1e9:.0f} GB/s)")
+    # the whole model over a 512-token prompt (the prefill GEMMs' M), every
+    # step on the GPU: one graph per prompt, timed from the same prompt rows
+    M = 512
+    prompt = decode.prompt_host(3, shape, M)
+    sw.load_prompt(prompt)
+    ctx.graph_begin()
+    sw.record_prefill(M, 0)
+    gp = ctx.graph_end()
+    times = []
+    for r in range(4):
+        sw.load_prompt(prompt)
+        ctx.sync()
+        ctx.timer_start()
+        gp.launch()
+        t_ms = ctx.timer_stop()
+        if r:
+            times.append(t_ms)
+    gp.destroy()
+    ms_pf = sorted(times)[len(times) // 2]
+    _, tok_pf, hid_pf = sw.prefill_results(M)
+    fl = decode.prefill_flops(shape, M)
+    log(f"[bench] prefill of {M} tokens through 32 layers + logits: {ms_pf:.3f} ms ({M / (ms_pf * 1e-3):.0f} tokens/s, "
+        f"{fl / (ms_pf * 1e-3) / 1e12:.0f} TFLOP/s in the layer GEMMs), argmax {tok_pf}")
     best = min(ms, ms_p)
     return {"ms_per_token": round(best, 5), "tokens": tokens, "bytes_per_token": b,
+            "prefill_512": {"ms": round(ms_pf, 4), "tokens_per_s": round(M / (ms_pf * 1e-3), 1),
+                            "gemm_flops": fl, "TFLOPs": round(fl / (ms_pf * 1e-3) / 1e12, 1),
+                            "frac_fp16_peak": round(fl / (ms_pf * 1e-3) / 2.5e15, 4), "argmax": tok_pf,
+                            "hidden_finite": bool(np.all(np.isfinite(hid_pf)))},
             "ms_per_token_at_pos_2047_with_attention": round(ms_a, 5),
             "q6k_token_embd_logits": {"ms_per_token": round(ms_q, 5), "bytes_per_token": bq,
                                       "GBs": round(bq / (ms_q * 1e-3) / 1e9, 1),

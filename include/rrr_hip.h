@@ -52,6 +52,7 @@ typedef enum rrr_status {
 /* GGUF tensor types on the path (gguf.rs:179, :187-189). */
 typedef enum rrr_ggml_type {
     RRR_TYPE_F32 = 0,
+    RRR_TYPE_F16 = 1,    /* activations only (prefill attention output) */
     RRR_TYPE_Q4_K = 12,
     RRR_TYPE_Q5_K = 13,
     RRR_TYPE_Q6_K = 14
@@ -207,6 +208,50 @@ int rrr_rope_kv_store(rrr_ctx *ctx, rrr_buf *qkv, const rrr_buf *rope_factors, u
 int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const rrr_buf *v_cache,
                   rrr_buf *out, uint32_t seq_len, uint32_t n_kv_heads, uint32_t heads_per_kv,
                   uint32_t head_dim);
+
+/* ---- prefill (forward_prefill_batched, phi4.rs:1200-1445, on the GPU) -- */
+
+/* rope_kv_store for `rows` prompt tokens in one launch: token t's qkv row
+ * (q_dim + 2 * kv_stride floats, rows back to back) at position pos0 + t,
+ * rotated in place and its K/V stored into cache row pos0 + t (the
+ * per-token rope_kv_store dispatches of phi4.rs:1285-1298).  Same arguments
+ * and checks as rrr_rope_kv_store otherwise. */
+int rrr_rope_kv_store_rows(rrr_ctx *ctx, rrr_buf *qkv, uint32_t rows, const rrr_buf *rope_factors,
+                           uint32_t n_factors, rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos0,
+                           uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t rope_dim,
+                           uint32_t q_dim, uint32_t kv_stride, float theta, float attn_factor);
+/* Causal attention of the prompt (the per-token attention dispatches of
+ * phi4.rs:1304-1312 in one launch): token t's query (the first
+ * n_kv_heads * heads_per_kv * head_dim floats of its qkv row, rows as in
+ * rrr_rope_kv_store_rows) attends over cache rows 0 .. pos0 + t, as
+ * rrr_attention with seq_len = pos0 + t + 1.  out: rows of n_heads * head_dim,
+ * out_type RRR_TYPE_F32 or RRR_TYPE_F16 (rounded to nearest even, the input
+ * of rrr_gemm_f16).  head_dim 128, heads_per_kv <= 8, pos0 + rows <= 2048;
+ * qkv and the caches 16-byte aligned. */
+int rrr_attention_prefill(rrr_ctx *ctx, const rrr_buf *qkv, uint32_t rows, const rrr_buf *k_cache,
+                          const rrr_buf *v_cache, rrr_buf *out, uint32_t out_type, uint32_t pos0,
+                          uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t head_dim);
+/* Y = P (accumulate 0) or Y += P (accumulate 1, the residual adds of
+ * phi4.rs:1321-1325 and :1396-1404 folded in), P = X . W^T with X an M x K
+ * f16 matrix, row m of P multiplied by row_scale[m] when row_scale is given
+ * (f32 powers of two, as rrr_silu_gate_f16 returns them; null: 1): the
+ * batched prompt GEMMs of phi4.rs:1257-1268, :1346-1391 on the prefill MFMA
+ * kernel (weights dequantized to f16 tiles, f32 accumulate).  Needs
+ * M % 128 == 0 and N % 64 == 0 (pad the prompt with zero rows). */
+int rrr_gemm_f16(rrr_ctx *ctx, const rrr_buf *X_f16, const rrr_buf *row_scale, const rrr_buf *W,
+                 uint32_t type, rrr_buf *Y, uint32_t K, uint32_t N, uint32_t M, uint32_t accumulate);
+/* rrr_rmsnorm (phi4.rs:593-599) with the same f32 results rounded to f16
+ * (nearest even), the input of rrr_gemm_f16 (|y| <= sqrt(d) * max|gamma|). */
+int rrr_rmsnorm_f16(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, rrr_buf *y_f16, uint32_t rows,
+                    uint32_t d, float eps);
+/* rrr_silu_gate (phi4.rs:1369-1373) in f16 block floating point: row r's f32
+ * results v, with max|v| = f * 2^e (f in [0.5, 1)), stored as
+ * f16(v * 2^(15 - e)) (nearest even; the scaling is exact) and
+ * row_scale[r] = 2^(e - 15) (f32); a row without a finite nonzero maximum
+ * is stored unscaled (row_scale 1).  Keeps f16's 11 significant bits for
+ * activations of any size; pass row_scale to rrr_gemm_f16. */
+int rrr_silu_gate_f16(rrr_ctx *ctx, const rrr_buf *gate_up, rrr_buf *mid_f16, rrr_buf *row_scale,
+                      uint32_t rows, uint32_t F);
 
 /* ---- fused decode-sweep ops (the four launches per layer) ------------ */
 

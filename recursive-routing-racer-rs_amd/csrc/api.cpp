@@ -662,12 +662,13 @@ int rrr_argmax_f32(rrr_ctx *ctx, const rrr_buf *logits, uint32_t V, rrr_buf *out
 
 // ---- decode glue: RoPE + f16 KV store, decode attention --------------------
 
-int rrr_rope_kv_store(rrr_ctx *ctx, rrr_buf *qkv, const rrr_buf *rope_factors, uint32_t n_factors, rrr_buf *k_cache,
-                      rrr_buf *v_cache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                      uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride, float theta, float attn_factor)
+// rows consecutive tokens at positions pos .. pos + rows - 1, their qkv rows
+// back to back
+static int rope_common(rrr_ctx *ctx, rrr_buf *qkv, uint32_t rows, const rrr_buf *rope_factors, uint32_t n_factors,
+                       rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads,
+                       uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride, float theta,
+                       float attn_factor, const char *what)
 {
-    TRY(check_ctx(ctx));
-    const char *what = "rrr_rope_kv_store";
     TRY(check_buf(ctx, qkv, what));
     TRY(check_buf(ctx, k_cache, what));
     TRY(check_buf(ctx, v_cache, what));
@@ -683,18 +684,41 @@ int rrr_rope_kv_store(rrr_ctx *ctx, rrr_buf *qkv, const rrr_buf *rope_factors, u
             return fail(RRR_ERR_BAD_SHAPE, "%s: kv_stride=%u is not n_kv_heads * head_dim", what, kv_stride);
         if (!(theta > 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: theta must be positive", what);
     }
-    TRY(need(qkv, 4 * ((uint64_t)q_dim + 2ull * kv_stride), what));
-    TRY(need(k_cache, 2 * ((uint64_t)pos + 1) * kv_stride, what));
-    TRY(need(v_cache, 2 * ((uint64_t)pos + 1) * kv_stride, what));
+    if (rows == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: rows must be positive", what);
+    if ((uint64_t)pos + rows > 0xFFFFFFFFull) return fail(RRR_ERR_BAD_SHAPE, "%s: positions past 2^32", what);
+    const uint64_t row = (uint64_t)q_dim + 2ull * kv_stride;
+    if (rows > 1 && row > 0xFFFFFFFFull) return fail(RRR_ERR_BAD_SHAPE, "%s: qkv row too long", what);
+    TRY(need(qkv, 4 * row * rows, what));
+    TRY(need(k_cache, 2 * ((uint64_t)pos + rows) * kv_stride, what));
+    TRY(need(v_cache, 2 * ((uint64_t)pos + rows) * kv_stride, what));
     if (n_factors) TRY(need(rope_factors, 4ull * n_factors, what));
     if (((uintptr_t)qkv->ptr | (uintptr_t)k_cache->ptr | (uintptr_t)v_cache->ptr) & 3)
         return fail(RRR_ERR_INVALID_ARG, "%s: buffers must be 4-byte aligned", what);
     TRY(device_ready(ctx));
     RopeArgs r{n_factors ? (const float *)rope_factors->ptr : nullptr, n_factors, pos, rope_dim ? n_heads : 0u,
-               head_dim, rope_dim, q_dim, kv_stride, theta, attn_factor};
+               head_dim, rope_dim, q_dim, kv_stride, theta, attn_factor, (uint32_t)row};
     return finish(ctx, launch_rope_kv_store((float *)qkv->ptr, r, (uint16_t *)k_cache->ptr, (uint16_t *)v_cache->ptr,
-                                            ctx->stream),
+                                            ctx->stream, rows),
                   what);
+}
+
+int rrr_rope_kv_store(rrr_ctx *ctx, rrr_buf *qkv, const rrr_buf *rope_factors, uint32_t n_factors, rrr_buf *k_cache,
+                      rrr_buf *v_cache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                      uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride, float theta, float attn_factor)
+{
+    TRY(check_ctx(ctx));
+    return rope_common(ctx, qkv, 1, rope_factors, n_factors, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim,
+                       rope_dim, q_dim, kv_stride, theta, attn_factor, "rrr_rope_kv_store");
+}
+
+int rrr_rope_kv_store_rows(rrr_ctx *ctx, rrr_buf *qkv, uint32_t rows, const rrr_buf *rope_factors, uint32_t n_factors,
+                           rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos0, uint32_t n_heads, uint32_t n_kv_heads,
+                           uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride, float theta,
+                           float attn_factor)
+{
+    TRY(check_ctx(ctx));
+    return rope_common(ctx, qkv, rows, rope_factors, n_factors, k_cache, v_cache, pos0, n_heads, n_kv_heads, head_dim,
+                       rope_dim, q_dim, kv_stride, theta, attn_factor, "rrr_rope_kv_store_rows");
 }
 
 int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const rrr_buf *v_cache, rrr_buf *out,
@@ -723,6 +747,108 @@ int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const 
     return finish(ctx, launch_attention((const float *)q->ptr, (const uint16_t *)k_cache->ptr,
                                         (const uint16_t *)v_cache->ptr, (float *)out->ptr, ctx->att_scratch, seq_len,
                                         n_kv_heads, heads_per_kv, sweep_cus(), ctx->stream),
+                  what);
+}
+
+// ---- prefill: causal attention over the prompt, f16-activation GEMMs --------
+
+int rrr_attention_prefill(rrr_ctx *ctx, const rrr_buf *qkv, uint32_t rows, const rrr_buf *k_cache,
+                          const rrr_buf *v_cache, rrr_buf *out, uint32_t out_type, uint32_t pos0, uint32_t n_kv_heads,
+                          uint32_t heads_per_kv, uint32_t head_dim)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_attention_prefill";
+    TRY(check_buf(ctx, qkv, what));
+    TRY(check_buf(ctx, k_cache, what));
+    TRY(check_buf(ctx, v_cache, what));
+    TRY(check_buf(ctx, out, what));
+    if (head_dim != ATT_HD) return fail(RRR_ERR_UNSUPPORTED, "%s: head_dim=%u (the kernels take %u)", what, head_dim, ATT_HD);
+    if (rows == 0 || n_kv_heads == 0 || heads_per_kv == 0)
+        return fail(RRR_ERR_BAD_SHAPE, "%s: rows, n_kv_heads and heads_per_kv must be positive", what);
+    if (out_type != RRR_TYPE_F32 && out_type != RRR_TYPE_F16)
+        return fail(RRR_ERR_BAD_TYPE, "%s: out_type %u (F32 or F16)", what, out_type);
+    if ((uint64_t)pos0 + rows > ATT_SEQ_MAX)
+        return fail(RRR_ERR_UNSUPPORTED, "%s: positions up to %llu exceed %u", what,
+                    (unsigned long long)pos0 + rows, ATT_SEQ_MAX);
+    if (heads_per_kv > 8 || (uint64_t)n_kv_heads * heads_per_kv > ATT_HEADS_MAX)
+        return fail(RRR_ERR_UNSUPPORTED, "%s: at most 8 query heads per KV head and %u query heads", what, ATT_HEADS_MAX);
+    const uint64_t nq = (uint64_t)n_kv_heads * heads_per_kv * head_dim, kvs = (uint64_t)n_kv_heads * head_dim;
+    const uint64_t row = nq + 2 * kvs;
+    TRY(need_f32(qkv, row * rows, what));
+    TRY(need(out, nq * rows * (out_type == RRR_TYPE_F16 ? 2 : 4), what));
+    TRY(need(k_cache, 2 * ((uint64_t)pos0 + rows) * kvs, what));
+    TRY(need(v_cache, 2 * ((uint64_t)pos0 + rows) * kvs, what));
+    if (((uintptr_t)qkv->ptr | (uintptr_t)k_cache->ptr | (uintptr_t)v_cache->ptr) & 15)
+        return fail(RRR_ERR_INVALID_ARG, "%s: qkv and caches must be 16-byte aligned", what);
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_attention_prefill((const float *)qkv->ptr, (uint32_t)row, rows,
+                                                (const uint16_t *)k_cache->ptr, (const uint16_t *)v_cache->ptr,
+                                                out->ptr, out_type == RRR_TYPE_F16, pos0, n_kv_heads, heads_per_kv,
+                                                ctx->stream),
+                  what);
+}
+
+int rrr_gemm_f16(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *row_scale, const rrr_buf *W, uint32_t type, rrr_buf *Y,
+                 uint32_t K, uint32_t N, uint32_t M, uint32_t accumulate)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_gemm_f16";
+    TRY(check_buf(ctx, X, what));
+    if (row_scale) {
+        TRY(check_buf(ctx, row_scale, what));
+        TRY(need_f32(row_scale, M, what));
+    }
+    TRY(check_buf(ctx, W, what));
+    TRY(check_buf(ctx, Y, what));
+    TRY(check_shape(type, K, N));
+    if (type == RRR_TYPE_F32) return fail(RRR_ERR_UNSUPPORTED, "%s: F32 weights are not a prefill shape", what);
+    if (M == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: M must be positive", what);
+    TRY(need(W, rrr_tensor_bytes(type, K, N), what));
+    TRY(need(X, (uint64_t)M * K * 2, what));
+    TRY(need_f32(Y, (uint64_t)M * N, what));
+    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2))
+        return fail(RRR_ERR_UNSUPPORTED, "%s: needs M %% 128 == 0 and N %% 64 == 0 (M=%u N=%u)", what, M, N);
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_gemm_f16((const uint16_t *)X->ptr, row_scale ? (const float *)row_scale->ptr : nullptr,
+                                       (const uint8_t *)W->ptr, type, (float *)Y->ptr, K, N, M, accumulate != 0,
+                                       ctx->stream),
+                  what);
+}
+
+int rrr_rmsnorm_f16(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, rrr_buf *y, uint32_t rows, uint32_t d,
+                    float eps)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_rmsnorm_f16";
+    TRY(check_buf(ctx, x, what));
+    TRY(check_buf(ctx, gamma, what));
+    TRY(check_buf(ctx, y, what));
+    if (rows == 0 || d == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: rows and d must be positive", what);
+    if (!(std::isfinite(eps) && eps >= 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: eps must be finite and >= 0", what);
+    TRY(need_f32(x, (uint64_t)rows * d, what));
+    TRY(need_f32(gamma, d, what));
+    TRY(need(y, 2ull * rows * d, what));
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_rmsnorm_f16((const float *)x->ptr, (const float *)gamma->ptr, (uint16_t *)y->ptr, rows, d,
+                                          eps, ctx->stream),
+                  what);
+}
+
+int rrr_silu_gate_f16(rrr_ctx *ctx, const rrr_buf *gate_up, rrr_buf *mid, rrr_buf *row_scale, uint32_t rows,
+                      uint32_t F)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_silu_gate_f16";
+    TRY(check_buf(ctx, gate_up, what));
+    TRY(check_buf(ctx, mid, what));
+    TRY(check_buf(ctx, row_scale, what));
+    if (rows == 0 || F == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: rows and F must be positive", what);
+    TRY(need_f32(gate_up, 2ull * rows * F, what));
+    TRY(need(mid, 2ull * rows * F, what));
+    TRY(need_f32(row_scale, rows, what));
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_silu_gate_f16((const float *)gate_up->ptr, (uint16_t *)mid->ptr,
+                                            (float *)row_scale->ptr, rows, F, ctx->stream),
                   what);
 }
 

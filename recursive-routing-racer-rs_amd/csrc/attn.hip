@@ -9,13 +9,14 @@ namespace rrr {
 
 __device__ __forceinline__ uint32_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
 
-// One rotation of apply_rope_cfg (phi4.rs:238-256) in f32: pair j of a head.
-__device__ __forceinline__ void rope_pair(float &x0, float &x1, uint32_t j, const RopeArgs &r)
+// One rotation of apply_rope_cfg (phi4.rs:238-256) in f32: pair j of a head
+// at position pos.
+__device__ __forceinline__ void rope_pair(float &x0, float &x1, uint32_t j, uint32_t pos, const RopeArgs &r)
 {
     const float base_freq = 1.0f / powf(r.theta, 2.0f * (float)j / (float)r.rope_dim);
     const float factor = j < r.n_factors ? r.factors[j] : 1.0f;
     const float freq = base_freq / factor;
-    const float angle = (float)r.pos * freq;
+    const float angle = (float)pos * freq;
     float sin_t, cos_t;
     sincosf(angle, &sin_t, &cos_t);
     const float cs = cos_t * r.attn_factor, ss = sin_t * r.attn_factor;
@@ -24,21 +25,24 @@ __device__ __forceinline__ void rope_pair(float &x0, float &x1, uint32_t j, cons
     x1 = a * ss + b * cs;
 }
 
-// Threads [0, nq): the Q rotation pairs (head i / (rope_dim/2), pair i %
-// (rope_dim/2)), rotated in place.  Threads [nq, nq + kv_stride/2): element
-// pair 2p of K (rotated in place when it lies in its head's first rope_dim
-// dims) and of V, both stored as f16 into row pos of the caches.
+// Token blockIdx.y (position pos + blockIdx.y, its qkv row_stride floats
+// after the previous one's).  Threads [0, nq): the Q rotation pairs (head
+// i / (rope_dim/2), pair i % (rope_dim/2)), rotated in place.  Threads
+// [nq, nq + kv_stride/2): element pair 2p of K (rotated in place when it lies
+// in its head's first rope_dim dims) and of V, both stored as f16 into the
+// token's row of the caches.
 __global__ __launch_bounds__(256) void rope_kv_store_kernel(float *__restrict__ qkv, RopeArgs r, uint32_t *__restrict__ kc,
                                                             uint32_t *__restrict__ vc)
 {
     const uint32_t half_rope = r.rope_dim / 2;
     const uint32_t nq = r.n_heads * half_rope, nkv = r.kv_stride / 2;
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x, pos = r.pos + blockIdx.y;
+    qkv += (size_t)blockIdx.y * r.row_stride;
     if (i < nq) {
         const uint32_t h = i / half_rope, j = i - h * half_rope;
         float *p = qkv + (size_t)h * r.head_dim + 2 * j;
         float x0 = p[0], x1 = p[1];
-        rope_pair(x0, x1, j, r);
+        rope_pair(x0, x1, j, pos, r);
         p[0] = x0;
         p[1] = x1;
     } else if (i < nq + nkv) {
@@ -48,21 +52,22 @@ __global__ __launch_bounds__(256) void rope_kv_store_kernel(float *__restrict__ 
         float k0 = k[0], k1 = k[1];
         const uint32_t d = r.rope_dim ? e % r.head_dim : 0u;   // head_dim is 0 in the kv_store form
         if (d < r.rope_dim) {
-            rope_pair(k0, k1, d / 2, r);
+            rope_pair(k0, k1, d / 2, pos, r);
             k[0] = k0;
             k[1] = k1;
         }
-        const size_t w = ((size_t)r.pos * r.kv_stride + e) / 2;
+        const size_t w = ((size_t)pos * r.kv_stride + e) / 2;
         kc[w] = f16_bits(k0) | (f16_bits(k1) << 16);
         vc[w] = f16_bits(v[0]) | (f16_bits(v[1]) << 16);
     }
 }
 
-hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uint16_t *vc, hipStream_t s)
+hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uint16_t *vc, hipStream_t s,
+                                uint32_t rows)
 {
     const uint32_t n = r.n_heads * (r.rope_dim / 2) + r.kv_stride / 2;
-    if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(rope_kv_store_kernel, dim3((n + 255) / 256), dim3(256), 0, s, qkv, r, (uint32_t *)kc,
+    if (n == 0 || rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_kv_store_kernel, dim3((n + 255) / 256, rows), dim3(256), 0, s, qkv, r, (uint32_t *)kc,
                        (uint32_t *)vc);
     return hipGetLastError();
 }
@@ -328,6 +333,155 @@ hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *
     default: return hipErrorInvalidValue;
     }
 #undef RRR_ATT_CASE
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Causal prefill attention (the per-token attention dispatches of
+// forward_prefill_batched, phi4.rs:1304-1312, for all prompt tokens in one
+// launch).  Workgroup (g, tok) takes KV head g for token tok at position
+// pos0 + tok, over cache rows 0 .. pos0 + tok.  The lane layout, scores and
+// online softmax are the decode kernel's; the rows are walked in chunks of
+// 16 * ATT_ROWS_PER_GROUP (lane group grp takes rows grp, grp + 16, ... of a
+// chunk), the next chunk's K/V loads issued before the current chunk is
+// scored (rows past the end repeat the last row: no branch around the loads).
+// The 16 lane groups are merged in LDS in a fixed order.
+template <int HPK, bool F16OUT>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restrict__ qkv, uint32_t row_stride,
+                                                           const uint16_t *__restrict__ kc,
+                                                           const uint16_t *__restrict__ vc, void *__restrict__ out,
+                                                           uint32_t pos0, uint32_t kv_stride, float qscale)
+{
+    constexpr uint32_t CH = 16 * ATT_ROWS_PER_GROUP;
+    __shared__ float gml[16][HPK][2];
+    __shared__ __attribute__((aligned(16))) float go[16][HPK][ATT_HD];
+    const uint32_t g = blockIdx.x, tok = blockIdx.y;
+    const uint32_t t = threadIdx.x, grp = t >> 4, li = t & 15;
+    const uint32_t L = pos0 + tok + 1, nch = (L + CH - 1) / CH;
+
+    u32x4 kr[ATT_ROWS_PER_GROUP], vr[ATT_ROWS_PER_GROUP], kn[ATT_ROWS_PER_GROUP], vn[ATT_ROWS_PER_GROUP];
+    auto load = [&](u32x4 *kd, u32x4 *vd, uint32_t c) {
+#pragma unroll
+        for (int k = 0; k < (int)ATT_ROWS_PER_GROUP; k++) {
+            const uint32_t row = min(c * CH + grp + 16 * k, L - 1);
+            const size_t off = (size_t)row * kv_stride + (size_t)g * ATT_HD + 8 * li;
+            kd[k] = *(const u32x4 *)(kc + off);
+            vd[k] = *(const u32x4 *)(vc + off);
+        }
+    };
+    load(kr, vr, 0);
+    const float *q = qkv + (size_t)tok * row_stride;
+    float qv[HPK][8];
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        const float4 *qp = (const float4 *)(q + (size_t)(g * HPK + h) * ATT_HD + 8 * li);
+        const float4 a = qp[0], b = qp[1];
+        qv[h][0] = a.x * qscale; qv[h][1] = a.y * qscale; qv[h][2] = a.z * qscale; qv[h][3] = a.w * qscale;
+        qv[h][4] = b.x * qscale; qv[h][5] = b.y * qscale; qv[h][6] = b.z * qscale; qv[h][7] = b.w * qscale;
+    }
+    float m[HPK], l[HPK], o[HPK][8];
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        m[h] = -__builtin_inff();
+        l[h] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; d++) o[h][d] = 0.0f;
+    }
+    for (uint32_t c = 0; c < nch; c++) {
+        load(kn, vn, min(c + 1, nch - 1));
+#pragma unroll
+        for (int k = 0; k < (int)ATT_ROWS_PER_GROUP; k++) {
+            const bool live = c * CH + grp + 16 * k < L;
+            float kf[8], v[8];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                kf[2 * w] = h2f(kr[k][w] & 0xFFFFu);
+                kf[2 * w + 1] = h2f(kr[k][w] >> 16);
+                v[2 * w] = h2f(vr[k][w] & 0xFFFFu);
+                v[2 * w + 1] = h2f(vr[k][w] >> 16);
+            }
+#pragma unroll
+            for (int h = 0; h < HPK; h++) {
+                float sc = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 8; d++) sc = fmaf(qv[h][d], kf[d], sc);
+                sc = row16_sum(sc);
+                if (live) {
+                    const float mn = fmaxf(m[h], sc);
+                    const float cf = exp2f(m[h] - mn), p = exp2f(sc - mn);
+                    l[h] = fmaf(l[h], cf, p);
+#pragma unroll
+                    for (int d = 0; d < 8; d++) o[h][d] = fmaf(o[h][d], cf, p * v[d]);
+                    m[h] = mn;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < (int)ATT_ROWS_PER_GROUP; k++) {
+            kr[k] = kn[k];
+            vr[k] = vn[k];
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        if (li == 0) {
+            gml[grp][h][0] = m[h];
+            gml[grp][h][1] = l[h];
+        }
+        float4 *dst = (float4 *)&go[grp][h][8 * li];
+        dst[0] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+        dst[1] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+    }
+    __syncthreads();
+    const size_t orow = (size_t)tok * gridDim.x * HPK * ATT_HD;
+    for (uint32_t i = t; i < HPK * ATT_HD; i += 256) {
+        const uint32_t h = i / ATT_HD, d = i % ATT_HD;
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int gi = 0; gi < 16; gi++) M = fmaxf(M, gml[gi][h][0]);
+        float Ls = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < 16; gi++) {
+            const float c = safe_scale(gml[gi][h][0], M);   // 0 for a group without rows
+            Ls = fmaf(gml[gi][h][1], c, Ls);
+            O = fmaf(go[gi][h][d], c, O);
+        }
+        const size_t oi = orow + (size_t)(g * HPK + h) * ATT_HD + d;
+        if constexpr (F16OUT)
+            ((_Float16 *)out)[oi] = (_Float16)(O / Ls);
+        else
+            ((float *)out)[oi] = O / Ls;
+    }
+}
+
+template <int HPK>
+static void go_attn_prefill(const float *qkv, uint32_t row_stride, uint32_t rows, const uint16_t *kc,
+                            const uint16_t *vc, void *out, bool out_f16, uint32_t pos0, uint32_t n_kv_heads,
+                            float qscale, hipStream_t s)
+{
+    const uint32_t kv_stride = n_kv_heads * ATT_HD;
+    if (out_f16)
+        hipLaunchKernelGGL((attn_prefill_kernel<HPK, true>), dim3(n_kv_heads, rows), dim3(256), 0, s, qkv, row_stride,
+                           kc, vc, out, pos0, kv_stride, qscale);
+    else
+        hipLaunchKernelGGL((attn_prefill_kernel<HPK, false>), dim3(n_kv_heads, rows), dim3(256), 0, s, qkv,
+                           row_stride, kc, vc, out, pos0, kv_stride, qscale);
+}
+
+hipError_t launch_attention_prefill(const float *qkv, uint32_t row_stride, uint32_t rows, const uint16_t *kc,
+                                    const uint16_t *vc, void *out, bool out_f16, uint32_t pos0, uint32_t n_kv_heads,
+                                    uint32_t heads_per_kv, hipStream_t s)
+{
+    if (rows == 0) return hipSuccess;
+    const float qscale = (float)(1.4426950408889634 / sqrt((double)ATT_HD));   // log2(e) / sqrt(head_dim)
+#define RRR_ATTP_CASE(H) \
+    case H: go_attn_prefill<H>(qkv, row_stride, rows, kc, vc, out, out_f16, pos0, n_kv_heads, qscale, s); break;
+    switch (heads_per_kv) {
+        RRR_ATTP_CASE(1) RRR_ATTP_CASE(2) RRR_ATTP_CASE(3) RRR_ATTP_CASE(4)
+        RRR_ATTP_CASE(5) RRR_ATTP_CASE(6) RRR_ATTP_CASE(7) RRR_ATTP_CASE(8)
+    default: return hipErrorInvalidValue;
+    }
+#undef RRR_ATTP_CASE
     return hipGetLastError();
 }
 

@@ -92,6 +92,13 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, RRR_WAVE));
+    return v;
+}
+
 // Workgroup (256 threads) sum of per-thread partials: a fixed wave butterfly,
 // then waves 0..3 in order.  `red` is 4 floats of LDS.  Every thread returns
 // the same value.

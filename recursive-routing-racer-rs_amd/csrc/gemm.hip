@@ -1,6 +1,7 @@
-// gemm.hip -- prefill dequant-GEMM: Y[M][N] = X_bf16[M][K] . W[N][K]^T with W
-// in raw Q4_K / Q5_K / Q6_K super-blocks (the batched shape of phi4.rs:1257-1268
-// at prompt length; the reference has no MFMA kernel for it).
+// gemm.hip -- prefill dequant-GEMM: Y[M][N] = X[M][K] . W[N][K]^T (or Y +=, the
+// residual of the layer folded in) with X in bf16 or f16 and W in raw Q4_K /
+// Q5_K / Q6_K super-blocks (the batched shape of phi4.rs:1257-1268 at prompt
+// length; the reference has no MFMA kernel for it).
 //
 // Workgroup: 512 threads.  Waves 0-3 (2 x 2) each own a (BM/2) x (BN/2)
 // block of 16x16 v_mfma_f32_16x16x32_f16 tiles with fp32 accumulators (lane
@@ -10,7 +11,7 @@
 // K steps of BK elements.  Per step each staging thread dequantizes
 // UE = BN*BK/256 consecutive elements of one weight row into an fp16 LDS tile
 // and converts BM*BK/256 elements of X from bf16 to fp16 (exact for |x| in
-// f16's normal range).  The dequant runs in packed fp16: v_perm places
+// f16's normal range; f16 X is copied as it is).  The dequant runs in packed fp16: v_perm places
 // each quant byte q under the exponent of 1024 (f16 0x64qq = 1024 + q), an
 // exact v_pk_add removes the 1024 (1056 for Q6_K's offset), and one
 // v_pk_fma / v_pk_mul applies the sub-block scale and min (phi4.rs:444-542:
@@ -169,9 +170,9 @@ struct GqQ6K {
 // into the other LDS buffer, so every SIMD holds one wave of each kind and the
 // staging VALU fills the matrix core's gaps.  Both roles pass one barrier per
 // step (plus one after the prologue) on separate straight-line paths.
-template <template <int> class QT, int BM, int BN, int BK>
+template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC>
 __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K,
-                                                      uint32_t N, uint32_t M, uint32_t tiles_n)
+                                                      uint32_t N, uint32_t M, uint32_t tiles_n, const float *rscale)
 {
     constexpr int LDK = BK + 8;                            // f16 per LDS row (16-byte pad)
     constexpr int TI = BM / 32, TJ = BN / 32;              // 16x16 tiles per MFMA wave
@@ -232,8 +233,13 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
             for (int i = 0; i < XE / 8; i++) {
                 const u32x4 v = st.xv[i];
                 u32x4 h;
+                if constexpr (XH) {
+                    h = v;
+                } else {
 #pragma unroll
-                for (int c = 0; c < 4; c++) h[c] = pk_f16(__uint_as_float(v[c] << 16), __uint_as_float(v[c] & 0xFFFF0000u));
+                    for (int c = 0; c < 4; c++)
+                        h[c] = pk_f16(__uint_as_float(v[c] << 16), __uint_as_float(v[c] & 0xFFFF0000u));
+                }
                 *(u32x4 *)(xd + 8 * i) = h;
             }
         };
@@ -295,7 +301,8 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         __syncthreads();
     }
 
-    // D rows 4*(l/16)+r of column l%16 in register r
+    // D rows 4*(l/16)+r of column l%16 in register r; the row scales (powers
+    // of two) are exact
 #pragma unroll
     for (int i = 0; i < TI; i++)
 #pragma unroll
@@ -304,50 +311,69 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint32_t m = m0 + wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + r;
-                Y[(uint64_t)m * N + n] = acc[i][j][r];
+                const float v = rscale ? acc[i][j][r] * rscale[m] : acc[i][j][r];
+                if constexpr (ACC)
+                    Y[(uint64_t)m * N + n] += v;
+                else
+                    Y[(uint64_t)m * N + n] = v;
             }
         }
 }
 
-template <template <int> class QT, int BM, int BN, int BK>
-static hipError_t go_gemm(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K, uint32_t N, uint32_t M,
-                          hipStream_t s)
+template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC>
+static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K, uint32_t N,
+                          uint32_t M, hipStream_t s)
 {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * 2;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
     const uint32_t tiles_n = N / BN, tiles = tiles_n * (M / BM);
-    hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK>), dim3(tiles), dim3(512), lds, s, X, W, Y, K, N, M, tiles_n);
+    hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC>), dim3(tiles), dim3(512), lds, s, X, W, Y, K, N, M,
+                       tiles_n, rscale);
     return hipGetLastError();
 }
 
-template <template <int> class QT>
-static hipError_t go_gemm_t(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K, uint32_t N, uint32_t M,
-                            hipStream_t s)
+template <template <int> class QT, bool XH, bool ACC>
+static hipError_t go_gemm_t(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K,
+                            uint32_t N, uint32_t M, hipStream_t s)
 {
     // 256 x 128 tiles when they cover at least half of the CUs, else 128 x 64
     // (with K steps of 128 so each barrier covers as much MFMA work)
     if (M % 256 == 0 && N % 128 == 0 && (N / 128) * (M / 256) >= 128)
-        return go_gemm<QT, 256, 128, 64>(X, W, Y, K, N, M, s);
-    return go_gemm<QT, 128, 64, 128>(X, W, Y, K, N, M, s);
+        return go_gemm<QT, 256, 128, 64, XH, ACC>(X, rscale, W, Y, K, N, M, s);
+    return go_gemm<QT, 128, 64, 128, XH, ACC>(X, rscale, W, Y, K, N, M, s);
 }
 
-bool gemm_bf16_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t w_bytes, uint64_t x_bytes)
+bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t x_bytes)
 {
-    (void)w_bytes;
     return (type == T_Q4_K || type == T_Q5_K || type == T_Q6_K) && K % 256 == 0 && N % 64 == 0 && M % 128 == 0 &&
            (uint64_t)N * (K / 256) * 210 + RRR_READ_SLACK < GM_OOB && x_bytes + RRR_READ_SLACK < GM_OOB;
+}
+
+template <bool XH, bool ACC>
+static hipError_t go_gemm_q(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
+                            uint32_t K, uint32_t N, uint32_t M, hipStream_t s)
+{
+    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2)) return hipErrorNotSupported;
+    switch (type) {
+    case T_Q4_K: return go_gemm_t<GqQ4K, XH, ACC>(X, rscale, W, Y, K, N, M, s);
+    case T_Q5_K: return go_gemm_t<GqQ5K, XH, ACC>(X, rscale, W, Y, K, N, M, s);
+    case T_Q6_K: return go_gemm_t<GqQ6K, XH, ACC>(X, rscale, W, Y, K, N, M, s);
+    default: return hipErrorNotSupported;
+    }
 }
 
 hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint64_t w_bytes, uint32_t type, float *Y,
                             uint32_t K, uint32_t N, uint32_t M, hipStream_t s)
 {
-    if (!gemm_bf16_supported(type, K, N, M, w_bytes, (uint64_t)M * K * 2)) return hipErrorNotSupported;
-    switch (type) {
-    case T_Q4_K: return go_gemm_t<GqQ4K>(X, W, Y, K, N, M, s);
-    case T_Q5_K: return go_gemm_t<GqQ5K>(X, W, Y, K, N, M, s);
-    case T_Q6_K: return go_gemm_t<GqQ6K>(X, W, Y, K, N, M, s);
-    default: return hipErrorNotSupported;
-    }
+    (void)w_bytes;
+    return go_gemm_q<false, false>(X, nullptr, W, type, Y, K, N, M, s);
+}
+
+hipError_t launch_gemm_f16(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
+                           uint32_t K, uint32_t N, uint32_t M, bool accumulate, hipStream_t s)
+{
+    return accumulate ? go_gemm_q<true, true>(X, rscale, W, type, Y, K, N, M, s)
+                      : go_gemm_q<true, false>(X, rscale, W, type, Y, K, N, M, s);
 }
 
 }  // namespace rrr

@@ -76,8 +76,11 @@ struct RopeArgs {
     uint32_t n_factors;
     uint32_t pos, n_heads, head_dim, rope_dim, q_dim, kv_stride;
     float theta, attn_factor;
+    uint32_t row_stride;    // floats from one token's qkv row to the next (rows > 1)
 };
-hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uint16_t *vc, hipStream_t s);
+// rows consecutive tokens at positions pos .. pos + rows - 1
+hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uint16_t *vc, hipStream_t s,
+                                uint32_t rows = 1);
 // Decode attention (attn.hip): head_dim ATT_HD, up to ATT_HEADS_MAX query
 // heads (ATT_HEADS_MAX KV heads), `scratch` of attention_scratch_bytes()
 // zeroed once before the first call (its counters return to zero after
@@ -89,7 +92,26 @@ void attention_plan(uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, ui
                     uint32_t &per);
 hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out, void *scratch,
                             uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t cus, hipStream_t s);
+// Causal prefill attention (attn.hip): token t (< rows) of qkv rows of
+// row_stride floats, at position pos0 + t, attends over cache rows
+// 0 .. pos0 + t; out rows of n_kv_heads * heads_per_kv * ATT_HD, f32 or f16.
+hipError_t launch_attention_prefill(const float *qkv, uint32_t row_stride, uint32_t rows, const uint16_t *kc,
+                                    const uint16_t *vc, void *out, bool out_f16, uint32_t pos0, uint32_t n_kv_heads,
+                                    uint32_t heads_per_kv, hipStream_t s);
+// Prefill dequant-GEMM (gemm.hip): X is M x K bf16 or f16 bits; Y = X . W^T,
+// or Y += X . W^T with accumulate; with rscale, row m of the product is
+// multiplied by rscale[m] (a power of two: exact) first
+bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t x_bytes);
 hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint64_t w_bytes, uint32_t type,
                             float *Y, uint32_t K, uint32_t N, uint32_t M, hipStream_t s);
+hipError_t launch_gemm_f16(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
+                           uint32_t K, uint32_t N, uint32_t M, bool accumulate, hipStream_t s);
+// f16 (round to nearest even) outputs of RMSNorm rows and of silu_gate rows
+// (the latter scaled per row by a power of two, rscale undoing it), the
+// activations of the prefill GEMMs (ops.hip)
+hipError_t launch_rmsnorm_f16(const float *x, const float *g, uint16_t *y, uint32_t rows, uint32_t d, float eps,
+                              hipStream_t s);
+hipError_t launch_silu_gate_f16(const float *gu, uint16_t *mid, float *rscale, uint32_t rows, uint32_t F,
+                                hipStream_t s);
 
 }  // namespace rrr

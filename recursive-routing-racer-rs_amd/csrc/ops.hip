@@ -79,16 +79,37 @@ hipError_t launch_dequant(uint32_t type, const uint8_t *W, uint64_t w_bytes, flo
     return hipGetLastError();
 }
 
+// An f32 result as output type TO: itself, or its f16 rounding (nearest
+// even).  The asm keeps the f32 value: without it the compiler may fold the
+// last multiply into one mixed-precision op that rounds the exact product to
+// f16 once, which is not the f32 result's rounding.
+template <typename TO>
+__device__ __forceinline__ TO to_out(float v)
+{
+    if constexpr (sizeof(TO) == 2) asm volatile("" : "+v"(v));
+    return (TO)v;
+}
+// Four outputs at float4 index f of a row: f32, or f16 rounded to nearest
+// even (the prefill GEMMs' activations).
+__device__ __forceinline__ void store4(float *y, uint32_t f, float4 v) { ((float4 *)y)[f] = v; }
+__device__ __forceinline__ void store4(_Float16 *y, uint32_t f, float4 v)
+{
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    ((h4 *)y)[f] = h4{to_out<_Float16>(v.x), to_out<_Float16>(v.y), to_out<_Float16>(v.z), to_out<_Float16>(v.w)};
+}
+
 // ---------------------------------------------------------------------------
 // RMSNorm (phi4.rs:593-599): one 256-thread workgroup per row; the sum of
 // squares uses the same fixed-order reduction as the fused GEMV staging, so
-// rmsnorm -> gemv and the fused gemv_rmsnorm produce identical bits.
+// rmsnorm -> gemv and the fused gemv_rmsnorm produce identical bits.  TO =
+// _Float16 rounds the same f32 results to f16.
+template <typename TO>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ g,
-                                                      float *__restrict__ y, uint32_t d, float eps)
+                                                      TO *__restrict__ y, uint32_t d, float eps)
 {
     __shared__ float red[4];
     const float *xr = x + (uint64_t)blockIdx.x * d;
-    float *yr = y + (uint64_t)blockIdx.x * d;
+    TO *yr = y + (uint64_t)blockIdx.x * d;
     const uint32_t t = threadIdx.x;
     if (d % 4 == 0 && d <= 8 * 4 * 256) {
         // the row stays in registers (one pass over x); thread t owns the
@@ -112,38 +133,83 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
             const uint32_t f = t + 256u * j;
             if (f < d / 4) {
                 const float4 w = ((const float4 *)g)[f];
-                ((float4 *)yr)[f] = make_float4(__fmul_rn(__fmul_rn(w.x, v[j].x), inv), __fmul_rn(__fmul_rn(w.y, v[j].y), inv),
-                                                __fmul_rn(__fmul_rn(w.z, v[j].z), inv), __fmul_rn(__fmul_rn(w.w, v[j].w), inv));
+                store4(yr, f, make_float4(__fmul_rn(__fmul_rn(w.x, v[j].x), inv), __fmul_rn(__fmul_rn(w.y, v[j].y), inv),
+                                          __fmul_rn(__fmul_rn(w.z, v[j].z), inv), __fmul_rn(__fmul_rn(w.w, v[j].w), inv)));
             }
         }
         return;
     }
     const float inv = rms_inv(block_sumsq_256(xr, d, red), d, eps);
-    for (uint32_t i = t; i < d; i += 256) yr[i] = __fmul_rn(__fmul_rn(g[i], xr[i]), inv);
+    for (uint32_t i = t; i < d; i += 256) yr[i] = to_out<TO>(__fmul_rn(__fmul_rn(g[i], xr[i]), inv));
 }
 
 hipError_t launch_rmsnorm(const float *x, const float *g, float *y, uint32_t rows, uint32_t d, float eps,
                           hipStream_t s)
 {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, g, y, d, eps);
+    hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3(rows), dim3(256), 0, s, x, g, y, d, eps);
     return hipGetLastError();
 }
 
-// silu_gate (phi4.rs:1369-1373): rows of [gate(F) | up(F)] -> rows of F.
-__global__ __launch_bounds__(256) void silu_gate_kernel(const float *__restrict__ gu, float *__restrict__ mid,
+hipError_t launch_rmsnorm_f16(const float *x, const float *g, uint16_t *y, uint32_t rows, uint32_t d, float eps,
+                              hipStream_t s)
+{
+    hipLaunchKernelGGL(rmsnorm_kernel<_Float16>, dim3(rows), dim3(256), 0, s, x, g, (_Float16 *)y, d, eps);
+    return hipGetLastError();
+}
+
+// silu_gate (phi4.rs:1369-1373): rows of [gate(F) | up(F)] -> rows of F (f32,
+// or the same values rounded to f16).
+template <typename TO>
+__global__ __launch_bounds__(256) void silu_gate_kernel(const float *__restrict__ gu, TO *__restrict__ mid,
                                                         uint32_t F, uint64_t total)
 {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= total) return;
     const uint64_t r = i / F, c = i - r * F;
     const float *row = gu + r * 2 * F;
-    mid[i] = silu_f(row[c]) * row[F + c];
+    mid[i] = to_out<TO>(silu_f(row[c]) * row[F + c]);
 }
 
 hipError_t launch_silu_gate(const float *gu, float *mid, uint32_t rows, uint32_t F, hipStream_t s)
 {
     const uint64_t total = (uint64_t)rows * F;
-    hipLaunchKernelGGL(silu_gate_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, gu, mid, F, total);
+    hipLaunchKernelGGL(silu_gate_kernel<float>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, gu, mid, F,
+                       total);
+    return hipGetLastError();
+}
+
+// silu_gate rows in f16 block floating point: one 256-thread workgroup per
+// row computes v = silu(gate) * up (the f32 values of silu_gate_kernel), the
+// row's largest |v| = f * 2^e (f in [0.5, 1)), and stores f16(v * 2^(15 - e))
+// (the scaling is exact, so the row's largest magnitude lands in [2^14,
+// 2^15) and every value keeps f16's 11 significant bits however large the
+// activations grow); rscale[row] = 2^(e - 15) undoes it.  A row with no
+// finite nonzero maximum is stored unscaled (rscale 1).
+__global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__restrict__ gu,
+                                                                 _Float16 *__restrict__ mid,
+                                                                 float *__restrict__ rscale, uint32_t F)
+{
+    __shared__ float red[4];
+    const float *row = gu + (uint64_t)blockIdx.x * 2 * F;
+    _Float16 *out = mid + (uint64_t)blockIdx.x * F;
+    const uint32_t t = threadIdx.x;
+    float m = 0.0f;
+    for (uint32_t i = t; i < F; i += 256) m = fmaxf(m, fabsf(silu_f(row[i]) * row[F + i]));
+    m = wave_max(m);
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 15;
+    if (m > 0.0f && __builtin_isfinite(m)) (void)frexpf(m, &e);
+    const float sc = ldexpf(1.0f, 15 - e);
+    for (uint32_t i = t; i < F; i += 256) out[i] = to_out<_Float16>((silu_f(row[i]) * row[F + i]) * sc);
+    if (t == 0) rscale[blockIdx.x] = ldexpf(1.0f, e - 15);
+}
+
+hipError_t launch_silu_gate_f16(const float *gu, uint16_t *mid, float *rscale, uint32_t rows, uint32_t F,
+                                hipStream_t s)
+{
+    hipLaunchKernelGGL(silu_gate_f16_rows_kernel, dim3(rows), dim3(256), 0, s, gu, (_Float16 *)mid, rscale, F);
     return hipGetLastError();
 }
 

@@ -98,7 +98,7 @@ def _stream(layer, slot):
 
 
 S_ATTN_NORM, S_QKV, S_O, S_FFN_NORM, S_UP, S_DOWN = range(6)
-S_OUT_NORM, S_EMB, S_X, S_ROPE, S_EMB_Q6K = 10, 11, 12, 13, 14
+S_OUT_NORM, S_EMB, S_X, S_ROPE, S_EMB_Q6K, S_PROMPT = 10, 11, 12, 13, 14, 15
 
 
 def gamma_host(seed, stream, d):
@@ -127,6 +127,17 @@ def embedding_q6k_host(seed, shape):
     256 blocks), the tensor the reference dequantizes into its F32 logits
     matrix (phi4.rs:709, :866-893)."""
     return synth.weight(seed, S_EMB_Q6K, E.Q6_K, shape.d_model, shape.vocab)
+
+
+def prompt_host(seed, shape, M):
+    """The hidden states of M prompt tokens (stand in for their embedding
+    rows), rows of d_model f32."""
+    return synth.normal_f32(seed, S_PROMPT, M * shape.d_model).reshape(M, shape.d_model)
+
+
+def prefill_flops(shape, M):
+    """2 M N K over the layer GEMMs of an M-token prompt (the MFMA work)."""
+    return sum(2 * M * N * K for i in range(shape.n_layers) for _, _, K, N in shape.layer_tensors(i))
 
 
 def rope_factors_host(seed, shape):
@@ -233,6 +244,93 @@ class DecodeSweep:
             c.logits_rmsnorm(self.hidden, self.out_norm, s.eps, self.emb, self.logits, s.d_model, s.vocab,
                              E.LOGITS_CHUNKED, s.chunk)
         c.argmax_f32(self.logits, s.vocab, self.token)
+
+    # ---- prefill: the prompt's tokens through every layer at once ----------
+    PREFILL_ROWS = 128   # the prefill GEMM's row block; prompts are padded to it with zero rows
+
+    def prefill_buffers(self, M):
+        """Activation rows of an M-token prompt, padded to a multiple of
+        PREFILL_ROWS rows (allocated once for the largest prompt so far)."""
+        s, c = self.shape, self.ctx
+        Mp = -(-M // self.PREFILL_ROWS) * self.PREFILL_ROWS
+        pf = getattr(self, "_pf", None)
+        if pf is None or pf["Mp"] < Mp:
+            if pf is not None:
+                for v in pf["last"].values():
+                    v.free()
+                for k, b in pf.items():
+                    if k not in ("Mp", "last"):
+                        b.free()
+            d, F = s.d_model, s.ffn_dim
+            pf = {"Mp": Mp, "hid": c.alloc(Mp * d * 4), "n16": c.alloc(Mp * d * 2),
+                  "qkv": c.alloc(Mp * s.qkv_dim * 4), "att16": c.alloc(Mp * d * 2),
+                  "gu": c.alloc(Mp * 2 * F * 4), "mid16": c.alloc(Mp * F * 2), "mid_scale": c.alloc(Mp * 4)}
+            for k, b in pf.items():
+                if k != "Mp":
+                    c.fill_u32(b, 0)
+            pf["last"] = {}   # views of the last prompt row, by prompt length
+            self._pf = pf
+        return pf
+
+    def record_prefill(self, M, pos0=0):
+        """The prompt's M tokens at positions pos0 .. pos0 + M - 1 through
+        every layer (forward_prefill_batched, phi4.rs:1200-1445, with every
+        step on the GPU): per layer RMSNorm rows -> QKV GEMM -> RoPE + KV
+        store of all rows -> causal attention -> O GEMM + residual -> RMSNorm
+        rows -> gate/up GEMM -> silu * up -> down GEMM + residual; then the
+        final RMSNorm, logits and argmax of the last token.  The GEMM inputs
+        are f16 (nearest even; silu * up in per-row block floating point);
+        the hidden states, qkv and gate/up stay f32.
+        The token rows must be in prefill_buffers(M)["hid"] (rows >= M zero),
+        e.g. from load_prompt().  Fills cache rows pos0 .. pos0 + M - 1."""
+        if not self.attention:
+            raise ValueError("prefill needs attention=True (the KV caches)")
+        s, c = self.shape, self.ctx
+        if M < 1 or pos0 + M > s.max_seq:
+            raise ValueError(f"positions {pos0}..{pos0 + M - 1} outside the cache")
+        pf = self.prefill_buffers(M)
+        Mp, d, F = pf["Mp"], s.d_model, s.ffn_dim
+        if M < Mp:   # rows past the prompt stay zero through every step
+            c.fill_u32(pf["att16"], 0, M * d * 2, (Mp - M) * d * 2)
+        for i, L in enumerate(self.layers):
+            kc, vc = self.kv[i]
+            c.rmsnorm_f16(pf["hid"], L["attn_norm"], pf["n16"], Mp, d, s.eps)
+            c.gemm_f16(pf["n16"], L["attn_qkv"], E.Q5_K, pf["qkv"], d, s.qkv_dim, Mp)
+            c.rope_kv_store_rows(pf["qkv"], M, self.rope_factors, s.rope_dim // 2, kc, vc, pos0, s.n_heads,
+                                 s.n_kv_heads, s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta,
+                                 s.rope_attn_factor)
+            c.attention_prefill(pf["qkv"], M, kc, vc, pf["att16"], pos0, s.n_kv_heads, s.heads_per_kv, s.head_dim,
+                                out_type=E.F16)
+            c.gemm_f16(pf["att16"], L["attn_output"], E.Q4_K, pf["hid"], d, d, Mp, accumulate=True)
+            c.rmsnorm_f16(pf["hid"], L["ffn_norm"], pf["n16"], Mp, d, s.eps)
+            c.gemm_f16(pf["n16"], L["ffn_up"], E.Q4_K, pf["gu"], d, 2 * F, Mp)
+            c.silu_gate_f16(pf["gu"], pf["mid16"], pf["mid_scale"], Mp, F)
+            c.gemm_f16(pf["mid16"], L["ffn_down"], s.down_type(i), pf["hid"], F, d, Mp, accumulate=True,
+                       row_scale=pf["mid_scale"])
+        if M not in pf["last"]:
+            pf["last"][M] = c.view(pf["hid"], (M - 1) * d * 4, d * 4)
+        hidden, self.hidden = self.hidden, pf["last"][M]
+        try:
+            self.record_logits()
+        finally:
+            self.hidden = hidden
+
+    def load_prompt(self, rows):
+        """Upload prompt hidden rows (M x d_model f32) into the prefill
+        buffers, zeroing the padding rows."""
+        M = rows.shape[0]
+        pf = self.prefill_buffers(M)
+        d = self.shape.d_model
+        self.ctx.upload(pf["hid"], np.ascontiguousarray(rows, np.float32))
+        if M < pf["Mp"]:
+            self.ctx.fill_u32(pf["hid"], 0, M * d * 4, (pf["Mp"] - M) * d * 4)
+        return pf
+
+    def prefill_results(self, M):
+        """(logits of the last token, argmax, hidden rows M x d_model)."""
+        c, s = self.ctx, self.shape
+        hid = c.download(self._pf["hid"], np.float32, M * s.d_model).reshape(M, s.d_model)
+        return (c.download(self.logits, np.float32, s.vocab), int(c.download(self.token, np.uint32, 1)[0]), hid)
 
     def sweep_ops(self):
         """The 4 fused GEMVs of every layer as one persistent sweep's op list

@@ -28,7 +28,7 @@ ERR_NO_DEVICE = -8
 ERR_STATE = -9
 ERR_STALE = -10
 
-F32, Q4_K, Q5_K, Q6_K = 0, 12, 13, 14
+F32, F16, Q4_K, Q5_K, Q6_K = 0, 1, 12, 13, 14
 LOGITS_ROWS, LOGITS_CHUNKED, LOGITS_Q6K = 0, 1, 2
 ACT_IDENTITY, ACT_SILU_GATE, ACT_GQA_V = 0, 1, 2
 SWEEP_GEMV_RMSNORM, SWEEP_GEMV_RESIDUAL = 0, 1
@@ -235,6 +235,29 @@ class Context:
     def attention(self, q, k_cache, v_cache, out, seq_len, n_kv_heads, heads_per_kv, head_dim):
         _check(self.lib.rrr_attention(self._h, q._h, k_cache._h, v_cache._h, out._h, seq_len, n_kv_heads,
                                       heads_per_kv, head_dim))
+
+    # ---- prefill -------------------------------------------------------
+    def rope_kv_store_rows(self, qkv, rows, rope_factors, n_factors, k_cache, v_cache, pos0, n_heads, n_kv_heads,
+                           head_dim, rope_dim, q_dim, kv_stride, theta=10000.0, attn_factor=1.190238):
+        _check(self.lib.rrr_rope_kv_store_rows(self._h, qkv._h, rows,
+                                               rope_factors._h if rope_factors is not None else None, n_factors,
+                                               k_cache._h, v_cache._h, pos0, n_heads, n_kv_heads, head_dim, rope_dim,
+                                               q_dim, kv_stride, theta, attn_factor))
+
+    def attention_prefill(self, qkv, rows, k_cache, v_cache, out, pos0, n_kv_heads, heads_per_kv, head_dim,
+                          out_type=F32):
+        _check(self.lib.rrr_attention_prefill(self._h, qkv._h, rows, k_cache._h, v_cache._h, out._h, out_type, pos0,
+                                              n_kv_heads, heads_per_kv, head_dim))
+
+    def gemm_f16(self, X, W, qtype, Y, K, N, M, accumulate=False, row_scale=None):
+        _check(self.lib.rrr_gemm_f16(self._h, X._h, row_scale._h if row_scale is not None else None, W._h, qtype,
+                                     Y._h, K, N, M, 1 if accumulate else 0))
+
+    def rmsnorm_f16(self, x, gamma, y, rows, d, eps=1e-5):
+        _check(self.lib.rrr_rmsnorm_f16(self._h, x._h, gamma._h, y._h, rows, d, eps))
+
+    def silu_gate_f16(self, gate_up, mid, row_scale, rows, F):
+        _check(self.lib.rrr_silu_gate_f16(self._h, gate_up._h, mid._h, row_scale._h, rows, F))
 
     def dispatch(self, name, bufs, push_u32, groups):
         arr = (ctypes.c_void_p * max(len(bufs), 1))(*[b.handle for b in bufs])

@@ -106,9 +106,9 @@ def vctx():
     c.close()
 
 
-def code_of(fn, *args):
+def code_of(fn, *args, **kw):
     with pytest.raises(rrr_hip.RrrError) as ei:
-        fn(*args)
+        fn(*args, **kw)
     return ei.value.code
 
 
@@ -257,6 +257,52 @@ def test_rope_kv_store_and_attention_validation(vctx):
     assert code_of(at, q, kc, vc, out, 2049, nkv, 3, hd) == ERR_UNSUPPORTED     # beyond 2048 cache rows
     assert code_of(at, q, kc, vc, out, 4, 8, 9, hd) == ERR_UNSUPPORTED
     assert code_of(at, q, kc, vc, out, 4, 16, 4, hd) in (ERR_UNSUPPORTED, ERR_SHORT_BUFFER)
+
+
+def test_prefill_validation(vctx):
+    nh, nkv, hd, rd = 24, 8, 128, 96
+    qd, kvs = nh * hd, nkv * hd
+    row = qd + 2 * kvs
+    rows = 4
+    qkv = vctx.alloc(rows * row * 4)
+    fac = vctx.alloc(48 * 4)
+    kc, vc = vctx.alloc(16 * kvs * 2), vctx.alloc(16 * kvs * 2)
+    rr = vctx.rope_kv_store_rows
+    assert code_of(rr, qkv, rows, fac, 48, kc, vc, 12, nh, nkv, hd, rd, qd, kvs) == ERR_NO_DEVICE
+    assert code_of(rr, qkv, rows, fac, 48, kc, vc, 13, nh, nkv, hd, rd, qd, kvs) == ERR_SHORT_BUFFER   # rows 13..16
+    assert code_of(rr, qkv, rows + 1, fac, 48, kc, vc, 0, nh, nkv, hd, rd, qd, kvs) == ERR_SHORT_BUFFER  # qkv
+    assert code_of(rr, qkv, 0, fac, 48, kc, vc, 0, nh, nkv, hd, rd, qd, kvs) == ERR_BAD_SHAPE
+    ap = vctx.attention_prefill
+    o32, o16 = vctx.alloc(rows * qd * 4), vctx.alloc(rows * qd * 2)
+    assert code_of(ap, qkv, rows, kc, vc, o32, 12, nkv, 3, hd) == ERR_NO_DEVICE
+    assert code_of(ap, qkv, rows, kc, vc, o16, 12, nkv, 3, hd, out_type=rrr_hip.F16) == ERR_NO_DEVICE
+    assert code_of(ap, qkv, rows, kc, vc, o16, 12, nkv, 3, hd) == ERR_SHORT_BUFFER          # f32 out in 2-byte room
+    assert code_of(ap, qkv, rows, kc, vc, o32, 13, nkv, 3, hd) == ERR_SHORT_BUFFER          # caches
+    assert code_of(ap, qkv, rows, kc, vc, o32, 12, nkv, 3, hd, out_type=14) == ERR_BAD_TYPE
+    assert code_of(ap, qkv, rows, kc, vc, o32, 2046, nkv, 3, hd) == ERR_UNSUPPORTED        # past 2048 rows
+    assert code_of(ap, qkv, rows, kc, vc, o32, 0, nkv, 3, 64) == ERR_UNSUPPORTED
+    assert code_of(ap, qkv, 0, kc, vc, o32, 0, nkv, 3, hd) == ERR_BAD_SHAPE
+    K, N, M = 3072, 3072, 128
+    W = vctx.alloc(rrr_hip.tensor_bytes(12, K, N))
+    X = vctx.alloc(M * K * 2)
+    Y = vctx.alloc(M * N * 4)
+    g = vctx.gemm_f16
+    assert code_of(g, X, W, 12, Y, K, N, M) == ERR_NO_DEVICE
+    assert code_of(g, X, W, 12, Y, K, N, M, accumulate=True) == ERR_NO_DEVICE
+    assert code_of(g, X, W, 12, Y, K, N, 100) == ERR_UNSUPPORTED        # M % 128
+    assert code_of(g, X, W, 12, Y, K, N - 64, M) == ERR_NO_DEVICE
+    assert code_of(g, X, W, 12, Y, K, N, 2 * M) == ERR_SHORT_BUFFER
+    assert code_of(g, X, W, 0, Y, K, N, M) == ERR_UNSUPPORTED
+    x, gm = vctx.alloc(M * K * 4), vctx.alloc(K * 4)
+    y16 = vctx.alloc(M * K * 2)
+    assert code_of(vctx.rmsnorm_f16, x, gm, y16, M, K) == ERR_NO_DEVICE
+    assert code_of(vctx.rmsnorm_f16, x, gm, y16, M + 1, K) == ERR_SHORT_BUFFER
+    rs = vctx.alloc(M * 4)
+    assert code_of(vctx.silu_gate_f16, x, y16, rs, M, K // 2) == ERR_NO_DEVICE
+    assert code_of(vctx.silu_gate_f16, x, y16, rs, M, K) == ERR_SHORT_BUFFER
+    assert code_of(vctx.silu_gate_f16, x, y16, rs, 2 * M, K // 4) == ERR_SHORT_BUFFER     # row scales
+    assert code_of(g, X, W, 12, Y, K, N, M, row_scale=rs) == ERR_NO_DEVICE
+    assert code_of(g, X, W, 12, Y, K, N, M, row_scale=vctx.alloc(4)) == ERR_SHORT_BUFFER
 
 
 def test_graph_state_rules(vctx):
