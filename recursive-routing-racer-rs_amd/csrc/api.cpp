@@ -83,6 +83,7 @@ struct rrr_ctx {
     hipEvent_t ev0, ev1;
     void *scratch;      // argmax partial candidates
     void *att_scratch;  // attention: per-KV-head counters (zero between calls) and split partials
+    void *gemm_ws;      // prefill GEMM: partials of split K (GEMM_WS_BYTES)
     std::unordered_set<rrr_buf *> bufs;
     std::unordered_set<rrr_graph *> graphs;
     std::unordered_set<rrr_sweep *> sweeps;
@@ -191,7 +192,7 @@ int rrr_init(int device, rrr_ctx **out)
     ctx->async = ctx->capturing = ctx->timer_started = false;
     ctx->stream = nullptr;
     ctx->ev0 = ctx->ev1 = nullptr;
-    ctx->scratch = ctx->att_scratch = nullptr;
+    ctx->scratch = ctx->att_scratch = ctx->gemm_ws = nullptr;
     if (!ctx->nodevice) {
         int n = rrr_device_count();
         if (device >= n) {
@@ -205,8 +206,10 @@ int rrr_init(int device, rrr_ctx **out)
         if (e == hipSuccess) e = hipMalloc(&ctx->scratch, argmax_partials_bytes());
         if (e == hipSuccess) e = hipMalloc(&ctx->att_scratch, attention_scratch_bytes());
         if (e == hipSuccess) e = hipMemset(ctx->att_scratch, 0, attention_scratch_bytes());
+        if (e == hipSuccess) e = hipMalloc(&ctx->gemm_ws, GEMM_WS_BYTES);
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) {
+            if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
             if (ctx->att_scratch) (void)hipFree(ctx->att_scratch);
             if (ctx->scratch) (void)hipFree(ctx->scratch);
             if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
@@ -251,6 +254,7 @@ int rrr_destroy(rrr_ctx *ctx)
             if (!b->parent && b->ptr) (void)hipFree(b->ptr);
         (void)hipFree(ctx->scratch);
         (void)hipFree(ctx->att_scratch);
+        (void)hipFree(ctx->gemm_ws);
         (void)hipEventDestroy(ctx->ev0);
         (void)hipEventDestroy(ctx->ev1);
         (void)hipStreamDestroy(ctx->stream);
@@ -531,8 +535,8 @@ int rrr_gemm_bf16(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t typ
     TRY(need(X, (uint64_t)M * K * 2, what));
     TRY(need_f32(Y, (uint64_t)M * N, what));
     TRY(device_ready(ctx));
-    hipError_t e = launch_gemm_bf16((const uint16_t *)X->ptr, (const uint8_t *)W->ptr, W->bytes, type, (float *)Y->ptr,
-                                    K, N, M, ctx->stream);
+    hipError_t e = launch_gemm_bf16((const uint16_t *)X->ptr, (const uint8_t *)W->ptr, type, (float *)Y->ptr, K, N, M,
+                                    (float *)ctx->gemm_ws, GEMM_WS_BYTES, ctx->stream);
     if (e == hipErrorNotSupported) return fail(RRR_ERR_UNSUPPORTED, "%s: shape not supported by this build", what);
     return finish(ctx, e, what);
 }
@@ -811,7 +815,7 @@ int rrr_gemm_f16(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *row_scale, const
     TRY(device_ready(ctx));
     return finish(ctx, launch_gemm_f16((const uint16_t *)X->ptr, row_scale ? (const float *)row_scale->ptr : nullptr,
                                        (const uint8_t *)W->ptr, type, (float *)Y->ptr, K, N, M, accumulate != 0,
-                                       ctx->stream),
+                                       (float *)ctx->gemm_ws, GEMM_WS_BYTES, ctx->stream),
                   what);
 }
 

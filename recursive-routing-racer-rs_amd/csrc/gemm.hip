@@ -23,6 +23,12 @@
 //
 // Tile order: the M/BM tiles of one N tile get workgroup ids congruent mod 8,
 // so they run on the same XCD and the weight tile is fetched from HBM once.
+//
+// Split K: when the BM x BN tiles are too few to fill the CUs (a 512-token
+// prompt against N = 3072 or 5120), workgroup (tile, ks) takes the K range
+// [ks * ksteps * BK, (ks + 1) * ksteps * BK) and writes its fp32 partial to a
+// workspace; gemm_splitk_reduce then adds the S partials of each output in
+// split order (deterministic), applies the row scale and stores or adds to Y.
 #include "device_common.h"
 #include "internal.h"
 
@@ -172,7 +178,8 @@ struct GqQ6K {
 // step (plus one after the prologue) on separate straight-line paths.
 template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC>
 __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K,
-                                                      uint32_t N, uint32_t M, uint32_t tiles_n, const float *rscale)
+                                                      uint32_t N, uint32_t M, uint32_t tiles_n, const float *rscale,
+                                                      uint32_t ksteps, float *ws)
 {
     constexpr int LDK = BK + 8;                            // f16 per LDS row (16-byte pad)
     constexpr int TI = BM / 32, TJ = BN / 32;              // 16x16 tiles per MFMA wave
@@ -185,8 +192,10 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     _Float16 *Bs = As + 2 * BM * LDK;                      // [2][BN][LDK]
 
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    // tile of this workgroup (same XCD for the M tiles of one N tile)
-    const uint32_t id = blockIdx.x, tiles_m = M / BM;
+    // tile of this workgroup (same XCD for the M tiles of one N tile) and its
+    // K split (the tile count is a multiple of 8 when K is split)
+    const uint32_t tiles_m = M / BM, ntile = tiles_n * tiles_m;
+    const uint32_t ks = blockIdx.x / ntile, id = blockIdx.x - ks * ntile;
     uint32_t nt, mt;
     if (tiles_n % 8 == 0) {
         nt = (id / (8 * tiles_m)) * 8 + id % 8;
@@ -196,7 +205,7 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         mt = id % tiles_m;
     }
     const uint32_t m0 = mt * BM, n0 = nt * BN;
-    const uint32_t nsteps = K / BK, B = K / 256;
+    const uint32_t nsteps = ksteps, s0 = ks * ksteps, B = K / 256;   // this split's steps, its first step
 
     if (wave >= 4) {
         // ---- producer: loads, dequant, conversion --------------------------
@@ -215,14 +224,14 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         // element e0 of the step's unit inside its super-block: chunk e0/64, lane part e0%64
         auto issue = [&](Set &st, uint32_t s) {
             const bool ok = s < nsteps;   // past the end: out-of-range offsets, zeros
-            const uint32_t e0 = (s * BK) % 256 + lb;
-            Q::load(st.raw, wrs, wvoff, ok ? (s * BK / 256) * Q::BS : GM_OOB, e0 >> 6, e0 & 63);
-            const uint32_t so = ok ? s * BK * 2 : GM_OOB;
+            const uint32_t sg = s0 + s, e0 = (sg * BK) % 256 + lb;
+            Q::load(st.raw, wrs, wvoff, ok ? (sg * BK / 256) * Q::BS : GM_OOB, e0 >> 6, e0 & 63);
+            const uint32_t so = ok ? sg * BK * 2 : GM_OOB;
 #pragma unroll
             for (int i = 0; i < XE / 8; i++) st.xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvoff + 16 * i, so, 0);
         };
         auto stage = [&](const Set &st, uint32_t s) {
-            const uint32_t buf = s & 1, e0 = (s * BK) % 256 + lb;
+            const uint32_t buf = s & 1, e0 = ((s0 + s) * BK) % 256 + lb;
             uint32_t o[UE / 2];
             Q::dequant(st.raw, e0 >> 6, e0 & 63, o);
             _Float16 *dst = Bs + (buf * BN + ur) * LDK + lb;
@@ -311,6 +320,10 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint32_t m = m0 + wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + r;
+                if (ws) {
+                    ws[((uint64_t)ks * M + m) * N + n] = acc[i][j][r];
+                    continue;
+                }
                 const float v = rscale ? acc[i][j][r] * rscale[m] : acc[i][j][r];
                 if constexpr (ACC)
                     Y[(uint64_t)m * N + n] += v;
@@ -320,27 +333,76 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         }
 }
 
+// Y (+)= rscale[m] * sum over the S partials of ws (in split order), four
+// outputs per thread (N % 4 == 0)
+template <bool ACC>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restrict__ ws, uint32_t S, uint32_t M,
+                                                          uint32_t N, float *__restrict__ Y,
+                                                          const float *__restrict__ rscale)
+{
+    const uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x, mn = (uint64_t)M * N;
+    if (4 * q >= mn) return;
+    float4 v = ((const float4 *)ws)[q];
+    for (uint32_t k = 1; k < S; k++) {
+        const float4 p = ((const float4 *)(ws + k * mn))[q];
+        v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+    }
+    if (rscale) {
+        const float r = rscale[(4 * q) / N];
+        v.x *= r; v.y *= r; v.z *= r; v.w *= r;
+    }
+    float4 *y = (float4 *)Y + q;
+    if constexpr (ACC) {
+        const float4 o = *y;
+        v.x = o.x + v.x; v.y = o.y + v.y; v.z = o.z + v.z; v.w = o.w + v.w;
+    }
+    *y = v;
+}
+
 template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC>
 static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K, uint32_t N,
-                          uint32_t M, hipStream_t s)
+                          uint32_t M, uint32_t S, float *ws, hipStream_t s)
 {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * 2;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
     const uint32_t tiles_n = N / BN, tiles = tiles_n * (M / BM);
-    hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC>), dim3(tiles), dim3(512), lds, s, X, W, Y, K, N, M,
-                       tiles_n, rscale);
+    hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC>), dim3(tiles * S), dim3(512), lds, s, X, W, Y, K, N, M,
+                       tiles_n, rscale, K / BK / S, S > 1 ? ws : nullptr);
+    if (S > 1) {
+        const uint64_t quads = (uint64_t)M * N / 4;
+        hipLaunchKernelGGL(gemm_splitk_reduce<ACC>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, ws, S, M,
+                           N, Y, rscale);
+    }
     return hipGetLastError();
+}
+
+// Splits of K for a grid of `tiles` large tiles: as many as keep every
+// workgroup in the first round over the MI355X's 256 CUs (a second round
+// costs a whole tile's time), at most 8, each a whole number of
+// super-blocks, their partials within the workspace; 1 when the tiles
+// already fill half of the CUs.
+static uint32_t gemm_splits(uint32_t tiles, uint32_t K, uint32_t M, uint32_t N, size_t ws_bytes)
+{
+    const uint32_t cus = 256;
+    if (tiles >= cus / 2 || tiles % 8) return 1;
+    uint32_t S = min(8u, cus / tiles);
+    while (S > 1 && ((K / 256) % S || (uint64_t)S * M * N * 4 > ws_bytes)) S--;
+    return S;
 }
 
 template <template <int> class QT, bool XH, bool ACC>
 static hipError_t go_gemm_t(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K,
-                            uint32_t N, uint32_t M, hipStream_t s)
+                            uint32_t N, uint32_t M, float *ws, size_t ws_bytes, hipStream_t s)
 {
-    // 256 x 128 tiles when they cover at least half of the CUs, else 128 x 64
-    // (with K steps of 128 so each barrier covers as much MFMA work)
-    if (M % 256 == 0 && N % 128 == 0 && (N / 128) * (M / 256) >= 128)
-        return go_gemm<QT, 256, 128, 64, XH, ACC>(X, rscale, W, Y, K, N, M, s);
-    return go_gemm<QT, 128, 64, 128, XH, ACC>(X, rscale, W, Y, K, N, M, s);
+    // 256 x 128 tiles when they cover at least half of the CUs, or with K
+    // split to do so; else 128 x 64 (with K steps of 128 so each barrier
+    // covers as much MFMA work)
+    if (M % 256 == 0 && N % 128 == 0) {
+        const uint32_t tiles = (N / 128) * (M / 256);
+        const uint32_t S = ws ? gemm_splits(tiles, K, M, N, ws_bytes) : 1u;
+        if (tiles * S >= 128) return go_gemm<QT, 256, 128, 64, XH, ACC>(X, rscale, W, Y, K, N, M, S, ws, s);
+    }
+    return go_gemm<QT, 128, 64, 128, XH, ACC>(X, rscale, W, Y, K, N, M, 1, nullptr, s);
 }
 
 bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t x_bytes)
@@ -351,29 +413,29 @@ bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t 
 
 template <bool XH, bool ACC>
 static hipError_t go_gemm_q(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
-                            uint32_t K, uint32_t N, uint32_t M, hipStream_t s)
+                            uint32_t K, uint32_t N, uint32_t M, float *ws, size_t ws_bytes, hipStream_t s)
 {
     if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2)) return hipErrorNotSupported;
     switch (type) {
-    case T_Q4_K: return go_gemm_t<GqQ4K, XH, ACC>(X, rscale, W, Y, K, N, M, s);
-    case T_Q5_K: return go_gemm_t<GqQ5K, XH, ACC>(X, rscale, W, Y, K, N, M, s);
-    case T_Q6_K: return go_gemm_t<GqQ6K, XH, ACC>(X, rscale, W, Y, K, N, M, s);
+    case T_Q4_K: return go_gemm_t<GqQ4K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, s);
+    case T_Q5_K: return go_gemm_t<GqQ5K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, s);
+    case T_Q6_K: return go_gemm_t<GqQ6K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, s);
     default: return hipErrorNotSupported;
     }
 }
 
-hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint64_t w_bytes, uint32_t type, float *Y,
-                            uint32_t K, uint32_t N, uint32_t M, hipStream_t s)
+hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K, uint32_t N,
+                            uint32_t M, float *ws, size_t ws_bytes, hipStream_t s)
 {
-    (void)w_bytes;
-    return go_gemm_q<false, false>(X, nullptr, W, type, Y, K, N, M, s);
+    return go_gemm_q<false, false>(X, nullptr, W, type, Y, K, N, M, ws, ws_bytes, s);
 }
 
 hipError_t launch_gemm_f16(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
-                           uint32_t K, uint32_t N, uint32_t M, bool accumulate, hipStream_t s)
+                           uint32_t K, uint32_t N, uint32_t M, bool accumulate, float *ws, size_t ws_bytes,
+                           hipStream_t s)
 {
-    return accumulate ? go_gemm_q<true, true>(X, rscale, W, type, Y, K, N, M, s)
-                      : go_gemm_q<true, false>(X, rscale, W, type, Y, K, N, M, s);
+    return accumulate ? go_gemm_q<true, true>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s)
+                      : go_gemm_q<true, false>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s);
 }
 
 }  // namespace rrr

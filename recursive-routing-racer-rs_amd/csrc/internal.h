@@ -100,12 +100,15 @@ hipError_t launch_attention_prefill(const float *qkv, uint32_t row_stride, uint3
                                     uint32_t heads_per_kv, hipStream_t s);
 // Prefill dequant-GEMM (gemm.hip): X is M x K bf16 or f16 bits; Y = X . W^T,
 // or Y += X . W^T with accumulate; with rscale, row m of the product is
-// multiplied by rscale[m] (a power of two: exact) first
+// multiplied by rscale[m] (a power of two: exact) first.  ws (ws_bytes, may
+// be null) holds the fp32 partials when K is split.
+constexpr size_t GEMM_WS_BYTES = 48ull << 20;
 bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t x_bytes);
-hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint64_t w_bytes, uint32_t type,
-                            float *Y, uint32_t K, uint32_t N, uint32_t M, hipStream_t s);
+hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K, uint32_t N,
+                            uint32_t M, float *ws, size_t ws_bytes, hipStream_t s);
 hipError_t launch_gemm_f16(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
-                           uint32_t K, uint32_t N, uint32_t M, bool accumulate, hipStream_t s);
+                           uint32_t K, uint32_t N, uint32_t M, bool accumulate, float *ws, size_t ws_bytes,
+                           hipStream_t s);
 // f16 (round to nearest even) outputs of RMSNorm rows and of silu_gate rows
 // (the latter scaled per row by a power of two, rscale undoing it), the
 // activations of the prefill GEMMs (ops.hip)

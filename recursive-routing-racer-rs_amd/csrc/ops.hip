@@ -185,6 +185,9 @@ hipError_t launch_silu_gate(const float *gu, float *mid, uint32_t rows, uint32_t
 // 2^15) and every value keeps f16's 11 significant bits however large the
 // activations grow); rscale[row] = 2^(e - 15) undoes it.  A row with no
 // finite nonzero maximum is stored unscaled (rscale 1).
+// NV > 0: the row's values stay in registers (F <= 256 * NV, one read of
+// gate / up); NV == 0: any F, gate / up read twice.
+template <int NV>
 __global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__restrict__ gu,
                                                                  _Float16 *__restrict__ mid,
                                                                  float *__restrict__ rscale, uint32_t F)
@@ -194,7 +197,17 @@ __global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__
     _Float16 *out = mid + (uint64_t)blockIdx.x * F;
     const uint32_t t = threadIdx.x;
     float m = 0.0f;
-    for (uint32_t i = t; i < F; i += 256) m = fmaxf(m, fabsf(silu_f(row[i]) * row[F + i]));
+    float v[NV > 0 ? NV : 1];
+    if constexpr (NV > 0) {
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const uint32_t i = t + 256u * j;
+            v[j] = i < F ? silu_f(row[i]) * row[F + i] : 0.0f;
+            m = fmaxf(m, fabsf(v[j]));
+        }
+    } else {
+        for (uint32_t i = t; i < F; i += 256) m = fmaxf(m, fabsf(silu_f(row[i]) * row[F + i]));
+    }
     m = wave_max(m);
     if ((t & 63) == 0) red[t >> 6] = m;
     __syncthreads();
@@ -202,14 +215,25 @@ __global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__
     int e = 15;
     if (m > 0.0f && __builtin_isfinite(m)) (void)frexpf(m, &e);
     const float sc = ldexpf(1.0f, 15 - e);
-    for (uint32_t i = t; i < F; i += 256) out[i] = to_out<_Float16>((silu_f(row[i]) * row[F + i]) * sc);
+    if constexpr (NV > 0) {
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const uint32_t i = t + 256u * j;
+            if (i < F) out[i] = to_out<_Float16>(v[j] * sc);
+        }
+    } else {
+        for (uint32_t i = t; i < F; i += 256) out[i] = to_out<_Float16>((silu_f(row[i]) * row[F + i]) * sc);
+    }
     if (t == 0) rscale[blockIdx.x] = ldexpf(1.0f, e - 15);
 }
 
 hipError_t launch_silu_gate_f16(const float *gu, uint16_t *mid, float *rscale, uint32_t rows, uint32_t F,
                                 hipStream_t s)
 {
-    hipLaunchKernelGGL(silu_gate_f16_rows_kernel, dim3(rows), dim3(256), 0, s, gu, (_Float16 *)mid, rscale, F);
+    if (F <= 256 * 32)
+        hipLaunchKernelGGL(silu_gate_f16_rows_kernel<32>, dim3(rows), dim3(256), 0, s, gu, (_Float16 *)mid, rscale, F);
+    else
+        hipLaunchKernelGGL(silu_gate_f16_rows_kernel<0>, dim3(rows), dim3(256), 0, s, gu, (_Float16 *)mid, rscale, F);
     return hipGetLastError();
 }
 

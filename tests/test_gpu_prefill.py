@@ -10,9 +10,10 @@ Bars.
   that f32 result rounded to nearest even (bitwise).
 - f16-activation GEMM: the MFMA bar, 2e-3 normwise against the fp64 product
   of the same f16 inputs with the exact dequantized weights (the kernel
-  rounds the weights to f16 tiles); the accumulate form adds its result to Y
-  in f32 (bitwise Y0 + product); with inputs exact in both bf16 and f16 it
-  gives the bits of the bf16-input GEMM.
+  rounds the weights to f16 tiles), with and without K split over
+  workgroups; the accumulate form adds its result to Y in f32 (bitwise Y0 +
+  product); with inputs exact in both bf16 and f16 it gives the bits of the
+  bf16-input GEMM.
 - RMSNorm with f16 output: the f32 kernel's results rounded to nearest even
   (bitwise); silu_gate in f16 block floating point: the f32 kernel's results
   times the row's power of two 2^(15 - e) (max = f * 2^e), rounded to nearest
@@ -136,8 +137,11 @@ def test_attention_prefill_parity(ctx, caches, pos0, rows, nkv, hpk):
         b.free()
 
 
+# the last three split K (too few 256 x 128 tiles at a 512-token prompt)
 @pytest.mark.parametrize("qtype,K,N,M", [(rrr_hip.Q5_K, 3072, 5120, 128), (rrr_hip.Q4_K, 3072, 16384, 256),
-                                         (rrr_hip.Q6_K, 8192, 3072, 128), (rrr_hip.Q4_K, 3072, 3072, 384)])
+                                         (rrr_hip.Q6_K, 8192, 3072, 128), (rrr_hip.Q4_K, 3072, 3072, 384),
+                                         (rrr_hip.Q4_K, 3072, 3072, 512), (rrr_hip.Q5_K, 3072, 5120, 512),
+                                         (rrr_hip.Q6_K, 8192, 3072, 512)])
 def test_gemm_f16_parity(ctx, qtype, K, N, M):
     raw = synth.weight(4, 50 + qtype, qtype, K, N)
     X = f16r(synth.normal_f32(4, 51, M * K).reshape(M, K))
@@ -211,8 +215,9 @@ def test_rmsnorm_and_silu_gate_f16(ctx):
         b.free()
 
 
-def test_gemm_f16_row_scale(ctx):
-    qtype, K, N, M = rrr_hip.Q6_K, 8192, 3072, 128
+@pytest.mark.parametrize("M", [128, 512])
+def test_gemm_f16_row_scale(ctx, M):
+    qtype, K, N = rrr_hip.Q6_K, 8192, 3072
     raw = synth.weight(7, 80, qtype, K, N)
     X = f16r(synth.normal_f32(7, 81, M * K).reshape(M, K))
     rs = np.ldexp(np.float32(1.0), np.random.default_rng(7).integers(-20, 20, M)).astype(np.float32)
@@ -224,6 +229,12 @@ def test_gemm_f16_row_scale(ctx):
     a = ctx.download(y1, np.float32, M * N).reshape(M, N)
     assert np.array_equal(ctx.download(y2, np.float32, M * N).reshape(M, N).view(np.uint32),
                           (a * rs[:, None]).view(np.uint32))
+    # and added to Y, as the prefill's down projection does
+    Y0 = synth.normal_f32(7, 82, M * N).reshape(M, N)
+    ctx.upload(y2, Y0)
+    ctx.gemm_f16(xb, W, qtype, y2, K, N, M, accumulate=True, row_scale=rb)
+    assert np.array_equal(ctx.download(y2, np.float32, M * N).reshape(M, N).view(np.uint32),
+                          (Y0 + a * rs[:, None]).view(np.uint32))
     for b in (W, xb, rb, y1, y2):
         b.free()
 
