@@ -454,12 +454,205 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
     }
 }
 
+// Causal prefill attention on the matrix cores.  Workgroup (g, tb) is one
+// wave: KV head g, tokens tb*16 .. tb*16+15 (lane l's token is l % 16).  Per
+// block of 32 cache rows and per query head h of the group:
+//   S^T = K . Q^T    (v_mfma_f32_16x16x32_f16, keys x tokens, K from the f16
+//                     cache as A operands, Q^T as B operands in f16 hi + lo,
+//                     so the scores carry ~2^-22 of Q's rounding)
+//   online softmax per token (exp2, queries pre-scaled by log2(e)/sqrt(128))
+//   O^T += V^T . P^T (dims x tokens; P in f16 hi + lo, V exact in f16)
+// In the MFMA layouts (lane l: A row / B column l % 16 at k slots
+// 8 (l / 16) .. +7; D rows 4 (l / 16) + r of column l % 16) lane l's D
+// registers of the two S^T key tiles hold keys 4 (l/16) + r and
+// 16 + 4 (l/16) + r of its token: exactly the 8 k slots it supplies as P^T's
+// B operand when V^T's A operand takes the same keys in the same order (the
+// k order inside one MFMA only has to agree between A and B).  V^T comes
+// from a transposed LDS copy of the block.  A token's scores of a block sit
+// in the 4 lanes l % 16 + 16 j: its max and sum are two cross-lane steps.
+// The hi + lo splits are taken of Q * 2^(14 - e) (per token and head, the
+// scaled query's largest component f * 2^e, f in [0.5, 1): it lands in
+// [2^13, 2^14), inside f16's range whatever the activations' size) and of
+// P * 2^12 (P <= 1), undone exactly on the scores and at the end; the lo
+// parts then stay in f16's normal range, where they keep their precision.
+constexpr uint32_t ATTM_LD = 36;   // f16 per V^T row in LDS (32 keys + pad; 72-byte rows)
+constexpr float ATTM_PS = 4096.0f;
+
+template <int HPK, bool F16OUT>
+__global__ __launch_bounds__(64) void attn_prefill_mfma_kernel(const float *__restrict__ qkv, uint32_t row_stride,
+                                                               const uint16_t *__restrict__ kc,
+                                                               const uint16_t *__restrict__ vc,
+                                                               void *__restrict__ out, uint32_t rows, uint32_t pos0,
+                                                               uint32_t kv_stride, float qscale)
+{
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) _Float16 vt[ATT_HD * ATTM_LD];
+    const uint32_t g = blockIdx.x, tb = blockIdx.y, l = threadIdx.x, n = l & 15, grp = l >> 4;
+    const uint32_t tok = tb * 16 + n, tq = min(tok, rows - 1), tpos = pos0 + tq;
+    const uint32_t last = pos0 + min(tb * 16 + 15, rows - 1);      // the last cache row the block's tokens see
+    const uint32_t nblk = last / 32 + 1;
+    const uint16_t *kbase = kc + (size_t)g * ATT_HD, *vbase = vc + (size_t)g * ATT_HD;
+
+    // Q^T operands of each head: token tq, dims 32 kk + 8 grp .. +7, scaled, hi + lo
+    h8 qh[HPK][4], ql[HPK][4];
+    float qs[HPK];   // the scale of head h's scores (undoes the query's power of two)
+    const float *q = qkv + (size_t)tq * row_stride;
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        float x[4][8], mx = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const float4 *qp = (const float4 *)(q + (size_t)(g * HPK + h) * ATT_HD + 32 * kk + 8 * grp);
+            const float4 a = qp[0], b = qp[1];
+            x[kk][0] = a.x; x[kk][1] = a.y; x[kk][2] = a.z; x[kk][3] = a.w;
+            x[kk][4] = b.x; x[kk][5] = b.y; x[kk][6] = b.z; x[kk][7] = b.w;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                x[kk][i] *= qscale;
+                mx = fmaxf(mx, fabsf(x[kk][i]));
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));   // the token's 128 dims sit in lanes n + 16 j
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        int e = 0;
+        if (mx > 0.0f && __builtin_isfinite(mx)) (void)frexpf(mx, &e);
+        const float up = ldexpf(1.0f, 14 - e);
+        qs[h] = ldexpf(1.0f, e - 14);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float v = x[kk][i] * up;
+                const _Float16 hi = (_Float16)v;
+                qh[h][kk][i] = hi;
+                ql[h][kk][i] = (_Float16)(v - (float)hi);
+            }
+    }
+    f4 o[HPK][8];
+    float m[HPK], ls[HPK];
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        m[h] = -__builtin_inff();
+        ls[h] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o[h][dt] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (uint32_t blk = 0; blk < nblk; blk++) {
+        const uint32_t c0 = 32 * blk;
+        // K A operands: key tile kt (rows c0 + 16 kt + n), dims 32 kk + 8 grp
+        h8 ka[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+            const uint32_t row = min(c0 + 16 * kt + n, last);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+                ka[kt][kk] = *(const h8 *)(kbase + (size_t)row * kv_stride + 32 * kk + 8 * grp);
+        }
+        // V rows c0 + 4 grp + {0..3} and c0 + 16 + 4 grp + {0..3}, dims 8 n .. 8 n + 7,
+        // written to V^T[dim][key] four keys at a time
+        h8 vr[2][4];
+#pragma unroll
+        for (int half = 0; half < 2; half++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t row = min(c0 + 16 * half + 4 * grp + j, last);
+                vr[half][j] = *(const h8 *)(vbase + (size_t)row * kv_stride + 8 * n);
+            }
+        __syncthreads();   // the previous block's V^T reads are done
+#pragma unroll
+        for (int half = 0; half < 2; half++)
+#pragma unroll
+            for (int d = 0; d < 8; d++)
+                *(h4 *)(vt + (8 * n + d) * ATTM_LD + 16 * half + 4 * grp) =
+                    h4{vr[half][0][d], vr[half][1][d], vr[half][2][d], vr[half][3][d]};
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < HPK; h++) {
+            f4 sc[2];
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+                sc[kt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][kk], qh[h][kk], sc[kt], 0, 0, 0);
+                    sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][kk], ql[h][kk], sc[kt], 0, 0, 0);
+                }
+            }
+            // lane l: sc[kt][r] = score of key c0 + 16 kt + 4 grp + r for its token
+            float bm = -__builtin_inff();
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    sc[kt][r] *= qs[h];
+                    if (c0 + 16 * kt + 4 * grp + r > tpos) sc[kt][r] = -__builtin_inff();
+                    bm = fmaxf(bm, sc[kt][r]);
+                }
+            bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            const float mn = fmaxf(m[h], bm);        // finite: key 0 is in every token's range
+            const float cf = exp2f(m[h] - mn);
+            float ps = 0.0f;
+            h8 pb, pl;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float p = exp2f(sc[kt][r] - mn), pp = p * ATTM_PS;
+                    ps += p;
+                    const _Float16 hi = (_Float16)pp;
+                    pb[4 * kt + r] = hi;
+                    pl[4 * kt + r] = (_Float16)(pp - (float)hi);
+                }
+            ps += __shfl_xor(ps, 16, 64);
+            ps += __shfl_xor(ps, 32, 64);
+            ls[h] = fmaf(ls[h], cf, ps);
+            m[h] = mn;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const _Float16 *vrow = vt + (16 * dt + n) * ATTM_LD;
+                const h4 a0 = *(const h4 *)(vrow + 4 * grp), a1 = *(const h4 *)(vrow + 16 + 4 * grp);
+                const h8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+                o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[h][dt] * cf, 0, 0, 0);
+                o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[h][dt], 0, 0, 0);
+            }
+        }
+    }
+    if (!(tok < rows)) return;
+    const size_t orow = (size_t)tok * gridDim.x * HPK * ATT_HD;
+#pragma unroll
+    for (int h = 0; h < HPK; h++) {
+        const float inv = (1.0f / ATTM_PS) / ls[h];
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            const size_t oi = orow + (size_t)(g * HPK + h) * ATT_HD + 16 * dt + 4 * grp;
+            const f4 v = o[h][dt] * inv;
+            if constexpr (F16OUT)
+                *(h4 *)((_Float16 *)out + oi) = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+            else
+                *(float4 *)((float *)out + oi) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+}
+
 template <int HPK>
 static void go_attn_prefill(const float *qkv, uint32_t row_stride, uint32_t rows, const uint16_t *kc,
                             const uint16_t *vc, void *out, bool out_f16, uint32_t pos0, uint32_t n_kv_heads,
                             float qscale, hipStream_t s)
 {
     const uint32_t kv_stride = n_kv_heads * ATT_HD;
+    if constexpr (HPK <= 4) {   // the matrix-core form (its accumulators take 32 registers per head)
+        const dim3 grid(n_kv_heads, (rows + 15) / 16);
+        if (out_f16)
+            hipLaunchKernelGGL((attn_prefill_mfma_kernel<HPK, true>), grid, dim3(64), 0, s, qkv, row_stride, kc, vc,
+                               out, rows, pos0, kv_stride, qscale);
+        else
+            hipLaunchKernelGGL((attn_prefill_mfma_kernel<HPK, false>), grid, dim3(64), 0, s, qkv, row_stride, kc, vc,
+                               out, rows, pos0, kv_stride, qscale);
+        return;
+    }
     if (out_f16)
         hipLaunchKernelGGL((attn_prefill_kernel<HPK, true>), dim3(n_kv_heads, rows), dim3(256), 0, s, qkv, row_stride,
                            kc, vc, out, pos0, kv_stride, qscale);

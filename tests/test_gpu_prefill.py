@@ -5,9 +5,12 @@ Bars.
 - RoPE + KV store of `rows` tokens: each row as the single-token op (V rows
   bit-exact, Q/K within the f32-angle bound of the decode tests), and the
   same bits as `rows` single-token launches.
-- Causal prefill attention, f32 output: 1e-4 normwise against the fp64
-  attention of each token over cache rows 0 .. pos0 + t; the f16 output is
-  that f32 result rounded to nearest even (bitwise).
+- Causal prefill attention, f32 output, against the fp64 attention of each
+  token over cache rows 0 .. pos0 + t: the matrix-core form (up to 4 query
+  heads per KV head) at the MFMA bar, 2e-3 (measured with Q and P in f16
+  hi + lo: median 4e-7 per token, worst 1.1e-4 at 2,029 rows, isolated
+  elements), the VALU form (more heads per KV head) at 1e-4; the f16 output
+  is the f32 result rounded to nearest even (bitwise).
 - f16-activation GEMM: the MFMA bar, 2e-3 normwise against the fp64 product
   of the same f16 inputs with the exact dequantized weights (the kernel
   rounds the weights to f16 tiles), with and without K split over
@@ -128,9 +131,13 @@ def test_attention_prefill_parity(ctx, caches, pos0, rows, nkv, hpk):
     ctx.attention_prefill(dq, rows, kc, vc, o32, pos0, nkv, hpk, HD)
     ctx.attention_prefill(dq, rows, kc, vc, o16, pos0, nkv, hpk, HD, out_type=rrr_hip.F16)
     got = ctx.download(o32, np.float32, rows * qd).reshape(rows, qd)
+    bar = MFMA_TOL if hpk <= 4 else TOL
+    errs = []
     for t in range(rows):
         ref = orc.attention_f64(qkv[t, :qd], k, v, pos0 + t + 1, nkv, hpk, HD)
-        assert orc.normwise_err(got[t], ref) < TOL, t
+        errs.append(orc.normwise_err(got[t], ref))
+        assert errs[-1] < bar, t
+    assert np.median(errs) < 1e-5
     h = ctx.download(o16, np.uint16, rows * qd).reshape(rows, qd)
     assert np.array_equal(h, got.astype(np.float16).view(np.uint16))
     for b in (dq, o32, o16):
@@ -138,6 +145,29 @@ def test_attention_prefill_parity(ctx, caches, pos0, rows, nkv, hpk):
 
 
 # the last three split K (too few 256 x 128 tiles at a 512-token prompt)
+def test_attention_prefill_large_queries(ctx, caches):
+    """Queries of ~4e4 (a random-init model reaches 3.3e4 by its eighth
+    layer): the matrix-core form scales each token's query by a power of two
+    before its f16 split, so nothing overflows."""
+    kc, vc = caches
+    pos0, rows, nkv, hpk = 0, 40, 8, 3
+    rng = np.random.default_rng(11)
+    k = orc.f32_to_f16_bits((rng.standard_normal(rows * nkv * HD) * 0.01).astype(np.float32))
+    v = orc.f32_to_f16_bits((rng.standard_normal(rows * nkv * HD) * 5e3).astype(np.float32))   # within f16
+    ctx.upload(kc, k)
+    ctx.upload(vc, v)
+    qd = nkv * hpk * HD
+    qkv = (rng.standard_normal((rows, qd + 2 * nkv * HD)) * 4e4).astype(np.float32)
+    dq, o32 = ctx.to_device(qkv), ctx.alloc(rows * qd * 4)
+    ctx.attention_prefill(dq, rows, kc, vc, o32, pos0, nkv, hpk, HD)
+    got = ctx.download(o32, np.float32, rows * qd).reshape(rows, qd)
+    assert np.all(np.isfinite(got))
+    for t in range(rows):
+        ref = orc.attention_f64(qkv[t, :qd], k, v, pos0 + t + 1, nkv, hpk, HD)
+        assert orc.normwise_err(got[t], ref) < MFMA_TOL, t
+    dq.free(); o32.free()
+
+
 @pytest.mark.parametrize("qtype,K,N,M", [(rrr_hip.Q5_K, 3072, 5120, 128), (rrr_hip.Q4_K, 3072, 16384, 256),
                                          (rrr_hip.Q6_K, 8192, 3072, 128), (rrr_hip.Q4_K, 3072, 3072, 384),
                                          (rrr_hip.Q4_K, 3072, 3072, 512), (rrr_hip.Q5_K, 3072, 5120, 512),
