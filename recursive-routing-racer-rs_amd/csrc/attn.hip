@@ -454,9 +454,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
     }
 }
 
-// Causal prefill attention on the matrix cores.  Workgroup (g, tb) is one
-// wave: KV head g, tokens tb*16 .. tb*16+15 (lane l's token is l % 16).  Per
-// block of 32 cache rows and per query head h of the group:
+// Causal prefill attention on the matrix cores.  Workgroup (g, tb): KV head
+// g, tokens tb*16 .. tb*16+15 (lane l's token is l % 16); its ATTM_WAVES
+// waves take every ATTM_WAVES-th block of 32 cache rows and merge their
+// (max, sum, output) at the end in a fixed order.  Per block and per query
+// head h of the group:
 //   S^T = K . Q^T    (v_mfma_f32_16x16x32_f16, keys x tokens, K from the f16
 //                     cache as A operands, Q^T as B operands in f16 hi + lo,
 //                     so the scores carry ~2^-22 of Q's rounding)
@@ -477,9 +479,25 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
 // parts then stay in f16's normal range, where they keep their precision.
 constexpr uint32_t ATTM_LD = 36;   // f16 per V^T row in LDS (32 keys + pad; 72-byte rows)
 constexpr float ATTM_PS = 4096.0f;
+constexpr uint32_t ATTM_WAVES = 4, ATTM_OLD = ATT_HD + 4;   // waves; floats per merged output row (padded)
+
+__device__ __forceinline__ void wave_lds_order()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int HPK>
+struct AttmLds {
+    static constexpr size_t VT = (size_t)ATTM_WAVES * ATT_HD * ATTM_LD * 2;            // V^T per wave
+    static constexpr size_t O = (size_t)ATTM_WAVES * HPK * 16 * ATTM_OLD * 4;          // merge: outputs
+    static constexpr size_t ML = (size_t)ATTM_WAVES * HPK * 16 * 2 * 4;                // merge: max, sum
+    static constexpr size_t BYTES = (VT > O ? VT : O) + ML;
+};
 
 template <int HPK, bool F16OUT>
-__global__ __launch_bounds__(64) void attn_prefill_mfma_kernel(const float *__restrict__ qkv, uint32_t row_stride,
+__global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(const float *__restrict__ qkv, uint32_t row_stride,
                                                                const uint16_t *__restrict__ kc,
                                                                const uint16_t *__restrict__ vc,
                                                                void *__restrict__ out, uint32_t rows, uint32_t pos0,
@@ -488,8 +506,13 @@ __global__ __launch_bounds__(64) void attn_prefill_mfma_kernel(const float *__re
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
     typedef float f4 __attribute__((ext_vector_type(4)));
-    __shared__ __attribute__((aligned(16))) _Float16 vt[ATT_HD * ATTM_LD];
-    const uint32_t g = blockIdx.x, tb = blockIdx.y, l = threadIdx.x, n = l & 15, grp = l >> 4;
+    using LD = AttmLds<HPK>;
+    __shared__ __attribute__((aligned(16))) uint8_t sm[LD::BYTES];
+    const uint32_t wv = threadIdx.x >> 6;
+    _Float16 *vt = (_Float16 *)sm + (size_t)wv * ATT_HD * ATTM_LD;   // this wave's V^T
+    float *mo = (float *)sm;                                        // merge outputs (after the loop)
+    float *mml = (float *)(sm + (LD::VT > LD::O ? LD::VT : LD::O)); // merge max / sum
+    const uint32_t g = blockIdx.x, tb = blockIdx.y, l = threadIdx.x & 63, n = l & 15, grp = l >> 4;
     const uint32_t tok = tb * 16 + n, tq = min(tok, rows - 1), tpos = pos0 + tq;
     const uint32_t last = pos0 + min(tb * 16 + 15, rows - 1);      // the last cache row the block's tokens see
     const uint32_t nblk = last / 32 + 1;
@@ -539,7 +562,7 @@ __global__ __launch_bounds__(64) void attn_prefill_mfma_kernel(const float *__re
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) o[h][dt] = f4{0.f, 0.f, 0.f, 0.f};
     }
-    for (uint32_t blk = 0; blk < nblk; blk++) {
+    for (uint32_t blk = wv; blk < nblk; blk += ATTM_WAVES) {
         const uint32_t c0 = 32 * blk;
         // K A operands: key tile kt (rows c0 + 16 kt + n), dims 32 kk + 8 grp
         h8 ka[2][4];
@@ -560,14 +583,16 @@ __global__ __launch_bounds__(64) void attn_prefill_mfma_kernel(const float *__re
                 const uint32_t row = min(c0 + 16 * half + 4 * grp + j, last);
                 vr[half][j] = *(const h8 *)(vbase + (size_t)row * kv_stride + 8 * n);
             }
-        __syncthreads();   // the previous block's V^T reads are done
+        // this wave's V^T (the wave's LDS operations run in order: the
+        // previous block's reads come before these writes)
+        wave_lds_order();
 #pragma unroll
         for (int half = 0; half < 2; half++)
 #pragma unroll
             for (int d = 0; d < 8; d++)
                 *(h4 *)(vt + (8 * n + d) * ATTM_LD + 16 * half + 4 * grp) =
                     h4{vr[half][0][d], vr[half][1][d], vr[half][2][d], vr[half][3][d]};
-        __syncthreads();
+        wave_lds_order();
 #pragma unroll
         for (int h = 0; h < HPK; h++) {
             f4 sc[2];
@@ -592,15 +617,18 @@ __global__ __launch_bounds__(64) void attn_prefill_mfma_kernel(const float *__re
                 }
             bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
             bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-            const float mn = fmaxf(m[h], bm);        // finite: key 0 is in every token's range
-            const float cf = exp2f(m[h] - mn);
+            // -inf while none of this wave's blocks so far holds a key of the
+            // token's range (a wave's first block may lie past the token)
+            const float mn = fmaxf(m[h], bm);
+            const bool none = mn == -__builtin_inff();
+            const float cf = none ? 1.0f : exp2f(m[h] - mn);
             float ps = 0.0f;
             h8 pb, pl;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float p = exp2f(sc[kt][r] - mn), pp = p * ATTM_PS;
+                    const float p = none ? 0.0f : exp2f(sc[kt][r] - mn), pp = p * ATTM_PS;
                     ps += p;
                     const _Float16 hi = (_Float16)pp;
                     pb[4 * kt + r] = hi;
@@ -620,19 +648,44 @@ __global__ __launch_bounds__(64) void attn_prefill_mfma_kernel(const float *__re
             }
         }
     }
-    if (!(tok < rows)) return;
-    const size_t orow = (size_t)tok * gridDim.x * HPK * ATT_HD;
+    // merge the waves: wave w's output rows (token, dims) and its max / sum
+    // per (head, token); a wave without blocks holds max -inf, sum 0
+    __syncthreads();   // every wave is done with its V^T
 #pragma unroll
     for (int h = 0; h < HPK; h++) {
-        const float inv = (1.0f / ATTM_PS) / ls[h];
+        float *orow = mo + ((size_t)(wv * HPK + h) * 16 + n) * ATTM_OLD;
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
-            const size_t oi = orow + (size_t)(g * HPK + h) * ATT_HD + 16 * dt + 4 * grp;
-            const f4 v = o[h][dt] * inv;
-            if constexpr (F16OUT)
-                *(h4 *)((_Float16 *)out + oi) = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-            else
-                *(float4 *)((float *)out + oi) = make_float4(v[0], v[1], v[2], v[3]);
+        for (int dt = 0; dt < 8; dt++)
+            *(float4 *)(orow + 16 * dt + 4 * grp) = make_float4(o[h][dt][0], o[h][dt][1], o[h][dt][2], o[h][dt][3]);
+        if (grp == 0) {
+            mml[((wv * HPK + h) * 16 + n) * 2] = m[h];
+            mml[((wv * HPK + h) * 16 + n) * 2 + 1] = ls[h];
+        }
+    }
+    __syncthreads();
+    const size_t qd = (size_t)gridDim.x * HPK * ATT_HD;
+    for (uint32_t i = threadIdx.x; i < HPK * 16 * ATT_HD; i += 64 * ATTM_WAVES) {
+        const uint32_t d = i % ATT_HD, ht = i / ATT_HD, h = ht % HPK, t = ht / HPK;   // dims fastest
+        const uint32_t tk = tb * 16 + t;
+        float M = -__builtin_inff();
+#pragma unroll
+        for (uint32_t w = 0; w < ATTM_WAVES; w++) M = fmaxf(M, mml[((w * HPK + h) * 16 + t) * 2]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (uint32_t w = 0; w < ATTM_WAVES; w++) {
+            const float c = safe_scale(mml[((w * HPK + h) * 16 + t) * 2], M);
+            L = fmaf(mml[((w * HPK + h) * 16 + t) * 2 + 1], c, L);
+            O = fmaf(mo[((size_t)(w * HPK + h) * 16 + t) * ATTM_OLD + d], c, O);
+        }
+        if (tk < rows) {
+            const size_t oi = (size_t)tk * qd + (size_t)(g * HPK + h) * ATT_HD + d;
+            float v = O * ((1.0f / ATTM_PS) / L);
+            if constexpr (F16OUT) {
+                asm volatile("" : "+v"(v));   // the f32 result, then its rounding (no mixed-precision fold)
+                ((_Float16 *)out)[oi] = (_Float16)v;
+            } else {
+                ((float *)out)[oi] = v;
+            }
         }
     }
 }
@@ -645,12 +698,13 @@ static void go_attn_prefill(const float *qkv, uint32_t row_stride, uint32_t rows
     const uint32_t kv_stride = n_kv_heads * ATT_HD;
     if constexpr (HPK <= 4) {   // the matrix-core form (its accumulators take 32 registers per head)
         const dim3 grid(n_kv_heads, (rows + 15) / 16);
+        static_assert(AttmLds<4>::BYTES <= 160 * 1024, "LDS per workgroup");
         if (out_f16)
-            hipLaunchKernelGGL((attn_prefill_mfma_kernel<HPK, true>), grid, dim3(64), 0, s, qkv, row_stride, kc, vc,
-                               out, rows, pos0, kv_stride, qscale);
+            hipLaunchKernelGGL((attn_prefill_mfma_kernel<HPK, true>), grid, dim3(64 * ATTM_WAVES), 0, s, qkv,
+                               row_stride, kc, vc, out, rows, pos0, kv_stride, qscale);
         else
-            hipLaunchKernelGGL((attn_prefill_mfma_kernel<HPK, false>), grid, dim3(64), 0, s, qkv, row_stride, kc, vc,
-                               out, rows, pos0, kv_stride, qscale);
+            hipLaunchKernelGGL((attn_prefill_mfma_kernel<HPK, false>), grid, dim3(64 * ATTM_WAVES), 0, s, qkv,
+                               row_stride, kc, vc, out, rows, pos0, kv_stride, qscale);
         return;
     }
     if (out_f16)

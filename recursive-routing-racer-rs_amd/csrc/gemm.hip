@@ -176,7 +176,7 @@ struct GqQ6K {
 // into the other LDS buffer, so every SIMD holds one wave of each kind and the
 // staging VALU fills the matrix core's gaps.  Both roles pass one barrier per
 // step (plus one after the prologue) on separate straight-line paths.
-template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC>
+template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC, bool SPLIT>
 __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K,
                                                       uint32_t N, uint32_t M, uint32_t tiles_n, const float *rscale,
                                                       uint32_t ksteps, float *ws)
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     // tile of this workgroup (same XCD for the M tiles of one N tile) and its
     // K split (the tile count is a multiple of 8 when K is split)
     const uint32_t tiles_m = M / BM, ntile = tiles_n * tiles_m;
-    const uint32_t ks = blockIdx.x / ntile, id = blockIdx.x - ks * ntile;
+    const uint32_t ks = SPLIT ? blockIdx.x / ntile : 0u, id = blockIdx.x - ks * ntile;
     uint32_t nt, mt;
     if (tiles_n % 8 == 0) {
         nt = (id / (8 * tiles_m)) * 8 + id % 8;
@@ -205,7 +205,8 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         mt = id % tiles_m;
     }
     const uint32_t m0 = mt * BM, n0 = nt * BN;
-    const uint32_t nsteps = ksteps, s0 = ks * ksteps, B = K / 256;   // this split's steps, its first step
+    // this split's K steps and its first step
+    const uint32_t nsteps = SPLIT ? ksteps : K / BK, s0 = ks * nsteps, B = K / 256;
 
     if (wave >= 4) {
         // ---- producer: loads, dequant, conversion --------------------------
@@ -320,7 +321,7 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint32_t m = m0 + wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + r;
-                if (ws) {
+                if constexpr (SPLIT) {
                     ws[((uint64_t)ks * M + m) * N + n] = acc[i][j][r];
                     continue;
                 }
@@ -366,8 +367,12 @@ static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t 
     constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * 2;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
     const uint32_t tiles_n = N / BN, tiles = tiles_n * (M / BM);
-    hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC>), dim3(tiles * S), dim3(512), lds, s, X, W, Y, K, N, M,
-                       tiles_n, rscale, K / BK / S, S > 1 ? ws : nullptr);
+    if (S > 1)
+        hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC, true>), dim3(tiles * S), dim3(512), lds, s, X, W, Y,
+                           K, N, M, tiles_n, rscale, K / BK / S, ws);
+    else
+        hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC, false>), dim3(tiles), dim3(512), lds, s, X, W, Y, K,
+                           N, M, tiles_n, rscale, K / BK, nullptr);
     if (S > 1) {
         const uint64_t quads = (uint64_t)M * N / 4;
         hipLaunchKernelGGL(gemm_splitk_reduce<ACC>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, ws, S, M,

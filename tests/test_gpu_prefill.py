@@ -113,8 +113,10 @@ def test_rope_kv_store_rows(ctx, caches, pos0, rows):
         buf.free()
 
 
+# (9, 40) and (25, 70): blocks of 32 cache rows that start past some of a
+# workgroup's tokens (a wave whose first block holds none of a token's keys)
 @pytest.mark.parametrize("pos0,rows,nkv,hpk", [(0, 1, 8, 3), (0, 130, 8, 3), (100, 37, 8, 3), (2000, 48, 8, 3),
-                                               (0, 64, 2, 8), (5, 20, 1, 1)])
+                                               (0, 64, 2, 8), (5, 20, 1, 1), (9, 40, 8, 3), (25, 70, 8, 3)])
 def test_attention_prefill_parity(ctx, caches, pos0, rows, nkv, hpk):
     kc, vc = caches
     rng = np.random.default_rng(pos0 * 7 + rows + nkv * hpk)
