@@ -26,6 +26,7 @@ import argparse
 import json
 import os
 import sys
+import tempfile
 import time
 
 REPO = os.path.dirname(os.path.abspath(__file__))
@@ -218,6 +219,43 @@ def skinny(ctx, reps=64):
     return out
 
 
+def gguf_load(ctx, sw, shape):
+    """The same model exported as a GGUF file, then mapped, parsed and
+    uploaded as stored (rrr_gguf_open + rrr_gguf_upload per tensor), the file
+    already in the page cache; one token on it must equal the in-memory
+    model's bit for bit."""
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "phi4-mini-synthetic.gguf")
+        t0 = time.perf_counter()
+        decode.write_synthetic_gguf(path, shape, seed=3)
+        t_write = time.perf_counter() - t0
+        size = os.path.getsize(path)
+        t0 = time.perf_counter()
+        model = rrr_hip.GGUFModel.load(path)
+        t_open = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        gs = decode.DecodeSweep(ctx, shape, seed=3, gguf=model, logits="q6k")
+        ctx.sync()
+        t_load = time.perf_counter() - t0
+        up = sum(i.nbytes for i in model.tensor_infos if len(i.shape) > 1)
+        ctx.upload(gs.x_in, ctx.download(sw.x_in, np.float32, shape.d_model))
+        mode, sw.logits_mode = sw.logits_mode, "q6k"
+        for m in (sw, gs):
+            m.record_token()
+        ctx.sync()
+        sw.logits_mode = mode
+        la, ta, _ = sw.results()
+        lb, tb, _ = gs.results()
+        same = bool(np.array_equal(la.view(np.uint32), lb.view(np.uint32)) and ta == tb)
+        del gs
+        model.close()
+    log(f"[bench] GGUF load: {size / 1e9:.2f} GB file written in {t_write:.1f} s; parse {t_open * 1e3:.1f} ms; "
+        f"{up / 1e9:.2f} GB of weights uploaded as stored in {t_load:.2f} s ({up / t_load / 1e9:.1f} GB/s, host "
+        f"to HBM through PCIe); token identical to the in-memory model: {same}")
+    return {"file_bytes": size, "parse_ms": round(t_open * 1e3, 2), "upload_bytes": up,
+            "load_s": round(t_load, 3), "upload_GBs": round(up / t_load / 1e9, 2), "token_identical": same}
+
+
 def decode_sweep(ctx, tokens):
     """Full Phi-4-mini-shaped decode sweep (32 layers + final RMSNorm + F32
     logits over 200,064 entries + argmax), one HIP graph per token; the
@@ -318,8 +356,9 @@ def decode_sweep(ctx, tokens):
     fl = decode.prefill_flops(shape, M)
     log(f"[bench] prefill of {M} tokens through 32 layers + logits: {ms_pf:.3f} ms ({M / (ms_pf * 1e-3):.0f} tokens/s, "
         f"{fl / (ms_pf * 1e-3) / 1e12:.0f} TFLOP/s in the layer GEMMs), argmax {tok_pf}")
+    gg = gguf_load(ctx, sw, shape)
     best = min(ms, ms_p)
-    return {"ms_per_token": round(best, 5), "tokens": tokens, "bytes_per_token": b,
+    return {"ms_per_token": round(best, 5), "tokens": tokens, "bytes_per_token": b, "gguf_load": gg,
             "prefill_512": {"ms": round(ms_pf, 4), "tokens_per_s": round(M / (ms_pf * 1e-3), 1),
                             "gemm_flops": fl, "TFLOPs": round(fl / (ms_pf * 1e-3) / 1e12, 1),
                             "frac_fp16_peak": round(fl / (ms_pf * 1e-3) / 2.5e15, 4), "argmax": tok_pf,

@@ -4,6 +4,7 @@
 // call, so a validation-only context (RRR_DEVICE_NONE) exercises all error
 // paths on a machine without a GPU.
 #include "rrr_hip.h"
+#include "rrr_gguf.h"
 
 #include <hip/hip_runtime.h>
 
@@ -46,6 +47,15 @@ int ok()
 }
 
 }  // namespace
+
+namespace rrr {
+int set_error(int code, const char *msg)
+{
+    if (code == RRR_OK) return ok();
+    g_err = msg;
+    return code;
+}
+}  // namespace rrr
 
 struct rrr_buf {
     uint32_t magic;
@@ -409,6 +419,29 @@ int rrr_weight_upload(rrr_ctx *ctx, uint32_t type, uint32_t K, uint32_t N, const
         return fail(rc, "%s", msg.c_str());
     }
     *out = b;
+    return ok();
+}
+
+int rrr_gguf_upload(rrr_ctx *ctx, const rrr_gguf *g, const char *name, rrr_buf **out)
+{
+    TRY(check_ctx(ctx));
+    if (!out) return fail(RRR_ERR_NULL, "rrr_gguf_upload: null output pointer");
+    *out = nullptr;
+    rrr_gguf_tensor t;
+    TRY(rrr_gguf_find_tensor(g, name, &t));
+    if (!valid_type(t.type))
+        return fail(RRR_ERR_BAD_TYPE, "tensor '%s' has ggml type %u; the kernels read types 0, 12, 13, 14", name,
+                    t.type);
+    if (t.dims[0] == 0 || t.n_elements == 0) return fail(RRR_ERR_BAD_SHAPE, "tensor '%s' is empty", name);
+    const uint64_t rows = t.n_elements / t.dims[0];
+    if (t.dims[0] > UINT32_MAX || rows > UINT32_MAX)
+        return fail(RRR_ERR_BAD_SHAPE, "tensor '%s': %llu rows of %llu elements exceed 32-bit sizes", name,
+                    (unsigned long long)rows, (unsigned long long)t.dims[0]);
+    const int rc = rrr_weight_upload(ctx, t.type, (uint32_t)t.dims[0], (uint32_t)rows, t.data, t.bytes, out);
+    if (rc != RRR_OK) {
+        std::string msg = g_err;
+        return fail(rc, "tensor '%s': %s", name, msg.c_str());
+    }
     return ok();
 }
 

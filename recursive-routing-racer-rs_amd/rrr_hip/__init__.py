@@ -8,11 +8,12 @@ from .engine import (ACT_GQA_V, ACT_IDENTITY, ACT_SILU_GATE, BLOCK_BYTES, DEVICE
                      LOGITS_CHUNKED, LOGITS_Q6K, LOGITS_ROWS, Q4_K, Q5_K, Q6_K, Buffer, ComputeEngine,
                      Context, DescSetHandle, GpuBuffer, Graph, RrrError, device_count,
                      tensor_bytes)
-from . import engine, synth
+from . import engine, gguf, synth
+from .gguf import GGUFModel, ModelConfig, write_gguf
 
 __all__ = [
     "ACT_GQA_V", "ACT_IDENTITY", "ACT_SILU_GATE", "BLOCK_BYTES", "DEVICE_NONE", "F16", "F32",
     "LOGITS_CHUNKED", "LOGITS_Q6K", "LOGITS_ROWS", "Q4_K", "Q5_K", "Q6_K", "Buffer", "ComputeEngine",
     "Context", "DescSetHandle", "GpuBuffer", "Graph", "RrrError", "device_count",
-    "tensor_bytes", "engine", "synth",
+    "tensor_bytes", "engine", "synth", "gguf", "GGUFModel", "ModelConfig", "write_gguf",
 ]

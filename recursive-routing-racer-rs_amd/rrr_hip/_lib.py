@@ -50,7 +50,35 @@ class SweepOp(ctypes.Structure):
     ]
 
 
-# name -> (restype, argtypes); every symbol include/rrr_hip.h declares.
+class GgufKv(ctypes.Structure):
+    """rrr_gguf_kv (include/rrr_gguf.h)."""
+    _fields_ = [
+        ("key", ctypes.c_char_p),
+        ("key_len", u64),
+        ("type", u32),
+        ("elem_type", u32),
+        ("count", u64),
+        ("data", vp),
+        ("bytes", u64),
+    ]
+
+
+class GgufTensor(ctypes.Structure):
+    """rrr_gguf_tensor (include/rrr_gguf.h)."""
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("name_len", u64),
+        ("n_dims", u32),
+        ("type", u32),
+        ("dims", u64 * 4),
+        ("offset", u64),
+        ("n_elements", u64),
+        ("bytes", u64),
+        ("data", vp),
+    ]
+
+
+# name -> (restype, argtypes); every symbol include/rrr_hip.h and include/rrr_gguf.h declare.
 SIGNATURES = {
     "rrr_init": (i32, [i32, ctypes.POINTER(c_ctx_p)]),
     "rrr_destroy": (i32, [c_ctx_p]),
@@ -102,6 +130,22 @@ SIGNATURES = {
     "rrr_timer_start": (i32, [c_ctx_p]),
     "rrr_timer_stop": (i32, [c_ctx_p, ctypes.POINTER(f32)]),
     "rrr_matmul_kquant": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, vp, vp, u32, u32]),
+    # GGUF reader (include/rrr_gguf.h)
+    "rrr_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+    "rrr_gguf_open_memory": (i32, [vp, u64, ctypes.POINTER(vp)]),
+    "rrr_gguf_close": (i32, [vp]),
+    "rrr_gguf_header": (i32, [vp, ctypes.POINTER(u32), ctypes.POINTER(u64), ctypes.POINTER(u64),
+                              ctypes.POINTER(u64), ctypes.POINTER(u64)]),
+    "rrr_gguf_kv_at": (i32, [vp, u64, ctypes.POINTER(GgufKv)]),
+    "rrr_gguf_find_kv": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(u64)]),
+    "rrr_gguf_kv_strings": (i32, [vp, u64, u64, u64, ctypes.POINTER(vp), ctypes.POINTER(u64)]),
+    "rrr_gguf_get_u64": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(u64)]),
+    "rrr_gguf_get_f64": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "rrr_gguf_get_str": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(vp), ctypes.POINTER(u64)]),
+    "rrr_gguf_tensor_at": (i32, [vp, u64, ctypes.POINTER(GgufTensor)]),
+    "rrr_gguf_find_tensor": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(GgufTensor)]),
+    "rrr_gguf_type_size": (i32, [u32, ctypes.POINTER(u32), ctypes.POINTER(u32)]),
+    "rrr_gguf_upload": (i32, [c_ctx_p, vp, ctypes.c_char_p, ctypes.POINTER(c_buf_p)]),
 }
 
 SYNTH_SIGNATURES = {

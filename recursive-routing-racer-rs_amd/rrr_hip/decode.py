@@ -28,8 +28,10 @@ with the attention rows in): rope_kv_store (RoPE on Q and K, K and V stored
 in row pos) and attention over rows 0..pos replace the position-0 gather,
 and the O-proj GEMV takes the attention output.
 
-Weights are seeded synthetic tensors (the recipes of synth.py); each tensor
-has its own stream id, so any subset can be regenerated on the host.
+Weights are seeded synthetic tensors (the recipes of synth.py; each tensor
+has its own stream id, so any subset can be regenerated on the host), or a
+GGUF model's tensors uploaded as stored (DecodeSweep(..., gguf=model)), the
+weight types then read per tensor from the file.
 """
 from dataclasses import dataclass
 
@@ -37,6 +39,7 @@ import numpy as np
 
 from . import engine as E
 from . import synth
+from .gguf import ModelConfig
 
 
 @dataclass(frozen=True)
@@ -90,6 +93,14 @@ class Phi4Shape:
         emb = E.tensor_bytes(E.Q6_K, d, self.vocab) if logits == "q6k" else self.vocab * d * 4
         total += emb + d * 4 + self.vocab * 4                          # logits
         return total
+
+
+def shape_from_config(cfg, max_seq=2048, chunk=8192):
+    """The decode shape of a model configuration read from GGUF metadata."""
+    return Phi4Shape(d_model=cfg.d_model, n_layers=cfg.n_layers, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
+                     head_dim=cfg.head_dim, ffn_dim=cfg.ffn_dim, vocab=cfg.vocab_size, eps=cfg.rms_eps, chunk=chunk,
+                     rope_dim=cfg.rope_dim, rope_theta=cfg.rope_theta, rope_attn_factor=cfg.rope_attn_factor,
+                     max_seq=max_seq)
 
 
 # stream ids of the synthetic tensors
@@ -151,25 +162,97 @@ def x_host(seed, shape):
     return synth.normal_f32(seed, S_X, shape.d_model)
 
 
+def write_synthetic_gguf(path, shape, seed=3, alignment=32):
+    """Writes the seeded synthetic model of `shape` as a Phi-3-architecture
+    GGUF file: the metadata keys ModelConfig.from_gguf reads, and the tensors
+    DecodeSweep(gguf=...) loads under their GGUF names, holding the same bytes
+    as the synthetic sweep of the same seed (the Q6_K token_embd tied to the
+    output).  Returns the data section's file offset."""
+    from . import gguf as G
+    a = "phi3"
+    md = [("general.architecture", G.STRING, a), ("general.name", G.STRING, f"synthetic seed {seed}"),
+          (f"{a}.context_length", G.UINT32, shape.max_seq), (f"{a}.embedding_length", G.UINT32, shape.d_model),
+          (f"{a}.feed_forward_length", G.UINT32, shape.ffn_dim), (f"{a}.block_count", G.UINT32, shape.n_layers),
+          (f"{a}.attention.head_count", G.UINT32, shape.n_heads),
+          (f"{a}.attention.head_count_kv", G.UINT32, shape.n_kv_heads),
+          (f"{a}.attention.layer_norm_rms_epsilon", G.FLOAT32, shape.eps),
+          (f"{a}.rope.dimension_count", G.UINT32, shape.rope_dim),
+          (f"{a}.rope.freq_base", G.FLOAT32, shape.rope_theta),
+          (f"{a}.rope.scaling.attn_factor", G.FLOAT32, shape.rope_attn_factor),
+          ("general.file_type", G.UINT32, 15), ("general.quantization_version", G.UINT32, 2)]
+    d = shape.d_model
+    fac = rope_factors_host(seed, shape)
+    tensors = [("token_embd.weight", E.Q6_K, (d, shape.vocab), embedding_q6k_host(seed, shape)),
+               ("output_norm.weight", E.F32, (d,), gamma_host(seed, S_OUT_NORM, d)),
+               ("rope_factors_long.weight", E.F32, (fac.size,), fac),
+               ("rope_factors_short.weight", E.F32, (fac.size,), fac)]
+    for i in range(shape.n_layers):
+        h = layer_host(seed, shape, i)
+        p = f"blk.{i}."
+        tensors.append((p + "attn_norm.weight", E.F32, (d,), h["attn_norm"]))
+        for name, qt, K, N in shape.layer_tensors(i):
+            tensors.append((p + name + ".weight", qt, (K, N), h[name]))
+            if name == "attn_output":
+                tensors.append((p + "ffn_norm.weight", E.F32, (d,), h["ffn_norm"]))
+    return G.write_gguf(path, md, tensors, alignment=alignment)
+
+
 class DecodeSweep:
     """Device weights and activations of the sweep; record_token() issues one
     token's operations on the context's stream."""
 
-    def __init__(self, ctx, shape=Phi4Shape(), seed=3, keep_host=False, attention=False, logits="f32"):
+    def __init__(self, ctx, shape=Phi4Shape(), seed=3, keep_host=False, attention=False, logits="f32", gguf=None):
         """logits: "f32" (the F32 matrix in the reference's transposed
         chunks), "q6k" (a raw Q6_K token_embd read as stored) or "both"
-        (both held; `logits_mode` picks the one a token uses)."""
+        (both held; `logits_mode` picks the one a token uses).
+
+        gguf: a GGUFModel to take the shape (ModelConfig.from_gguf) and every
+        weight from, uploaded as stored; `shape` then only gives max_seq and
+        chunk, logits must be "q6k" (the raw Q6_K output matrix) and the
+        token's input row comes from embed(token)."""
         if logits not in ("f32", "q6k", "both"):
             raise ValueError(f"logits={logits!r}")
-        self.ctx, self.shape, self.seed = ctx, shape, seed
+        if gguf is not None:
+            if logits != "q6k":
+                raise ValueError("a GGUF model's logits read its raw Q6_K output matrix: use logits='q6k'")
+            shape = shape_from_config(ModelConfig.from_gguf(gguf), max_seq=shape.max_seq, chunk=shape.chunk)
+        self.ctx, self.shape, self.seed, self.gguf = ctx, shape, seed, gguf
         self.host = {} if keep_host else None
+        d = shape.d_model
+        self.emb = self.emb_q6k = self.tok_emb = None
+        if gguf is None:
+            self._load_synthetic(logits)
+        else:
+            self._load_gguf()
+        self.logits_mode = "q6k" if logits == "q6k" else "f32"
+        self.zero = ctx.to_device(np.zeros(d, np.float32))
+        self.hidden = ctx.alloc(d * 4)
+        self.qkv = ctx.alloc(shape.qkv_dim * 4)
+        self.gate_up = ctx.alloc(2 * shape.ffn_dim * 4)
+        self.logits = ctx.alloc(shape.vocab * 4)
+        self.token = ctx.alloc(4)
+        self.attention = attention
+        if attention:
+            fac = self._rope_factors_host
+            self.n_rope_factors = 0 if fac is None else fac.size
+            self.rope_factors = ctx.to_device(np.ones(1, np.float32) if fac is None else fac)
+            if keep_host:
+                self.host["rope_factors"] = fac
+            cache_bytes = shape.max_seq * shape.kv_stride * 2
+            self.kv = [(ctx.alloc(cache_bytes), ctx.alloc(cache_bytes)) for _ in range(shape.n_layers)]
+            self.attn_out = ctx.alloc(d * 4)
+
+    def _load_synthetic(self, logits):
+        ctx, shape, seed, keep_host = self.ctx, self.shape, self.seed, self.host is not None
         d = shape.d_model
         self.layers = []
         for i in range(shape.n_layers):
             h = layer_host(seed, shape, i)
-            dev = {"attn_norm": ctx.to_device(h["attn_norm"]), "ffn_norm": ctx.to_device(h["ffn_norm"])}
+            dev = {"attn_norm": ctx.to_device(h["attn_norm"]), "ffn_norm": ctx.to_device(h["ffn_norm"]),
+                   "types": {}}
             for name, qt, K, N in shape.layer_tensors(i):
                 dev[name] = ctx.weight_upload(qt, K, N, h[name])
+                dev["types"][name] = qt
             self.layers.append(dev)
             if keep_host:
                 self.host[i] = h
@@ -179,7 +262,6 @@ class DecodeSweep:
         self.x_in = ctx.to_device(x)
         if keep_host:
             self.host.update(out_norm=out_norm, x=x)
-        self.emb = self.emb_q6k = None
         if logits in ("f32", "both"):
             emb = embedding_chunks_host(seed, shape)
             self.emb = ctx.to_device(emb)
@@ -192,22 +274,86 @@ class DecodeSweep:
             if keep_host:
                 self.host["emb_q6k"] = raw
             del raw
-        self.logits_mode = "q6k" if logits == "q6k" else "f32"
-        self.zero = ctx.to_device(np.zeros(d, np.float32))
-        self.hidden = ctx.alloc(d * 4)
-        self.qkv = ctx.alloc(shape.qkv_dim * 4)
-        self.gate_up = ctx.alloc(2 * shape.ffn_dim * 4)
-        self.logits = ctx.alloc(shape.vocab * 4)
-        self.token = ctx.alloc(4)
-        self.attention = attention
-        if attention:
-            fac = rope_factors_host(seed, shape)
-            self.rope_factors = ctx.to_device(fac)
+        self._rope_factors_host = rope_factors_host(seed, shape)
+
+    def _gguf_vector(self, name, n):
+        """A 1-D F32 or F16 tensor of n elements as float32 (norm weights,
+        rope factors; dequant_tensor_f32, phi4.rs:572-587, for these types)."""
+        g = self.gguf
+        info = g.tensor_info(name)
+        if info.n_elements != n or info.typ not in (E.F32, E.F16):
+            raise ValueError(f"{name}: {info.n_elements} elements of ggml type {info.typ}; "
+                             f"{n} elements of F32 or F16 expected")
+        raw = g.tensor_bytes(name)
+        return (raw.view(np.float32) if info.typ == E.F32 else raw.view(np.float16)).astype(np.float32)
+
+    def _gguf_weight(self, name, K, N, types=(E.Q4_K, E.Q5_K, E.Q6_K)):
+        info = self.gguf.tensor_info(name)
+        if info.shape[:2] != (K, N) or info.n_elements != K * N:
+            raise ValueError(f"{name}: shape {info.shape}, expected ({K}, {N})")
+        if info.typ not in types:
+            raise ValueError(f"{name}: ggml type {info.typ}; this path reads types {types}")
+        return self.gguf.upload(self.ctx, name), info.typ
+
+    def _load_gguf(self):
+        """Weights of a Phi-3/4-layout GGUF (combined attn_qkv and ffn_up;
+        load_from_gguf, phi4.rs:704-869), raw bytes uploaded unchanged."""
+        g, s, keep_host = self.gguf, self.shape, self.host is not None
+        cfg = ModelConfig.from_gguf(g)
+        if cfg.separate_qkv or cfg.separate_gate_up or cfg.has_qkv_bias:
+            raise ValueError("separate Q/K/V or gate/up tensors and QKV biases (the Qwen2 layout) are not on "
+                             "this decode path")
+        if s.n_heads * s.head_dim != s.d_model or s.head_dim != 128:
+            raise ValueError(f"head_dim {s.head_dim} x {s.n_heads} heads: the attention kernels need "
+                             "head_dim 128 and n_heads * head_dim = d_model")
+        d, f = s.d_model, s.ffn_dim
+        self.layers = []
+        for i in range(s.n_layers):
+            p = f"blk.{i}."
+            dev = {"types": {}}
+            h = {}
+            for name in ("attn_norm", "ffn_norm"):
+                h[name] = self._gguf_vector(p + name + ".weight", d)
+                dev[name] = self.ctx.to_device(h[name])
+            for name, K, N in (("attn_qkv", d, s.qkv_dim), ("attn_output", d, d), ("ffn_up", d, 2 * f),
+                               ("ffn_down", f, d)):
+                dev[name], dev["types"][name] = self._gguf_weight(p + name + ".weight", K, N)
+                if keep_host:
+                    h[name] = g.tensor_bytes(p + name + ".weight")
+            self.layers.append(dev)
             if keep_host:
-                self.host["rope_factors"] = fac
-            cache_bytes = shape.max_seq * shape.kv_stride * 2
-            self.kv = [(ctx.alloc(cache_bytes), ctx.alloc(cache_bytes)) for _ in range(shape.n_layers)]
-            self.attn_out = ctx.alloc(d * 4)
+                self.host[i] = h
+        out_norm = self._gguf_vector("output_norm.weight", d)
+        self.out_norm = self.ctx.to_device(out_norm)
+        out_name = "output.weight" if cfg.has_output_weight else "token_embd.weight"
+        self.emb_q6k, _ = self._gguf_weight(out_name, d, s.vocab, (E.Q6_K,))
+        if cfg.has_output_weight:
+            self.tok_emb, self.tok_emb_type = self._gguf_weight("token_embd.weight", d, s.vocab,
+                                                                (E.F32, E.Q4_K, E.Q5_K, E.Q6_K))
+        else:
+            self.tok_emb, self.tok_emb_type = self.emb_q6k, E.Q6_K
+        self.tok_row_bytes = E.tensor_bytes(self.tok_emb_type, d, 1)
+        self.x_in = self.ctx.alloc(d * 4)
+        self.embed(0)
+        if keep_host:
+            self.host.update(out_norm=out_norm, emb_q6k=g.tensor_bytes(out_name))
+        self._rope_factors_host = None
+        if cfg.has_rope_factors:
+            self._rope_factors_host = self._gguf_vector("rope_factors_short.weight", s.rope_dim // 2)
+
+    def embed(self, token):
+        """The step's input row: row `token` of token_embd dequantized on the
+        device into x_in (Phi4Model::embed, phi4.rs:2085-2089; bit-exact with
+        the reference's host-dequantized embedding).  GGUF models only."""
+        if self.tok_emb is None:
+            raise ValueError("embed() needs a model loaded from GGUF (the synthetic input row is fixed)")
+        if not 0 <= token < self.shape.vocab:
+            raise ValueError(f"token {token} outside the vocabulary of {self.shape.vocab}")
+        row = self.ctx.view(self.tok_emb, token * self.tok_row_bytes, self.tok_row_bytes)
+        try:
+            self.ctx.dequant(self.tok_emb_type, row, self.x_in, self.shape.d_model)
+        finally:
+            row.free()
 
     def record_token(self, pos=None):
         """One token: the position-0 weight sweep (pos None), or with
@@ -219,17 +365,18 @@ class DecodeSweep:
             raise ValueError("a position needs attention=True and pos < max_seq")
         c.residual_add(self.x_in, self.zero, self.hidden, d)       # hidden = embedding row
         for i, L in enumerate(self.layers):
-            c.gemv_rmsnorm(self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], E.Q5_K, self.qkv, d, s.qkv_dim)
+            T = L["types"]
+            c.gemv_rmsnorm(self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], T["attn_qkv"], self.qkv, d, s.qkv_dim)
             if pos is None:
-                c.gemv_residual(self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], E.Q4_K, self.hidden, d, d)
+                c.gemv_residual(self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], T["attn_output"], self.hidden, d, d)
             else:
                 kc, vc = self.kv[i]
-                c.rope_kv_store(self.qkv, self.rope_factors, s.rope_dim // 2, kc, vc, pos, s.n_heads, s.n_kv_heads,
+                c.rope_kv_store(self.qkv, self.rope_factors, self.n_rope_factors, kc, vc, pos, s.n_heads, s.n_kv_heads,
                                 s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta, s.rope_attn_factor)
                 c.attention(self.qkv, kc, vc, self.attn_out, pos + 1, s.n_kv_heads, s.heads_per_kv, s.head_dim)
-                c.gemv_residual(self.attn_out, E.ACT_IDENTITY, 0, L["attn_output"], E.Q4_K, self.hidden, d, d)
-            c.gemv_rmsnorm(self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], E.Q4_K, self.gate_up, d, 2 * s.ffn_dim)
-            c.gemv_residual(self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], s.down_type(i), self.hidden,
+                c.gemv_residual(self.attn_out, E.ACT_IDENTITY, 0, L["attn_output"], T["attn_output"], self.hidden, d, d)
+            c.gemv_rmsnorm(self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], T["ffn_up"], self.gate_up, d, 2 * s.ffn_dim)
+            c.gemv_residual(self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], T["ffn_down"], self.hidden,
                             s.ffn_dim, d)
         self.record_logits()
 
@@ -293,19 +440,20 @@ class DecodeSweep:
         if M < Mp:   # rows past the prompt stay zero through every step
             c.fill_u32(pf["att16"], 0, M * d * 2, (Mp - M) * d * 2)
         for i, L in enumerate(self.layers):
+            T = L["types"]
             kc, vc = self.kv[i]
             c.rmsnorm_f16(pf["hid"], L["attn_norm"], pf["n16"], Mp, d, s.eps)
-            c.gemm_f16(pf["n16"], L["attn_qkv"], E.Q5_K, pf["qkv"], d, s.qkv_dim, Mp)
-            c.rope_kv_store_rows(pf["qkv"], M, self.rope_factors, s.rope_dim // 2, kc, vc, pos0, s.n_heads,
+            c.gemm_f16(pf["n16"], L["attn_qkv"], T["attn_qkv"], pf["qkv"], d, s.qkv_dim, Mp)
+            c.rope_kv_store_rows(pf["qkv"], M, self.rope_factors, self.n_rope_factors, kc, vc, pos0, s.n_heads,
                                  s.n_kv_heads, s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta,
                                  s.rope_attn_factor)
             c.attention_prefill(pf["qkv"], M, kc, vc, pf["att16"], pos0, s.n_kv_heads, s.heads_per_kv, s.head_dim,
                                 out_type=E.F16)
-            c.gemm_f16(pf["att16"], L["attn_output"], E.Q4_K, pf["hid"], d, d, Mp, accumulate=True)
+            c.gemm_f16(pf["att16"], L["attn_output"], T["attn_output"], pf["hid"], d, d, Mp, accumulate=True)
             c.rmsnorm_f16(pf["hid"], L["ffn_norm"], pf["n16"], Mp, d, s.eps)
-            c.gemm_f16(pf["n16"], L["ffn_up"], E.Q4_K, pf["gu"], d, 2 * F, Mp)
+            c.gemm_f16(pf["n16"], L["ffn_up"], T["ffn_up"], pf["gu"], d, 2 * F, Mp)
             c.silu_gate_f16(pf["gu"], pf["mid16"], pf["mid_scale"], Mp, F)
-            c.gemm_f16(pf["mid16"], L["ffn_down"], s.down_type(i), pf["hid"], F, d, Mp, accumulate=True,
+            c.gemm_f16(pf["mid16"], L["ffn_down"], T["ffn_down"], pf["hid"], F, d, Mp, accumulate=True,
                        row_scale=pf["mid_scale"])
         if M not in pf["last"]:
             pf["last"][M] = c.view(pf["hid"], (M - 1) * d * 4, d * 4)
@@ -340,11 +488,13 @@ class DecodeSweep:
         gqa = s.head_dim | (s.heads_per_kv << 16)
         ops = []
         for i, L in enumerate(self.layers):
-            ops += [("rmsnorm", self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], E.Q5_K, self.qkv, d, s.qkv_dim),
-                    ("residual", self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], E.Q4_K, self.hidden, d, d),
-                    ("rmsnorm", self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], E.Q4_K, self.gate_up, d,
+            T = L["types"]
+            ops += [("rmsnorm", self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], T["attn_qkv"], self.qkv, d,
+                     s.qkv_dim),
+                    ("residual", self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], T["attn_output"], self.hidden, d, d),
+                    ("rmsnorm", self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], T["ffn_up"], self.gate_up, d,
                      2 * s.ffn_dim),
-                    ("residual", self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], s.down_type(i), self.hidden,
+                    ("residual", self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], T["ffn_down"], self.hidden,
                      s.ffn_dim, d)]
         return ops
 

@@ -27,6 +27,9 @@ ERR_UNSUPPORTED = -7
 ERR_NO_DEVICE = -8
 ERR_STATE = -9
 ERR_STALE = -10
+ERR_FORMAT = -11
+ERR_NOT_FOUND = -12
+ERR_IO = -13
 
 F32, F16, Q4_K, Q5_K, Q6_K = 0, 1, 12, 13, 14
 LOGITS_ROWS, LOGITS_CHUNKED, LOGITS_Q6K = 0, 1, 2

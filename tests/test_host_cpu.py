@@ -14,11 +14,12 @@ from rrr_hip.engine import (ERR_BAD_SHAPE, ERR_BAD_TYPE, ERR_INVALID_ARG, ERR_NO
                             ERR_SHORT_BUFFER, ERR_STALE, ERR_STATE, ERR_UNSUPPORTED)
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(REPO, "include", "rrr_hip.h")
+HEADERS = [os.path.join(REPO, "include", h) for h in sorted(os.listdir(os.path.join(REPO, "include")))
+           if h.endswith(".h")]
 
 
 def header_symbols():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(rrr_[a-z0-9_]+)\s*\(", text)))
 
