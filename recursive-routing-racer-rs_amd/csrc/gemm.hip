@@ -9,7 +9,7 @@
 // 4*(l/16)+r of column l%16 in register r).  Waves 4-7 stage the operands.
 //
 // K steps of BK elements.  Per step each staging thread dequantizes
-// UE = BN*BK/256 consecutive elements of one weight row into an fp16 LDS tile
+// 32 elements (two runs of 16) of one weight row into an fp16 LDS tile
 // and converts BM*BK/256 elements of X from bf16 to fp16 (exact for |x| in
 // f16's normal range; f16 X is copied as it is).  The dequant runs in packed fp16: v_perm places
 // each quant byte q under the exponent of 1024 (f16 0x64qq = 1024 + q), an
@@ -62,112 +62,136 @@ __device__ __forceinline__ void q4_to_f16(uint32_t v, f16x2v &p01, f16x2v &p23)
     p23 = f16x2_bits(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u));
 }
 
-// Units of UE consecutive elements e0 .. e0+UE-1 of one super-block row
-// (e0 = 64c + lp, lp % UE == 0, lp < 64, UE in {16, 32}).  Loads take the row
-// and in-block offset in voff and the block start in the scalar offset blk.
-// dequant() writes UE/2 dwords of fp16 pairs in element order.
+// Units of 32 * NP elements of one super-block row: part p (0 or 1) of
+// 64-element chunk c holds the two runs of 16 elements 64c + 16p + (0..15)
+// and 64c + 32 + 16p + (0..15), which come from the same 16 quant bytes (low
+// and high nibbles), so the two parts of a chunk load disjoint bytes.  A unit
+// is parts p0 .. p0 + NP - 1 of one chunk (the kernel below takes NP = 1: two
+// staging threads per chunk; NP = 2 is the whole chunk with one header load).
+// Loads take the row and in-block offset in voff and the block start in the
+// scalar offset blk.  dequant() writes 16 dwords of fp16 pairs per part: run 0
+// in element order, then run 1.
 
 // Q4_K (phi4.rs:481-510): element 64g + 32h + l is the h-th nibble of qs[32g + l]
 // of sub-block 2g + h; w = (d*sc)*q - dmin*m.
-template <int UE>
+template <int NP>
 struct GqQ4K {
     static constexpr uint32_t BS = 144;
-    struct Raw { u32x4 hdr, q[UE / 16]; };
-    // chunk c (64 elements, = pair g), lane part lp = UE * p inside the chunk
-    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t lp)
+    struct Raw { u32x4 hdr, q[NP]; };
+    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t p0)
     {
         r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, blk, 0);
 #pragma unroll
-        for (int i = 0; i < UE / 16; i++)
-            r.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 + 32 * c + (lp & 31) + 16 * i, blk, 0);
+        for (int k = 0; k < NP; k++)
+            r.q[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 + 32 * c + 16 * (p0 + k), blk, 0);
     }
-    __device__ static void dequant(const Raw &r, uint32_t c, uint32_t lp, uint32_t *out)
+    __device__ static void dequant(const Raw &r, uint32_t c, uint32_t, uint32_t *out)
     {
-        const uint32_t sb = 2 * c + (lp >> 5), h = lp >> 5;
-        uint32_t sc, mn;
-        scale_min_k4(sb, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
-        const _Float16 A = (_Float16)__fmul_rn(h2f(r.hdr.x), (float)sc);
-        const _Float16 Bn = (_Float16)(-__fmul_rn(h2f(r.hdr.x >> 16), (float)mn));
-        const f16x2v A2 = {A, A}, B2 = {Bn, Bn}, K2 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const f16x2v K2 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
-        for (int i = 0; i < UE / 4; i++) {
-            const uint32_t v = (r.q[i >> 2][i & 3] >> (4 * h)) & 0x0F0F0F0Fu;
-            f16x2v p01, p23;
-            q4_to_f16(v, p01, p23);
-            out[2 * i] = bits_f16x2(__builtin_elementwise_fma(A2, p01 - K2, B2));
-            out[2 * i + 1] = bits_f16x2(__builtin_elementwise_fma(A2, p23 - K2, B2));
+        for (int h = 0; h < 2; h++) {
+            uint32_t sc, mn;
+            scale_min_k4(2 * c + h, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
+            const _Float16 A = (_Float16)__fmul_rn(h2f(r.hdr.x), (float)sc);
+            const _Float16 Bn = (_Float16)(-__fmul_rn(h2f(r.hdr.x >> 16), (float)mn));
+            const f16x2v A2 = {A, A}, B2 = {Bn, Bn};
+#pragma unroll
+            for (int k = 0; k < NP; k++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t v = (r.q[k][i] >> (4 * h)) & 0x0F0F0F0Fu;
+                    f16x2v p01, p23;
+                    q4_to_f16(v, p01, p23);
+                    out[16 * k + 8 * h + 2 * i] = bits_f16x2(__builtin_elementwise_fma(A2, p01 - K2, B2));
+                    out[16 * k + 8 * h + 2 * i + 1] = bits_f16x2(__builtin_elementwise_fma(A2, p23 - K2, B2));
+                }
         }
     }
 };
 
 // Q5_K (phi4.rs:512-542): Q4_K plus bit sb of qh[l] as bit 4.
-template <int UE>
+template <int NP>
 struct GqQ5K {
     static constexpr uint32_t BS = 176;
-    struct Raw { u32x4 hdr, qh[UE / 16], q[UE / 16]; };
-    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t lp)
+    struct Raw { u32x4 hdr, qh[NP], q[NP]; };
+    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t p0)
     {
         r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, blk, 0);
 #pragma unroll
-        for (int i = 0; i < UE / 16; i++) {
-            r.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 + (lp & 31) + 16 * i, blk, 0);
-            r.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 48 + 32 * c + (lp & 31) + 16 * i, blk, 0);
+        for (int k = 0; k < NP; k++) {
+            r.qh[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 + 16 * (p0 + k), blk, 0);
+            r.q[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 48 + 32 * c + 16 * (p0 + k), blk, 0);
         }
     }
-    __device__ static void dequant(const Raw &r, uint32_t c, uint32_t lp, uint32_t *out)
+    __device__ static void dequant(const Raw &r, uint32_t c, uint32_t, uint32_t *out)
     {
-        const uint32_t sb = 2 * c + (lp >> 5), h = lp >> 5;
-        uint32_t sc, mn;
-        scale_min_k4(sb, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
-        const _Float16 A = (_Float16)__fmul_rn(h2f(r.hdr.x), (float)sc);
-        const _Float16 Bn = (_Float16)(-__fmul_rn(h2f(r.hdr.x >> 16), (float)mn));
-        const f16x2v A2 = {A, A}, B2 = {Bn, Bn}, K2 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const f16x2v K2 = {(_Float16)1024.0f, (_Float16)1024.0f};
 #pragma unroll
-        for (int i = 0; i < UE / 4; i++) {
-            const uint32_t v = ((r.q[i >> 2][i & 3] >> (4 * h)) & 0x0F0F0F0Fu) |
-                               (((r.qh[i >> 2][i & 3] >> sb) & 0x01010101u) << 4);
-            f16x2v p01, p23;
-            q4_to_f16(v, p01, p23);
-            out[2 * i] = bits_f16x2(__builtin_elementwise_fma(A2, p01 - K2, B2));
-            out[2 * i + 1] = bits_f16x2(__builtin_elementwise_fma(A2, p23 - K2, B2));
+        for (int h = 0; h < 2; h++) {
+            const uint32_t sb = 2 * c + h;
+            uint32_t sc, mn;
+            scale_min_k4(sb, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
+            const _Float16 A = (_Float16)__fmul_rn(h2f(r.hdr.x), (float)sc);
+            const _Float16 Bn = (_Float16)(-__fmul_rn(h2f(r.hdr.x >> 16), (float)mn));
+            const f16x2v A2 = {A, A}, B2 = {Bn, Bn};
+#pragma unroll
+            for (int k = 0; k < NP; k++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t v = ((r.q[k][i] >> (4 * h)) & 0x0F0F0F0Fu) | (((r.qh[k][i] >> sb) & 0x01010101u) << 4);
+                    f16x2v p01, p23;
+                    q4_to_f16(v, p01, p23);
+                    out[16 * k + 8 * h + 2 * i] = bits_f16x2(__builtin_elementwise_fma(A2, p01 - K2, B2));
+                    out[16 * k + 8 * h + 2 * i + 1] = bits_f16x2(__builtin_elementwise_fma(A2, p23 - K2, B2));
+                }
         }
     }
 };
 
 // Q6_K (phi4.rs:444-479): element 128h6 + 32Qd + l is ql[64h6 + 32(Qd&1) + l]
 // (high nibble when Qd >= 2) with qh[32h6 + l] bits 2Qd; scale sc[e/16] (the
-// is = g*8 + l/16 rule, phi4.rs:463); w = (d*sc)*(q - 32).
-template <int UE>
+// is = g*8 + l/16 rule, phi4.rs:463); w = (d*sc)*(q - 32).  Chunk c is
+// h6 = c/2 with Qd = 2(c&1) + j for run j, so l = 16p + (0..15) in both runs.
+template <int NP>
 struct GqQ6K {
     static constexpr uint32_t BS = 210;
-    struct Raw { u32x4 ql[UE / 16], qh[UE / 16]; uint32_t sc, d; };
-    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t lp)
+    struct Raw { u32x4 ql[NP][2], qh[NP]; uint32_t sc, d; };
+    __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t p0)
     {
-        const uint32_t h6 = c >> 1, l0 = lp & 31, qd1 = (lp >> 5) & 1;
+        const uint32_t h6 = c >> 1;
 #pragma unroll
-        for (int i = 0; i < UE / 16; i++) {
-            r.ql[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * h6 + 32 * qd1 + l0 + 16 * i, blk, 0);
-            r.qh[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 128 + 32 * h6 + l0 + 16 * i, blk, 0);
+        for (int k = 0; k < NP; k++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                r.ql[k][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * h6 + 32 * j + 16 * (p0 + k), blk, 0);
+            r.qh[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 128 + 32 * h6 + 16 * (p0 + k), blk, 0);
         }
         r.sc = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 192 + 4 * c, blk, 0);
         r.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, voff + 208, blk, 0);
     }
-    __device__ static void dequant(const Raw &r, uint32_t c, uint32_t lp, uint32_t *out)
+    __device__ static void dequant(const Raw &r, uint32_t c, uint32_t p0, uint32_t *out)
     {
-        const uint32_t qd = 2 * (c & 1) + (lp >> 5), hi = c & 1, is0 = lp >> 4;   // is = 4c + lp/16 (+1)
+        const uint32_t hi = c & 1;
         const float d = h2f(r.d);
         const f16x2v K2 = {(_Float16)1056.0f, (_Float16)1056.0f};
 #pragma unroll
-        for (int i = 0; i < UE / 4; i++) {
-            const _Float16 A = (_Float16)__fmul_rn(d, (float)(int8_t)byte_of(r.sc, is0 + (i >> 2)));
-            const f16x2v A2 = {A, A};
-            const uint32_t v = ((r.ql[i >> 2][i & 3] >> (4 * hi)) & 0x0F0F0F0Fu) |
-                               (((r.qh[i >> 2][i & 3] >> (2 * qd)) & 0x03030303u) << 4);
-            f16x2v p01, p23;
-            q4_to_f16(v, p01, p23);
-            out[2 * i] = bits_f16x2(A2 * (p01 - K2));
-            out[2 * i + 1] = bits_f16x2(A2 * (p23 - K2));
-        }
+        for (int k = 0; k < NP; k++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t qd = 2 * hi + j;
+                // scale of elements 64c + 32j + 16p .. +15: sc[4c + 2j + p]
+                const _Float16 A = (_Float16)__fmul_rn(d, (float)(int8_t)byte_of(r.sc, 2 * j + p0 + k));
+                const f16x2v A2 = {A, A};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t v = ((r.ql[k][j][i] >> (4 * hi)) & 0x0F0F0F0Fu) |
+                                       (((r.qh[k][i] >> (2 * qd)) & 0x03030303u) << 4);
+                    f16x2v p01, p23;
+                    q4_to_f16(v, p01, p23);
+                    out[16 * k + 8 * j + 2 * i] = bits_f16x2(A2 * (p01 - K2));
+                    out[16 * k + 8 * j + 2 * i + 1] = bits_f16x2(A2 * (p23 - K2));
+                }
+            }
     }
 };
 
@@ -184,9 +208,10 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     constexpr int LDK = BK + 8;                            // f16 per LDS row (16-byte pad)
     constexpr int TI = BM / 32, TJ = BN / 32;              // 16x16 tiles per MFMA wave
     constexpr int UE = BN * BK / 256, TPW = BK / UE;       // weight elements per producer thread, threads per row
-    constexpr int XE = BM * BK / 256, TPX = BK / XE;       // X elements per producer thread, threads per row
-    static_assert((UE == 16 || UE == 32) && XE % 8 == 0 && BK % 64 == 0, "tile shape");
-    using Q = QT<UE>;
+    constexpr int XE = BM * BK / 256;                      // X elements per producer thread
+    constexpr int XC = BK / 8, XRS = 256 / XC;             // 16-byte chunks per X row and step, rows per pass
+    static_assert(UE == 32 && XE % 8 == 0 && BK % 64 == 0, "tile shape");
+    using Q = QT<1>;
     extern __shared__ float smem[];
     _Float16 *As = (_Float16 *)smem;                       // [2][BM][LDK]
     _Float16 *Bs = As + 2 * BM * LDK;                      // [2][BN][LDK]
@@ -211,10 +236,14 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     if (wave >= 4) {
         // ---- producer: loads, dequant, conversion --------------------------
         const uint32_t tp = t - 256;
-        const uint32_t ur = tp / TPW, lb = UE * (tp % TPW);   // row, first element inside the step
+        // weight row, the step's 64-element chunk (its start lb) and the part wp of it
+        const uint32_t ur = tp / TPW, lb = 64 * ((tp % TPW) >> 1), wp = tp & 1;
         const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, (uint64_t)N * B * Q::BS);
         const uint32_t wvoff = (n0 + ur) * B * Q::BS;
-        const uint32_t xr = tp / TPX, xk = XE * (tp % TPX);
+        // X: pass i covers rows XRS*i .. XRS*(i+1)-1 of the step, consecutive
+        // threads on consecutive 16-byte chunks of a row (whole cache lines per
+        // wave load)
+        const uint32_t xr = tp / XC, xk = 8 * (tp % XC);
         const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X, (uint64_t)M * K * 2);
         const uint32_t xvoff = ((m0 + xr) * K + xk) * 2;
         struct Set {
@@ -226,19 +255,21 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         auto issue = [&](Set &st, uint32_t s) {
             const bool ok = s < nsteps;   // past the end: out-of-range offsets, zeros
             const uint32_t sg = s0 + s, e0 = (sg * BK) % 256 + lb;
-            Q::load(st.raw, wrs, wvoff, ok ? (sg * BK / 256) * Q::BS : GM_OOB, e0 >> 6, e0 & 63);
+            Q::load(st.raw, wrs, wvoff, ok ? (sg * BK / 256) * Q::BS : GM_OOB, e0 >> 6, wp);
             const uint32_t so = ok ? sg * BK * 2 : GM_OOB;
 #pragma unroll
-            for (int i = 0; i < XE / 8; i++) st.xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvoff + 16 * i, so, 0);
+            for (int i = 0; i < XE / 8; i++)
+                st.xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvoff + XRS * i * K * 2, so, 0);
         };
         auto stage = [&](const Set &st, uint32_t s) {
             const uint32_t buf = s & 1, e0 = ((s0 + s) * BK) % 256 + lb;
-            uint32_t o[UE / 2];
-            Q::dequant(st.raw, e0 >> 6, e0 & 63, o);
-            _Float16 *dst = Bs + (buf * BN + ur) * LDK + lb;
+            uint32_t o[16];
+            Q::dequant(st.raw, e0 >> 6, wp, o);
+            _Float16 *dst = Bs + (buf * BN + ur) * LDK + lb + 16 * wp;   // runs at +0 and +32
 #pragma unroll
-            for (int i = 0; i < UE / 8; i++) *(u32x4 *)(dst + 8 * i) = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
-            _Float16 *xd = As + (buf * BM + xr) * LDK + xk;
+            for (int i = 0; i < 4; i++)
+                *(u32x4 *)(dst + 8 * (i & 1) + 32 * (i >> 1)) = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+            _Float16 *xd = As + (buf * BM + xr) * LDK + xk;   // pass i: + XRS*i rows
 #pragma unroll
             for (int i = 0; i < XE / 8; i++) {
                 const u32x4 v = st.xv[i];
@@ -250,7 +281,7 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
                     for (int c = 0; c < 4; c++)
                         h[c] = pk_f16(__uint_as_float(v[c] << 16), __uint_as_float(v[c] & 0xFFFF0000u));
                 }
-                *(u32x4 *)(xd + 8 * i) = h;
+                *(u32x4 *)(xd + XRS * i * LDK) = h;
             }
         };
         issue(S0, 0);
