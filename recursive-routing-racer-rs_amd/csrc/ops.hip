@@ -199,11 +199,21 @@ __global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__
     float m = 0.0f;
     float v[NV > 0 ? NV : 1];
     if constexpr (NV > 0) {
+        // thread t holds elements 4 (t + 256 j) .. +3 (F % 4 == 0: 16-byte loads)
 #pragma unroll
-        for (int j = 0; j < NV; j++) {
-            const uint32_t i = t + 256u * j;
-            v[j] = i < F ? silu_f(row[i]) * row[F + i] : 0.0f;
-            m = fmaxf(m, fabsf(v[j]));
+        for (int j = 0; j < NV / 4; j++) {
+            const uint32_t i = 4 * (t + 256u * j);
+            float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
+            if (i < F) {
+                g = *(const float4 *)(row + i);
+                u = *(const float4 *)(row + F + i);
+            }
+            v[4 * j] = silu_f(g.x) * u.x;
+            v[4 * j + 1] = silu_f(g.y) * u.y;
+            v[4 * j + 2] = silu_f(g.z) * u.z;
+            v[4 * j + 3] = silu_f(g.w) * u.w;
+#pragma unroll
+            for (int c = 0; c < 4; c++) m = fmaxf(m, fabsf(v[4 * j + c]));
         }
     } else {
         for (uint32_t i = t; i < F; i += 256) m = fmaxf(m, fabsf(silu_f(row[i]) * row[F + i]));
@@ -216,10 +226,13 @@ __global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__
     if (m > 0.0f && __builtin_isfinite(m)) (void)frexpf(m, &e);
     const float sc = ldexpf(1.0f, 15 - e);
     if constexpr (NV > 0) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-        for (int j = 0; j < NV; j++) {
-            const uint32_t i = t + 256u * j;
-            if (i < F) out[i] = to_out<_Float16>(v[j] * sc);
+        for (int j = 0; j < NV / 4; j++) {
+            const uint32_t i = 4 * (t + 256u * j);
+            if (i < F)
+                *(h4 *)(out + i) = h4{to_out<_Float16>(v[4 * j] * sc), to_out<_Float16>(v[4 * j + 1] * sc),
+                                      to_out<_Float16>(v[4 * j + 2] * sc), to_out<_Float16>(v[4 * j + 3] * sc)};
         }
     } else {
         for (uint32_t i = t; i < F; i += 256) out[i] = to_out<_Float16>((silu_f(row[i]) * row[F + i]) * sc);
@@ -230,7 +243,7 @@ __global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__
 hipError_t launch_silu_gate_f16(const float *gu, uint16_t *mid, float *rscale, uint32_t rows, uint32_t F,
                                 hipStream_t s)
 {
-    if (F <= 256 * 32)
+    if (F <= 256 * 32 && F % 4 == 0)
         hipLaunchKernelGGL(silu_gate_f16_rows_kernel<32>, dim3(rows), dim3(256), 0, s, gu, (_Float16 *)mid, rscale, F);
     else
         hipLaunchKernelGGL(silu_gate_f16_rows_kernel<0>, dim3(rows), dim3(256), 0, s, gu, (_Float16 *)mid, rscale, F);

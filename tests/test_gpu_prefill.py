@@ -223,8 +223,11 @@ def block_f16(v):
     return (v * sc[:, None]).astype(np.float16), np.ldexp(np.float32(1.0), e - 15).astype(np.float32)
 
 
-def test_rmsnorm_and_silu_gate_f16(ctx):
-    rows, d, F = 130, 3072, 8192
+@pytest.mark.parametrize("rows,F", [(130, 8192), (12, 1000), (12, 1002), (12, 9000)])
+def test_rmsnorm_and_silu_gate_f16(ctx, rows, F):
+    """F = 8192 and 1000: the register form with 16-byte loads (a partial
+    last pass at 1000); 1002 and 9000: the general form."""
+    d = 3072
     x = synth.normal_f32(6, 70, rows * d)
     g = synth.normal_f32(6, 71, d, 1.0, 0.1)
     gu = synth.normal_f32(6, 72, rows * 2 * F, 0.0, 2.0)
