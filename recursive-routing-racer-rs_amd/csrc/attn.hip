@@ -462,7 +462,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
 //   S^T = K . Q^T    (v_mfma_f32_16x16x32_f16, keys x tokens, K from the f16
 //                     cache as A operands, Q^T as B operands in f16 hi + lo,
 //                     so the scores carry ~2^-22 of Q's rounding)
-//   online softmax per token (exp2, queries pre-scaled by log2(e)/sqrt(128))
+//   online softmax per token (exp2, queries pre-scaled by log2(e)/sqrt(128)),
+//                    its reference max moved lazily (P <= 8)
 //   O^T += V^T . P^T (dims x tokens; P in f16 hi + lo, V exact in f16)
 // In the MFMA layouts (lane l: A row / B column l % 16 at k slots
 // 8 (l / 16) .. +7; D rows 4 (l / 16) + r of column l % 16) lane l's D
@@ -475,8 +476,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
 // The hi + lo splits are taken of Q * 2^(14 - e) (per token and head, the
 // scaled query's largest component f * 2^e, f in [0.5, 1): it lands in
 // [2^13, 2^14), inside f16's range whatever the activations' size) and of
-// P * 2^12 (P <= 1), undone exactly on the scores and at the end; the lo
+// P * 2^12 (P <= 8), undone exactly on the scores and at the end; the lo
 // parts then stay in f16's normal range, where they keep their precision.
+// The Q^T operands sit in LDS (one head's are read per block), so the
+// accumulators need no moves between register files.
 constexpr uint32_t ATTM_LD = 36;   // f16 per V^T row in LDS (32 keys + pad; 72-byte rows)
 constexpr float ATTM_PS = 4096.0f;
 constexpr uint32_t ATTM_WAVES = 4, ATTM_OLD = ATT_HD + 4;   // waves; floats per merged output row (padded)
@@ -493,7 +496,10 @@ struct AttmLds {
     static constexpr size_t VT = (size_t)ATTM_WAVES * ATT_HD * ATTM_LD * 2;            // V^T per wave
     static constexpr size_t O = (size_t)ATTM_WAVES * HPK * 16 * ATTM_OLD * 4;          // merge: outputs
     static constexpr size_t ML = (size_t)ATTM_WAVES * HPK * 16 * 2 * 4;                // merge: max, sum
-    static constexpr size_t BYTES = (VT > O ? VT : O) + ML;
+    static constexpr size_t Q = (size_t)HPK * 4 * 2 * 64 * 16;                        // Q^T operands, hi + lo
+    // the loop's V^T and Q^T share their bytes with the merge's outputs
+    static constexpr size_t LOOP = VT + Q, MAIN = LOOP > O ? LOOP : O;
+    static constexpr size_t BYTES = MAIN + ML;
 };
 
 template <int HPK, bool F16OUT>
@@ -511,15 +517,17 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
     const uint32_t wv = threadIdx.x >> 6;
     _Float16 *vt = (_Float16 *)sm + (size_t)wv * ATT_HD * ATTM_LD;   // this wave's V^T
     float *mo = (float *)sm;                                        // merge outputs (after the loop)
-    float *mml = (float *)(sm + (LD::VT > LD::O ? LD::VT : LD::O)); // merge max / sum
+    float *mml = (float *)(sm + LD::MAIN);                          // merge max / sum
+    h8 *qop = (h8 *)(sm + LD::VT);                                  // Q^T operands [h][kk][hi, lo][lane]
     const uint32_t g = blockIdx.x, tb = blockIdx.y, l = threadIdx.x & 63, n = l & 15, grp = l >> 4;
     const uint32_t tok = tb * 16 + n, tq = min(tok, rows - 1), tpos = pos0 + tq;
     const uint32_t last = pos0 + min(tb * 16 + 15, rows - 1);      // the last cache row the block's tokens see
     const uint32_t nblk = last / 32 + 1;
     const uint16_t *kbase = kc + (size_t)g * ATT_HD, *vbase = vc + (size_t)g * ATT_HD;
 
-    // Q^T operands of each head: token tq, dims 32 kk + 8 grp .. +7, scaled, hi + lo
-    h8 qh[HPK][4], ql[HPK][4];
+    // Q^T operands of each head: token tq, dims 32 kk + 8 grp .. +7, scaled,
+    // hi + lo; every wave computes them, wave 0 keeps them in LDS (the block
+    // loop reads one head's at a time, so the accumulators fit the VGPRs)
     float qs[HPK];   // the scale of head h's scores (undoes the query's power of two)
     const float *q = qkv + (size_t)tq * row_stride;
 #pragma unroll
@@ -544,15 +552,22 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
         const float up = ldexpf(1.0f, 14 - e);
         qs[h] = ldexpf(1.0f, e - 14);
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++)
+        for (int kk = 0; kk < 4; kk++) {
+            h8 qh, ql;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float v = x[kk][i] * up;
                 const _Float16 hi = (_Float16)v;
-                qh[h][kk][i] = hi;
-                ql[h][kk][i] = (_Float16)(v - (float)hi);
+                qh[i] = hi;
+                ql[i] = (_Float16)(v - (float)hi);
             }
+            if (wv == 0) {
+                qop[((h * 4 + kk) * 2) * 64 + l] = qh;
+                qop[((h * 4 + kk) * 2 + 1) * 64 + l] = ql;
+            }
+        }
     }
+    __syncthreads();   // the Q^T operands are in LDS
     f4 o[HPK][8];
     float m[HPK], ls[HPK];
 #pragma unroll
@@ -595,14 +610,20 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
         wave_lds_order();
 #pragma unroll
         for (int h = 0; h < HPK; h++) {
+            h8 qh[4], ql[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                qh[kk] = qop[((h * 4 + kk) * 2) * 64 + l];
+                ql[kk] = qop[((h * 4 + kk) * 2 + 1) * 64 + l];
+            }
             f4 sc[2];
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
                 sc[kt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
-                    sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][kk], qh[h][kk], sc[kt], 0, 0, 0);
-                    sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][kk], ql[h][kk], sc[kt], 0, 0, 0);
+                    sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][kk], qh[kk], sc[kt], 0, 0, 0);
+                    sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][kk], ql[kk], sc[kt], 0, 0, 0);
                 }
             }
             // lane l: sc[kt][r] = score of key c0 + 16 kt + 4 grp + r for its token
@@ -617,11 +638,21 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
                 }
             bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
             bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-            // -inf while none of this wave's blocks so far holds a key of the
-            // token's range (a wave's first block may lie past the token)
-            const float mn = fmaxf(m[h], bm);
+            // Lazy reference max: it moves only when the block's max passes it
+            // by more than 3 (so P <= 8 and P * 2^12 stays inside f16), which
+            // after the first blocks is rare, and the accumulators are then
+            // rescaled in a branch the whole wave skips otherwise.  -inf while
+            // none of this wave's blocks so far holds a key of the token's
+            // range (a wave's first block may lie past the token).
+            const float mo = m[h];
+            const bool upd = bm > mo + 3.0f;   // -inf + 3 = -inf: a first finite block moves it
+            const float mn = upd ? bm : mo;
             const bool none = mn == -__builtin_inff();
-            const float cf = none ? 1.0f : exp2f(m[h] - mn);
+            const float cf = upd && mo != -__builtin_inff() ? exp2f(mo - mn) : 1.0f;
+            if (__builtin_amdgcn_ballot_w64(cf != 1.0f)) {
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) o[h][dt] = o[h][dt] * cf;
+            }
             float ps = 0.0f;
             h8 pb, pl;
 #pragma unroll
@@ -643,7 +674,7 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
                 const _Float16 *vrow = vt + (16 * dt + n) * ATTM_LD;
                 const h4 a0 = *(const h4 *)(vrow + 4 * grp), a1 = *(const h4 *)(vrow + 16 + 4 * grp);
                 const h8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-                o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[h][dt] * cf, 0, 0, 0);
+                o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[h][dt], 0, 0, 0);
                 o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[h][dt], 0, 0, 0);
             }
         }
