@@ -25,6 +25,7 @@ the result that fills roofline.traffic.
 import argparse
 import json
 import os
+import shutil
 import sys
 import tempfile
 import time
@@ -226,8 +227,16 @@ def gguf_load(ctx, sw, shape):
     model's bit for bit."""
     with tempfile.TemporaryDirectory() as tmp:
         path = os.path.join(tmp, "phi4-mini-synthetic.gguf")
+        need = int(2.6e9)
+        if shutil.disk_usage(tmp).free < need:
+            log(f"[bench] GGUF load skipped: less than {need / 1e9:.1f} GB free in {tmp}")
+            return {"skipped": f"less than {need / 1e9:.1f} GB free in the temporary directory"}
         t0 = time.perf_counter()
-        decode.write_synthetic_gguf(path, shape, seed=3)
+        try:
+            decode.write_synthetic_gguf(path, shape, seed=3)
+        except OSError as e:
+            log(f"[bench] GGUF load skipped: writing the file failed ({e})")
+            return {"skipped": f"writing the file failed: {e}"}
         t_write = time.perf_counter() - t0
         size = os.path.getsize(path)
         t0 = time.perf_counter()
