@@ -523,7 +523,7 @@ int rrr_gguf_kv_strings(const rrr_gguf *g, uint64_t index, uint64_t first, uint6
     if (count && (!ptrs || !lens)) return err(RRR_ERR_NULL, "rrr_gguf_kv_strings: null output arrays");
     const rrr_gguf::Kv &kv = g->kvs[index];
     if (kv.type == RRR_GGUF_STRING) {
-        if (first + count > 1 || first > 1)
+        if (first > 1 || count > 1 - first)
             return err(RRR_ERR_INVALID_ARG, "key '%s' is one string; strings %llu..+%llu requested", kv.key.c_str(),
                        (ull)first, (ull)count);
         if (count) {

@@ -382,6 +382,8 @@ def test_string_array_ranges():
             assert lib.rrr_gguf_kv_strings(m._h, 1, 0, 1, ptrs, lens) == 0
             assert import_ct.string_at(ptrs[0], lens[0]) == b"solo"
             assert lib.rrr_gguf_kv_strings(m._h, 1, 1, 1, ptrs, lens) == ERR_INVALID_ARG
+            assert lib.rrr_gguf_kv_strings(m._h, 1, 1, 2 ** 64 - 1, ptrs, lens) == ERR_INVALID_ARG   # no wrap
+            assert lib.rrr_gguf_kv_strings(m._h, 0, 1, 2 ** 64 - 1, ptrs, lens) == ERR_INVALID_ARG
 
 
 def test_upload_validation_without_device(tmp_path):
