@@ -980,7 +980,12 @@ static int dispatch_one(rrr_ctx *ctx, const char *name, rrr_buf *const *bufs, ui
         TRY(push_u32(push, push_bytes, 7, p7, name));
         const uint32_t rp = (p7[1] + p7[2]) * (p7[4] / 2), hkv = p7[6] / 2;
         TRY(want_grid(groups, (std::max(rp, hkv) + 63) / 64, 1, 1, name));
-        const uint32_t nf = bufs[1] ? (uint32_t)std::min<uint64_t>(bufs[1]->bytes / 4, p7[4] / 2) : 0u;
+        // A model without rope factors binds a one-float placeholder that is
+        // never uploaded (rope_factor_len = 1, phi4.rs:965-967); like
+        // apply_rope_cfg's empty list (phi4.rs:243) it means factor 1 for
+        // every pair, so a single float is read only when there is a single pair.
+        uint32_t nf = bufs[1] ? (uint32_t)std::min<uint64_t>(bufs[1]->bytes / 4, p7[4] / 2) : 0u;
+        if (nf == 1 && p7[4] / 2 > 1) nf = 0;
         return rrr_rope_kv_store(ctx, bufs[0], bufs[1], nf, bufs[2], bufs[3], p7[0], p7[1], p7[2], p7[3], p7[4], p7[5],
                                  p7[6], 10000.0f, 1.190238f);
     }

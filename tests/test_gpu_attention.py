@@ -113,6 +113,31 @@ def test_rope_kv_store_dispatch_names(ctx, caches):
         buf.free()
 
 
+def test_rope_kv_store_dispatch_placeholder_factor(ctx, caches):
+    """A model without rope factors binds a one-float buffer that is never
+    uploaded (phi4.rs:965-967); the shim reads it as no factors (factor 1,
+    apply_rope_cfg's empty list, phi4.rs:243), whatever the float holds."""
+    kc, vc = caches
+    rng = np.random.default_rng(11)
+    qkv = rng.standard_normal(QD + 2 * KVS).astype(np.float32)
+    a, c = ctx.to_device(qkv), ctx.to_device(qkv)
+    junk = ctx.to_device(np.array([7.25], np.float32))
+    pos = 9
+    ctx.rope_kv_store(a, None, 0, kc, vc, pos, NH, NKV, HD, RD, QD, KVS)
+    k_typed = ctx.download(kc, np.uint16, KVS, offset=pos * KVS * 2)
+    ctx.fill_u32(kc, 0)
+    rp = (NH + NKV) * (RD // 2)
+    ctx.dispatch("rope_kv_store", [c, junk, kc, vc], [pos, NH, NKV, HD, RD, QD, KVS],
+                 [(max(rp, KVS // 2) + 63) // 64, 1, 1])
+    assert np.array_equal(ctx.download(c, np.float32, QD + 2 * KVS), ctx.download(a, np.float32, QD + 2 * KVS))
+    assert np.array_equal(ctx.download(kc, np.uint16, KVS, offset=pos * KVS * 2), k_typed)
+    ref, _, _ = orc.rope_kv_store(qkv, np.zeros((pos + 1) * KVS, np.uint16), np.zeros((pos + 1) * KVS, np.uint16),
+                                  pos, NH, NKV, HD, RD, factors=None)
+    assert orc.normwise_err(ctx.download(c, np.float32, QD)[:QD], ref[:QD]) < rope_bound(pos)
+    for buf in (a, c, junk):
+        buf.free()
+
+
 def _random_cache(rng, seq, nkv, scale=1.0):
     k = orc.f32_to_f16_bits((rng.standard_normal(seq * nkv * HD) * scale).astype(np.float32))
     v = orc.f32_to_f16_bits(rng.standard_normal(seq * nkv * HD).astype(np.float32))

@@ -290,6 +290,45 @@ def test_logits_parity_both_layouts(ctx, V, chunk):
     xb.free(); yb.free(); Eb.free()
 
 
+def test_logits_full_vocab_both_layouts(ctx):
+    """The full 200,064-entry vocabulary (2.46 GB of F32 weights) in both
+    layouts: rows, and the reference's 25 transposed 8192-entry chunks
+    (phi4.rs:874-893), whose last three start past 2 GiB of the buffer."""
+    K, V, chunk = 3072, 200064, 8192
+    E = synth.normal_f32(11, V, V * K, 0.0, 0.02)
+    x = synth.normal_f32(11, 1, K)
+    ref = orc.logits(x, E, K, V, threads=THREADS, f64=True)
+    xb, yb = ctx.to_device(x), ctx.alloc(V * 4)
+    Eb = ctx.to_device(E)
+    ctx.fill_u32(yb, 0x7FC00000)
+    ctx.logits_f32(xb, Eb, yb, K, V, rrr_hip.LOGITS_ROWS)
+    y_rows = ctx.download(yb)
+    assert np.all(np.isfinite(y_rows))
+    assert err(y_rows, ref) < TOL
+    Ec = orc.logits_chunk_build(E, K, V, chunk)
+    del E
+    ctx.upload(Eb, Ec)
+    del Ec
+    ctx.fill_u32(yb, 0x7FC00000)
+    ctx.logits_f32(xb, Eb, yb, K, V, rrr_hip.LOGITS_CHUNKED, chunk)
+    y_chunk = ctx.download(yb)
+    assert np.all(np.isfinite(y_chunk))
+    assert err(y_chunk, ref) < TOL
+    # every chunk on its own, the ones past 2 GiB included
+    for c in range(0, V, chunk):
+        n = min(chunk, V - c)
+        assert err(y_chunk[c:c + n], ref[c:c + n]) < 4 * TOL, c // chunk
+    # fused RMSNorm over the chunks equals RMSNorm then the chunked logits
+    g = synth.normal_f32(11, 2, K, 1.0, 0.1)
+    gb, nb, y2 = ctx.to_device(g), ctx.alloc(K * 4), ctx.alloc(V * 4)
+    ctx.rmsnorm(xb, gb, nb, 1, K, 1e-5)
+    ctx.logits_f32(nb, Eb, yb, K, V, rrr_hip.LOGITS_CHUNKED, chunk)
+    ctx.logits_rmsnorm(xb, gb, 1e-5, Eb, y2, K, V, rrr_hip.LOGITS_CHUNKED, chunk)
+    assert np.array_equal(ctx.download(yb), ctx.download(y2))
+    for b in (xb, yb, Eb, gb, nb, y2):
+        b.free()
+
+
 def ref_argmax(v):
     """The sequential loop of phi4.rs:1172-1183."""
     best_val, best_id = -np.inf, 0
@@ -364,7 +403,12 @@ def bf16_to_f32(bits):
 @pytest.mark.parametrize("qtype,K,N,M", [(12, 3072, 16384, 128), (14, 8192, 192, 128), (13, 3072, 256, 256),
                                          (12, 512, 128, 384), (14, 256, 64, 128),
                                          # 256 x 128 workgroup tiles
-                                         (12, 512, 16384, 256), (14, 768, 16384, 256), (13, 256, 16384, 256)])
+                                         (12, 512, 16384, 256), (14, 768, 16384, 256), (13, 256, 16384, 256),
+                                         # config 5 as benchmarked (512-token prompt): gate+up in one round of
+                                         # 256 x 128 tiles; down (48 tiles) with K split 4 ways, 8 super-blocks
+                                         # a split; Q4_K down and Q5_K QKV (80 tiles, split 3 ways)
+                                         (12, 3072, 16384, 512), (14, 8192, 3072, 512), (12, 8192, 3072, 512),
+                                         (13, 3072, 5120, 512)])
 def test_gemm_bf16_parity(ctx, qtype, K, N, M):
     raw = weights(qtype, K, N, seed=11, stream=qtype)
     xb = synth.normal_bf16(11, 50 + qtype, M * K)
