@@ -28,7 +28,7 @@ import pytest
 import oracle.oracle as orc
 import rrr_hip
 from rrr_hip import decode
-from test_gpu_decode import oracle_step
+from decode_ref import oracle_step
 
 pytestmark = pytest.mark.gpu
 
