@@ -14,8 +14,9 @@ Inputs:
   shapes of every weight type, plain, fused RMSNorm, fused silu * up and
   batched (4 token rows);
 - from the model: gate/up of the last of 8 Phi-4-mini-shaped random-init
-  layers (the hidden state grows by orders of magnitude layer by layer),
-  through the Q4_K and Q6_K down GEMVs, plain and fused.
+  layers (the hidden state grows by orders of magnitude layer by layer, to
+  silu * up of order 1e7), through the Q4_K and Q6_K down GEMVs, plain and
+  fused.
 """
 import dataclasses
 
@@ -127,12 +128,13 @@ def deep_gate_up(ctx):
     return gu, hidden
 
 
-def test_deep_layer_activations_have_outliers(deep_gate_up):
+def test_deep_layer_activations_are_large(deep_gate_up):
     gu, hidden = deep_gate_up
     assert np.all(np.isfinite(gu)) and np.all(np.isfinite(hidden))
     mid = orc.silu_gate(gu, 8192)
-    # heavy-tailed: the largest element is far past the typical one
-    assert np.max(np.abs(mid)) > 50 * np.median(np.abs(mid))
+    # the random-init hidden state drifts upward layer by layer: by layer 8
+    # silu * up is of order 1e7 (a first layer's is of order 1)
+    assert np.median(np.abs(mid)) > 1e5
 
 
 @pytest.mark.parametrize("qtype", [12, 14])
