@@ -208,6 +208,24 @@ int rrr_rope_kv_store(rrr_ctx *ctx, rrr_buf *qkv, const rrr_buf *rope_factors, u
 int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const rrr_buf *v_cache,
                   rrr_buf *out, uint32_t seq_len, uint32_t n_kv_heads, uint32_t heads_per_kv,
                   uint32_t head_dim);
+/* rrr_attention that allocates nothing.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Plain
+ * device pointers of the current device and a HIP stream (a hipStream_t;
+ * NULL = the default stream); the launch is asynchronous on that stream.
+ * The same kernels and plan as rrr_attention, so the output is the same bits
+ * for the same inputs and seq_len.  The split partials and arrival counters
+ * live in a 1,097,728-byte device array of the library (held by each device
+ * it runs on until the process ends), not in a context: every call on one
+ * device shares it, so calls that overlap on one device (two streams, two
+ * threads) race; the counters are cleared by a fill kernel at the start of
+ * each call.  Limits, checked before any launch (RRR_ERR_UNSUPPORTED beyond
+ * them): seq_len <= 2048, heads_per_kv <= 8, n_kv_heads * heads_per_kv <= 64,
+ * head_dim 128; q, out and the caches 16-byte aligned.  Calls no hipMalloc,
+ * hipFree or allocating library routine. */
+int rrr_attention_noalloc(const float *q, const uint16_t *k_cache, const uint16_t *v_cache, float *out,
+                          uint32_t seq_len, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t head_dim,
+                          void *stream);
 
 /* ---- prefill (forward_prefill_batched, phi4.rs:1200-1445, on the GPU) -- */
 

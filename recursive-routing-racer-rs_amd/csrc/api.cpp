@@ -218,6 +218,8 @@ int rrr_init(int device, rrr_ctx **out)
         if (e == hipSuccess) e = hipMemset(ctx->att_scratch, 0, attention_scratch_bytes());
         if (e == hipSuccess) e = hipMalloc(&ctx->gemm_ws, GEMM_WS_BYTES);
         if (e == hipSuccess) e = hipDeviceSynchronize();
+        void *static_scratch = nullptr;   // rrr_attention_noalloc's array on this device
+        if (e == hipSuccess && attention_static_setup(device, &static_scratch) != RRR_OK) e = hipErrorInvalidSymbol;
         if (e != hipSuccess) {
             if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
             if (ctx->att_scratch) (void)hipFree(ctx->att_scratch);

@@ -87,8 +87,6 @@ hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uin
 // agent-scope counter) merges the splits and writes the output, then resets
 // the counter for the next call.  Every merge runs in a fixed order, so the
 // result depends on seq_len only.
-constexpr uint32_t ATT_PART = ATT_HD + 4;   // floats of one split's partial: output, max, sum (16-byte rows)
-constexpr uint32_t ATT_COUNTER_STRIDE = 64;  // u32 words between two KV heads' counters
 
 __device__ __forceinline__ float safe_scale(float m, float M) { return m == -__builtin_inff() ? 0.0f : exp2f(m - M); }
 
@@ -287,10 +285,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
     if (t == 0) __hip_atomic_store(counters + g * ATT_COUNTER_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// counters (one u32 per KV head, each on its own 256-byte line) then the
-// split partials
-constexpr uint64_t ATT_COUNTER_BYTES = (uint64_t)ATT_HEADS_MAX * ATT_COUNTER_STRIDE * 4;
-uint64_t attention_scratch_bytes() { return ATT_COUNTER_BYTES + (uint64_t)ATT_HEADS_MAX * ATT_SPLITS_MAX * ATT_PART * 4; }
+uint64_t attention_scratch_bytes() { return ATT_SCRATCH_BYTES; }
 
 // Rows per split: enough splits for about two workgroups per CU, at least 16
 // rows (one per lane group) and at most 16 * ATT_ROWS_PER_GROUP rows each,

@@ -87,7 +87,19 @@ hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uin
 // every call; calls on one scratch area must not overlap).
 constexpr uint32_t ATT_HD = 128, ATT_HEADS_MAX = 64, ATT_SPLITS_MAX = 32, ATT_ROWS_PER_GROUP = 4;
 constexpr uint32_t ATT_SEQ_MAX = ATT_SPLITS_MAX * 16 * ATT_ROWS_PER_GROUP;   // 2048 cache rows (MAX_SEQ)
+// scratch layout: one u32 arrival counter per KV head, each on its own
+// 256-byte line, then the split partials (per split and query head: the
+// unnormalised output, max and sum, ATT_PART floats)
+constexpr uint32_t ATT_PART = ATT_HD + 4;
+constexpr uint32_t ATT_COUNTER_STRIDE = 64;   // u32 words between two KV heads' counters
+constexpr uint64_t ATT_COUNTER_BYTES = (uint64_t)ATT_HEADS_MAX * ATT_COUNTER_STRIDE * 4;
+constexpr uint64_t ATT_SCRATCH_BYTES = ATT_COUNTER_BYTES + (uint64_t)ATT_HEADS_MAX * ATT_SPLITS_MAX * ATT_PART * 4;
 uint64_t attention_scratch_bytes();
+// The device address of the library's own attention scratch array on device
+// `dev` (current), looked up once per device (attn_static.hip).
+int attention_static_setup(int dev, void **out);
+// Records the thread's error message (RRR_OK clears it); returns code (api.cpp).
+int set_error(int code, const char *msg);
 void attention_plan(uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t cus, uint32_t &splits,
                     uint32_t &per);
 hipError_t launch_attention(const float *q, const uint16_t *kc, const uint16_t *vc, float *out, void *scratch,

@@ -260,6 +260,22 @@ def test_rope_kv_store_and_attention_validation(vctx):
     assert code_of(at, q, kc, vc, out, 4, 16, 4, hd) in (ERR_UNSUPPORTED, ERR_SHORT_BUFFER)
 
 
+def test_attention_noalloc_validation():
+    # argument checks run before any HIP call (the pointers are never touched)
+    lib = _lib.hip()
+    p = 0x10000
+    na = lib.rrr_attention_noalloc
+    assert na(None, p, p, p, 16, 8, 3, 128, None) == ERR_NULL
+    assert na(p, p, p, None, 16, 8, 3, 128, None) == ERR_NULL
+    assert na(p, p, p, p, 16, 8, 3, 64, None) == ERR_UNSUPPORTED                # head_dim
+    assert na(p, p, p, p, 0, 8, 3, 128, None) == ERR_BAD_SHAPE
+    assert na(p, p, p, p, 2049, 8, 3, 128, None) == ERR_UNSUPPORTED             # the scratch array's rows
+    assert b"2048" in lib.rrr_last_error()
+    assert na(p, p, p, p, 16, 16, 8, 128, None) == ERR_UNSUPPORTED              # 128 query heads
+    assert na(p, p, p, p, 16, 2, 9, 128, None) == ERR_UNSUPPORTED               # 9 per KV head
+    assert na(p + 4, p, p, p, 16, 8, 3, 128, None) == ERR_INVALID_ARG           # alignment
+
+
 def test_prefill_validation(vctx):
     nh, nkv, hd, rd = 24, 8, 128, 96
     qd, kvs = nh * hd, nkv * hd
