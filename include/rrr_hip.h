@@ -376,14 +376,21 @@ typedef struct rrr_sweep_op {
  * workgroup per CU): the MI355X counterpart of replaying the layer dispatches
  * through dispatch_batch_persistent_v2 with a barrier between dependent
  * dispatches (engine.rs:317-370, phi4.rs:1163-1168).  Each op starts once
- * every row of the previous op is written; its weights start streaming
- * before that.  Results are bit-identical to issuing the ops one by one.
- * Supported: the decode layer's forms -- RMSNorm + Q5_K or Q4_K with
- * K <= 4096, GQA-V + Q4_K with K <= 4096, SiLU-gate + Q6_K or Q4_K with
- * 4096 < K <= 8192; RRR_ERR_UNSUPPORTED otherwise.  The buffers are referenced, not copied: they must outlive the
- * sweep and stay at their size. */
+ * every row of the previous op is written; its weights stream into LDS while
+ * the previous op runs.  Results meet the same 1e-4 bar as the ops issued one
+ * by one (not the same bits: the down GEMVs split K three ways per wave and
+ * an RMSNorm takes its sum of squares from the previous op's workgroups in
+ * workgroup order) and are the same bits on every run.  Supported: the decode
+ * layer's sequence -- RMSNorm + Q5_K (QKV), GQA-V + Q4_K (O-proj),
+ * RMSNorm + Q4_K (gate/up), SiLU-gate + Q6_K or Q4_K (down), K <= 3072 for
+ * the first three and 3072 < K <= 9216 for the down GEMV -- where an RMSNorm
+ * op past the first follows the residual op that writes its input;
+ * RRR_ERR_UNSUPPORTED otherwise.  The buffers are referenced, not copied:
+ * they must outlive the sweep and stay at their size. */
 int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_sweep **out);
-/* Runs the sweep on the context stream (not inside rrr_graph_begin/end). */
+/* Runs the sweep on the context stream; may be recorded between
+ * rrr_graph_begin and rrr_graph_end and replayed (its epochs live in device
+ * memory).  Runs of one sweep must not overlap. */
 int rrr_sweep_run(rrr_ctx *ctx, rrr_sweep *sw);
 /* Waits for the stream; RRR_ERR_HIP if a run gave up waiting for an op (a
  * bounded wait of about 2 s expired: its outputs are invalid), else RRR_OK.

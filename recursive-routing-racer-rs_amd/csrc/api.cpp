@@ -67,12 +67,10 @@ struct rrr_buf {
 
 struct rrr_sweep {
     uint32_t magic;
-    void *ops;          // device SweepOpDev[nops]
-    uint32_t *flags;    // device: progress flags, error word, go words
-    uint32_t *err;      // device, inside the flag area
+    void *ops;          // device SwOpDev[nops]
+    uint32_t *state;    // device: completion records, run counters, error word
+    uint32_t *err;      // device, inside the state
     uint32_t nops, grid;
-    size_t lds;
-    uint64_t runs;
 };
 
 struct rrr_graph {
@@ -258,7 +256,7 @@ int rrr_destroy(rrr_ctx *ctx)
         }
         for (rrr_sweep *sw : ctx->sweeps) {
             (void)hipFree(sw->ops);
-            (void)hipFree(sw->flags);
+            (void)hipFree(sw->state);
             sw->magic = 0;
             delete sw;
         }
@@ -1134,10 +1132,10 @@ int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_swee
     if (n == 0) return fail(RRR_ERR_INVALID_ARG, "%s: no ops", what);
     if (ctx->capturing) return fail(RRR_ERR_INVALID_ARG, "%s: not inside rrr_graph_begin/end", what);
     TRY(device_ready(ctx));
-    const uint32_t cus = sweep_cus();
+    const uint32_t grid = sweep_grid(0);
+    if (grid == 0) return fail(RRR_ERR_UNSUPPORTED, "%s: the sweep's workgroup does not fit a CU", what);
     std::vector<GemvArgs> args(n);
     std::vector<uint32_t> acts(n), variants(n), ntiles(n), trs(n);
-    size_t lds = 0;
     for (uint32_t i = 0; i < n; i++) {
         const rrr_sweep_op &o = ops[i];
         GemvArgs &a = args[i];
@@ -1157,32 +1155,38 @@ int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_swee
             return fail(RRR_ERR_INVALID_ARG, "%s: op %u: kind %u", what, i, o.kind);
         }
         size_t l;
-        if (!sweep_plan_op(a, acts[i], cus, variants[i], ntiles[i], trs[i], l))
+        if (!sweep_plan_op(a, acts[i], grid, variants[i], ntiles[i], trs[i], l))
             return fail(RRR_ERR_UNSUPPORTED, "%s: op %u (type %u, K=%u, N=%u) is not a sweep shape", what, i, o.type,
                         o.K, o.N);
-        lds = std::max(lds, l);
+        // an RMSNorm op past the first takes its input's sum of squares from
+        // the previous op's completion records: that op must write its input
+        if (i > 0 && acts[i] == ACT_RMSNORM &&
+            (ops[i - 1].kind != RRR_SWEEP_GEMV_RESIDUAL || ops[i - 1].y != o.x || ops[i - 1].N != o.K))
+            return fail(RRR_ERR_UNSUPPORTED, "%s: op %u: an RMSNorm op must follow the residual op that writes its input",
+                        what, i);
+        if (i > 0 && !sweep_pair_ok(variants[i - 1], ntiles[i - 1], trs[i - 1], variants[i], ntiles[i], trs[i], grid))
+            return fail(RRR_ERR_UNSUPPORTED, "%s: op %u cannot follow op %u in one sweep (not a decode-layer sequence)",
+                        what, i, i - 1);
     }
-    const uint32_t grid = sweep_grid(lds);
-    if (grid == 0) return fail(RRR_ERR_UNSUPPORTED, "%s: a 1024-thread workgroup with %zu B of LDS does not fit", what, lds);
     std::vector<uint8_t> packed((size_t)n * sweep_op_bytes());
-    for (uint32_t i = 0; i < n; i++) sweep_pack_op(packed.data() + (size_t)i * sweep_op_bytes(), args[i], variants[i], ntiles[i], trs[i]);
+    for (uint32_t i = 0; i < n; i++)
+        sweep_pack_op(packed.data() + (size_t)i * sweep_op_bytes(), args[i], variants[i], ntiles[i], trs[i], grid);
     rrr_sweep *sw = new rrr_sweep{};
     sw->magic = SWEEP_MAGIC;
     sw->nops = n;
     sw->grid = grid;
-    sw->lds = lds;
     hipError_t e = hipMalloc(&sw->ops, packed.size());
-    const size_t fbytes = 4 * sweep_flag_words(grid);
-    if (e == hipSuccess) e = hipMalloc((void **)&sw->flags, fbytes);
+    const size_t sbytes = 4 * sweep_state_words();
+    if (e == hipSuccess) e = hipMalloc((void **)&sw->state, sbytes);
     if (e == hipSuccess) {
-        sw->err = sw->flags + sweep_err_word(grid);
+        sw->err = sw->state + sweep_err_word();
         e = hipMemcpyAsync(sw->ops, packed.data(), packed.size(), hipMemcpyHostToDevice, ctx->stream);
     }
-    if (e == hipSuccess) e = hipMemsetAsync(sw->flags, 0, fbytes, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(sw->state, 0, sbytes, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         (void)hipFree(sw->ops);
-        (void)hipFree(sw->flags);
+        (void)hipFree(sw->state);
         delete sw;
         return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
     }
@@ -1196,19 +1200,10 @@ int rrr_sweep_run(rrr_ctx *ctx, rrr_sweep *sw)
     TRY(check_ctx(ctx));
     const char *what = "rrr_sweep_run";
     TRY(check_sweep(ctx, sw, what));
-    if (ctx->capturing) return fail(RRR_ERR_UNSUPPORTED, "%s: a sweep cannot be recorded into a graph", what);
     TRY(device_ready(ctx));
-    // flags only grow: run r waits for values above everything run r-1 wrote
-    uint64_t epoch = sw->runs * (sw->nops + 1ull);
-    if (epoch + sw->nops >= (1ull << 30)) {
-        hipError_t e = hipMemsetAsync(sw->flags, 0, 4 * sweep_flag_words(sw->grid), ctx->stream);
-        if (e != hipSuccess) return finish(ctx, e, what);
-        sw->runs = 0;
-        epoch = 0;
-    }
-    sw->runs++;
-    return finish(ctx, launch_sweep(sw->ops, sw->nops, sw->flags, (uint32_t)epoch, sw->grid, sw->lds, ctx->stream),
-                  what);
+    // the epochs come from run counters in device memory: the launch may be
+    // recorded into a graph and replayed
+    return finish(ctx, launch_sweep(sw->ops, sw->nops, sw->state, sw->grid, ctx->stream), what);
 }
 
 int rrr_sweep_check(rrr_ctx *ctx, rrr_sweep *sw)
@@ -1222,9 +1217,8 @@ int rrr_sweep_check(rrr_ctx *ctx, rrr_sweep *sw)
     if (e == hipSuccess) e = hipMemcpy(&err, sw->err, 4, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
     if (err) {
-        // start over: flags and the error word back to zero
-        e = hipMemset(sw->flags, 0, 4 * sweep_flag_words(sw->grid));
-        sw->runs = 0;
+        // start over: records, run counters and the error word back to zero
+        e = hipMemset(sw->state, 0, 4 * sweep_state_words());
         if (e != hipSuccess) return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
         return fail(RRR_ERR_HIP, "%s: a sweep run gave up waiting for an op; its outputs are invalid", what);
     }
@@ -1238,7 +1232,7 @@ int rrr_sweep_destroy(rrr_ctx *ctx, rrr_sweep *sw)
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipFree(sw->ops);
-    (void)hipFree(sw->flags);
+    (void)hipFree(sw->state);
     ctx->sweeps.erase(sw);
     sw->magic = 0;
     delete sw;

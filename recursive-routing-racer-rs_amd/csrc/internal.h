@@ -47,16 +47,18 @@ hipError_t launch_skinny(const GemvArgs &a, hipStream_t s);
 // Persistent decode sweep (sweep.hip): per-op plan, packing and the launch
 bool sweep_plan_op(const GemvArgs &a, uint32_t act, uint32_t grid, uint32_t &variant, uint32_t &ntiles, uint32_t &tr,
                    size_t &lds);
+// whether op `next` may follow op `cur` in one sweep (forms and LDS)
+bool sweep_pair_ok(uint32_t cur, uint32_t cur_ntiles, uint32_t cur_tr, uint32_t next, uint32_t next_ntiles,
+                   uint32_t next_tr, uint32_t grid);
 size_t sweep_op_bytes();
-void sweep_pack_op(void *dst, const GemvArgs &a, uint32_t variant, uint32_t ntiles, uint32_t tr);
+void sweep_pack_op(void *dst, const GemvArgs &a, uint32_t variant, uint32_t ntiles, uint32_t tr, uint32_t grid);
 uint32_t sweep_cus();
 uint32_t sweep_grid(size_t lds);
-// words of the flag area (progress flags, error word, go words), and the
-// index of the error word in it
-size_t sweep_flag_words(uint32_t grid);
-size_t sweep_err_word(uint32_t grid);
-hipError_t launch_sweep(const void *ops, uint32_t nops, uint32_t *flags, uint32_t epoch, uint32_t grid, size_t lds,
-                        hipStream_t s);
+// u32 words of a sweep's device state (completion records, run counters,
+// error word) and the index of the error word in it
+size_t sweep_state_words();
+size_t sweep_err_word();
+hipError_t launch_sweep(const void *ops, uint32_t nops, uint32_t *state, uint32_t grid, hipStream_t s);
 hipError_t launch_dequant(uint32_t type, const uint8_t *W, uint64_t w_bytes, float *out,
                           uint64_t n_elements, hipStream_t s);
 hipError_t launch_rmsnorm(const float *x, const float *g, float *y, uint32_t rows, uint32_t d,
