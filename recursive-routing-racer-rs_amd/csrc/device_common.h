@@ -72,16 +72,16 @@ __device__ __forceinline__ uint32_t byte_of(uint32_t w, uint32_t i) { return (w 
 __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2,
                                              uint32_t &sc, uint32_t &mn)
 {
-    // q[i] for i in 0..11 is byte (i & 3) of dword s[i >> 2]
-    if (j < 4) {
-        sc = byte_of(s0, j) & 63u;
-        mn = byte_of(s1, j) & 63u;
-    } else {
-        uint32_t i = j - 4;
-        uint32_t q8 = byte_of(s2, i), q0 = byte_of(s0, i), q4 = byte_of(s1, i);
-        sc = (q8 & 0x0Fu) | ((q0 >> 6) << 4);
-        mn = (q8 >> 4) | ((q4 >> 6) << 4);
-    }
+    // q[i] for i in 0..11 is byte (i & 3) of dword s[i >> 2].  Both cases are
+    // computed and one is selected (j often differs across the lanes of a
+    // wave, and a branch would run both sides anyway):
+    //   j < 4:  sc = q[j] & 63,                      mn = q[j+4] & 63
+    //   j >= 4: sc = (q[j+4] & 15) | (q[j-4] >> 6) << 4, mn = (q[j+4] >> 4) | (q[j] >> 6) << 4
+    const uint32_t i = j & 3u;
+    const uint32_t q0 = byte_of(s0, i), q4 = byte_of(s1, i), q8 = byte_of(s2, i);
+    const bool hi = j >= 4;
+    sc = hi ? (q8 & 0x0Fu) | ((q0 >> 2) & 0x30u) : q0 & 63u;
+    mn = hi ? (q8 >> 4) | ((q4 >> 2) & 0x30u) : q4 & 63u;
 }
 
 // Deterministic full-wave sum: fixed butterfly order, identical on every call.

@@ -8,8 +8,7 @@ namespace rrr {
 template <class Q, int BPW, int ACT, bool MULTI, int TR>
 __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntiles, uint32_t tr)
 {
-    SweepWait none{nullptr, nullptr, 0u, nullptr, nullptr};
-    (void)mq_body<Q, BPW, ACT, MULTI, false, TR>(a, ntiles, tr, none);
+    mq_body<Q, BPW, ACT, MULTI, TR>(a, ntiles, tr);
 }
 
 // Super-blocks per wave and waves per workgroup (at least 4, the canonical

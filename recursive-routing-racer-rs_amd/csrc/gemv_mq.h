@@ -1,7 +1,7 @@
 // gemv_mq.h -- batch-1 K-quant GEMV on the int8 matrix cores: quant unit
-// decoders, activation encoding and the per-workgroup body shared by the
-// standalone launch (gemv_mfma.hip) and the persistent decode sweep
-// (sweep.hip).
+// decoders and activation encoding (shared with the persistent decode sweep,
+// sweep.hip) and the per-workgroup body of the standalone launch
+// (gemv_mfma.hip).
 //
 // y[n] = sum_k x[k] * W[n][k] for Q4_K / Q5_K / Q6_K rows (phi4.rs:628-630),
 // with the multiply-accumulate on v_mfma_i32_16x16x64_i8 instead of VALU FMAs.
@@ -212,9 +212,11 @@ __device__ __forceinline__ uint32_t quad_sum_u32(uint32_t v)
 // Wave-private LDS layout of one wave (BPW super-blocks of 16 rows):
 //   weights: 16 rows x RS bytes, block j of row r at r*RS + j*LB (16-byte
 //            aligned pieces of UPB units; Q6_K pieces carry 14 bytes of the
-//            next block in their last unit).  Load slot s covers rows
-//            s*RPS .. s*RPS + RPS-1, lane l unit l % UPR of row l / UPR, so a
-//            lane's offsets are fixed and only a uniform per-slot offset moves.
+//            next block in their last unit).  The loads are block by block:
+//            load slot s of block j covers rows s*RPS .. s*RPS + RPS-1 of
+//            that block (lane l: unit l % UPB of row l / UPB), so a lane's
+//            offsets are fixed and only a uniform per-slot offset moves, and
+//            a block's MFMAs can start while the next block is still landing.
 //   digits:  3 planes x DG bytes (plane p, local element e at p*DG + e)
 //   aux:     per 16-element group 16 bytes = MFMA accumulator input
 //            {-32 * sum Q (Q6_K only, else 0), 0, 0, bits of 2^(E-14)}
@@ -224,9 +226,7 @@ struct MwGeom {
     static constexpr uint32_t UPB = (Q::BS + 15) / 16;            // 16-byte units per block piece
     static constexpr uint32_t LB = 16 * UPB;
     static constexpr uint32_t RS = (BPW * LB) % 32 == 0 ? BPW * LB + 16 : BPW * LB;  // odd multiple of 16
-    static constexpr uint32_t UPR = BPW * UPB;                     // units per row
-    static constexpr uint32_t RPS = 64 / UPR;                      // rows per load slot
-    static constexpr int S = (16 + RPS - 1) / RPS;                 // load slots of a 16-row tile
+    static constexpr uint32_t RPS = 64 / UPB;                      // rows per load slot
     static constexpr uint32_t DG = BPW * 256;
     static constexpr uint32_t NGW = BPW * 16;
     static constexpr uint32_t D_OFF = 16 * RS;
@@ -286,130 +286,28 @@ __device__ __forceinline__ void wave_lds_sync()
 // w_bytes + RRR_READ_SLACK < MQ_OOB): such loads return zeros and move no data.
 constexpr uint32_t MQ_OOB = 0x80000000u;
 
-
-// ---------------------------------------------------------------------------
-// Sweep form (SW): the body runs once per op inside the persistent decode
-// sweep.  Its activations and outputs are written by other workgroups of the
-// same launch, on other XCDs whose L2s are not coherent with this one: they
-// are read and written with agent-scope (sc1) buffer operations, which go
-// through to the coherent level.  The weights of the workgroup's first tile
-// are requested before the wait for the previous op, so HBM keeps streaming
-// through the hand-off.
-
-// Wait of one op for the previous one: every workgroup's progress flag has
-// reached `target` (flags only grow; 0 = no wait).  Workgroup 0 gathers the
-// flags (one wave, 16 bytes a lane) and publishes `target` in SWEEP_GO_COPIES
-// go words, 128 bytes apart; every other workgroup polls one go word with a
-// single lane, so the coherent level sees a few hundred loads per round
-// instead of one per workgroup and flag.  The spins are bounded (about 2 s of
-// the 100 MHz real-time clock): on expiry the error word is set and the
-// workgroup abandons the sweep instead of hanging.
-constexpr uint32_t SWEEP_GO_COPIES = 8, SWEEP_GO_STRIDE = 32;   // u32 words
-struct SweepWait {
-    const uint32_t *flags;   // one per workgroup, 16-byte padded to a multiple of 4
-    uint32_t *go;            // SWEEP_GO_COPIES x SWEEP_GO_STRIDE words
-    uint32_t target;
-    uint32_t *err;
-    uint32_t *bail;          // LDS word shared by the workgroup
-};
-
-__device__ __forceinline__ uint32_t coh_load_u32(const uint32_t *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ bool sweep_reached(uint32_t v, uint32_t target) { return (int)(v - target) >= 0; }
-
-// every thread of the workgroup calls it; the result is uniform
-__device__ __forceinline__ bool sweep_wait(SweepWait &sw)
-{
-    if (sw.target == 0) return true;
-    const uint32_t t = threadIdx.x;
-    if (t == 0) *sw.bail = 0u;
-    if (t < 64) {
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        bool expired = false;
-        if (blockIdx.x == 0) {
-            // gather: lane l covers flags 4l .. 4l+3 (padding flags read as done)
-            const uint32_t G = gridDim.x;
-            for (;;) {
-                bool ok = true;
-                if (4 * t < G) {
-                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(sw.flags, 16ull * ((G + 3) / 4)),
-                                                                          16 * t, 0, RRR_CPOL_SC1);
-                    ok = sweep_reached(v.x, sw.target) && (4 * t + 1 >= G || sweep_reached(v.y, sw.target)) &&
-                         (4 * t + 2 >= G || sweep_reached(v.z, sw.target)) &&
-                         (4 * t + 3 >= G || sweep_reached(v.w, sw.target));
-                }
-                if (__all(ok)) break;
-                if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) { expired = true; break; }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            if (!expired && t < SWEEP_GO_COPIES)
-                __hip_atomic_store(sw.go + t * SWEEP_GO_STRIDE, sw.target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else if (t == 0) {
-            const uint32_t *g = sw.go + (blockIdx.x % SWEEP_GO_COPIES) * SWEEP_GO_STRIDE;
-            while (!sweep_reached(coh_load_u32(g), sw.target)) {
-                if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) { expired = true; break; }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-        if (expired) {
-            *sw.bail = 1u;
-            __hip_atomic_store(sw.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    __syncthreads();
-    return *sw.bail == 0u;
-}
-
-// Activation inputs of 4 consecutive elements at k (k % 4 == 0), as
-// src_load4 (act.h); SW reads them through the coherent level.
-template <int ACT, bool SW>
-__device__ __forceinline__ void mq_src_load4(const GemvArgs &a, __amdgpu_buffer_rsrc_t rx, uint32_t k, float4 &xa,
-                                             float4 &xb)
-{
-    if constexpr (!SW) {
-        src_load4<ACT>(a, k, xa, xb);
-    } else {
-        uint32_t i = k;
-        if constexpr (ACT == ACT_GQA_V) {
-            const uint32_t hd = a.head_dim, hpk = a.heads_per_kv;
-            i = a.K + a.K / hpk + (k / (hd * hpk)) * hd + k % hd;
-        }
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, 4 * i, 0, RRR_CPOL_SC1);
-        xa = make_float4(u2f(v.x), u2f(v.y), u2f(v.z), u2f(v.w));
-        if constexpr (ACT == ACT_RMSNORM) xb = *(const float4 *)(a.gamma + k);   // weights: read-only
-        if constexpr (ACT == ACT_SILU) {
-            const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rx, 4 * (a.K + k), 0, RRR_CPOL_SC1);
-            xb = make_float4(u2f(u.x), u2f(u.y), u2f(u.z), u2f(u.w));
-        }
-    }
-}
-
 // A tile is tr <= 16 rows (the MFMA's 16 columns, the rest idle), chosen by
 // the launcher so that the tiles spread evenly over the CUs (K <= 4096,
 // N = 3072: 256 tiles of 12 rows rather than 192 of 16).
 // Persistent form (MULTI): workgroup b takes the tiles b, b + G, ...
 // (G = gridDim.x) with the same wave <-> K-slice split for every tile, so the
 // activation slice is encoded once per workgroup and, with one super-block per
-// wave, the MFMA A operands and accumulator inputs stay in registers.  The
-// loads of tile i+1 are issued as soon as tile i is staged in LDS, before it
-// is multiplied.  The
-// single-tile form (one tile per workgroup) issues no prefetch: even loads
-// past the buffer end cost texture-addresser time.  Row sums are added over
-// the waves in wave order, so results depend on neither form, G nor the
-// number of waves.  Returns false when a sweep wait was abandoned.
+// wave, the MFMA A operands and accumulator inputs stay in registers.  A
+// block's registers take the next tile's loads of that block as soon as the
+// block is staged in LDS, before it is multiplied.  The single-tile form (one
+// tile per workgroup) issues no prefetch: even loads past the buffer end cost
+// texture-addresser time.  Row sums are added over the waves in wave order,
+// so results depend on neither form, G nor the number of waves.
 // TR: the most rows a tile of the launch has (tr <= TR <= 16); a wave issues
 // the load slots that cover TR rows, so a launch of shorter tiles issues no
 // empty slots.
-template <class Q, int BPW, int ACT, bool MULTI, bool SW, int TR = 16>
-__device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr, SweepWait &sw)
+template <class Q, int BPW, int ACT, bool MULTI, int TR = 16>
+__device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr)
 {
     extern __shared__ float smem[];
     using G = MwGeom<Q, BPW>;
     static_assert(TR >= 1 && TR <= 16, "tile rows");
-    constexpr int S = (TR + (int)G::RPS - 1) / (int)G::RPS;     // load slots
+    constexpr int SB = (TR + (int)G::RPS - 1) / (int)G::RPS;     // load slots of one block
     constexpr bool AREG = BPW == 1;
     const uint32_t K = a.K, B = K / 256;
     const uint32_t W = blockDim.x >> 6, NT = blockDim.x;
@@ -425,69 +323,56 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint
     // every buffer has RRR_READ_SLACK readable bytes past its end: a Q6_K
     // piece's last unit runs 14 bytes past its block
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.W, a.w_bytes + RRR_READ_SLACK);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, 0xFFFFFFFFull);
     const uint32_t b0 = wave * BPW;                              // first super-block of this wave
     const uint32_t nb = b0 < B ? min((uint32_t)BPW, B - b0) : 0u;
 
-    // weight units of this wave's slice of a tile (layout above); lanes past
-    // RPS rows and blocks past nb reload a valid unit and are not stored, and
-    // rows past the tile's tr rows read nothing
-    const uint32_t rsel = min(lane / G::UPR, G::RPS - 1), wl = lane - (lane / G::UPR) * G::UPR;
-    const uint32_t jl = wl / G::UPB, vl = wl - jl * G::UPB;
-    const bool lane_ok = lane < G::RPS * G::UPR && jl < nb;
-    const uint32_t blk = b0 + min(jl, nb ? nb - 1 : 0u);
+    // weight units of this wave's blocks (layout above); lanes past RPS rows,
+    // rows past the tile's tr rows and blocks past nb read nothing (an
+    // out-of-range offset: no memory request)
+    const uint32_t rsel = min(lane / G::UPB, G::RPS - 1), ul = lane - (lane / G::UPB) * G::UPB;
+    const bool lane_ok = lane < G::RPS * G::UPB;
     constexpr bool REALIGN = Q::BS % 4 != 0;
-    const uint32_t sh = REALIGN ? (blk * Q::BS) & 3u : 0u;     // 0 or 2 bytes
-    const uint32_t voff = rsel * row_bytes + blk * Q::BS - sh + 16 * vl;
-    const uint32_t loff = rsel * G::RS + jl * G::LB + 16 * vl;
-    u32x4 wa[S];
-    auto issue = [&](u32x4 *w, uint32_t tl) {
+    uint32_t voff[BPW], sh[BPW];
+#pragma unroll
+    for (int j = 0; j < BPW; j++) {
+        const uint32_t blk = b0 + min((uint32_t)j, nb ? nb - 1 : 0u);
+        sh[j] = REALIGN ? (blk * Q::BS) & 3u : 0u;             // 0 or 2 bytes (the same for every row)
+        voff[j] = rsel * row_bytes + blk * Q::BS - sh[j] + 16 * ul;
+    }
+    const uint32_t loff = rsel * G::RS + 16 * ul;
+    u32x4 wa[BPW][SB];
+    auto issue = [&](int j, uint32_t tl) {
         const uint32_t tb = tl < ntl ? (tile0 + tl * GR) * tile_bytes : MQ_OOB;
 #pragma unroll
-        for (int s = 0; s < S; s++)
-            w[s] = bload16_nt_so(rs, s * G::RPS + rsel < tr ? voff : MQ_OOB, tb + s * G::RPS * row_bytes);
+        for (int s = 0; s < SB; s++)
+            wa[j][s] = bload16_nt_so(rs, lane_ok && j < (int)nb && s * G::RPS + rsel < tr ? voff[j] : MQ_OOB,
+                                     tb + s * G::RPS * row_bytes);
     };
 
     // The loads below are unconditional (clamped indices, out-of-range scalar
     // offsets): loads under a branch make the compiler wait for every
     // outstanding load at the join.
-    // 0. in the sweep: this op's first tile, then the wait for the previous op
-    if constexpr (SW) {
-        issue(wa, 0);
-        if (!sweep_wait(sw)) return false;
-    }
     // the residual of this thread's first output row, read now rather than
     // on the kernel's tail (a clamped row when there is none)
-    const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, 4ull * a.N);
     const uint32_t row_first = min((tile0 + (t >> 4) * GR) * tr + (t & 15), a.N - 1);
-    const float yres = SW ? u2f(__builtin_amdgcn_raw_buffer_load_b32(ry, 4 * row_first, 0, RRR_CPOL_SC1))
-                          : a.y[row_first];
+    const float yres = a.y[row_first];
     // 1. fused RMSNorm: the whole of x in the canonical order (K <= 1024 NSQ)
     constexpr int NSQ = ACT == ACT_RMSNORM ? 4 * BPW : 1;
     float4 cx[NSQ];
     if constexpr (ACT == ACT_RMSNORM) {
 #pragma unroll
-        for (int j = 0; j < NSQ; j++) {
-            const uint32_t f = min(t + 256 * j, K / 4 - 1);
-            if constexpr (SW) {
-                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, 16 * f, 0, RRR_CPOL_SC1);
-                cx[j] = make_float4(u2f(v.x), u2f(v.y), u2f(v.z), u2f(v.w));
-            } else {
-                cx[j] = ((const float4 *)a.x)[f];
-            }
-        }
+        for (int j = 0; j < NSQ; j++) cx[j] = ((const float4 *)a.x)[min(t + 256 * j, K / 4 - 1)];
     }
     // 2. this wave's activation inputs: float4 lane + 64 j of its slice
     float4 xa[BPW], xb[BPW];
 #pragma unroll
-    for (int j = 0; j < BPW; j++) mq_src_load4<ACT, SW>(a, rx, min(b0 * 256 + 4 * (lane + 64 * j), K - 4), xa[j], xb[j]);
+    for (int j = 0; j < BPW; j++) src_load4<ACT>(a, min(b0 * 256 + 4 * (lane + 64 * j), K - 4), xa[j], xb[j]);
 
-    if constexpr (!SW) {
-        // every wave's activation loads enter the memory pipeline before any
-        // weight load of the workgroup (a bare barrier: no wait on the loads)
-        __builtin_amdgcn_s_barrier();
-        issue(wa, 0);
-    }
+    // every wave's activation loads enter the memory pipeline before any
+    // weight load of the workgroup (a bare barrier: no wait on the loads)
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int j = 0; j < BPW; j++) issue(j, 0);
 
     // 3. activation staging of this wave's slice
     float inv = 1.0f;
@@ -545,21 +430,23 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint
         av[0] = i32x4{0, 0, 0, 0};
     }
 
-    // 4. per tile: this tile's units to LDS (the registers then take the
-    // next tile's loads), MFMAs, row partials to part[]
+    // 4. per tile, block by block: the block's units to LDS (its registers
+    // then take the next tile's loads of the block), its MFMAs; row partials
+    // to part[]
     auto process = [&](uint32_t tl) {
-        wave_lds_sync();
-#pragma unroll
-        for (int s = 0; s < S; s++) {
-            u32x4 v = wa[s];
-            if constexpr (REALIGN) v = q6_realign(v, sh);
-            if (lane_ok && s * G::RPS + rsel < tr) *(u32x4 *)(L + loff + s * G::RPS * G::RS) = v;
-        }
-        if constexpr (MULTI) issue(wa, tl + 1);
-        wave_lds_sync();
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < BPW; j++) {
+            wave_lds_sync();
+#pragma unroll
+            for (int s = 0; s < SB; s++) {
+                u32x4 v = wa[j][s];
+                if constexpr (REALIGN) v = q6_realign(v, sh[j]);
+                if (lane_ok && j < (int)nb && s * G::RPS + rsel < tr)
+                    *(u32x4 *)(L + loff + s * G::RPS * G::RS + j * G::LB) = v;
+            }
+            if constexpr (MULTI) issue(j, tl + 1);
+            wave_lds_sync();
             if (j < (int)nb) {
                 typename Q::Raw raw;
                 Q::load(raw, L, n * G::RS + j * G::LB, g);
@@ -610,19 +497,10 @@ __device__ __forceinline__ bool mq_body(const GemvArgs &a, uint32_t ntiles, uint
         if (r < tr && row < a.N) {
             float v = part[tl * W * 16 + r];
             for (uint32_t w = 1; w < W; w++) v += part[(tl * W + w) * 16 + r];
-            if (a.residual) {
-                const float h = i == t ? yres
-                                : SW ? u2f(__builtin_amdgcn_raw_buffer_load_b32(ry, 4 * row, 0, RRR_CPOL_SC1))
-                                     : a.y[row];
-                v = h + v;
-            }
-            if constexpr (SW)
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, 4 * row, 0, RRR_CPOL_SC1);
-            else
-                a.y[row] = v;
+            if (a.residual) v = (i == t ? yres : a.y[row]) + v;
+            a.y[row] = v;
         }
     }
-    return true;
 }
 
 // Rows per tile and tiles per workgroup for `wgs` workgroups: the fewest
