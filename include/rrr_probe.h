@@ -1,0 +1,38 @@
+/*
+ * rrr_probe.h -- platform probes of librrr_hip.so, used by the benchmark to
+ * report what the device itself reaches next to what the decode-path kernels
+ * reach.  They have no counterpart in the reference (its benchmark reports
+ * only end-to-end timings).  Same conventions as rrr_hip.h: int status,
+ * arguments checked before any HIP call, asynchronous when the context is.
+ */
+#ifndef RRR_PROBE_H
+#define RRR_PROBE_H
+
+#include "rrr_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Streaming read of the first `bytes` (a multiple of 16) of `buf`: every
+ * 16-byte unit is loaded once (non-temporal, 4 workgroups of 1024 threads per
+ * CU); nothing is written except, under a condition no input meets, the
+ * 4-byte `sink`.  bytes / time is the HBM read rate one launch of that size
+ * reaches; a read of twice the Infinity Cache's 256 MB evicts it. */
+int rrr_probe_read(rrr_ctx *ctx, const rrr_buf *buf, uint64_t bytes, rrr_buf *sink);
+
+/* Matrix-core rate: `waves_per_cu` waves on every CU (a multiple of 4, at most
+ * 32) each run `iters` rounds of 4 independent MFMAs of `kind`.  Operations per
+ * launch = CUs * waves_per_cu * iters * 4 * ops_per_mfma, ops_per_mfma
+ * = 2*16*16*32 (16x16x32 f16), 2*32*32*16 (32x32x16 f16), 2*16*16*64
+ * (16x16x64 int8). */
+enum { RRR_PROBE_MFMA_F16_16X16X32 = 0, RRR_PROBE_MFMA_F16_32X32X16 = 1, RRR_PROBE_MFMA_I8_16X16X64 = 2 };
+int rrr_probe_mfma(rrr_ctx *ctx, uint32_t kind, uint32_t waves_per_cu, uint32_t iters, rrr_buf *sink);
+/* CUs of the context's device (the probes' grid unit); 0 without a device. */
+uint32_t rrr_probe_cus(rrr_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RRR_PROBE_H */

@@ -5,6 +5,7 @@
 // paths on a machine without a GPU.
 #include "rrr_hip.h"
 #include "rrr_gguf.h"
+#include "rrr_probe.h"
 
 #include <hip/hip_runtime.h>
 
@@ -1279,6 +1280,41 @@ int rrr_timer_stop(rrr_ctx *ctx, float *ms)
     if (e != hipSuccess) return fail(RRR_ERR_HIP, "rrr_timer_stop: %s", hipGetErrorString(e));
     ctx->timer_started = false;
     return ok();
+}
+
+// ---- platform probes ------------------------------------------------------------
+
+int rrr_probe_read(rrr_ctx *ctx, const rrr_buf *buf, uint64_t bytes, rrr_buf *sink)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_probe_read";
+    TRY(check_buf(ctx, buf, what));
+    TRY(check_buf(ctx, sink, what));
+    if (bytes == 0 || bytes % 16) return fail(RRR_ERR_INVALID_ARG, "%s: bytes must be a positive multiple of 16", what);
+    TRY(need(buf, bytes, what));
+    TRY(need(sink, 4, what));
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_probe_read(buf->ptr, bytes, (uint32_t *)sink->ptr, ctx->stream), what);
+}
+
+int rrr_probe_mfma(rrr_ctx *ctx, uint32_t kind, uint32_t waves_per_cu, uint32_t iters, rrr_buf *sink)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_probe_mfma";
+    TRY(check_buf(ctx, sink, what));
+    if (kind > RRR_PROBE_MFMA_I8_16X16X64) return fail(RRR_ERR_INVALID_ARG, "%s: kind %u", what, kind);
+    if (waves_per_cu == 0 || waves_per_cu % 4 || waves_per_cu > 32)
+        return fail(RRR_ERR_INVALID_ARG, "%s: waves_per_cu must be a multiple of 4 up to 32", what);
+    if (iters == 0) return fail(RRR_ERR_INVALID_ARG, "%s: iters must be positive", what);
+    TRY(need(sink, 4, what));
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_probe_mfma(kind, waves_per_cu, iters, (uint32_t *)sink->ptr, ctx->stream), what);
+}
+
+uint32_t rrr_probe_cus(rrr_ctx *ctx)
+{
+    if (check_ctx(ctx) != RRR_OK || ctx->nodevice || device_ready(ctx) != RRR_OK) return 0;
+    return sweep_cus();
 }
 
 // ---- one-call helper ------------------------------------------------------------

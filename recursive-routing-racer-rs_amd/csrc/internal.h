@@ -131,4 +131,8 @@ hipError_t launch_rmsnorm_f16(const float *x, const float *g, uint16_t *y, uint3
 hipError_t launch_silu_gate_f16(const float *gu, uint16_t *mid, float *rscale, uint32_t rows, uint32_t F,
                                 hipStream_t s);
 
+// Platform probes (probe.hip)
+hipError_t launch_probe_read(const void *p, uint64_t bytes, uint32_t *out, hipStream_t s);
+hipError_t launch_probe_mfma(uint32_t kind, uint32_t waves_per_cu, uint32_t iters, uint32_t *out, hipStream_t s);
+
 }  // namespace rrr

@@ -1,0 +1,115 @@
+// probe.hip -- platform probes for the measurements: a streaming read of a
+// device buffer (the HBM rate one launch of a given size reaches, and the
+// read that flushes the Infinity Cache before a timed region) and loops of
+// independent MFMAs (the matrix cores' dense rate).
+#include "rrr_probe.h"
+
+#include <hip/hip_runtime.h>
+
+#include "device_common.h"
+#include "internal.h"
+
+namespace rrr {
+
+// Every thread reads 16-byte units i, i + T, ... (T threads in the grid),
+// four loads in flight per iteration, non-temporal; the XOR of what it read
+// goes to out[] only if it equals a value no sane input produces, which keeps
+// the loads without a write per thread.
+__global__ __launch_bounds__(1024) void probe_read_kernel(const u32x4 *p, uint64_t n16, uint32_t *out)
+{
+    const uint64_t T = (uint64_t)gridDim.x * blockDim.x;
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + 3 * T < n16; i += 4 * T) {
+        const u32x4 a = __builtin_nontemporal_load(p + i), b = __builtin_nontemporal_load(p + i + T);
+        const u32x4 c = __builtin_nontemporal_load(p + i + 2 * T), d = __builtin_nontemporal_load(p + i + 3 * T);
+        acc ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^ (d.x ^ d.y ^ d.z ^ d.w);
+    }
+    for (; i < n16; i += T) {
+        const u32x4 a = __builtin_nontemporal_load(p + i);
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    if (acc == 0x9E3779B9u) out[0] = acc;
+}
+
+// Each wave runs `iters` rounds of 4 independent MFMAs (no dependence between
+// the 4 accumulators of a round); the accumulators go to out[] only under the
+// same never-taken condition.
+template <int KIND>
+__global__ __launch_bounds__(256) void probe_mfma_kernel(uint32_t iters, uint32_t *out)
+{
+    const uint32_t lane = threadIdx.x & 63;
+    if constexpr (KIND == RRR_PROBE_MFMA_F16_16X16X32) {
+        f16x8 a, b;
+        for (int k = 0; k < 8; k++) {
+            a[k] = (_Float16)(float)((lane + k) & 7);
+            b[k] = (_Float16)(float)((lane * 3 + k) & 7);
+        }
+        f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+        for (uint32_t it = 0; it < iters; it++) {
+            c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c3, 0, 0, 0);
+        }
+        const float s = (c0[0] + c1[1]) + (c2[2] + c3[3]);
+        if (s == -1.0f) out[0] = __float_as_uint(s);
+    } else if constexpr (KIND == RRR_PROBE_MFMA_F16_32X32X16) {
+        f16x8 a, b;
+        for (int k = 0; k < 8; k++) {
+            a[k] = (_Float16)(float)((lane + k) & 7);
+            b[k] = (_Float16)(float)((lane * 3 + k) & 7);
+        }
+        f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        for (uint32_t it = 0; it < iters; it++) {
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c3, 0, 0, 0);
+        }
+        const float s = (c0[0] + c1[1]) + (c2[2] + c3[3]);
+        if (s == -1.0f) out[0] = __float_as_uint(s);
+    } else {
+        i32x4 a, b;
+        for (int k = 0; k < 4; k++) {
+            a[k] = (int)(0x01010101u * ((lane + k) & 7));
+            b[k] = (int)(0x01010101u * ((lane * 3 + k) & 7));
+        }
+        i32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+        for (uint32_t it = 0; it < iters; it++) {
+            c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, a), __builtin_bit_cast(i8x16, b), c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, a), __builtin_bit_cast(i8x16, b), c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, a), __builtin_bit_cast(i8x16, b), c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, a), __builtin_bit_cast(i8x16, b), c3, 0, 0, 0);
+        }
+        const int s = (c0[0] + c1[1]) + (c2[2] + c3[3]);
+        if (s == -1) out[0] = (uint32_t)s;
+    }
+}
+
+hipError_t launch_probe_read(const void *p, uint64_t bytes, uint32_t *out, hipStream_t s)
+{
+    const uint32_t grid = 4 * sweep_cus();
+    hipLaunchKernelGGL(probe_read_kernel, dim3(grid), dim3(1024), 0, s, (const u32x4 *)p, bytes / 16, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_probe_mfma(uint32_t kind, uint32_t waves_per_cu, uint32_t iters, uint32_t *out, hipStream_t s)
+{
+    // 4 waves a workgroup, waves_per_cu / 4 workgroups per CU
+    const uint32_t grid = sweep_cus() * (waves_per_cu / 4);
+    switch (kind) {
+    case RRR_PROBE_MFMA_F16_16X16X32:
+        hipLaunchKernelGGL(probe_mfma_kernel<RRR_PROBE_MFMA_F16_16X16X32>, dim3(grid), dim3(256), 0, s, iters, out);
+        break;
+    case RRR_PROBE_MFMA_F16_32X32X16:
+        hipLaunchKernelGGL(probe_mfma_kernel<RRR_PROBE_MFMA_F16_32X32X16>, dim3(grid), dim3(256), 0, s, iters, out);
+        break;
+    default:
+        hipLaunchKernelGGL(probe_mfma_kernel<RRR_PROBE_MFMA_I8_16X16X64>, dim3(grid), dim3(256), 0, s, iters, out);
+        break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace rrr

@@ -109,6 +109,9 @@ SIGNATURES = {
                                 f32, f32]),
     "rrr_attention": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, c_buf_p, u32, u32, u32, u32]),
     "rrr_attention_noalloc": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
+    "rrr_probe_read": (i32, [c_ctx_p, c_buf_p, u64, c_buf_p]),
+    "rrr_probe_mfma": (i32, [c_ctx_p, u32, u32, u32, c_buf_p]),
+    "rrr_probe_cus": (u32, [c_ctx_p]),
     "rrr_rope_kv_store_rows": (i32, [c_ctx_p, c_buf_p, u32, c_buf_p, u32, c_buf_p, c_buf_p, u32, u32, u32, u32, u32,
                                      u32, u32, f32, f32]),
     "rrr_attention_prefill": (i32, [c_ctx_p, c_buf_p, u32, c_buf_p, c_buf_p, c_buf_p, u32, u32, u32, u32, u32]),

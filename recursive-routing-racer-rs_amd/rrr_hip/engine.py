@@ -34,6 +34,7 @@ ERR_IO = -13
 F32, F16, Q4_K, Q5_K, Q6_K = 0, 1, 12, 13, 14
 LOGITS_ROWS, LOGITS_CHUNKED, LOGITS_Q6K = 0, 1, 2
 ACT_IDENTITY, ACT_SILU_GATE, ACT_GQA_V = 0, 1, 2
+PROBE_MFMA_F16_16X16X32, PROBE_MFMA_F16_32X32X16, PROBE_MFMA_I8_16X16X64 = 0, 1, 2
 SWEEP_GEMV_RMSNORM, SWEEP_GEMV_RESIDUAL = 0, 1
 DEVICE_NONE = -1
 BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, F32: 1024}
@@ -300,6 +301,16 @@ class Context:
 
     def set_async(self, flag):
         _check(self.lib.rrr_set_async(self._h, 1 if flag else 0))
+
+    # ---- platform probes (include/rrr_probe.h) ---------------------------
+    def probe_read(self, buf, nbytes, sink):
+        _check(self.lib.rrr_probe_read(self._h, buf._h, nbytes, sink._h))
+
+    def probe_mfma(self, kind, waves_per_cu, iters, sink):
+        _check(self.lib.rrr_probe_mfma(self._h, kind, waves_per_cu, iters, sink._h))
+
+    def probe_cus(self):
+        return int(self.lib.rrr_probe_cus(self._h))
 
     def sync(self):
         _check(self.lib.rrr_sync(self._h))
