@@ -34,7 +34,10 @@ __global__ __launch_bounds__(1024) void probe_read_kernel(const u32x4 *p, uint64
 
 // Each wave runs `iters` rounds of 4 independent MFMAs (no dependence between
 // the 4 accumulators of a round); the accumulators go to out[] only under the
-// same never-taken condition.
+// same never-taken condition.  The accumulators are one array, each started
+// from its own lane-dependent value: written as four named vectors, the
+// 16x16 forms compiled to eight accumulator-register moves per round between
+// the MFMAs, which the probe would then have measured instead.
 template <int KIND>
 __global__ __launch_bounds__(256) void probe_mfma_kernel(uint32_t iters, uint32_t *out)
 {
@@ -45,14 +48,15 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(uint32_t iters, uint32_
             a[k] = (_Float16)(float)((lane + k) & 7);
             b[k] = (_Float16)(float)((lane * 3 + k) & 7);
         }
-        f32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+        f32x4 c[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) c[j] = (f32x4){(float)(lane + j), 0, 0, 0};
         for (uint32_t it = 0; it < iters; it++) {
-            c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c1, 0, 0, 0);
-            c2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c2, 0, 0, 0);
-            c3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c3, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; j++) c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c[j], 0, 0, 0);
         }
-        const float s = (c0[0] + c1[1]) + (c2[2] + c3[3]);
+        const f32x4 t = (c[0] + c[1]) + (c[2] + c[3]);
+        const float s = (t[0] + t[1]) + (t[2] + t[3]);
         if (s == -1.0f) out[0] = __float_as_uint(s);
     } else if constexpr (KIND == RRR_PROBE_MFMA_F16_32X32X16) {
         f16x8 a, b;
@@ -60,7 +64,12 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(uint32_t iters, uint32_
             a[k] = (_Float16)(float)((lane + k) & 7);
             b[k] = (_Float16)(float)((lane * 3 + k) & 7);
         }
+        const float l = (float)lane;
         f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        c0[0] = l;
+        c1[1] = l;
+        c2[2] = l;
+        c3[3] = l;
         for (uint32_t it = 0; it < iters; it++) {
             c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
             c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c1, 0, 0, 0);
@@ -75,14 +84,17 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(uint32_t iters, uint32_
             a[k] = (int)(0x01010101u * ((lane + k) & 7));
             b[k] = (int)(0x01010101u * ((lane * 3 + k) & 7));
         }
-        i32x4 c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+        i32x4 c[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) c[j] = (i32x4){(int)lane + j, 0, 0, 0};
         for (uint32_t it = 0; it < iters; it++) {
-            c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, a), __builtin_bit_cast(i8x16, b), c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, a), __builtin_bit_cast(i8x16, b), c1, 0, 0, 0);
-            c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, a), __builtin_bit_cast(i8x16, b), c2, 0, 0, 0);
-            c3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, a), __builtin_bit_cast(i8x16, b), c3, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                c[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, a), __builtin_bit_cast(i8x16, b),
+                                                             c[j], 0, 0, 0);
         }
-        const int s = (c0[0] + c1[1]) + (c2[2] + c3[3]);
+        const i32x4 t = (c[0] + c[1]) + (c[2] + c[3]);
+        const int s = (t[0] + t[1]) + (t[2] + t[3]);
         if (s == -1) out[0] = (uint32_t)s;
     }
 }
