@@ -92,7 +92,8 @@ struct rrr_ctx {
     hipEvent_t ev0, ev1;
     void *scratch;      // argmax partial candidates
     void *att_scratch;  // attention: per-KV-head counters (zero between calls) and split partials
-    void *gemm_ws;      // prefill GEMM: partials of split K (GEMM_WS_BYTES)
+    void *gemm_ws;      // GEMM_WS_BYTES: prefill GEMM partials of split K; the skinny GEMV's encoded
+                        // activations (stream order keeps the users apart)
     std::unordered_set<rrr_buf *> bufs;
     std::unordered_set<rrr_graph *> graphs;
     std::unordered_set<rrr_sweep *> sweeps;
@@ -493,6 +494,8 @@ static int gemv_prepare(rrr_ctx *ctx, const rrr_buf *X, uint64_t x_floats, const
     a.N = N;
     a.M = M;
     a.residual = residual;
+    a.ws = ctx->gemm_ws;
+    a.ws_bytes = GEMM_WS_BYTES;
     return RRR_OK;
 }
 

@@ -27,6 +27,8 @@ struct GemvArgs {
     float *y;
     uint32_t K, N, M;
     uint32_t residual;    // y += result instead of y = result
+    void *ws;             // device workspace of the skinny path's encoded activations
+    uint64_t ws_bytes;
 };
 
 // Every device buffer is allocated with at least this many bytes past its

@@ -22,11 +22,26 @@
 // k = 8(l/16) .. +7; 16x16x16 f16 -- the same at k = 4(l/16) .. +3; D rows
 // 4(l/16)+r of column l%16 in register r.
 //
+// Encoding pass (M > 8: two A tiles).  The A operands depend only on X, so a
+// small kernel (skinny_encode_kernel, one wave per A tile and super-block
+// column) builds them once per call into the workspace, in the lane order of
+// the MFMA:
+//   av   [TOK][W][8][64] f16x8  lane's 8 values of sub-block s
+//   amin [TOK][W][64]    f16x4  lane's 4 sub-block sums (min-term A operand)
+//   ex   [TOK][W][16]    int    E of A row r
+// (W = K/256 columns, TOK A tiles), 8,768 bytes per (tile, column).  Every
+// workgroup of the main kernel then loads its operands with 16-byte loads
+// instead of reading all of X in f32 and converting it again.  With one A
+// tile (M <= 8) each wave encodes its own slice: there the pass's launch
+// costs more than the staging it saves (gate+up 16384x3072 at M = 4:
+// 16.5 us with it, 14.4 us without).
+//
 // Work split: a workgroup of K/256 waves, wave w owns super-block w of every
-// row; it builds its A operands once, then walks the workgroup's 16-row tiles
-// b, b + G, ... (G = gridDim.x), staging the tile's 16 blocks of its column in
-// its private LDS region by LDS DMA (the next tiles' loads in flight
-// meanwhile).  Row partials of the waves are added in wave order per tile.
+// row; it gets its A operands (its first tiles' weight loads in flight), then
+// walks the workgroup's 16-row tiles b, b + G, ... (G = gridDim.x), staging the
+// tile's 16 blocks of its column in its private LDS region by LDS DMA (the
+// next tiles' loads in flight meanwhile).  Row partials of the waves are added
+// in wave order per tile.
 #include "device_common.h"
 #include "internal.h"
 
@@ -125,11 +140,122 @@ __device__ __forceinline__ void sk_wait_vm()
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// HILO: 8 tokens (hi, lo rows) per A tile, else 16 tokens (hi rows); TOK A
-// tiles.  TPT = tokens per A tile, DPT = of them per lane in the D layout.
-// NB tile buffers per wave: tiles i+1 .. i+NB-1 stream in while tile i is
-// multiplied.
-template <class Q, bool HILO, int TOK, int NB>
+// Workspace layout of the encoded activations (see the top of this file).
+constexpr uint32_t SK_AV_UNIT = 8 * 64 * 16, SK_AMIN_UNIT = 64 * 8, SK_EX_UNIT = 16 * 4;
+__host__ __device__ constexpr uint64_t sk_ws_bytes(uint32_t tok, uint32_t W)
+{
+    return (uint64_t)tok * W * (SK_AV_UNIT + SK_AMIN_UNIT + SK_EX_UNIT);
+}
+struct SkWs {
+    u32x4 *av;
+    u32x2 *amin;
+    int *ex;
+    __host__ __device__ SkWs(void *base, uint32_t tok, uint32_t W)
+    {
+        uint8_t *p = (uint8_t *)base;
+        av = (u32x4 *)p;
+        amin = (u32x2 *)(p + (uint64_t)tok * W * SK_AV_UNIT);
+        ex = (int *)(p + (uint64_t)tok * W * (SK_AV_UNIT + SK_AMIN_UNIT));
+    }
+};
+
+// A operands of A tile tt and super-block column w, built by one wave:
+// lane (row r16, group kg) gets token tok's values k0 + 32 s + 8 kg + i
+// (i < 8) of every sub-block s, its 4 sub-block sums (min-term A operand) and
+// the block exponent E of its A row.  HILO: 8 tokens (hi, lo rows) per A
+// tile, else 16 tokens (hi rows).  after_loads() runs once the activation
+// loads are issued (the caller queues its weight loads behind them).
+template <bool HILO, class F>
+__device__ __forceinline__ void sk_encode(const float *__restrict__ x, uint32_t M, uint32_t K, uint32_t tt,
+                                          uint32_t w, uint32_t lane, f16x8s (&av)[8], f16x4s &am, int &e,
+                                          F &&after_loads)
+{
+    const uint32_t r16 = lane & 15, kg = lane >> 4;
+    const uint32_t k0 = w * 256;
+    const uint32_t tok = HILO ? tt * 8 + (r16 >> 1) : tt * 16 + r16;
+    const bool lo = HILO && (r16 & 1);
+    const bool live = tok < M;
+    const float4 *xp = (const float4 *)(x + (uint64_t)min(tok, M - 1) * K + k0 + 8 * kg);
+    float4 xv[16];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        xv[2 * s] = xp[8 * s];
+        xv[2 * s + 1] = xp[8 * s + 1];
+    }
+    after_loads();
+    float mx = 0.0f, gs[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const float4 u = xv[2 * s], v = xv[2 * s + 1];
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        gs[s] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
+    }
+    // the token's four k-groups (lanes r16 + 16 kg)
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        gs[s] = gs[s] + __shfl_xor(gs[s], 16, 64);
+        gs[s] = gs[s] + __shfl_xor(gs[s], 32, 64);
+    }
+    e = 0;
+    if (mx > 0.0f && __builtin_isfinite(mx)) {
+        int ex;
+        (void)frexpf(mx, &ex);
+        e = ex - 14;  // mx / 2^e in [2^13, 2^14)
+    }
+    const float sx = ldexpf(1.0f, -e), sg = ldexpf(1.0f, -e - 5);
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const float4 u = xv[2 * s], v = xv[2 * s + 1];
+        const float f[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+        f16x8s h;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float y = f[i] * sx;
+            const _Float16 hi = (_Float16)y;
+            h[i] = live ? (lo ? (_Float16)(y - (float)hi) : hi) : (_Float16)0.0f;
+        }
+        av[s] = h;
+    }
+    // X_s of sub-blocks 4 kg .. 4 kg + 3 (k-groups 2, 3 are padding)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float g = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            if (s == (int)(4 * kg) + i) g = gs[s];
+        const float y = g * sg;
+        const _Float16 hi = (_Float16)y;
+        am[i] = live && kg < 2 ? (lo ? (_Float16)(y - (float)hi) : hi) : (_Float16)0.0f;
+    }
+}
+
+// The encoding pass: one wave per (super-block column, A tile), grid (W, TOK).
+template <bool HILO>
+__global__ __launch_bounds__(64) void skinny_encode_kernel(const float *__restrict__ x, uint32_t M, uint32_t K,
+                                                           void *ws, uint32_t tok_tiles)
+{
+    const uint32_t W = K / 256, w = blockIdx.x, tt = blockIdx.y, lane = threadIdx.x;
+    const SkWs o(ws, tok_tiles, W);
+    f16x8s av[8];
+    f16x4s am;
+    int e;
+    sk_encode<HILO>(x, M, K, tt, w, lane, av, am, e, [] {});
+    u32x4 *ap = o.av + (uint64_t)(tt * W + w) * 8 * 64 + lane;
+#pragma unroll
+    for (int s = 0; s < 8; s++) ap[s * 64] = __builtin_bit_cast(u32x4, av[s]);
+    o.amin[(uint64_t)(tt * W + w) * 64 + lane] = __builtin_bit_cast(u32x2, am);
+    if (lane < 16) o.ex[(tt * W + w) * 16 + lane] = e;
+}
+
+// TOK A tiles (TPT tokens each); DPT = tokens of a tile per lane in the D
+// layout.  NB tile buffers per wave: tiles i+1 .. i+NB-1 stream in while
+// tile i is multiplied.  PRE: the A operands come from the encoding pass,
+// else each wave builds its own (one A tile: the f32 activations are no more
+// bytes than their encoding, and the pass would cost a launch).
+template <class Q, bool HILO, int TOK, int NB, bool PRE>
 __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs a, uint32_t ntiles)
 {
     using G = SkGeom<Q>;
@@ -162,80 +288,38 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
             sk_dma16(rs, dst + 1024 * s, s == G::S - 1 ? voff_last : voff, tb + s * G::RPS * row_bytes);
     };
 
-    // 1. A operands of this wave's slice, tile by tile: lane (row r16, group
-    // kg) holds token tok's values k0 + 32 s + 8 kg + i (i < 8) of every s
+    // 1. A operands, the first tiles' weights streaming in meanwhile (queued
+    // before the loads of encoded operands, after those of f32 activations,
+    // which the encoding needs first)
     f16x8s av[TOK][8];
     f16x4s amin[TOK];
     int eexp[TOK][DPT];   // E of the lane's D-layout tokens
-    const uint32_t k0 = wave * 256;
+    // D row 4 kg + j holds A row 4 kg + j: the token of A row 4 kg + 2 j
+    // (HILO: rows 2t, 2t+1 are token t's hi and lo) or 4 kg + j
+    if constexpr (PRE) {
+        for (uint32_t i = 0; i + 1 < NB; i++) dma(i);
+        const SkWs o(a.ws, TOK, W);
 #pragma unroll
-    for (int tt = 0; tt < TOK; tt++) {
-        // one A tile's activations in registers at a time
-        asm volatile("" ::: "memory");
-        const uint32_t tok = HILO ? tt * 8 + (r16 >> 1) : tt * 16 + r16;
-        const bool lo = HILO && (r16 & 1);
-        const bool live = tok < M;
-        const float4 *xp = (const float4 *)(a.x + (uint64_t)min(tok, M - 1) * K + k0 + 8 * kg);
-        float4 xv[16];
+        for (int tt = 0; tt < TOK; tt++) {
+            const u32x4 *ap = o.av + (uint64_t)(tt * W + wave) * 8 * 64 + lane;
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            xv[2 * s] = xp[8 * s];
-            xv[2 * s + 1] = xp[8 * s + 1];
+            for (int s = 0; s < 8; s++) av[tt][s] = __builtin_bit_cast(f16x8s, ap[s * 64]);
+            amin[tt] = __builtin_bit_cast(f16x4s, o.amin[(uint64_t)(tt * W + wave) * 64 + lane]);
+#pragma unroll
+            for (int j = 0; j < DPT; j++)
+                eexp[tt][j] = o.ex[(tt * W + wave) * 16 + (HILO ? 4 * kg + 2 * j : 4 * kg + j)];
         }
-        // the first tiles' weights stream in while the activations are staged
-        if (tt == 0)
-            for (uint32_t i = 0; i + 1 < NB; i++) dma(i);
-        float mx = 0.0f, gs[8];
+    } else {
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const float4 u = xv[2 * s], v = xv[2 * s + 1];
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-            gs[s] = ((u.x + u.y) + (u.z + u.w)) + ((v.x + v.y) + (v.z + v.w));
+        for (int tt = 0; tt < TOK; tt++) {
+            int e;
+            sk_encode<HILO>(a.x, M, K, tt, wave, lane, av[tt], amin[tt], e, [&] {
+                if (tt == 0)
+                    for (uint32_t i = 0; i + 1 < NB; i++) dma(i);
+            });
+#pragma unroll
+            for (int j = 0; j < DPT; j++) eexp[tt][j] = __shfl(e, HILO ? 4 * kg + 2 * j : 4 * kg + j, 64);
         }
-        // the token's four k-groups (lanes r16 + 16 kg)
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            gs[s] = gs[s] + __shfl_xor(gs[s], 16, 64);
-            gs[s] = gs[s] + __shfl_xor(gs[s], 32, 64);
-        }
-        int e = 0;
-        if (mx > 0.0f && __builtin_isfinite(mx)) {
-            int ex;
-            (void)frexpf(mx, &ex);
-            e = ex - 14;  // mx / 2^e in [2^13, 2^14)
-        }
-        const float sx = ldexpf(1.0f, -e), sg = ldexpf(1.0f, -e - 5);
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const float4 u = xv[2 * s], v = xv[2 * s + 1];
-            const float f[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-            f16x8s h;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float y = f[i] * sx;
-                const _Float16 hi = (_Float16)y;
-                h[i] = live ? (lo ? (_Float16)(y - (float)hi) : hi) : (_Float16)0.0f;
-            }
-            av[tt][s] = h;
-        }
-        // X_s of sub-blocks 4 kg .. 4 kg + 3 (k-groups 2, 3 are padding)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float g = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 8; s++)
-                if (s == (int)(4 * kg) + i) g = gs[s];
-            const float y = g * sg;
-            const _Float16 hi = (_Float16)y;
-            amin[tt][i] = live && kg < 2 ? (lo ? (_Float16)(y - (float)hi) : hi) : (_Float16)0.0f;
-        }
-        // scales of the D-layout tokens of this lane: D row 4 kg + j holds
-        // A row 4 kg + j, i.e. the token of lane 4 kg + j's A operands
-#pragma unroll
-        for (int j = 0; j < DPT; j++) eexp[tt][j] = __shfl(e, HILO ? 4 * kg + 2 * j : 4 * kg + j, 64);
     }
 
     // 2. tiles: tile tl + NB - 1 into the buffer tile tl - 1 used, wait for
@@ -330,11 +414,14 @@ template <class Q, bool HILO, int TOK, int NB>
 static hipError_t go_skinny_nb(const GemvArgs &a, hipStream_t s)
 {
     const uint32_t W = a.K / 256, ntiles = (a.N + 15) / 16;
+    constexpr bool PRE = TOK > 1;
+    if (PRE)
+        hipLaunchKernelGGL(skinny_encode_kernel<HILO>, dim3(W, TOK), dim3(64), 0, s, a.x, a.M, a.K, a.ws, (uint32_t)TOK);
     // up to one workgroup per CU, the tiles spread evenly over them
     const uint32_t per = (ntiles + sk_cus() - 1) / sk_cus();
     const uint32_t grid = (ntiles + per - 1) / per;
     const size_t lds = sk_lds<Q, HILO, TOK, NB>(W);
-    hipLaunchKernelGGL((skinny_kernel<Q, HILO, TOK, NB>), dim3(grid), dim3(64 * W), lds, s, a, ntiles);
+    hipLaunchKernelGGL((skinny_kernel<Q, HILO, TOK, NB, PRE>), dim3(grid), dim3(64 * W), lds, s, a, ntiles);
     return hipGetLastError();
 }
 
@@ -357,6 +444,7 @@ bool skinny_supported(const GemvArgs &a)
     // waves per workgroup: up to 16 with one A tile (M <= 8), up to 12 with
     // two, whose A operands need more registers
     if (a.K > (a.M <= 8 ? 4096u : 3072u)) return false;
+    if (!a.ws || a.ws_bytes < sk_ws_bytes(2, a.K / 256)) return false;
     return a.w_bytes + RRR_READ_SLACK < SK_OOB;
 }
 
