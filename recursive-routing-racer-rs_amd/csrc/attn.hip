@@ -81,12 +81,13 @@ hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uin
 // V; a score is one DPP row sum).  The HPK query heads of the KV group share
 // every K/V load.  Scores go through exp2 with the queries pre-scaled by
 // log2(e) / sqrt(head_dim); each lane group keeps a running max, sum and
-// output (online softmax).  The 16 lane groups are merged in LDS, and the
-// workgroup's {output, max, sum} per query head is written through
-// the coherent level; the last workgroup of KV head g to arrive (an
-// agent-scope counter) merges the splits and writes the output, then resets
-// the counter for the next call.  Every merge runs in a fixed order, so the
-// result depends on seq_len only.
+// output (online softmax).  The 4 lane groups of a wave are merged by lane
+// swaps (rows 0+1 and 2+3, then the two halves, lower partner first), the 4
+// waves in LDS, and the workgroup's {output, max, sum}
+// per query head is written through the coherent level; the last workgroup of
+// KV head g to arrive (an agent-scope counter) merges the splits and writes
+// the output, then resets the counter for the next call.  Every merge runs in
+// a fixed order, so the result depends on seq_len only.
 
 __device__ __forceinline__ float safe_scale(float m, float M) { return m == -__builtin_inff() ? 0.0f : exp2f(m - M); }
 
@@ -101,17 +102,57 @@ __device__ __forceinline__ float row16_sum(float v)
     return v;
 }
 
+// The values of v in lane (lane & ~X) and in lane (lane | X), X = 16 or 32,
+// by the gfx950 lane swaps (VALU, no LDS round trip): v_permlane16_swap
+// exchanges the odd 16-lane rows of its first operand with the even rows of
+// its second, v_permlane32_swap the upper half of the first with the lower
+// half of the second, so with both operands v the results are v of the
+// lower and of the upper partner.
+template <int X>
+__device__ __forceinline__ void lane_pair(float v, float &lo, float &hi)
+{
+    const uint32_t u = __float_as_uint(v);
+    if constexpr (X == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    }
+}
+
+// Online-softmax state {m, l, o[8]} of lanes (lane & ~X) and (lane | X)
+// merged, lower partner first: both lanes end with the same state.
+template <int X>
+__device__ __forceinline__ void merge_pair(float &m, float &l, float (&o)[8])
+{
+    float m0, m1, l0, l1;
+    lane_pair<X>(m, m0, m1);
+    lane_pair<X>(l, l0, l1);
+    const float M = fmaxf(m0, m1), c0 = safe_scale(m0, M), c1 = safe_scale(m1, M);
+    l = l0 * c0 + l1 * c1;
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+        float o0, o1;
+        lane_pair<X>(o[d], o0, o1);
+        o[d] = o0 * c0 + o1 * c1;
+    }
+    m = M;
+}
+
 template <int HPK>
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, const uint16_t *__restrict__ kc,
                                                    const uint16_t *__restrict__ vc, float *part, uint32_t *counters,
                                                    float *__restrict__ out, uint32_t seq, uint32_t per,
                                                    uint32_t kv_stride, float qscale)
 {
-    __shared__ float gml[16][HPK][2];
-    __shared__ __attribute__((aligned(16))) float go[16][HPK][ATT_HD];
-    __shared__ float sw[HPK][ATT_SPLITS_MAX];      // split weights exp2(m_s - M), then the merged sums
-    __shared__ float sL[HPK];
-    __shared__ __attribute__((aligned(16))) float so[HPK][8][ATT_HD];   // sums over split subsets
+    __shared__ float gml[4][HPK][2];
+    __shared__ __attribute__((aligned(16))) float go[4][HPK][ATT_HD];
+    __shared__ float sw[HPK][ATT_SPLITS_MAX];   // split weights exp2(m_s - M)
+    __shared__ float sL[HPK];                   // the heads' merged sums
+    __shared__ __attribute__((aligned(16))) float so[HPK][8][ATT_HD];    // sums over split subsets
     __shared__ uint32_t last;
     const uint32_t g = blockIdx.x, sp = blockIdx.y, splits = gridDim.y;
     const uint32_t t = threadIdx.x, grp = t >> 4, li = t & 15;
@@ -172,30 +213,33 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
             }
         }
     }
-    // the workgroup's 16 lane groups, in LDS
+    // the wave's 4 lane groups by lane swaps, then the workgroup's 4 waves in LDS
+    const uint32_t wv = t >> 6;
 #pragma unroll
     for (int h = 0; h < HPK; h++) {
-        if (li == 0) {
-            gml[grp][h][0] = m[h];
-            gml[grp][h][1] = l[h];
+        merge_pair<16>(m[h], l[h], o[h]);
+        merge_pair<32>(m[h], l[h], o[h]);
+        if ((t & 63) < 16) {
+            if (li == 0) {
+                gml[wv][h][0] = m[h];
+                gml[wv][h][1] = l[h];
+            }
+            float4 *dst = (float4 *)&go[wv][h][8 * li];
+            dst[0] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+            dst[1] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
         }
-        float4 *dst = (float4 *)&go[grp][h][8 * li];
-        dst[0] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-        dst[1] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
     }
     __syncthreads();
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, (uint64_t)gridDim.x * HPK * splits * ATT_PART * 4);
     for (uint32_t i = t; i < HPK * ATT_HD; i += 256) {
         const uint32_t h = i / ATT_HD, d = i % ATT_HD;
-        float M = -__builtin_inff();
-#pragma unroll
-        for (int gi = 0; gi < 16; gi++) M = fmaxf(M, gml[gi][h][0]);
+        const float M = fmaxf(fmaxf(gml[0][h][0], gml[1][h][0]), fmaxf(gml[2][h][0], gml[3][h][0]));
         float L = 0.0f, O = 0.0f;
 #pragma unroll
-        for (int gi = 0; gi < 16; gi++) {
-            const float c = safe_scale(gml[gi][h][0], M);   // 0 for a group without rows
-            L = fmaf(gml[gi][h][1], c, L);
-            O = fmaf(go[gi][h][d], c, O);
+        for (int wi = 0; wi < 4; wi++) {
+            const float c = safe_scale(gml[wi][h][0], M);   // 0 for a wave without rows
+            L = fmaf(gml[wi][h][1], c, L);
+            O = fmaf(go[wi][h][d], c, O);
         }
         if (splits == 1) {
             out[(size_t)(g * HPK + h) * ATT_HD + d] = O / L;
@@ -233,31 +277,31 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
                                         rp, (((g * splits + s) * HPK + h) * ATT_PART + 4 * dq) * 4, 0, RRR_CPOL_SC1)
                                   : u32x4{0u, 0u, 0u, 0u};
         }
-    float ms = -__builtin_inff(), ls = 0.0f;
-    const uint32_t sh = t / HPK, hh = t % HPK;   // (split, head) of the max / sum this thread reads
-    if (t < splits * HPK) {
-        const uint32_t base = (((g * splits + sh) * HPK + hh) * ATT_PART) * 4;
-        ms = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, base + 4 * ATT_HD, 0, RRR_CPOL_SC1));
-        ls = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, base + 4 * ATT_HD + 4, 0, RRR_CPOL_SC1));
-        sw[hh][sh] = ms;
+    // thread t: split t % 32 of head t / 32; the 32 lanes of a head reduce
+    // its maximum and sum by butterflies (both partners of a step compute
+    // the same a + b, so every lane gets the same value, every run)
+    {
+        const uint32_t hh = t >> 5, sh = t & 31;
+        float ms = -__builtin_inff(), ls = 0.0f;
+        if (hh < HPK && sh < splits) {
+            const uint32_t base = (((g * splits + sh) * HPK + hh) * ATT_PART) * 4;
+            ms = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, base + 4 * ATT_HD, 0, RRR_CPOL_SC1));
+            ls = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, base + 4 * ATT_HD + 4, 0, RRR_CPOL_SC1));
+        }
+        float M = ms;
+#pragma unroll
+        for (int x = 16; x >= 1; x >>= 1) M = fmaxf(M, __shfl_xor(M, x, 64));
+        const float w = safe_scale(ms, M);
+        float L = ls * w;
+#pragma unroll
+        for (int x = 16; x >= 1; x >>= 1) L = L + __shfl_xor(L, x, 64);
+        if (hh < HPK) {
+            sw[hh][sh] = w;
+            if (sh == 0) sL[hh] = L;
+        }
     }
     __syncthreads();
-    if (t < HPK) {   // the head's max over its splits, then its weights and sum, in split order
-        float M = -__builtin_inff();
-        for (uint32_t s = 0; s < splits; s++) M = fmaxf(M, sw[t][s]);
-        sL[t] = M;
-    }
-    __syncthreads();
-    if (t < splits * HPK) sw[hh][sh] = exp2f(ms - sL[hh]);
-    __syncthreads();
-    if (t < splits * HPK) so[hh][0][sh] = ls * sw[hh][sh];   // staged for the ordered sum below
-    __syncthreads();
-    if (t < HPK) {
-        float L = 0.0f;
-        for (uint32_t s = 0; s < splits; s++) L += so[t][0][s];
-        sL[t] = L;
-    }
-    __syncthreads();
+    // its own splits' output quads, weighted and added in split order
 #pragma unroll
     for (int h = 0; h < HPK; h++) {
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
