@@ -279,6 +279,15 @@ int rrr_silu_gate_f16(rrr_ctx *ctx, const rrr_buf *gate_up, rrr_buf *mid_f16, rr
  * rrr_gemv. */
 int rrr_gemv_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps,
                      const rrr_buf *W, uint32_t type, rrr_buf *Y, uint32_t K, uint32_t N);
+/* Y[f] = silu(g[f]) * u[f] for f < F, where [g | u] = W . rmsnorm(x, gamma,
+ * eps) over W's 2F rows (F gate rows, then F up rows): the ffn_up matmul into
+ * the 2F gate_up buffer followed by silu_gate (phi4.rs:1025-1029) as one
+ * launch, so the down GEMV reads F activations instead of 2F.  The silu is
+ * RRR_ACT_SILU_GATE's, on the row sums rrr_gemv_rmsnorm computes: Y is
+ * bitwise that activation of rrr_gemv_rmsnorm's 2F outputs.  Q4_K, Q5_K and
+ * Q6_K rows, K % 256 == 0, K <= 8192 (RRR_ERR_UNSUPPORTED otherwise). */
+int rrr_gemv_rmsnorm_silu(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps,
+                          const rrr_buf *W, uint32_t type, rrr_buf *Y, uint32_t K, uint32_t F);
 /* hidden[n] += sum_k act(x)[k] * W[n][k] (residual_add folded into the GEMV's
  * epilogue, phi4.rs:1020-1023 and :1030-1033).  act_kind:
  *   RRR_ACT_IDENTITY  act(x) = x[0..K)

@@ -466,7 +466,8 @@ int rrr_dequant(rrr_ctx *ctx, uint32_t type, const rrr_buf *W, rrr_buf *out, uin
 // Checks of one GEMV-family call and its launch arguments.
 static int gemv_prepare(rrr_ctx *ctx, const rrr_buf *X, uint64_t x_floats, const rrr_buf *gamma, float eps,
                         uint32_t act, uint32_t hd, uint32_t hpk, const rrr_buf *W, uint32_t type, rrr_buf *Y,
-                        uint32_t K, uint32_t N, uint32_t M, uint32_t residual, const char *what, GemvArgs &a)
+                        uint32_t K, uint32_t N, uint32_t M, uint32_t residual, const char *what, GemvArgs &a,
+                        uint64_t y_floats = 0)   // 0: M * N
 {
     TRY(check_buf(ctx, X, what));
     TRY(check_buf(ctx, W, what));
@@ -477,7 +478,7 @@ static int gemv_prepare(rrr_ctx *ctx, const rrr_buf *X, uint64_t x_floats, const
     if (M > 65535) return fail(RRR_ERR_UNSUPPORTED, "%s: M=%u exceeds 65535", what, M);
     TRY(need(W, rrr_tensor_bytes(type, K, N), what));
     TRY(need_f32(X, x_floats, what));
-    TRY(need_f32(Y, (uint64_t)M * N, what));
+    TRY(need_f32(Y, y_floats ? y_floats : (uint64_t)M * N, what));
     if (gamma) TRY(need_f32(gamma, K, what));
     if (act == ACT_RMSNORM && !(std::isfinite(eps) && eps >= 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: eps", what);
     a = GemvArgs{};
@@ -544,6 +545,26 @@ int rrr_gemv_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float
     TRY(check_ctx(ctx));
     if (!gamma) return fail(RRR_ERR_NULL, "rrr_gemv_rmsnorm: null gamma");
     return gemv_common(ctx, x, K, gamma, eps, ACT_RMSNORM, 0, 0, W, type, Y, K, N, 1, 0, "rrr_gemv_rmsnorm");
+}
+
+int rrr_gemv_rmsnorm_silu(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps, const rrr_buf *W,
+                          uint32_t type, rrr_buf *Y, uint32_t K, uint32_t F)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_gemv_rmsnorm_silu";
+    if (!gamma) return fail(RRR_ERR_NULL, "%s: null gamma", what);
+    if (F == 0 || F > 0x7FFFFFFFu) return fail(RRR_ERR_BAD_SHAPE, "%s: F=%u", what, F);
+    if (type != RRR_TYPE_Q4_K && type != RRR_TYPE_Q5_K && type != RRR_TYPE_Q6_K)
+        return fail(RRR_ERR_UNSUPPORTED, "%s: type %u (Q4_K, Q5_K or Q6_K rows)", what, type);
+    if (K > 8192) return fail(RRR_ERR_UNSUPPORTED, "%s: K=%u exceeds 8192", what, K);
+    // the checks of a GEMV into all 2F rows, with an output of F floats
+    GemvArgs a;
+    TRY(gemv_prepare(ctx, x, K, gamma, eps, ACT_RMSNORM, 0, 0, W, type, Y, K, 2 * F, 1, 0, what, a, F));
+    a.N = F;
+    a.pair = 1;
+    if (!gemv_mfma_supported(a)) return fail(RRR_ERR_UNSUPPORTED, "%s: shape", what);
+    TRY(device_ready(ctx));
+    return finish(ctx, launch_gemv(a, ACT_RMSNORM, ctx->stream), what);
 }
 
 int rrr_gemv_residual(rrr_ctx *ctx, const rrr_buf *x, uint32_t act_kind, uint32_t act_param, const rrr_buf *W,

@@ -5,10 +5,10 @@
 
 namespace rrr {
 
-template <class Q, int BPW, int ACT, bool MULTI, int TR>
+template <class Q, int BPW, int ACT, bool MULTI, int TR, bool PAIR = false>
 __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntiles, uint32_t tr)
 {
-    mq_body<Q, BPW, ACT, MULTI, TR>(a, ntiles, tr);
+    mq_body<Q, BPW, ACT, MULTI, TR, PAIR>(a, ntiles, tr);
 }
 
 // Super-blocks per wave and waves per workgroup (at least 4, the canonical
@@ -38,6 +38,27 @@ static void launch_mq(const GemvArgs &a, uint32_t W, uint32_t grid, size_t lds, 
         hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, false, TR>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
     else
         hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, true, TR>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
+}
+
+// The silu pair form (a.pair): per 16 output rows a gate tile and its up
+// tile, fused RMSNorm; always the persistent form (a workgroup holds both
+// tiles of a pair).
+template <class Q, int BPW>
+static hipError_t go_mq_pair(const GemvArgs &a, hipStream_t s)
+{
+    using G = MwGeom<Q, BPW>;
+    const uint32_t B = a.K / 256;
+    const uint32_t W = max(4u, (B + BPW - 1) / BPW);
+    const size_t fixed = W * G::BYTES + 16;
+    const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64)) / 2;   // pairs: two tiles each
+    if (per_max == 0) return hipErrorInvalidValue;
+    const uint32_t npairs = (a.N + 15) / 16, cus = device_cus();
+    const uint32_t per = min((npairs + cus - 1) / cus, per_max);
+    const uint32_t grid = (npairs + per - 1) / per;
+    const size_t lds = fixed + (size_t)2 * per * W * 64;
+    hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT_RMSNORM, true, 16, true>), dim3(grid), dim3(64 * W), lds, s, a,
+                       npairs, 16u);
+    return hipGetLastError();
 }
 
 template <class Q, int BPW, int ACT>
@@ -84,6 +105,16 @@ bool gemv_mfma_supported(const GemvArgs &a)
 
 hipError_t launch_gemv_mfma(const GemvArgs &a, uint32_t act, hipStream_t s)
 {
+    if (a.pair) {
+        if (act != ACT_RMSNORM || a.residual) return hipErrorInvalidValue;
+        const bool one = a.K <= 16 * 256;
+        switch (a.type) {
+        case T_Q4_K: return one ? go_mq_pair<MqQ4K, 1>(a, s) : go_mq_pair<MqQ4K, 2>(a, s);
+        case T_Q5_K: return one ? go_mq_pair<MqQ5K, 1>(a, s) : go_mq_pair<MqQ5K, 2>(a, s);
+        case T_Q6_K: return one ? go_mq_pair<MqQ6K, 1>(a, s) : go_mq_pair<MqQ6K, 2>(a, s);
+        default: return hipErrorInvalidValue;
+        }
+    }
     switch (a.type) {
     case T_Q4_K: return go_mq_act<MqQ4K>(a, act, s);
     case T_Q5_K: return go_mq_act<MqQ5K>(a, act, s);

@@ -301,20 +301,34 @@ constexpr uint32_t MQ_OOB = 0x80000000u;
 // TR: the most rows a tile of the launch has (tr <= TR <= 16); a wave issues
 // the load slots that cover TR rows, so a launch of shorter tiles issues no
 // empty slots.
-template <class Q, int BPW, int ACT, bool MULTI, int TR = 16>
+// PAIR (a.pair, MULTI, tr = 16): W holds 2N rows, N gate rows then N up rows
+// (the ffn_up matmul into the 2F gate_up buffer that silu_gate reads,
+// phi4.rs:1025-1029); ntiles counts 16-row pairs, and the workgroup's tile
+// 2q is gate rows 16P .. 16P+15 of its q-th pair P, tile 2q+1 the matching up
+// rows (each a contiguous run of rows, as in a plain launch).  It writes
+// y[16P + r] = silu(gate) * up with the RRR_ACT_SILU_GATE formula, on the
+// same row sums a plain launch computes: the result is bitwise what a GEMV
+// into 2N rows followed by that activation gives.
+template <class Q, int BPW, int ACT, bool MULTI, int TR = 16, bool PAIR = false>
 __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr)
 {
     extern __shared__ float smem[];
     using G = MwGeom<Q, BPW>;
     static_assert(TR >= 1 && TR <= 16, "tile rows");
     constexpr int SB = (TR + (int)G::RPS - 1) / (int)G::RPS;     // load slots of one block
-    constexpr bool AREG = BPW == 1;
+    // A operands in registers, except in the persistent two-block form, whose
+    // next-tile prefetch registers leave no room for them (it reads them from
+    // LDS before each MFMA)
+    constexpr bool AREG = BPW == 1 || !MULTI;
+    constexpr int AJ = AREG ? BPW : 1;
     const uint32_t K = a.K, B = K / 256;
     const uint32_t W = blockDim.x >> 6, NT = blockDim.x;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t GR = gridDim.x, tile0 = blockIdx.x;
-    const uint32_t ntl = MULTI ? (tile0 < ntiles ? (ntiles - tile0 + GR - 1) / GR : 0u) : 1u;  // tiles of this workgroup
+    static_assert(!PAIR || (MULTI && TR == 16), "a pair is a gate tile and an up tile of 16 rows");
+    const uint32_t nown = tile0 < ntiles ? (ntiles - tile0 + GR - 1) / GR : 0u;   // tiles (PAIR: pairs) of this workgroup
+    const uint32_t ntl = MULTI ? (PAIR ? 2 * nown : nown) : 1u;                    // tiles of this workgroup
     uint8_t *L = (uint8_t *)smem + wave * G::BYTES;              // this wave's region
     float *red = (float *)((uint8_t *)smem + W * G::BYTES);      // 4
     float *part = red + 4;                                       // ntl x W x 16 per-wave row partials
@@ -341,11 +355,21 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     }
     const uint32_t loff = rsel * G::RS + 16 * ul;
     u32x4 wa[BPW][SB];
+    // first row of this workgroup's tile tl in W, and its rows
+    auto tile_row0 = [&](uint32_t tl) -> uint32_t {
+        if constexpr (PAIR) return 16 * (tile0 + (tl >> 1) * GR) + ((tl & 1) ? a.N : 0u);
+        return (tile0 + tl * GR) * tr;
+    };
+    auto tile_rows = [&](uint32_t tl) -> uint32_t {
+        if constexpr (PAIR) return min(16u, a.N - 16 * (tile0 + (tl >> 1) * GR));
+        return tr;
+    };
     auto issue = [&](int j, uint32_t tl) {
-        const uint32_t tb = tl < ntl ? (tile0 + tl * GR) * tile_bytes : MQ_OOB;
+        const uint32_t tb = tl < ntl ? tile_row0(tl) * row_bytes : MQ_OOB;
+        const uint32_t rows = tl < ntl ? tile_rows(tl) : 0u;
 #pragma unroll
         for (int s = 0; s < SB; s++)
-            wa[j][s] = bload16_nt_so(rs, lane_ok && j < (int)nb && s * G::RPS + rsel < tr ? voff[j] : MQ_OOB,
+            wa[j][s] = bload16_nt_so(rs, lane_ok && j < (int)nb && s * G::RPS + rsel < rows ? voff[j] : MQ_OOB,
                                      tb + s * G::RPS * row_bytes);
     };
 
@@ -354,8 +378,8 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     // outstanding load at the join.
     // the residual of this thread's first output row, read now rather than
     // on the kernel's tail (a clamped row when there is none)
-    const uint32_t row_first = min((tile0 + (t >> 4) * GR) * tr + (t & 15), a.N - 1);
-    const float yres = a.y[row_first];
+    const uint32_t row_first = PAIR ? 0u : min((tile0 + (t >> 4) * GR) * tr + (t & 15), a.N - 1);
+    const float yres = PAIR ? 0.0f : a.y[row_first];
     // 1. fused RMSNorm: the whole of x in the canonical order (K <= 1024 NSQ)
     constexpr int NSQ = ACT == ACT_RMSNORM ? 4 * BPW : 1;
     float4 cx[NSQ];
@@ -409,25 +433,27 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     wave_lds_sync();
 
     // A operands (zero in the non-live lanes), accumulator inputs and group
-    // sums of the slice; lane (n, g) supplies A = its digit row (m = n: plane
-    // n%4 of group n/4) when n/4 == g
+    // sums of the slice, into registers while the weights are in flight; lane
+    // (n, g) supplies A = its digit row (m = n: plane n%4 of group n/4) when
+    // n/4 == g
     const bool a_live = (n >> 2) == g && (n & 3) < 3;
     const uint32_t a_base = G::D_OFF + (n & 3) * G::DG;
-    i32x4 av[AREG ? 4 : 1], aux[AREG ? 4 : 1];
-    float gs[AREG ? 4 : 1];
-    if constexpr (AREG) {
+    i32x4 av[AJ][4], aux[AJ][4];
+    float gs[AJ][4];
+#pragma unroll
+    for (int j = 0; j < AJ; j++)
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            av[u] = i32x4{0, 0, 0, 0};
-            aux[u] = *(const i32x4 *)(L + G::A_OFF + Q::koff(g, u));
-            gs[u] = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + Q::koff(g, u) / 4) : 0.0f;
+            const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
+            av[j][u] = i32x4{0, 0, 0, 0};
+            aux[j][u] = *(const i32x4 *)(L + G::A_OFF + 16 * grp);
+            gs[j][u] = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + 4 * grp) : 0.0f;
         }
-        if (a_live) {
+    if (a_live) {
 #pragma unroll
-            for (int u = 0; u < 4; u++) av[u] = *(const i32x4 *)(L + a_base + Q::koff(g, u));
-        }
-    } else {
-        av[0] = i32x4{0, 0, 0, 0};
+        for (int j = 0; j < AJ; j++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) av[j][u] = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
     }
 
     // 4. per tile, block by block: the block's units to LDS (its registers
@@ -456,15 +482,15 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
                 float acc_s = 0.0f, acc_m = 0.0f;
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
                     i32x4 A, C;
                     float gsum;
                     if constexpr (AREG) {
-                        A = av[u];
-                        C = aux[u];
-                        gsum = gs[u];
+                        A = av[j][u];
+                        C = aux[j][u];
+                        gsum = gs[j][u];
                     } else {
-                        A = av[0];
+                        const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
+                        A = i32x4{0, 0, 0, 0};
                         if (a_live) A = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
                         C = *(const i32x4 *)(L + G::A_OFF + 16 * grp);
                         gsum = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + 4 * grp) : 0.0f;
@@ -492,6 +518,21 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
 
     // 5. rows of every tile of this workgroup: the W waves' partials in order
     __syncthreads();
+    if constexpr (PAIR) {
+        for (uint32_t i = t; i < nown * 16; i += NT) {
+            const uint32_t q = i >> 4, r = i & 15, row = (tile0 + q * GR) * 16 + r;
+            if (row < a.N) {
+                const float *pg = part + 2 * q * W * 16 + r, *pu = pg + W * 16;
+                float gv = pg[0], uv = pu[0];
+                for (uint32_t w = 1; w < W; w++) {
+                    gv += pg[w * 16];
+                    uv += pu[w * 16];
+                }
+                a.y[row] = silu_fast(gv) * uv;
+            }
+        }
+        return;
+    }
     for (uint32_t i = t; i < ntl * 16; i += NT) {
         const uint32_t tl = i >> 4, r = i & 15, row = (tile0 + tl * GR) * tr + r;
         if (r < tr && row < a.N) {

@@ -29,6 +29,7 @@ struct GemvArgs {
     uint32_t residual;    // y += result instead of y = result
     void *ws;             // device workspace of the skinny path's encoded activations
     uint64_t ws_bytes;
+    uint32_t pair;        // W holds 2N rows [gate | up]; y[n] = silu(gate row n) * (up row n)
 };
 
 // Every device buffer is allocated with at least this many bytes past its

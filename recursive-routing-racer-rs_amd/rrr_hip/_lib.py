@@ -103,6 +103,7 @@ SIGNATURES = {
     "rrr_logits_f32": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, u32, u32, u32]),
     "rrr_argmax_f32": (i32, [c_ctx_p, c_buf_p, u32, c_buf_p]),
     "rrr_gemv_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, u32, c_buf_p, u32, u32]),
+    "rrr_gemv_rmsnorm_silu": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, u32, c_buf_p, u32, u32]),
     "rrr_gemv_residual": (i32, [c_ctx_p, c_buf_p, u32, u32, c_buf_p, u32, c_buf_p, u32, u32]),
     "rrr_logits_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, c_buf_p, u32, u32, u32, u32]),
     "rrr_rope_kv_store": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, c_buf_p, c_buf_p, u32, u32, u32, u32, u32, u32, u32,

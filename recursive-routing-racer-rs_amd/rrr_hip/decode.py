@@ -13,9 +13,12 @@ fused where the numerics allow it:
                                                attention output is V gathered per
                                                GQA head)
     O-proj GEMV -> residual_add               rrr_gemv_residual(GQA_V)  Q4_K 3072x3072
-    rmsnorm(ffn_norm) -> gate+up GEMV         rrr_gemv_rmsnorm          Q4_K 16384x3072
-    silu_gate -> down GEMV -> residual_add    rrr_gemv_residual(SILU)   Q6_K (even layers) /
+    rmsnorm(ffn_norm) -> gate+up GEMV         rrr_gemv_rmsnorm_silu     Q4_K 16384x3072
+      -> silu_gate                            (silu * up in its epilogue)
+    down GEMV -> residual_add                 rrr_gemv_residual         Q6_K (even layers) /
                                                                         Q4_K (odd) 3072x8192
+    (silu_fused False: rrr_gemv_rmsnorm into the 2F gate/up rows, then
+    rrr_gemv_residual(SILU) with silu_gate in the down GEMV's prologue)
 
 then rmsnorm(output_norm) -> F32 logits over the transposed 8192-entry vocab
 chunks (phi4.rs:874-893, 1049-1064) as rrr_logits_rmsnorm, and the argmax
@@ -229,6 +232,11 @@ class DecodeSweep:
         self.hidden = ctx.alloc(d * 4)
         self.qkv = ctx.alloc(shape.qkv_dim * 4)
         self.gate_up = ctx.alloc(2 * shape.ffn_dim * 4)
+        self.ffn_mid = ctx.alloc(shape.ffn_dim * 4)
+        # silu(gate) * up fused into the gate/up GEMV (rrr_gemv_rmsnorm_silu);
+        # False: the GEMV into gate_up and silu in the down GEMV's prologue
+        # (the same values bit for bit)
+        self.silu_fused = True
         self.logits = ctx.alloc(shape.vocab * 4)
         self.token = ctx.alloc(4)
         self.attention = attention
@@ -375,9 +383,18 @@ class DecodeSweep:
                                 s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta, s.rope_attn_factor)
                 c.attention(self.qkv, kc, vc, self.attn_out, pos + 1, s.n_kv_heads, s.heads_per_kv, s.head_dim)
                 c.gemv_residual(self.attn_out, E.ACT_IDENTITY, 0, L["attn_output"], T["attn_output"], self.hidden, d, d)
-            c.gemv_rmsnorm(self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], T["ffn_up"], self.gate_up, d, 2 * s.ffn_dim)
-            c.gemv_residual(self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], T["ffn_down"], self.hidden,
-                            s.ffn_dim, d)
+            if self.silu_fused and T["ffn_up"] in (E.Q4_K, E.Q5_K, E.Q6_K):
+                # silu(gate) * up in the gate/up GEMV's epilogue: the down
+                # GEMV reads F activations instead of 2F
+                c.gemv_rmsnorm_silu(self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], T["ffn_up"], self.ffn_mid, d,
+                                    s.ffn_dim)
+                c.gemv_residual(self.ffn_mid, E.ACT_IDENTITY, 0, L["ffn_down"], T["ffn_down"], self.hidden,
+                                s.ffn_dim, d)
+            else:
+                c.gemv_rmsnorm(self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], T["ffn_up"], self.gate_up, d,
+                               2 * s.ffn_dim)
+                c.gemv_residual(self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], T["ffn_down"], self.hidden,
+                                s.ffn_dim, d)
         self.record_logits()
 
     def record_logits(self):

@@ -224,6 +224,10 @@ class Context:
     def gemv_rmsnorm(self, x, gamma, eps, W, qtype, Y, K, N):
         _check(self.lib.rrr_gemv_rmsnorm(self._h, x._h, gamma._h, eps, W._h, qtype, Y._h, K, N))
 
+    def gemv_rmsnorm_silu(self, x, gamma, eps, W, qtype, Y, K, F):
+        """Y[F] = silu(gate) * up of W (2F rows: gate, then up) . rmsnorm(x)."""
+        _check(self.lib.rrr_gemv_rmsnorm_silu(self._h, x._h, gamma._h, eps, W._h, qtype, Y._h, K, F))
+
     def gemv_residual(self, x, act_kind, act_param, W, qtype, hidden, K, N):
         _check(self.lib.rrr_gemv_residual(self._h, x._h, act_kind, act_param, W._h, qtype, hidden._h, K, N))
 

@@ -99,6 +99,24 @@ def test_decode_token_q6k_logits_matches_oracle(ctx, sweep):
     g.destroy()
 
 
+def test_decode_silu_fused_is_bitwise_the_two_launch_form(ctx, sweep):
+    """silu(gate) * up in the gate/up GEMV's epilogue (rrr_gemv_rmsnorm_silu,
+    the default) and in the down GEMV's prologue (the 2F gate/up rows kept)
+    give the same token bit for bit."""
+    logits0, tok0, hidden0 = sweep.results()
+    assert sweep.silu_fused
+    sweep.silu_fused = False
+    try:
+        sweep.record_token()
+        ctx.sync()
+    finally:
+        sweep.silu_fused = True
+    logits, tok, hidden = sweep.results()
+    assert tok == tok0
+    assert np.array_equal(hidden.view(np.uint32), hidden0.view(np.uint32))
+    assert np.array_equal(logits.view(np.uint32), logits0.view(np.uint32))
+
+
 def test_decode_graph_replay_matches_eager(ctx, sweep):
     logits0, tok0, hidden0 = sweep.results()
     g = sweep.graph()

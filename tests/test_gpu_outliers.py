@@ -120,6 +120,7 @@ def deep_gate_up(ctx):
     random-init model after one token, and the final hidden state."""
     s = dataclasses.replace(decode.Phi4Shape(), n_layers=8, vocab=256, chunk=256)
     sw = decode.DecodeSweep(ctx, s, seed=3)
+    sw.silu_fused = False   # keeps the 2F gate/up rows in sw.gate_up
     sw.record_token()
     ctx.sync()
     gu = ctx.download(sw.gate_up, np.float32, 2 * s.ffn_dim)

@@ -228,6 +228,41 @@ def test_gemv_rmsnorm_fused_bitwise(ctx, qtype, K, N):
         t.free()
 
 
+@pytest.mark.parametrize("qtype,K,F", [(12, 3072, 8192), (13, 3072, 300), (14, 8192, 1000), (12, 1024, 13),
+                                       (13, 1024, 20000)])
+def test_gemv_rmsnorm_silu(ctx, qtype, K, F):
+    """silu(gate) * up fused into the gate/up GEMV: against the oracle, and
+    bitwise the activation the down GEMV's silu prologue builds from the 2F
+    gate/up rows (a down GEMV on either gives the same result)."""
+    raw = weights(qtype, K, 2 * F, seed=11, stream=qtype)
+    x = synth.normal_f32(11, 1, K)
+    g = synth.normal_f32(11, 2, K, 1.0, 0.1)
+    W = ctx.weight_upload(qtype, K, 2 * F, raw)
+    xb, gb = ctx.to_device(x), ctx.to_device(g)
+    mid, gu = ctx.alloc(F * 4), ctx.alloc(2 * F * 4)
+    ctx.gemv_rmsnorm_silu(xb, gb, 1e-5, W, qtype, mid, K, F)
+    ctx.gemv_rmsnorm(xb, gb, 1e-5, W, qtype, gu, K, 2 * F)
+    ref_gu = orc.gemv(qtype, raw, orc.rms_norm(x, g), K, 2 * F, 1, THREADS, f64=True)[0]
+    ref = ref_gu[:F] / (1.0 + np.exp(-ref_gu[:F])) * ref_gu[F:]
+    y = ctx.download(mid)
+    assert err(y, ref) < TOL
+    # a down GEMV (N = 64 rows of K = F) on the fused output and, with the
+    # silu prologue, on the 2F rows: the same activation values give the
+    # same sums
+    if F % 256 == 0:
+        N = 64
+        rawd = weights(12, F, N, seed=11, stream=40)
+        Wd = ctx.weight_upload(12, F, N, rawd)
+        y1, y2 = ctx.to_device(np.zeros(N, np.float32)), ctx.to_device(np.zeros(N, np.float32))
+        ctx.gemv_residual(mid, rrr_hip.ACT_IDENTITY, 0, Wd, 12, y1, F, N)
+        ctx.gemv_residual(gu, rrr_hip.ACT_SILU_GATE, 0, Wd, 12, y2, F, N)
+        assert np.array_equal(ctx.download(y1), ctx.download(y2))
+        for t in (Wd, y1, y2):
+            t.free()
+    for t in (W, xb, gb, mid, gu):
+        t.free()
+
+
 def test_gemv_residual_kinds(ctx):
     K, N = 3072, 3072
     # identity: O-proj + residual

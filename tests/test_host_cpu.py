@@ -212,6 +212,21 @@ def test_fused_validation(vctx):
     assert code_of(vctx.gemv_residual, hid, rrr_hip.ACT_SILU_GATE, 0, W, 12, hid, K, K) == ERR_SHORT_BUFFER
 
 
+def test_gemv_rmsnorm_silu_validation(vctx):
+    K, F = 3072, 64
+    x, g = vctx.alloc(K * 4), vctx.alloc(K * 4)
+    W = vctx.alloc(rrr_hip.tensor_bytes(12, K, 2 * F))
+    y = vctx.alloc(F * 4)                    # F outputs, not 2F
+    assert code_of(vctx.gemv_rmsnorm_silu, x, g, 1e-5, W, 12, y, K, F) == ERR_NO_DEVICE   # valid call, no GPU
+    assert code_of(vctx.gemv_rmsnorm_silu, x, g, 1e-5, W, 12, y, K, F + 1) == ERR_SHORT_BUFFER   # W holds 2F rows
+    assert code_of(vctx.gemv_rmsnorm_silu, x, g, 1e-5, W, 12, vctx.alloc(F * 4 - 4), K, F) == ERR_SHORT_BUFFER
+    assert code_of(vctx.gemv_rmsnorm_silu, x, g, 1e-5, W, 12, y, K, 0) == ERR_BAD_SHAPE
+    assert code_of(vctx.gemv_rmsnorm_silu, x, g, 1e-5, W, 0, y, K, F) == ERR_UNSUPPORTED       # F32 rows
+    assert code_of(vctx.gemv_rmsnorm_silu, x, g, float("nan"), W, 12, y, K, F) == ERR_INVALID_ARG
+    nullbuf = rrr_hip.Buffer(vctx, None, 0)
+    assert code_of(vctx.gemv_rmsnorm_silu, x, nullbuf, 1e-5, W, 12, y, K, F) == ERR_NULL
+
+
 def test_dispatch_shim_validation(vctx):
     K, N = 3072, 16
     x, y = vctx.alloc(K * 4), vctx.alloc(N * 4)
