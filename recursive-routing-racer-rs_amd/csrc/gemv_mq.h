@@ -380,12 +380,19 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     // on the kernel's tail (a clamped row when there is none)
     const uint32_t row_first = PAIR ? 0u : min((tile0 + (t >> 4) * GR) * tr + (t & 15), a.N - 1);
     const float yres = PAIR ? 0.0f : a.y[row_first];
-    // 1. fused RMSNorm: the whole of x in the canonical order (K <= 1024 NSQ)
+    // 1. fused RMSNorm: the whole of x in the canonical order (K <= 1024 NSQ),
+    // read by the threads that sum it (t < 256); the other threads' and
+    // the past-the-end loads go out of range (no memory request)
     constexpr int NSQ = ACT == ACT_RMSNORM ? 4 * BPW : 1;
     float4 cx[NSQ];
     if constexpr (ACT == ACT_RMSNORM) {
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint64_t)K * 4);
 #pragma unroll
-        for (int j = 0; j < NSQ; j++) cx[j] = ((const float4 *)a.x)[min(t + 256 * j, K / 4 - 1)];
+        for (int j = 0; j < NSQ; j++) {
+            const uint32_t f = t + 256 * j;
+            const u32x4 v = bload16(rx, t < 256 && f < K / 4 ? 16 * f : MQ_OOB);
+            cx[j] = make_float4(u2f(v.x), u2f(v.y), u2f(v.z), u2f(v.w));
+        }
     }
     // 2. this wave's activation inputs: float4 lane + 64 j of its slice
     float4 xa[BPW], xb[BPW];
