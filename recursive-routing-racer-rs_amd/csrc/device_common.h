@@ -128,33 +128,109 @@ __device__ __forceinline__ float block_sum_w(float acc, float *red)
     return s;
 }
 
-// Canonical per-thread sum-of-squares order shared by every RMSNorm on the
-// path (standalone and fused), so that they agree bit for bit: for d % 4 == 0
-// thread t owns the float4s t, t + 256, t + 512, ... of the vector and
-// accumulates x^2 with fmaf float4 by float4, component by component;
-// otherwise it owns the elements t, t + 256, ...
-__device__ __forceinline__ float thread_sumsq(const float *__restrict__ x, uint32_t d)
+// Canonical sum-of-squares order shared by every RMSNorm on the path
+// (standalone and fused), so that they agree bit for bit.  It is the
+// activation split of the batch-1 MFMA GEMV, whose waves then square the x
+// they already hold.  For d % 4 == 0 the float4s of the vector fall into at
+// most 16 slices of 64 P float4s, P = ceil(d / 4096); lane l of slice s
+// accumulates x^2 with fmaf over the float4s 64 P s + l + 64 j (j < P, those
+// below d / 4), component by component; the 64 lane sums of a slice are added
+// by the wave butterfly, and the slice sums in slice order 0, 1, ..., 15
+// (slices past the end add +0, which changes no sum).  For d % 4 != 0 thread
+// t of a 256-thread workgroup accumulates the elements t, t + 256, ..., and
+// the four wave butterflies are added in wave order.
+__device__ __forceinline__ uint32_t sumsq_parts(uint32_t d) { return (d + 4095) / 4096; }
+
+// A 256-thread workgroup takes the slices wave, wave + 4, wave + 8, wave + 12
+// in each wave.  The k-th of the NV float4s a thread holds is part k % P of
+// slice wave + 4 (k / P): f[k] is its float4 index in the vector, sl[k] =
+// k / P (counted, not divided).  Every float4 of a vector of d <= NV * 1024
+// elements is held by some thread.
+template <int NV>
+__device__ __forceinline__ void sumsq_slots(uint32_t P, uint32_t (&f)[NV], uint32_t (&sl)[NV])
 {
-    const uint32_t t = threadIdx.x;
-    float acc = 0.0f;
-    if (d % 4 == 0) {
-        const float4 *p = (const float4 *)x;
-        for (uint32_t f = t; f < d / 4; f += 256) {
-            const float4 v = p[f];
-            acc = __builtin_fmaf(v.x, v.x, acc);
-            acc = __builtin_fmaf(v.y, v.y, acc);
-            acc = __builtin_fmaf(v.z, v.z, acc);
-            acc = __builtin_fmaf(v.w, v.w, acc);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t i = 0, j = 0;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        sl[k] = i;
+        f[k] = 64 * P * (wave + 4 * i) + lane + 64 * j;
+        if (++j == P) {
+            j = 0;
+            ++i;
         }
-    } else {
-        for (uint32_t i = t; i < d; i += 256) acc = __builtin_fmaf(x[i], x[i], acc);
     }
+}
+
+__device__ __forceinline__ float sumsq4(const float4 &v, float acc)
+{
+    acc = __builtin_fmaf(v.x, v.x, acc);
+    acc = __builtin_fmaf(v.y, v.y, acc);
+    acc = __builtin_fmaf(v.z, v.z, acc);
+    acc = __builtin_fmaf(v.w, v.w, acc);
     return acc;
 }
 
+// The total of a 256-thread workgroup's slice sums: sq[i] of wave w is the
+// (wave-summed) slice w + 4 i.  `red` is 16 floats of LDS.  Every thread
+// returns the same value.
+__device__ __forceinline__ float slices_total_256(const float (&sq)[4], float *red)
+{
+    const uint32_t wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) red[wave + 4 * i] = sq[i];
+    }
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < 16; w++) s = s + red[w];
+    __syncthreads();
+    return s;
+}
+
+// Canonical sum of squares from the float4s a thread of a 256-thread
+// workgroup holds, v[k] = float4 f[k] of the vector (sumsq_slots; those at or
+// past nf = d / 4 are not used).
+template <int NV>
+__device__ __forceinline__ float sumsq_held_256(const float4 *v, const uint32_t (&f)[NV], const uint32_t (&sl)[NV],
+                                                uint32_t nf, float *red)
+{
+    float sq[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; k++)
+            if (sl[k] == (uint32_t)i && f[k] < nf) acc = sumsq4(v[k], acc);
+        sq[i] = wave_sum(acc);
+    }
+    return slices_total_256(sq, red);
+}
+
+// Canonical sum of squares of x[0..d) by a 256-thread workgroup, read from
+// memory.  `red` is 16 floats of LDS.
 __device__ __forceinline__ float block_sumsq_256(const float *__restrict__ x, uint32_t d, float *red)
 {
-    return block_sum_256(thread_sumsq(x, d), red);
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (d % 4 != 0) {
+        float acc = 0.0f;
+        for (uint32_t i = t; i < d; i += 256) acc = __builtin_fmaf(x[i], x[i], acc);
+        return block_sum_256(acc, red);
+    }
+    const uint32_t nf = d / 4, P = sumsq_parts(d);
+    const float4 *p = (const float4 *)x;
+    float sq[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float acc = 0.0f;
+        const uint32_t f0 = 64 * P * (wave + 4 * i) + lane;
+        for (uint32_t j = 0; j < P; j++)
+            if (f0 + 64 * j < nf) acc = sumsq4(p[f0 + 64 * j], acc);
+        sq[i] = wave_sum(acc);
+    }
+    return slices_total_256(sq, red);
 }
 
 // 1 / sqrt(sumsq / d + eps) with correctly rounded divide and square root,

@@ -262,19 +262,6 @@ __device__ __forceinline__ void src_load(const GemvArgs &a, uint32_t m, uint32_t
     }
 }
 
-// sum of squares of the 16 raw values in order (the canonical RMSNorm order)
-__device__ __forceinline__ float src_sumsq(const Src16 &s, float acc)
-{
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        acc = __builtin_fmaf(s.a[i].x, s.a[i].x, acc);
-        acc = __builtin_fmaf(s.a[i].y, s.a[i].y, acc);
-        acc = __builtin_fmaf(s.a[i].z, s.a[i].z, acc);
-        acc = __builtin_fmaf(s.a[i].w, s.a[i].w, acc);
-    }
-    return acc;
-}
-
 template <int ACT>
 __device__ __forceinline__ void src_xform(const Src16 &s, float inv, float4 *v)
 {
@@ -312,7 +299,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a, uint32_t KC)
     extern __shared__ float smem[];
     float *xs = smem;                    // MT * KC activations
     float *gs = xs + MT * KC;            // MT * KC/16 partial sums
-    float *red = gs + MT * (KC / 16);    // 4 floats for the RMSNorm reduction
+    float *red = gs + MT * (KC / 16);    // 16 floats for the RMSNorm reduction
 
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     // 1-D grid, token tile fastest: the workgroups that read the same weight
@@ -407,13 +394,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a, uint32_t KC)
 // ---------------------------------------------------------------------------
 // Batch-1 kernel for rows of at most IT wave iterations (every decode-path
 // GEMV).  Order of work per workgroup:
-//   1. thread t fetches the raw inputs of activation float4s t, t + 256, ...
-//      (coalesced; L2 hits after the first workgroup of an XCD);
+//   1. each thread fetches the raw inputs of its activation float4s of the
+//      canonical sum-of-squares split (runs of 64 float4s per wave:
+//      coalesced; L2 hits after the first workgroup of an XCD);
 //   2. every wave issues ALL of its weight loads, so HBM latency overlaps the
 //      staging (vmcnt retires in order, which is why the activation loads go
 //      first);
 //   3. the fused RMSNorm reduces the sum of squares of those registers in the
-//      canonical float4 order of thread_sumsq; activations are transformed,
+//      canonical order; activations are transformed,
 //      written to LDS, and their 16-element sums formed with two lane
 //      shuffles ((f0 + f1) + (f2 + f3) over the four float4s of a group);
 //   4. per iteration each lane reads its spans from LDS once and runs the dot
@@ -434,7 +422,7 @@ __global__ __launch_bounds__(256) void gemv_pf_kernel(GemvArgs a)
     const uint32_t K = a.K;
     float4 *xs4 = (float4 *)smem;                               // IT * 64 * STR float4
     float *gs = smem + 4 * IT * 64 * STR;                       // IT * 16 * BPI
-    float *red = gs + IT * 16 * BPI;                            // 4
+    float *red = gs + IT * 16 * BPI;                            // 16
 
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t wg_row0 = blockIdx.x * (4 * R);
@@ -446,11 +434,15 @@ __global__ __launch_bounds__(256) void gemv_pf_kernel(GemvArgs a)
     const Dec dec(lane);
     const uint32_t slot = Dec::slot(lane);
 
-    // 1. activation inputs (NF is a multiple of 64, so each guard is wave-uniform)
+    // 1. activation inputs, the thread's float4s of the canonical
+    // sum-of-squares split (NF is a multiple of 64, so each guard is
+    // wave-uniform)
+    uint32_t fo[JF], sl[JF];
+    sumsq_slots<JF>(sumsq_parts(K), fo, sl);
     float4 xa[JF], xb[JF];
 #pragma unroll
     for (int j = 0; j < JF; j++)
-        if (t + 256u * j < NF) src_load4<ACT>(a, 4 * (t + 256u * j), xa[j], xb[j]);
+        if (fo[j] < NF) src_load4<ACT>(a, 4 * fo[j], xa[j], xb[j]);
 
     // 2. all weight loads of this wave
     typename Dec::Raw raw[IT][R];
@@ -465,21 +457,10 @@ __global__ __launch_bounds__(256) void gemv_pf_kernel(GemvArgs a)
 
     // 3. RMSNorm scale, transform, stage
     float inv = 1.0f;
-    if constexpr (ACT == ACT_RMSNORM) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < JF; j++)
-            if (t + 256u * j < NF) {
-                acc = __builtin_fmaf(xa[j].x, xa[j].x, acc);
-                acc = __builtin_fmaf(xa[j].y, xa[j].y, acc);
-                acc = __builtin_fmaf(xa[j].z, xa[j].z, acc);
-                acc = __builtin_fmaf(xa[j].w, xa[j].w, acc);
-            }
-        inv = rms_inv(block_sum_256(acc, red), K, a.eps);
-    }
+    if constexpr (ACT == ACT_RMSNORM) inv = rms_inv(sumsq_held_256<JF>(xa, fo, sl, NF, red), K, a.eps);
 #pragma unroll
     for (int j = 0; j < JF; j++) {
-        const uint32_t f = t + 256u * j;
+        const uint32_t f = fo[j];
         if (f < NF) {
             const float4 v = xform4<ACT>(xa[j], xb[j], inv);
             const uint32_t b = f / 64, q = f % 64, I = b / BPI, s = b % BPI;
@@ -546,7 +527,7 @@ static hipError_t go(const GemvArgs &a, hipStream_t s)
 {
     uint32_t kcmax = (MT == 1 ? 8192u : MT == 2 ? 4096u : 2048u);
     uint32_t KC = a.K < kcmax ? a.K : kcmax;
-    size_t lds = ((size_t)MT * KC + (size_t)MT * (KC / 16) + 4) * sizeof(float);
+    size_t lds = ((size_t)MT * KC + (size_t)MT * (KC / 16) + 16) * sizeof(float);
     dim3 grid(((a.M + MT - 1) / MT) * ((a.N + 4 * R - 1) / (4 * R)));
     hipLaunchKernelGGL((gemv_kernel<Dec, R, MT, ACT>), grid, dim3(256), lds, s, a, KC);
     return hipGetLastError();
@@ -555,7 +536,7 @@ static hipError_t go(const GemvArgs &a, hipStream_t s)
 template <class Dec, int R, int IT, int ACT>
 static hipError_t go_pf(const GemvArgs &a, hipStream_t s)
 {
-    const size_t lds = ((size_t)4 * IT * 64 * Dec::STR + (size_t)IT * 16 * Dec::BPI + 4) * sizeof(float);
+    const size_t lds = ((size_t)4 * IT * 64 * Dec::STR + (size_t)IT * 16 * Dec::BPI + 16) * sizeof(float);
     const dim3 grid((a.N + 4 * R - 1) / (4 * R));
     hipLaunchKernelGGL((gemv_pf_kernel<Dec, R, IT, ACT>), grid, dim3(256), lds, s, a);
     return hipGetLastError();
@@ -579,7 +560,7 @@ static hipError_t go_rows(const GemvArgs &a, hipStream_t s)
 {
     const uint32_t it = (a.K / 256 + Dec::BPI - 1) / Dec::BPI;
     const uint32_t it_inst = it <= 1 ? 1 : it <= 2 ? 2 : 4;
-    const size_t lds = ((size_t)4 * it_inst * 64 * Dec::STR + (size_t)it_inst * 16 * Dec::BPI + 4) * sizeof(float);
+    const size_t lds = ((size_t)4 * it_inst * 64 * Dec::STR + (size_t)it_inst * 16 * Dec::BPI + 16) * sizeof(float);
     const bool f32 = Dec::BS == 1024;
     if (it <= 4 && lds <= 65536 && !(f32 && a.N > 16384)) {
         if (a.N >= 12288 && !f32) return go_pf_it<Dec, 4, ACT>(a, s);

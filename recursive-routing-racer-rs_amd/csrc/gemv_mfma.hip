@@ -11,8 +11,8 @@ __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntil
     mq_body<Q, BPW, ACT, MULTI, TR, PAIR>(a, ntiles, tr);
 }
 
-// Super-blocks per wave and waves per workgroup (at least 4, the canonical
-// RMSNorm order needs them; waves past the last super-block only encode).
+// Super-blocks per wave and waves per workgroup (at least 4; waves past the
+// last super-block only encode).
 // Up to one workgroup per CU, each taking its tiles as far as its row
 // partials fit in LDS.  Tiles split evenly over the CUs (a wave issues only
 // the load slots its tile height needs, so short tiles cost no empty loads).
@@ -22,7 +22,7 @@ static void mq_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds,
     using G = MwGeom<Q, BPW>;
     const uint32_t B = a.K / 256;
     W = max(4u, (B + BPW - 1) / BPW);
-    const size_t fixed = W * G::BYTES + 16;
+    const size_t fixed = W * G::BYTES + 64;
     const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64));
     uint32_t per;
     mq_tiles(a.N, device_cus(), per_max, 1u, tr, ntiles, per);
@@ -49,7 +49,7 @@ static hipError_t go_mq_pair(const GemvArgs &a, hipStream_t s)
     using G = MwGeom<Q, BPW>;
     const uint32_t B = a.K / 256;
     const uint32_t W = max(4u, (B + BPW - 1) / BPW);
-    const size_t fixed = W * G::BYTES + 16;
+    const size_t fixed = W * G::BYTES + 64;
     const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64)) / 2;   // pairs: two tiles each
     if (per_max == 0) return hipErrorInvalidValue;
     const uint32_t npairs = (a.N + 15) / 16, cus = device_cus();
@@ -64,7 +64,7 @@ static hipError_t go_mq_pair(const GemvArgs &a, hipStream_t s)
 template <class Q, int BPW, int ACT>
 static hipError_t go_mq(const GemvArgs &a, hipStream_t s)
 {
-    static_assert(16 * MwGeom<Q, BPW>::BYTES + 16 + 16 * 64 <= 160 * 1024, "LDS per workgroup");
+    static_assert(16 * MwGeom<Q, BPW>::BYTES + 64 + 16 * 64 <= 160 * 1024, "LDS per workgroup");
     uint32_t W, grid, tr, ntiles;
     size_t lds;
     mq_plan<Q, BPW>(a, W, grid, lds, tr, ntiles);

@@ -249,32 +249,6 @@ __device__ __forceinline__ u32x4 q6_realign(const u32x4 &v, uint32_t sh)
                  __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(nx, v.w, sh)};
 }
 
-// Sum of squares of x[0..K) in the order of the standalone RMSNorm kernel
-// (thread t < 256 owns float4s t, t + 256, ...; wave butterfly; waves 0..3
-// added in order), so the fused scale is bitwise that kernel's.  cx[j] holds
-// float4 t + 256 j (loaded earlier, index clamped).  Needs at least 4 waves;
-// every thread must call it (one barrier).
-template <int NSQ>
-__device__ __forceinline__ float canonical_sumsq(const float4 *cx, uint32_t K, float *red)
-{
-    const uint32_t t = threadIdx.x;
-    float acc = 0.0f;
-    if (t < 256) {
-#pragma unroll
-        for (int j = 0; j < NSQ; j++)
-            if (t + 256 * j < K / 4) {
-                acc = __builtin_fmaf(cx[j].x, cx[j].x, acc);
-                acc = __builtin_fmaf(cx[j].y, cx[j].y, acc);
-                acc = __builtin_fmaf(cx[j].z, cx[j].z, acc);
-                acc = __builtin_fmaf(cx[j].w, cx[j].w, acc);
-            }
-    }
-    acc = wave_sum(acc);
-    if (t < 256 && (t & 63) == 0) red[t >> 6] = acc;
-    __syncthreads();
-    return ((red[0] + red[1]) + red[2]) + red[3];
-}
-
 __device__ __forceinline__ void wave_lds_sync()
 {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -330,10 +304,10 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     const uint32_t nown = tile0 < ntiles ? (ntiles - tile0 + GR - 1) / GR : 0u;   // tiles (PAIR: pairs) of this workgroup
     const uint32_t ntl = MULTI ? (PAIR ? 2 * nown : nown) : 1u;                    // tiles of this workgroup
     uint8_t *L = (uint8_t *)smem + wave * G::BYTES;              // this wave's region
-    float *red = (float *)((uint8_t *)smem + W * G::BYTES);      // 4
-    float *part = red + 4;                                       // ntl x W x 16 per-wave row partials
+    float *red = (float *)((uint8_t *)smem + W * G::BYTES);      // 16: RMSNorm slice sums
+    float *part = red + 16;                                      // ntl x W x 16 per-wave row partials
 
-    const uint32_t row_bytes = B * Q::BS, tile_bytes = tr * row_bytes;
+    const uint32_t row_bytes = B * Q::BS;
     // every buffer has RRR_READ_SLACK readable bytes past its end: a Q6_K
     // piece's last unit runs 14 bytes past its block
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.W, a.w_bytes + RRR_READ_SLACK);
@@ -380,21 +354,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     // on the kernel's tail (a clamped row when there is none)
     const uint32_t row_first = PAIR ? 0u : min((tile0 + (t >> 4) * GR) * tr + (t & 15), a.N - 1);
     const float yres = PAIR ? 0.0f : a.y[row_first];
-    // 1. fused RMSNorm: the whole of x in the canonical order (K <= 1024 NSQ),
-    // read by the threads that sum it (t < 256); the other threads' and
-    // the past-the-end loads go out of range (no memory request)
-    constexpr int NSQ = ACT == ACT_RMSNORM ? 4 * BPW : 1;
-    float4 cx[NSQ];
-    if constexpr (ACT == ACT_RMSNORM) {
-        const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint64_t)K * 4);
-#pragma unroll
-        for (int j = 0; j < NSQ; j++) {
-            const uint32_t f = t + 256 * j;
-            const u32x4 v = bload16(rx, t < 256 && f < K / 4 ? 16 * f : MQ_OOB);
-            cx[j] = make_float4(u2f(v.x), u2f(v.y), u2f(v.z), u2f(v.w));
-        }
-    }
-    // 2. this wave's activation inputs: float4 lane + 64 j of its slice
+    // 1. this wave's activation inputs: float4 lane + 64 j of its slice
     float4 xa[BPW], xb[BPW];
 #pragma unroll
     for (int j = 0; j < BPW; j++) src_load4<ACT>(a, min(b0 * 256 + 4 * (lane + 64 * j), K - 4), xa[j], xb[j]);
@@ -405,9 +365,25 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
 #pragma unroll
     for (int j = 0; j < BPW; j++) issue(j, 0);
 
-    // 3. activation staging of this wave's slice
+    // 2. fused RMSNorm: the wave's slice of x is slice `wave` of the canonical
+    // sum-of-squares split (BPW float4s per lane is its P = ceil(K / 4096)
+    // for K <= 8192); the slice sums are added in wave order (waves without
+    // a super-block add +0)
     float inv = 1.0f;
-    if constexpr (ACT == ACT_RMSNORM) inv = rms_inv(canonical_sumsq<NSQ>(cx, K, red), K, a.eps);
+    if constexpr (ACT == ACT_RMSNORM) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < BPW; j++)
+            if (j < (int)nb) sq = sumsq4(xa[j], sq);
+        sq = wave_sum(sq);
+        if (lane == 0) red[wave] = sq;
+        __syncthreads();
+        float s = red[0];
+        for (uint32_t w = 1; w < W; w++) s = s + red[w];
+        inv = rms_inv(s, K, a.eps);
+    }
+
+    // 3. activation staging of this wave's slice
 #pragma unroll
     for (int j = 0; j < BPW; j++) {
         const uint32_t f = lane + 64 * j;                        // local float4 index

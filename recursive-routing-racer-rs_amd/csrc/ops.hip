@@ -107,33 +107,25 @@ template <typename TO>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ g,
                                                       TO *__restrict__ y, uint32_t d, float eps)
 {
-    __shared__ float red[4];
+    __shared__ float red[16];
     const float *xr = x + (uint64_t)blockIdx.x * d;
     TO *yr = y + (uint64_t)blockIdx.x * d;
     const uint32_t t = threadIdx.x;
     if (d % 4 == 0 && d <= 8 * 4 * 256) {
-        // the row stays in registers (one pass over x); thread t owns the
-        // float4s t, t + 256, ..., the canonical order of thread_sumsq
+        // the row stays in registers (one pass over x); the thread holds its
+        // float4s of the canonical sum-of-squares split
+        const uint32_t nf = d / 4;
+        uint32_t f[8], sl[8];
+        sumsq_slots<8>(sumsq_parts(d), f, sl);
         float4 v[8];
-        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = f[j] < nf ? ((const float4 *)xr)[f[j]] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float inv = rms_inv(sumsq_held_256<8>(v, f, sl, nf, red), d, eps);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const uint32_t f = t + 256u * j;
-            if (f < d / 4) {
-                v[j] = ((const float4 *)xr)[f];
-                acc = __builtin_fmaf(v[j].x, v[j].x, acc);
-                acc = __builtin_fmaf(v[j].y, v[j].y, acc);
-                acc = __builtin_fmaf(v[j].z, v[j].z, acc);
-                acc = __builtin_fmaf(v[j].w, v[j].w, acc);
-            }
-        }
-        const float inv = rms_inv(block_sum_256(acc, red), d, eps);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t f = t + 256u * j;
-            if (f < d / 4) {
-                const float4 w = ((const float4 *)g)[f];
-                store4(yr, f, make_float4(__fmul_rn(__fmul_rn(w.x, v[j].x), inv), __fmul_rn(__fmul_rn(w.y, v[j].y), inv),
+            if (f[j] < nf) {
+                const float4 w = ((const float4 *)g)[f[j]];
+                store4(yr, f[j], make_float4(__fmul_rn(__fmul_rn(w.x, v[j].x), inv), __fmul_rn(__fmul_rn(w.y, v[j].y), inv),
                                           __fmul_rn(__fmul_rn(w.z, v[j].z), inv), __fmul_rn(__fmul_rn(w.w, v[j].w), inv)));
             }
         }
@@ -295,7 +287,7 @@ __global__ __launch_bounds__(256) void logits_chunked_kernel(const float *__rest
     extern __shared__ float sm[];
     float *xs = sm;             // K
     float *part = xs + K;       // 4 waves x 64 entries
-    float *red = part + 256;    // 4
+    float *red = part + 256;    // 16
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     float inv = 1.0f;
     if (gamma) inv = rms_inv(block_sumsq_256(x, K, red), K, eps);
@@ -359,7 +351,7 @@ __global__ __launch_bounds__(256) void logits_chunked_kernel(const float *__rest
 hipError_t launch_logits_chunked(const float *x, const float *gamma, float eps, const float *E, float *y,
                                  uint32_t K, uint32_t V, uint32_t chunk, hipStream_t s)
 {
-    const size_t lds = ((size_t)K + 256 + 4) * sizeof(float);
+    const size_t lds = ((size_t)K + 256 + 16) * sizeof(float);
     // 64-entry groups of each chunk (a partial last chunk may leave a
     // partial group)
     uint32_t nwg = 0;
