@@ -93,7 +93,8 @@ struct rrr_ctx {
     void *scratch;      // argmax partial candidates
     void *att_scratch;  // attention: per-KV-head counters (zero between calls) and split partials
     void *gemm_ws;      // GEMM_WS_BYTES: prefill GEMM partials of split K; the skinny GEMV's encoded
-                        // activations (stream order keeps the users apart)
+                        // activations; the split-K logits' partials (stream order keeps the users apart)
+    void *logits_cnt;   // split-K logits: per-slab counters (zero between calls)
     std::unordered_set<rrr_buf *> bufs;
     std::unordered_set<rrr_graph *> graphs;
     std::unordered_set<rrr_sweep *> sweeps;
@@ -202,7 +203,7 @@ int rrr_init(int device, rrr_ctx **out)
     ctx->async = ctx->capturing = ctx->timer_started = false;
     ctx->stream = nullptr;
     ctx->ev0 = ctx->ev1 = nullptr;
-    ctx->scratch = ctx->att_scratch = ctx->gemm_ws = nullptr;
+    ctx->scratch = ctx->att_scratch = ctx->gemm_ws = ctx->logits_cnt = nullptr;
     if (!ctx->nodevice) {
         int n = rrr_device_count();
         if (device >= n) {
@@ -217,10 +218,13 @@ int rrr_init(int device, rrr_ctx **out)
         if (e == hipSuccess) e = hipMalloc(&ctx->att_scratch, attention_scratch_bytes());
         if (e == hipSuccess) e = hipMemset(ctx->att_scratch, 0, attention_scratch_bytes());
         if (e == hipSuccess) e = hipMalloc(&ctx->gemm_ws, GEMM_WS_BYTES);
+        if (e == hipSuccess) e = hipMalloc(&ctx->logits_cnt, logits_counter_bytes());
+        if (e == hipSuccess) e = hipMemset(ctx->logits_cnt, 0, logits_counter_bytes());
         if (e == hipSuccess) e = hipDeviceSynchronize();
         void *static_scratch = nullptr;   // rrr_attention_noalloc's array on this device
         if (e == hipSuccess && attention_static_setup(device, &static_scratch) != RRR_OK) e = hipErrorInvalidSymbol;
         if (e != hipSuccess) {
+            if (ctx->logits_cnt) (void)hipFree(ctx->logits_cnt);
             if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
             if (ctx->att_scratch) (void)hipFree(ctx->att_scratch);
             if (ctx->scratch) (void)hipFree(ctx->scratch);
@@ -267,6 +271,7 @@ int rrr_destroy(rrr_ctx *ctx)
         (void)hipFree(ctx->scratch);
         (void)hipFree(ctx->att_scratch);
         (void)hipFree(ctx->gemm_ws);
+        (void)hipFree(ctx->logits_cnt);
         (void)hipEventDestroy(ctx->ev0);
         (void)hipEventDestroy(ctx->ev1);
         (void)hipStreamDestroy(ctx->stream);
@@ -688,8 +693,14 @@ static int logits_common(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, f
     const uint64_t cn = chunk < V ? chunk : V;
     if (cn * K * 4 > 0xFFFFFFFFull) return fail(RRR_ERR_UNSUPPORTED, "%s: one chunk exceeds 4 GiB", what);
     TRY(device_ready(ctx));
-    return finish(ctx, launch_logits_chunked((const float *)x->ptr, gamma ? (const float *)gamma->ptr : nullptr, eps,
-                                             (const float *)E->ptr, (float *)y->ptr, K, V, (uint32_t)cn, ctx->stream),
+    const float *g = gamma ? (const float *)gamma->ptr : nullptr;
+    if (logits_split_supported(K, V, (uint32_t)cn, GEMM_WS_BYTES))
+        return finish(ctx, launch_logits_split((const float *)x->ptr, g, eps, (const float *)E->ptr, (float *)y->ptr, K, V,
+                                               (uint32_t)cn, (float *)ctx->gemm_ws, (uint32_t *)ctx->logits_cnt,
+                                               ctx->stream),
+                      what);
+    return finish(ctx, launch_logits_chunked((const float *)x->ptr, g, eps, (const float *)E->ptr, (float *)y->ptr, K, V,
+                                             (uint32_t)cn, ctx->stream),
                   what);
 }
 

@@ -360,6 +360,129 @@ hipError_t launch_logits_chunked(const float *x, const float *gamma, float eps, 
     return hipGetLastError();
 }
 
+// Split-K form of the transposed-chunk logits.  Workgroup (slab, h) takes
+// the 256 vocab entries of one slab of a chunk and rows [h*K/NS, (h+1)*K/NS)
+// of the chunk's [d][n] matrix, i.e. row pieces of 1 KB: lane l of a wave
+// reads entries 4l .. 4l+3 of one row per load, so each load instruction is
+// 1 KB of whole cache lines, and the 8 d-ranges make 6,256 workgroups of
+// 384 KB for the 200,064 x 3072 logits (balanced over the CUs).  Wave w
+// takes the rows w, w+4, ... of the range (U loads in flight), the waves'
+// sums are added in wave order, and the NS partial sums of an entry are
+// written through to the coherent level; the last workgroup of the slab to
+// arrive (an agent-scope counter, reset by that workgroup for the next call)
+// adds them in order h = 0, 1, ..., NS-1 and writes the logits.
+constexpr uint32_t LOGITS_SPLITS = 8, LOGITS_SLAB = 256, LOGITS_COUNTER_STRIDE = 64, LOGITS_U = 8;
+// scalar+vector offset past every chunk byte (a chunk is below 2 GiB on this
+// path): such loads return zeros and move no data
+constexpr uint32_t MQ_OOB_LOGITS = 0x80000000u;
+
+template <int U>
+__global__ __launch_bounds__(256) void logits_split_kernel(const float *__restrict__ x, const float *__restrict__ gamma,
+                                                           float eps, const float *__restrict__ E, float *__restrict__ y,
+                                                           uint32_t K, uint32_t V, uint32_t chunk, float *part,
+                                                           uint32_t *counters)
+{
+    constexpr uint32_t NS = LOGITS_SPLITS;
+    extern __shared__ float sm[];
+    const uint32_t Dr = K / NS;
+    float *xs = sm;                 // Dr
+    float *wsum = xs + Dr;          // 4 waves x 256 entries
+    float *red = wsum + 4 * 256;    // 16
+    __shared__ uint32_t last;
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t sb = blockIdx.x / NS, h = blockIdx.x % NS;
+    const uint32_t spc = chunk / LOGITS_SLAB;                 // slabs per full chunk
+    const uint32_t c = sb / spc, j = sb - c * spc;
+    const uint32_t cstart = c * chunk;
+    const uint32_t n = (V - cstart) < chunk ? (V - cstart) : chunk;
+    const uint32_t d0 = h * Dr;
+
+    const uint32_t vin = j * LOGITS_SLAB + 4 * lane;          // entry inside the chunk
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(E + (uint64_t)cstart * K, (uint64_t)n * K * 4);
+    const uint32_t voff = vin < n ? 4 * vin : MQ_OOB_LOGITS;
+    const uint32_t rstep = 4 * n * 4;                          // 4 rows
+    uint32_t soff = (d0 + wave) * n * 4;
+    const uint32_t nr = Dr / 4;                                // rows of this wave (a multiple of U)
+    // the first U rows are requested before the RMSNorm prologue, which then
+    // runs while they are in flight
+    u32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) w[u] = bload16_nt_so(rs, voff, soff + u * rstep);
+    soff += U * rstep;
+
+    float inv = 1.0f;
+    if (gamma) inv = rms_inv(block_sumsq_256(x, K, red), K, eps);
+    for (uint32_t i = t; i < Dr; i += 256) xs[i] = gamma ? __fmul_rn(__fmul_rn(gamma[d0 + i], x[d0 + i]), inv) : x[d0 + i];
+    __syncthreads();
+
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    for (uint32_t r = 0; r < nr; r += U) {
+        u32x4 wn[U];
+        const bool more = r + U < nr;
+#pragma unroll
+        for (int u = 0; u < U; u++) wn[u] = bload16_nt_so(rs, more ? voff : MQ_OOB_LOGITS, soff + u * rstep);
+        soff += U * rstep;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float xv = xs[wave + 4 * (r + u)];
+            a0 = fmaf(xv, u2f(w[u].x), a0);
+            a1 = fmaf(xv, u2f(w[u].y), a1);
+            a2 = fmaf(xv, u2f(w[u].z), a2);
+            a3 = fmaf(xv, u2f(w[u].w), a3);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) w[u] = wn[u];
+    }
+    ((float4 *)wsum)[wave * 64 + lane] = make_float4(a0, a1, a2, a3);
+    __syncthreads();
+    const float p = ((wsum[t] + wsum[256 + t]) + wsum[512 + t]) + wsum[768 + t];
+    const uint32_t v = cstart + j * LOGITS_SLAB + t;          // this thread's entry
+    const bool live = j * LOGITS_SLAB + t < n;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, (uint64_t)NS * V * 4);
+    if (live) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(p), rp, 4 * (h * V + v), 0, RRR_CPOL_SC1);
+    // publish: this workgroup's partials are at the coherent level, then count
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == 0)
+        last = __hip_atomic_fetch_add(counters + sb * LOGITS_COUNTER_STRIDE, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == NS - 1;
+    __syncthreads();
+    if (!last) return;
+    if (live) {
+        float q[NS];
+#pragma unroll
+        for (uint32_t k = 0; k < NS; k++)
+            q[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, 4 * (k * V + v), 0, RRR_CPOL_SC1));
+        float r = q[0];
+#pragma unroll
+        for (uint32_t k = 1; k < NS; k++) r = r + q[k];
+        y[v] = r;
+    }
+    if (t == 0) __hip_atomic_store(counters + sb * LOGITS_COUNTER_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+uint64_t logits_counter_bytes() { return (uint64_t)LOGITS_MAX_SLABS * LOGITS_COUNTER_STRIDE * 4; }
+
+bool logits_split_supported(uint32_t K, uint32_t V, uint32_t chunk, uint64_t ws_bytes)
+{
+    if (K % (4 * LOGITS_SPLITS * LOGITS_U) || K > 12288 || chunk % LOGITS_SLAB) return false;
+    if ((uint64_t)(chunk < V ? chunk : V) * K * 4 >= MQ_OOB_LOGITS) return false;
+    uint64_t slabs = 0;
+    for (uint64_t c0 = 0; c0 < V; c0 += chunk) slabs += ((V - c0 < chunk ? V - c0 : chunk) + LOGITS_SLAB - 1) / LOGITS_SLAB;
+    return slabs <= LOGITS_MAX_SLABS && (uint64_t)LOGITS_SPLITS * V * 4 <= ws_bytes;
+}
+
+hipError_t launch_logits_split(const float *x, const float *gamma, float eps, const float *E, float *y, uint32_t K,
+                               uint32_t V, uint32_t chunk, float *part, uint32_t *counters, hipStream_t s)
+{
+    uint32_t slabs = 0;
+    for (uint32_t c0 = 0; c0 < V; c0 += chunk) slabs += ((V - c0 < chunk ? V - c0 : chunk) + LOGITS_SLAB - 1) / LOGITS_SLAB;
+    const size_t lds = ((size_t)K / LOGITS_SPLITS + 4 * 256 + 16) * sizeof(float);
+    hipLaunchKernelGGL(logits_split_kernel<LOGITS_U>, dim3(slabs * LOGITS_SPLITS), dim3(256), lds, s, x, gamma, eps, E, y, K, V,
+                       chunk, part, counters);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Argmax with the semantics of the sequential loop at phi4.rs:1172-1183:
 // start from (value -inf, index 0), replace only on strictly greater, so the

@@ -301,7 +301,7 @@ def test_gemv_residual_kinds(ctx):
 
 # ---- logits and argmax -------------------------------------------------------------
 
-@pytest.mark.parametrize("V,chunk", [(20000, 8192), (8192, 8192), (3456, 8192), (1000, 256), (700, 700)])
+@pytest.mark.parametrize("V,chunk", [(20000, 8192), (8192, 8192), (3456, 8192), (1000, 256), (700, 700), (8195, 4096)])
 def test_logits_parity_both_layouts(ctx, V, chunk):
     K = 3072
     E = synth.normal_f32(11, V, V * K, 0.0, 0.02)
