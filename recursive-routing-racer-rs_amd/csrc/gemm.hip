@@ -460,9 +460,37 @@ static hipError_t go_gemm_q(const uint16_t *X, const float *rscale, const uint8_
     }
 }
 
+// bf16 -> f16 of the whole activation matrix once, 8 elements a thread, with
+// the conversion the staging waves apply (pk_f16: exact for |x| in f16's
+// normal range), so the f16-activation GEMM on the result is bitwise the
+// bf16 GEMM while the N/BN column tiles no longer convert X again each.
+__global__ __launch_bounds__(256) void bf16_to_f16_kernel(const u32x4 *__restrict__ X, u32x4 *__restrict__ Xh,
+                                                          uint64_t n8)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    const u32x4 v = X[i];
+    u32x4 h;
+#pragma unroll
+    for (int c = 0; c < 4; c++) h[c] = pk_f16(__uint_as_float(v[c] << 16), __uint_as_float(v[c] & 0xFFFF0000u));
+    Xh[i] = h;
+}
+
 hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K, uint32_t N,
                             uint32_t M, float *ws, size_t ws_bytes, hipStream_t s)
 {
+    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2)) return hipErrorNotSupported;
+    // the f16 copy of X at the start of the workspace (256-byte aligned
+    // remainder for the split-K partials), when it fits
+    const uint64_t xh_bytes = ((uint64_t)M * K * 2 + 255) & ~255ull;
+    if (ws && (uint64_t)M * K % 8 == 0 && xh_bytes + (ws_bytes / 2) <= ws_bytes && xh_bytes <= ws_bytes / 2) {
+        const uint64_t n8 = (uint64_t)M * K / 8;
+        uint16_t *Xh = (uint16_t *)ws;
+        hipLaunchKernelGGL(bf16_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const u32x4 *)X,
+                           (u32x4 *)Xh, n8);
+        return go_gemm_q<true, false>(Xh, nullptr, W, type, Y, K, N, M, (float *)((uint8_t *)ws + xh_bytes),
+                                      ws_bytes - xh_bytes, s);
+    }
     return go_gemm_q<false, false>(X, nullptr, W, type, Y, K, N, M, ws, ws_bytes, s);
 }
 
