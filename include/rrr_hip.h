@@ -197,6 +197,21 @@ int rrr_rope_kv_store(rrr_ctx *ctx, rrr_buf *qkv, const rrr_buf *rope_factors, u
                       uint32_t n_kv_heads, uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim,
                       uint32_t kv_stride, float theta, float attn_factor);
 
+/* The layer's first three dispatches, rmsnorm -> matmul (QKV) ->
+ * rope_kv_store (phi4.rs:1006-1017), as one launch: rrr_gemv_rmsnorm of x
+ * (K floats, gamma, eps) against W (type, K x N, N = q_dim + 2 * kv_stride)
+ * into qkv, with the rope_kv_store of that row at position pos in the GEMV's
+ * epilogue (same arguments and checks as rrr_rope_kv_store).  qkv, k_cache
+ * and v_cache end bit for bit as after rrr_gemv_rmsnorm followed by
+ * rrr_rope_kv_store; shapes the fused epilogue does not take run those two
+ * launches. */
+int rrr_gemv_rmsnorm_rope_kv(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps,
+                             const rrr_buf *W, uint32_t type, rrr_buf *qkv, uint32_t K,
+                             const rrr_buf *rope_factors, uint32_t n_factors, rrr_buf *k_cache,
+                             rrr_buf *v_cache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads,
+                             uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride,
+                             float theta, float attn_factor);
+
 /* The attention pipeline (phi4.rs:1018, :1304-1312; push [seq_len,
  * n_kv_heads, heads_per_kv, head_dim], one workgroup per query head in the
  * reference): for query head h (h < n_kv_heads * heads_per_kv) and KV head

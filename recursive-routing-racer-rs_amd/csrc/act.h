@@ -1,5 +1,7 @@
 // act.h -- activation sources shared by the GEMV kernels: how a GEMV builds
-// its activation vector (plain, RMS-normalised, silu-gated, GQA-gathered).
+// its activation vector (plain, RMS-normalised, silu-gated, GQA-gathered),
+// and the RoPE + f16 KV-cache store shared by rope_kv_store_kernel and the
+// QKV GEMV's fused epilogue.
 #pragma once
 
 #include "device_common.h"
@@ -20,6 +22,47 @@ __device__ __forceinline__ void src_load4(const GemvArgs &a, uint32_t k, float4 
     }
     if constexpr (ACT == ACT_RMSNORM) xb = *(const float4 *)(a.gamma + k);
     if constexpr (ACT == ACT_SILU) xb = *(const float4 *)(a.x + a.K + k);
+}
+
+__device__ __forceinline__ uint32_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+
+// One rotation of apply_rope_cfg (phi4.rs:238-256) in f32: pair j of a head
+// at position pos.
+__device__ __forceinline__ void rope_pair(float &x0, float &x1, uint32_t j, uint32_t pos, const RopeArgs &r)
+{
+    const float base_freq = 1.0f / powf(r.theta, 2.0f * (float)j / (float)r.rope_dim);
+    const float factor = j < r.n_factors ? r.factors[j] : 1.0f;
+    const float freq = base_freq / factor;
+    const float angle = (float)pos * freq;
+    float sin_t, cos_t;
+    sincosf(angle, &sin_t, &cos_t);
+    const float cs = cos_t * r.attn_factor, ss = sin_t * r.attn_factor;
+    const float a = x0, b = x1;
+    x0 = a * cs - b * ss;
+    x1 = a * ss + b * cs;
+}
+
+// rope_kv_store (rope_kv_store_kernel, attn.hip) of the qkv row pair (row,
+// row + 1), row even, as the GEMV stores it: Q and K pairs in their heads'
+// first rope_dim dims rotated, every value stored to y, the K and V pairs
+// also as f16 into cache row pos.
+__device__ __forceinline__ void rope_store_pair(const GemvArgs &a, uint32_t row, float v0, float v1)
+{
+    const RopeArgs &r = a.rope;
+    if (row < r.q_dim) {
+        if (row < r.n_heads * r.head_dim && row % r.head_dim < r.rope_dim)
+            rope_pair(v0, v1, (row % r.head_dim) / 2, r.pos, r);
+    } else if (row < r.q_dim + r.kv_stride) {
+        const uint32_t e = row - r.q_dim;
+        const uint32_t d = r.rope_dim ? e % r.head_dim : 0u;
+        if (d < r.rope_dim) rope_pair(v0, v1, d / 2, r.pos, r);
+        a.kc[((size_t)r.pos * r.kv_stride + e) / 2] = f16_bits(v0) | (f16_bits(v1) << 16);
+    } else {
+        const uint32_t e = row - r.q_dim - r.kv_stride;
+        a.vc[((size_t)r.pos * r.kv_stride + e) / 2] = f16_bits(v0) | (f16_bits(v1) << 16);
+    }
+    a.y[row] = v0;
+    a.y[row + 1] = v1;
 }
 
 template <int ACT>

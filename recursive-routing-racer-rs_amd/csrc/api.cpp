@@ -737,10 +737,11 @@ int rrr_argmax_f32(rrr_ctx *ctx, const rrr_buf *logits, uint32_t V, rrr_buf *out
 
 // rows consecutive tokens at positions pos .. pos + rows - 1, their qkv rows
 // back to back
-static int rope_common(rrr_ctx *ctx, rrr_buf *qkv, uint32_t rows, const rrr_buf *rope_factors, uint32_t n_factors,
-                       rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads,
-                       uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride, float theta,
-                       float attn_factor, const char *what)
+// The checks of the rope_kv_store pipeline; fills its RopeArgs.
+static int rope_check(rrr_ctx *ctx, rrr_buf *qkv, uint32_t rows, const rrr_buf *rope_factors, uint32_t n_factors,
+                      rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads,
+                      uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride, float theta,
+                      float attn_factor, const char *what, RopeArgs &r)
 {
     TRY(check_buf(ctx, qkv, what));
     TRY(check_buf(ctx, k_cache, what));
@@ -767,11 +768,58 @@ static int rope_common(rrr_ctx *ctx, rrr_buf *qkv, uint32_t rows, const rrr_buf 
     if (n_factors) TRY(need(rope_factors, 4ull * n_factors, what));
     if (((uintptr_t)qkv->ptr | (uintptr_t)k_cache->ptr | (uintptr_t)v_cache->ptr) & 3)
         return fail(RRR_ERR_INVALID_ARG, "%s: buffers must be 4-byte aligned", what);
+    r = RopeArgs{n_factors ? (const float *)rope_factors->ptr : nullptr, n_factors, pos, rope_dim ? n_heads : 0u,
+                 head_dim, rope_dim, q_dim, kv_stride, theta, attn_factor, (uint32_t)row};
+    return RRR_OK;
+}
+
+static int rope_common(rrr_ctx *ctx, rrr_buf *qkv, uint32_t rows, const rrr_buf *rope_factors, uint32_t n_factors,
+                       rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads,
+                       uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride, float theta,
+                       float attn_factor, const char *what)
+{
+    RopeArgs r;
+    TRY(rope_check(ctx, qkv, rows, rope_factors, n_factors, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim,
+                   rope_dim, q_dim, kv_stride, theta, attn_factor, what, r));
     TRY(device_ready(ctx));
-    RopeArgs r{n_factors ? (const float *)rope_factors->ptr : nullptr, n_factors, pos, rope_dim ? n_heads : 0u,
-               head_dim, rope_dim, q_dim, kv_stride, theta, attn_factor, (uint32_t)row};
     return finish(ctx, launch_rope_kv_store((float *)qkv->ptr, r, (uint16_t *)k_cache->ptr, (uint16_t *)v_cache->ptr,
                                             ctx->stream, rows),
+                  what);
+}
+
+int rrr_gemv_rmsnorm_rope_kv(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps, const rrr_buf *W,
+                             uint32_t type, rrr_buf *qkv, uint32_t K, const rrr_buf *rope_factors, uint32_t n_factors,
+                             rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads,
+                             uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim, uint32_t kv_stride, float theta,
+                             float attn_factor)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_gemv_rmsnorm_rope_kv";
+    if (!gamma) return fail(RRR_ERR_NULL, "%s: null gamma", what);
+    const uint64_t n64 = (uint64_t)q_dim + 2ull * kv_stride;
+    if (n64 == 0 || n64 > 0xFFFFFFFFull) return fail(RRR_ERR_BAD_SHAPE, "%s: qkv row of %llu floats", what,
+                                                     (unsigned long long)n64);
+    const uint32_t N = (uint32_t)n64;
+    RopeArgs r;
+    TRY(rope_check(ctx, qkv, 1, rope_factors, n_factors, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim,
+                   rope_dim, q_dim, kv_stride, theta, attn_factor, what, r));
+    GemvArgs a;
+    TRY(gemv_prepare(ctx, x, K, gamma, eps, ACT_RMSNORM, 0, 0, W, type, qkv, K, N, 1, 0, what, a));
+    TRY(device_ready(ctx));
+    if (N % 2 == 0 && gemv_mfma_supported(a)) {
+        a.rope_on = 1;
+        a.rope = r;
+        a.kc = (uint32_t *)k_cache->ptr;
+        a.vc = (uint32_t *)v_cache->ptr;
+        const hipError_t e = launch_gemv_mfma(a, ACT_RMSNORM, ctx->stream);
+        if (e != hipErrorNotSupported) return finish(ctx, e, what);
+        a.rope_on = 0;
+    }
+    // the two launches (a shape the fused epilogue does not take)
+    const hipError_t e = launch_gemv(a, ACT_RMSNORM, ctx->stream);
+    if (e != hipSuccess) return finish(ctx, e, what);
+    return finish(ctx, launch_rope_kv_store((float *)qkv->ptr, r, (uint16_t *)k_cache->ptr, (uint16_t *)v_cache->ptr,
+                                            ctx->stream, 1),
                   what);
 }
 

@@ -2,28 +2,9 @@
 // KV-cache store (the rope_kv_store / kv_store pipelines, phi4.rs:1016-1017,
 // :1666-1677) and decode attention over the cache (the attention pipeline,
 // phi4.rs:1018, :1304-1312).
-#include "device_common.h"
-#include "internal.h"
+#include "act.h"
 
 namespace rrr {
-
-__device__ __forceinline__ uint32_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
-
-// One rotation of apply_rope_cfg (phi4.rs:238-256) in f32: pair j of a head
-// at position pos.
-__device__ __forceinline__ void rope_pair(float &x0, float &x1, uint32_t j, uint32_t pos, const RopeArgs &r)
-{
-    const float base_freq = 1.0f / powf(r.theta, 2.0f * (float)j / (float)r.rope_dim);
-    const float factor = j < r.n_factors ? r.factors[j] : 1.0f;
-    const float freq = base_freq / factor;
-    const float angle = (float)pos * freq;
-    float sin_t, cos_t;
-    sincosf(angle, &sin_t, &cos_t);
-    const float cs = cos_t * r.attn_factor, ss = sin_t * r.attn_factor;
-    const float a = x0, b = x1;
-    x0 = a * cs - b * ss;
-    x1 = a * ss + b * cs;
-}
 
 // Token blockIdx.y (position pos + blockIdx.y, its qkv row_stride floats
 // after the previous one's).  Threads [0, nq): the Q rotation pairs (head

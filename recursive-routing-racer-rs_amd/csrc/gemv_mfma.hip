@@ -5,10 +5,10 @@
 
 namespace rrr {
 
-template <class Q, int BPW, int ACT, bool MULTI, int TR, bool PAIR = false>
+template <class Q, int BPW, int ACT, bool MULTI, int TR, bool PAIR = false, bool ROPE = false>
 __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntiles, uint32_t tr)
 {
-    mq_body<Q, BPW, ACT, MULTI, TR, PAIR>(a, ntiles, tr);
+    mq_body<Q, BPW, ACT, MULTI, TR, PAIR, ROPE>(a, ntiles, tr);
 }
 
 // Super-blocks per wave and waves per workgroup (at least 4; waves past the
@@ -79,6 +79,34 @@ static hipError_t go_mq(const GemvArgs &a, hipStream_t s)
     return hipGetLastError();
 }
 
+// The QKV GEMV with rope_kv_store in its epilogue (fused RMSNorm): plain
+// tiles of an even height, so that a RoPE pair never straddles two tiles.
+template <class Q, int BPW>
+static hipError_t go_mq_rope(const GemvArgs &a, hipStream_t s)
+{
+    uint32_t W, grid, tr, ntiles;
+    size_t lds;
+    mq_plan<Q, BPW>(a, W, grid, lds, tr, ntiles);
+    if (tr % 2) return hipErrorNotSupported;
+    const bool multi = grid != ntiles;
+    if (tr <= 10) {
+        if (multi)
+            hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT_RMSNORM, true, 10, false, true>), dim3(grid), dim3(64 * W),
+                               lds, s, a, ntiles, tr);
+        else
+            hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT_RMSNORM, false, 10, false, true>), dim3(grid), dim3(64 * W),
+                               lds, s, a, ntiles, tr);
+    } else {
+        if (multi)
+            hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT_RMSNORM, true, 16, false, true>), dim3(grid), dim3(64 * W),
+                               lds, s, a, ntiles, tr);
+        else
+            hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT_RMSNORM, false, 16, false, true>), dim3(grid), dim3(64 * W),
+                               lds, s, a, ntiles, tr);
+    }
+    return hipGetLastError();
+}
+
 template <class Q, int ACT>
 static hipError_t go_mq_k(const GemvArgs &a, hipStream_t s)
 {
@@ -105,6 +133,16 @@ bool gemv_mfma_supported(const GemvArgs &a)
 
 hipError_t launch_gemv_mfma(const GemvArgs &a, uint32_t act, hipStream_t s)
 {
+    if (a.rope_on) {
+        if (act != ACT_RMSNORM || a.pair || a.residual || a.N % 2) return hipErrorNotSupported;
+        const bool one = a.K <= 16 * 256;
+        switch (a.type) {
+        case T_Q4_K: return one ? go_mq_rope<MqQ4K, 1>(a, s) : go_mq_rope<MqQ4K, 2>(a, s);
+        case T_Q5_K: return one ? go_mq_rope<MqQ5K, 1>(a, s) : go_mq_rope<MqQ5K, 2>(a, s);
+        case T_Q6_K: return one ? go_mq_rope<MqQ6K, 1>(a, s) : go_mq_rope<MqQ6K, 2>(a, s);
+        default: return hipErrorNotSupported;
+        }
+    }
     if (a.pair) {
         if (act != ACT_RMSNORM || a.residual) return hipErrorInvalidValue;
         const bool one = a.K <= 16 * 256;

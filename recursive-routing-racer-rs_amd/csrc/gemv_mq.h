@@ -283,7 +283,10 @@ constexpr uint32_t MQ_OOB = 0x80000000u;
 // y[16P + r] = silu(gate) * up with the RRR_ACT_SILU_GATE formula, on the
 // same row sums a plain launch computes: the result is bitwise what a GEMV
 // into 2N rows followed by that activation gives.
-template <class Q, int BPW, int ACT, bool MULTI, int TR = 16, bool PAIR = false>
+// ROPE (a.rope_on, tr even): the rows go out in pairs through
+// rope_store_pair (act.h), the rope_kv_store of the token's qkv row; each
+// row's value is the sum a plain launch stores.
+template <class Q, int BPW, int ACT, bool MULTI, int TR = 16, bool PAIR = false, bool ROPE = false>
 __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr)
 {
     extern __shared__ float smem[];
@@ -512,6 +515,21 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
                     uv += pu[w * 16];
                 }
                 a.y[row] = silu_fast(gv) * uv;
+            }
+        }
+        return;
+    }
+    if constexpr (ROPE) {
+        static_assert(!PAIR, "rope epilogue on a plain row layout");
+        for (uint32_t i = t; i < ntl * 8; i += NT) {
+            const uint32_t tl = i >> 3, r = 2 * (i & 7), row = (tile0 + tl * GR) * tr + r;
+            if (r < tr && row < a.N) {
+                float v0 = part[tl * W * 16 + r], v1 = part[tl * W * 16 + r + 1];
+                for (uint32_t w = 1; w < W; w++) {
+                    v0 += part[(tl * W + w) * 16 + r];
+                    v1 += part[(tl * W + w) * 16 + r + 1];
+                }
+                rope_store_pair(a, row, v0, v1);
             }
         }
         return;

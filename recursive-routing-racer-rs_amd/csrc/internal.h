@@ -16,6 +16,14 @@ enum ActKind : uint32_t {
     ACT_RMSNORM = 3   // x[k] = (gamma[k] * src[k]) * inv_rms(src)
 };
 
+struct RopeArgs {
+    const float *factors;   // LongRoPE divisors of the first n_factors pairs
+    uint32_t n_factors;
+    uint32_t pos, n_heads, head_dim, rope_dim, q_dim, kv_stride;
+    float theta, attn_factor;
+    uint32_t row_stride;    // floats from one token's qkv row to the next (rows > 1)
+};
+
 struct GemvArgs {
     uint32_t type;        // GgmlType of W
     const float *x;       // activation source
@@ -30,6 +38,12 @@ struct GemvArgs {
     void *ws;             // device workspace of the skinny path's encoded activations
     uint64_t ws_bytes;
     uint32_t pair;        // W holds 2N rows [gate | up]; y[n] = silu(gate row n) * (up row n)
+    // rope_kv_store in the epilogue (y = qkv of one token at rope.pos): RoPE
+    // pairs rotated before they are stored, K and V also stored as f16 into
+    // row rope.pos of kc / vc (rrr_gemv_rmsnorm_rope_kv)
+    uint32_t rope_on;
+    RopeArgs rope;
+    uint32_t *kc, *vc;
 };
 
 // Every device buffer is allocated with at least this many bytes past its
@@ -85,13 +99,6 @@ hipError_t launch_logits_split(const float *x, const float *gamma, float eps, co
 uint64_t argmax_partials_bytes();
 hipError_t launch_argmax(const float *v, uint32_t n, void *partials, uint32_t *out, hipStream_t s);
 // RoPE + f16 KV store (attn.hip): the rope_kv_store / kv_store pipelines.
-struct RopeArgs {
-    const float *factors;   // LongRoPE divisors of the first n_factors pairs
-    uint32_t n_factors;
-    uint32_t pos, n_heads, head_dim, rope_dim, q_dim, kv_stride;
-    float theta, attn_factor;
-    uint32_t row_stride;    // floats from one token's qkv row to the next (rows > 1)
-};
 // rows consecutive tokens at positions pos .. pos + rows - 1
 hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uint16_t *vc, hipStream_t s,
                                 uint32_t rows = 1);

@@ -108,6 +108,8 @@ SIGNATURES = {
     "rrr_logits_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, c_buf_p, u32, u32, u32, u32]),
     "rrr_rope_kv_store": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, c_buf_p, c_buf_p, u32, u32, u32, u32, u32, u32, u32,
                                 f32, f32]),
+    "rrr_gemv_rmsnorm_rope_kv": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, u32, c_buf_p, u32, c_buf_p, u32,
+                                       c_buf_p, c_buf_p, u32, u32, u32, u32, u32, u32, u32, f32, f32]),
     "rrr_attention": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, c_buf_p, u32, u32, u32, u32]),
     "rrr_attention_noalloc": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
     "rrr_probe_read": (i32, [c_ctx_p, c_buf_p, u64, c_buf_p]),

@@ -28,8 +28,9 @@ The fused entry points are bitwise equal to their unfused sequences.
 With attention=True the sweep also owns per-layer f16 KV caches and
 record_token(pos) runs the full decode step at position pos (phi4.rs:1006-1033
 with the attention rows in): rope_kv_store (RoPE on Q and K, K and V stored
-in row pos) and attention over rows 0..pos replace the position-0 gather,
-and the O-proj GEMV takes the attention output.
+in row pos; in the QKV GEMV's epilogue, rrr_gemv_rmsnorm_rope_kv) and
+attention over rows 0..pos replace the position-0 gather, and the O-proj GEMV
+takes the attention output.
 
 Weights are seeded synthetic tensors (the recipes of synth.py; each tensor
 has its own stream id, so any subset can be regenerated on the host), or a
@@ -237,6 +238,10 @@ class DecodeSweep:
         # False: the GEMV into gate_up and silu in the down GEMV's prologue
         # (the same values bit for bit)
         self.silu_fused = True
+        # at a position (attention=True): rmsnorm -> QKV -> rope_kv_store as
+        # one launch (rrr_gemv_rmsnorm_rope_kv); False: the two launches
+        # (the same values bit for bit)
+        self.rope_fused = True
         self.logits = ctx.alloc(shape.vocab * 4)
         self.token = ctx.alloc(4)
         self.attention = attention
@@ -374,13 +379,24 @@ class DecodeSweep:
         c.residual_add(self.x_in, self.zero, self.hidden, d)       # hidden = embedding row
         for i, L in enumerate(self.layers):
             T = L["types"]
-            c.gemv_rmsnorm(self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], T["attn_qkv"], self.qkv, d, s.qkv_dim)
             if pos is None:
+                c.gemv_rmsnorm(self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], T["attn_qkv"], self.qkv, d,
+                               s.qkv_dim)
                 c.gemv_residual(self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], T["attn_output"], self.hidden, d, d)
             else:
                 kc, vc = self.kv[i]
-                c.rope_kv_store(self.qkv, self.rope_factors, self.n_rope_factors, kc, vc, pos, s.n_heads, s.n_kv_heads,
-                                s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta, s.rope_attn_factor)
+                if self.rope_fused:
+                    # rmsnorm -> QKV -> rope_kv_store as one launch (bitwise the two)
+                    c.gemv_rmsnorm_rope_kv(self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], T["attn_qkv"], self.qkv,
+                                           d, self.rope_factors, self.n_rope_factors, kc, vc, pos, s.n_heads,
+                                           s.n_kv_heads, s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta,
+                                           s.rope_attn_factor)
+                else:
+                    c.gemv_rmsnorm(self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], T["attn_qkv"], self.qkv, d,
+                                   s.qkv_dim)
+                    c.rope_kv_store(self.qkv, self.rope_factors, self.n_rope_factors, kc, vc, pos, s.n_heads,
+                                    s.n_kv_heads, s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta,
+                                    s.rope_attn_factor)
                 c.attention(self.qkv, kc, vc, self.attn_out, pos + 1, s.n_kv_heads, s.heads_per_kv, s.head_dim)
                 c.gemv_residual(self.attn_out, E.ACT_IDENTITY, 0, L["attn_output"], T["attn_output"], self.hidden, d, d)
             if self.silu_fused and T["ffn_up"] in (E.Q4_K, E.Q5_K, E.Q6_K):

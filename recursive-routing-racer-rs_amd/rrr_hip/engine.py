@@ -240,6 +240,14 @@ class Context:
                                           n_factors, k_cache._h, v_cache._h, pos, n_heads, n_kv_heads, head_dim,
                                           rope_dim, q_dim, kv_stride, theta, attn_factor))
 
+    def gemv_rmsnorm_rope_kv(self, x, gamma, eps, W, qtype, qkv, K, rope_factors, n_factors, k_cache, v_cache, pos,
+                             n_heads, n_kv_heads, head_dim, rope_dim, q_dim, kv_stride, theta=10000.0,
+                             attn_factor=1.190238):
+        _check(self.lib.rrr_gemv_rmsnorm_rope_kv(self._h, x._h, gamma._h, eps, W._h, qtype, qkv._h, K,
+                                                 rope_factors._h if rope_factors is not None else None, n_factors,
+                                                 k_cache._h, v_cache._h, pos, n_heads, n_kv_heads, head_dim, rope_dim,
+                                                 q_dim, kv_stride, theta, attn_factor))
+
     def attention(self, q, k_cache, v_cache, out, seq_len, n_kv_heads, heads_per_kv, head_dim):
         _check(self.lib.rrr_attention(self._h, q._h, k_cache._h, v_cache._h, out._h, seq_len, n_kv_heads,
                                       heads_per_kv, head_dim))

@@ -204,3 +204,37 @@ def test_attention_dispatch_name_and_graph_replay(ctx, caches):
     g.destroy()
     for b in (dq, o1, o2):
         b.free()
+
+
+@pytest.mark.parametrize("pos,with_factors", [(0, True), (1, True), (77, False), (2047, True)])
+def test_gemv_rmsnorm_rope_kv_is_the_two_launches(ctx, caches, pos, with_factors):
+    """rrr_gemv_rmsnorm_rope_kv (rmsnorm -> QKV -> rope_kv_store in one
+    launch, phi4.rs:1006-1017) leaves qkv and both cache rows bit for bit as
+    rrr_gemv_rmsnorm followed by rrr_rope_kv_store, on the Phi-4-mini QKV
+    shape (Q5_K 5120 x 3072: tiles of 10 rows, RoPE pairs inside a tile)."""
+    from rrr_hip import synth
+    kc, vc = caches
+    K, N = QD, QD + 2 * KVS
+    raw = synth.weight(7, 90 + pos, rrr_hip.Q5_K, K, N)
+    W = ctx.weight_upload(rrr_hip.Q5_K, K, N, raw)
+    x = ctx.to_device(synth.normal_f32(7, 91, K))
+    g = ctx.to_device(synth.normal_f32(7, 92, K, 1.0, 0.1))
+    fac = ctx.to_device(factors()) if with_factors else None
+    nf = RD // 2 if with_factors else 0
+    q1, q2 = ctx.alloc(N * 4), ctx.alloc(N * 4)
+    rows = []
+    for fused, q in ((False, q1), (True, q2)):
+        ctx.fill_u32(kc, 0x5A5A5A5A, pos * KVS * 2, KVS * 2)
+        ctx.fill_u32(vc, 0x5A5A5A5A, pos * KVS * 2, KVS * 2)
+        if fused:
+            ctx.gemv_rmsnorm_rope_kv(x, g, 1e-5, W, rrr_hip.Q5_K, q, K, fac, nf, kc, vc, pos, NH, NKV, HD, RD, QD, KVS)
+        else:
+            ctx.gemv_rmsnorm(x, g, 1e-5, W, rrr_hip.Q5_K, q, K, N)
+            ctx.rope_kv_store(q, fac, nf, kc, vc, pos, NH, NKV, HD, RD, QD, KVS)
+        rows.append((ctx.download(q, np.uint32, N), ctx.download(kc, np.uint16, KVS, offset=pos * KVS * 2),
+                     ctx.download(vc, np.uint16, KVS, offset=pos * KVS * 2)))
+    for a, b in zip(rows[0], rows[1]):
+        assert np.array_equal(a, b)
+    assert not np.all(rows[1][2] == 0x5A5A)   # the V row was written
+    for b in (W, x, g, q1, q2) + ((fac,) if fac is not None else ()):
+        b.free()

@@ -245,5 +245,17 @@ def test_decode_steps_with_attention_match_oracle(ctx):
         assert np.array_equal(logits.view(np.uint32), logits0.view(np.uint32))
         assert np.array_equal(hidden.view(np.uint32), hidden0.view(np.uint32))
     g.destroy()
+    # rope_kv_store in the QKV GEMV's epilogue (the default) and as its own
+    # launch give the same step bit for bit
+    assert sw.rope_fused
+    sw.rope_fused = False
+    try:
+        sw.record_token(ATT_POSITIONS[-1])
+        ctx.sync()
+    finally:
+        sw.rope_fused = True
+    logits, tok, hidden = sw.results()
+    assert np.array_equal(logits.view(np.uint32), logits0.view(np.uint32))
+    assert np.array_equal(hidden.view(np.uint32), hidden0.view(np.uint32))
     with pytest.raises(ValueError):
         sw.record_token(s.max_seq)
