@@ -26,9 +26,10 @@ __device__ __forceinline__ void src_load4(const GemvArgs &a, uint32_t k, float4 
 
 __device__ __forceinline__ uint32_t f16_bits(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
 
-// One rotation of apply_rope_cfg (phi4.rs:238-256) in f32: pair j of a head
-// at position pos.
-__device__ __forceinline__ void rope_pair(float &x0, float &x1, uint32_t j, uint32_t pos, const RopeArgs &r)
+// apply_rope_cfg (phi4.rs:238-256) in f32, pair j of a head at position
+// pos: the coefficients (cos and sin of the angle, scaled by attn_factor)
+// and the rotation; rope_pair is the two in order.
+__device__ __forceinline__ void rope_coef(uint32_t j, uint32_t pos, const RopeArgs &r, float &cs, float &ss)
 {
     const float base_freq = 1.0f / powf(r.theta, 2.0f * (float)j / (float)r.rope_dim);
     const float factor = j < r.n_factors ? r.factors[j] : 1.0f;
@@ -36,26 +37,42 @@ __device__ __forceinline__ void rope_pair(float &x0, float &x1, uint32_t j, uint
     const float angle = (float)pos * freq;
     float sin_t, cos_t;
     sincosf(angle, &sin_t, &cos_t);
-    const float cs = cos_t * r.attn_factor, ss = sin_t * r.attn_factor;
+    cs = cos_t * r.attn_factor;
+    ss = sin_t * r.attn_factor;
+}
+
+__device__ __forceinline__ void rope_rotate(float &x0, float &x1, float cs, float ss)
+{
     const float a = x0, b = x1;
     x0 = a * cs - b * ss;
     x1 = a * ss + b * cs;
 }
 
+__device__ __forceinline__ void rope_pair(float &x0, float &x1, uint32_t j, uint32_t pos, const RopeArgs &r)
+{
+    float cs, ss;
+    rope_coef(j, pos, r, cs, ss);
+    rope_rotate(x0, x1, cs, ss);
+}
+
 // rope_kv_store (rope_kv_store_kernel, attn.hip) of the qkv row pair (row,
 // row + 1), row even, as the GEMV stores it: Q and K pairs in their heads'
-// first rope_dim dims rotated, every value stored to y, the K and V pairs
-// also as f16 into cache row pos.
-__device__ __forceinline__ void rope_store_pair(const GemvArgs &a, uint32_t row, float v0, float v1)
+// first rope_dim dims rotated (coefficients of pair j at coef[2j], coef[2j+1],
+// from rope_coef at the launch's position), every value stored to y, the K
+// and V pairs also as f16 into cache row pos.
+__device__ __forceinline__ void rope_store_pair(const GemvArgs &a, uint32_t row, float v0, float v1,
+                                                const float *coef)
 {
     const RopeArgs &r = a.rope;
     if (row < r.q_dim) {
-        if (row < r.n_heads * r.head_dim && row % r.head_dim < r.rope_dim)
-            rope_pair(v0, v1, (row % r.head_dim) / 2, r.pos, r);
+        if (row < r.n_heads * r.head_dim && row % r.head_dim < r.rope_dim) {
+            const uint32_t j = (row % r.head_dim) / 2;
+            rope_rotate(v0, v1, coef[2 * j], coef[2 * j + 1]);
+        }
     } else if (row < r.q_dim + r.kv_stride) {
         const uint32_t e = row - r.q_dim;
         const uint32_t d = r.rope_dim ? e % r.head_dim : 0u;
-        if (d < r.rope_dim) rope_pair(v0, v1, d / 2, r.pos, r);
+        if (d < r.rope_dim) rope_rotate(v0, v1, coef[d], coef[d + 1]);
         a.kc[((size_t)r.pos * r.kv_stride + e) / 2] = f16_bits(v0) | (f16_bits(v1) << 16);
     } else {
         const uint32_t e = row - r.q_dim - r.kv_stride;

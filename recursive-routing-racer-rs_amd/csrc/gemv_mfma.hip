@@ -88,6 +88,8 @@ static hipError_t go_mq_rope(const GemvArgs &a, hipStream_t s)
     size_t lds;
     mq_plan<Q, BPW>(a, W, grid, lds, tr, ntiles);
     if (tr % 2) return hipErrorNotSupported;
+    lds += 4 * (size_t)a.rope.rope_dim;   // the rotation coefficients
+    if (lds > 160 * 1024) return hipErrorNotSupported;
     const bool multi = grid != ntiles;
     if (tr <= 10) {
         if (multi)

@@ -285,7 +285,9 @@ constexpr uint32_t MQ_OOB = 0x80000000u;
 // into 2N rows followed by that activation gives.
 // ROPE (a.rope_on, tr even): the rows go out in pairs through
 // rope_store_pair (act.h), the rope_kv_store of the token's qkv row; each
-// row's value is the sum a plain launch stores.
+// row's value is the sum a plain launch stores.  The rope_dim rotation
+// coefficients sit in LDS past the row partials (the launcher adds their
+// rope_dim floats).
 template <class Q, int BPW, int ACT, bool MULTI, int TR = 16, bool PAIR = false, bool ROPE = false>
 __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr)
 {
@@ -367,6 +369,12 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int j = 0; j < BPW; j++) issue(j, 0);
+    // ROPE: the position's rotation coefficients, one pair per thread, while
+    // the weights are in flight (read after the final barrier)
+    float *coef = part + ntl * W * 16;
+    if constexpr (ROPE) {
+        if (t < a.rope.rope_dim / 2) rope_coef(t, a.rope.pos, a.rope, coef[2 * t], coef[2 * t + 1]);
+    }
 
     // 2. fused RMSNorm: the wave's slice of x is slice `wave` of the canonical
     // sum-of-squares split (BPW float4s per lane is its P = ceil(K / 4096)
@@ -529,7 +537,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
                     v0 += part[(tl * W + w) * 16 + r];
                     v1 += part[(tl * W + w) * 16 + r + 1];
                 }
-                rope_store_pair(a, row, v0, v1);
+                rope_store_pair(a, row, v0, v1, coef);
             }
         }
         return;
