@@ -206,12 +206,15 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
                                                       uint32_t ksteps, float *ws)
 {
     constexpr int LDK = BK + 8;                            // f16 per LDS row (16-byte pad)
-    constexpr int TI = BM / 32, TJ = BN / 32;              // 16x16 tiles per MFMA wave
     constexpr int UE = BN * BK / 256, TPW = BK / UE;       // weight elements per producer thread, threads per row
+    constexpr int NPW = UE / 32;                           // 32-element parts per producer thread
     constexpr int XE = BM * BK / 256;                      // X elements per producer thread
     constexpr int XC = BK / 8, XRS = 256 / XC;             // 16-byte chunks per X row and step, rows per pass
-    static_assert(UE == 32 && XE % 8 == 0 && BK % 64 == 0, "tile shape");
-    using Q = QT<1>;
+    static_assert((UE == 32 || UE == 64) && XE % 8 == 0 && BK % 64 == 0, "tile shape");
+    using Q = QT<NPW>;
+    // register sets of the producer's load ring: four (loads issued four
+    // steps ahead) where the registers allow it, else three
+    constexpr int NSET = (XH && BK == 64 && Q::BS != 210) ? 4 : 3;
     extern __shared__ float smem[];
     _Float16 *As = (_Float16 *)smem;                       // [2][BM][LDK]
     _Float16 *Bs = As + 2 * BM * LDK;                      // [2][BN][LDK]
@@ -236,8 +239,9 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     if (wave >= 4) {
         // ---- producer: loads, dequant, conversion --------------------------
         const uint32_t tp = t - 256;
-        // weight row, the step's 64-element chunk (its start lb) and the part wp of it
-        const uint32_t ur = tp / TPW, lb = 64 * ((tp % TPW) >> 1), wp = tp & 1;
+        // weight row, the step's 64-element chunk (its start lb) and the first
+        // part wp of it (two parts a thread: the whole chunk, wp = 0)
+        const uint32_t ur = tp / TPW, lb = 64 * ((tp % TPW) * NPW / 2), wp = (tp % TPW) * NPW % 2;
         const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, (uint64_t)N * B * Q::BS);
         const uint32_t wvoff = (n0 + ur) * B * Q::BS;
         // X: pass i covers rows XRS*i .. XRS*(i+1)-1 of the step, consecutive
@@ -250,7 +254,7 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
             typename Q::Raw raw;
             u32x4 xv[XE / 8];
         };
-        Set S0, S1, S2;
+        Set S0, S1, S2, S3;
         // element e0 of the step's unit inside its super-block: chunk e0/64, lane part e0%64
         auto issue = [&](Set &st, uint32_t s) {
             const bool ok = s < nsteps;   // past the end: out-of-range offsets, zeros
@@ -263,12 +267,13 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         };
         auto stage = [&](const Set &st, uint32_t s) {
             const uint32_t buf = s & 1, e0 = ((s0 + s) * BK) % 256 + lb;
-            uint32_t o[16];
+            uint32_t o[16 * NPW];
             Q::dequant(st.raw, e0 >> 6, wp, o);
-            _Float16 *dst = Bs + (buf * BN + ur) * LDK + lb + 16 * wp;   // runs at +0 and +32
+            _Float16 *dst = Bs + (buf * BN + ur) * LDK + lb + 16 * wp;   // part k: runs at 16k + 0 and 16k + 32
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                *(u32x4 *)(dst + 8 * (i & 1) + 32 * (i >> 1)) = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+            for (int i = 0; i < 4 * NPW; i++)
+                *(u32x4 *)(dst + 16 * (i >> 2) + 8 * (i & 1) + 32 * ((i >> 1) & 1)) =
+                    u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
             _Float16 *xd = As + (buf * BM + xr) * LDK + xk;   // pass i: + XRS*i rows
 #pragma unroll
             for (int i = 0; i < XE / 8; i++) {
@@ -287,71 +292,107 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         issue(S0, 0);
         issue(S1, 1);
         issue(S2, 2);
+        if constexpr (NSET == 4) issue(S3, 3);
         stage(S0, 0);
-        issue(S0, 3);
+        issue(S0, NSET);
         __syncthreads();
-        // step s: stage s+1 (its set then takes the loads of s+4); steps past
-        // the end (nsteps rounded up to 3) stage zeros
-        for (uint32_t s = 0; s < nsteps; s += 3) {
+        // step s: stage s+1 (its set then takes the loads of s+1+NSET); steps
+        // past the end (nsteps rounded up to NSET) stage zeros
+        for (uint32_t s = 0; s < nsteps; s += NSET) {
             stage(S1, s + 1);
-            issue(S1, s + 4);
+            issue(S1, s + 1 + NSET);
             __syncthreads();
             stage(S2, s + 2);
-            issue(S2, s + 5);
+            issue(S2, s + 2 + NSET);
             __syncthreads();
-            stage(S0, s + 3);
-            issue(S0, s + 6);
+            if constexpr (NSET == 4) {
+                stage(S3, s + 3);
+                issue(S3, s + 3 + NSET);
+                __syncthreads();
+            }
+            stage(S0, s + NSET);
+            issue(S0, s + 2 * NSET);
             __syncthreads();
         }
         return;
     }
 
     // ---- consumer: MFMAs on LDS buffer s&1 ----------------------------------
+    // 32x32x16 f16 MFMAs (the matrix core's best rate at one wave per SIMD);
+    // lane l holds A row l % 32 and B column l % 32 at k = 8 (l / 32) + 0..7
+    // of the 16-wide slice, and D column l % 32, rows 8 (r / 4) + 4 (l / 32)
+    // + r % 4 in accumulator register r.
+    constexpr int UI = BM / 64, UJ = BN / 64;   // 32x32 tiles per wave
     const uint32_t wm = wave >> 1, wn = wave & 1;
-    f32x4 acc[TI][TJ];
+    f32x16 acc[UI][UJ];
 #pragma unroll
-    for (int i = 0; i < TI; i++)
+    for (int i = 0; i < UI; i++)
 #pragma unroll
-        for (int j = 0; j < TJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint32_t fr = lane & 15, fk = 8 * (lane >> 4);
-    auto mfma_step = [&](uint32_t s) {
-        const uint32_t cur = s & 1;
-        const _Float16 *Ab = As + (cur * BM + wm * (BM / 2) + fr) * LDK + fk;
-        const _Float16 *Bb = Bs + (cur * BN + wn * (BN / 2) + fr) * LDK + fk;
+        for (int j = 0; j < UJ; j++)
 #pragma unroll
-        for (int kk = 0; kk < BK / 32; kk++) {
-            f16x8v a[TI], b[TJ];
-#pragma unroll
-            for (int i = 0; i < TI; i++) a[i] = *(const f16x8v *)(Ab + 16 * i * LDK + 32 * kk);
-#pragma unroll
-            for (int j = 0; j < TJ; j++) b[j] = *(const f16x8v *)(Bb + 16 * j * LDK + 32 * kk);
-#pragma unroll
-            for (int i = 0; i < TI; i++)
-#pragma unroll
-                for (int j = 0; j < TJ; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+    const uint32_t fr = lane & 31, fk = 8 * (lane >> 5);
+    // The fragments of one 16-wide k slice; two sets alternate so that the
+    // LDS reads of slice kq + 1 are in flight while the MFMAs of slice kq
+    // run.  The scheduling fences keep that order: left to itself the
+    // compiler reloads one fragment register per row of tiles and waits out
+    // the LDS latency before each row's MFMAs.
+    struct Frag {
+        f16x8v a[UI], b[UJ];
     };
+    auto frag_load = [&](Frag &f, uint32_t buf, int kq) {
+        const _Float16 *Ab = As + (buf * BM + wm * (BM / 2) + fr) * LDK + fk + 16 * kq;
+        const _Float16 *Bb = Bs + (buf * BN + wn * (BN / 2) + fr) * LDK + fk + 16 * kq;
+#pragma unroll
+        for (int i = 0; i < UI; i++) f.a[i] = *(const f16x8v *)(Ab + 32 * i * LDK);
+#pragma unroll
+        for (int j = 0; j < UJ; j++) f.b[j] = *(const f16x8v *)(Bb + 32 * j * LDK);
+    };
+    auto frag_mfma = [&](const Frag &f) {
+#pragma unroll
+        for (int i = 0; i < UI; i++)
+#pragma unroll
+            for (int j = 0; j < UJ; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    };
+    constexpr int KQ = BK / 16;   // even
+    // one barrier per step, as many steps as the producer stages (nsteps
+    // rounded up to NSET); the barrier of step s comes once this wave's reads
+    // of buffer s & 1 have landed, and the first slice of step s + 1 is read
+    // from the other buffer while the last slice of step s multiplies
+    const uint32_t steps3 = (nsteps + NSET - 1) / NSET * NSET;
+    Frag f0, f1;
     __syncthreads();
-    for (uint32_t s = 0; s < nsteps; s += 3) {
-        mfma_step(s);
-        __syncthreads();
-        mfma_step(s + 1);
-        __syncthreads();
-        mfma_step(s + 2);
-        __syncthreads();
+    frag_load(f0, 0, 0);
+    for (uint32_t s = 0; s < steps3; s++) {
+        const uint32_t cur = s & 1;
+#pragma unroll
+        for (int kq = 0; kq < KQ; kq += 2) {
+            frag_load(f1, cur, kq + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            frag_mfma(f0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kq + 2 < KQ) {
+                frag_load(f0, cur, kq + 2);
+            } else {
+                __syncthreads();
+                frag_load(f0, cur ^ 1u, 0);   // past the last step: stale, unused
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            frag_mfma(f1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 
-    // D rows 4*(l/16)+r of column l%16 in register r; the row scales (powers
-    // of two) are exact
+    // the row scales (powers of two) are exact
 #pragma unroll
-    for (int i = 0; i < TI; i++)
+    for (int i = 0; i < UI; i++)
 #pragma unroll
-        for (int j = 0; j < TJ; j++) {
-            const uint32_t n = n0 + wn * (BN / 2) + 16 * j + fr;
+        for (int j = 0; j < UJ; j++) {
+            const uint32_t n = n0 + wn * (BN / 2) + 32 * j + fr;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t m = m0 + wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + r;
+            for (int r = 0; r < 16; r++) {
+                const uint32_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if constexpr (SPLIT) {
                     ws[((uint64_t)ks * M + m) * N + n] = acc[i][j][r];
                     continue;
