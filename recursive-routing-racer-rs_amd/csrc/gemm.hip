@@ -205,7 +205,14 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
                                                       uint32_t N, uint32_t M, uint32_t tiles_n, const float *rscale,
                                                       uint32_t ksteps, float *ws)
 {
-    constexpr int LDK = BK + 8;                            // f16 per LDS row (16-byte pad)
+    // LDS rows of BK f16, unpadded; 16-byte chunk c of row r sits at chunk
+    // c ^ swz(r), swz(r) = (r / RPL) % CPR with RPL rows per 64-bank line
+    // and CPR chunks per row, so that 16 consecutive rows read at one chunk
+    // (and 8 lanes writing one row) fall in distinct banks.  swz depends on
+    // r % 16 only; every tile base and row stride below is a multiple of 16.
+    constexpr int LDK = BK, CPR = BK / 8, RPL = 128 / BK;
+    static_assert(RPL * CPR == 16, "swizzle period");
+    auto swz = [](uint32_t r) { return (r / RPL) % CPR; };
     constexpr int UE = BN * BK / 256, TPW = BK / UE;       // weight elements per producer thread, threads per row
     constexpr int NPW = UE / 32;                           // 32-element parts per producer thread
     constexpr int XE = BM * BK / 256;                      // X elements per producer thread
@@ -269,12 +276,14 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
             const uint32_t buf = s & 1, e0 = ((s0 + s) * BK) % 256 + lb;
             uint32_t o[16 * NPW];
             Q::dequant(st.raw, e0 >> 6, wp, o);
-            _Float16 *dst = Bs + (buf * BN + ur) * LDK + lb + 16 * wp;   // part k: runs at 16k + 0 and 16k + 32
+            // part k: runs at chunks c0 + 2k + (0, 1) and c0 + 2k + (4, 5)
+            _Float16 *dst = Bs + (buf * BN + ur) * LDK;
+            const uint32_t c0 = (lb + 16 * wp) / 8, gu = swz(ur);
 #pragma unroll
             for (int i = 0; i < 4 * NPW; i++)
-                *(u32x4 *)(dst + 16 * (i >> 2) + 8 * (i & 1) + 32 * ((i >> 1) & 1)) =
+                *(u32x4 *)(dst + 8 * ((c0 + 2 * (i >> 2) + (i & 1) + 4 * ((i >> 1) & 1)) ^ gu)) =
                     u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
-            _Float16 *xd = As + (buf * BM + xr) * LDK + xk;   // pass i: + XRS*i rows
+            _Float16 *xd = As + (buf * BM + xr) * LDK + 8 * ((xk / 8) ^ swz(xr));   // pass i: + XRS*i rows
 #pragma unroll
             for (int i = 0; i < XE / 8; i++) {
                 const u32x4 v = st.xv[i];
@@ -341,8 +350,9 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         f16x8v a[UI], b[UJ];
     };
     auto frag_load = [&](Frag &f, uint32_t buf, int kq) {
-        const _Float16 *Ab = As + (buf * BM + wm * (BM / 2) + fr) * LDK + fk + 16 * kq;
-        const _Float16 *Bb = Bs + (buf * BN + wn * (BN / 2) + fr) * LDK + fk + 16 * kq;
+        const uint32_t ch = 8 * (((fk / 8) + 2 * kq) ^ swz(fr));
+        const _Float16 *Ab = As + (buf * BM + wm * (BM / 2) + fr) * LDK + ch;
+        const _Float16 *Bb = Bs + (buf * BN + wn * (BN / 2) + fr) * LDK + ch;
 #pragma unroll
         for (int i = 0; i < UI; i++) f.a[i] = *(const f16x8v *)(Ab + 32 * i * LDK);
 #pragma unroll
@@ -436,7 +446,7 @@ template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC>
 static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K, uint32_t N,
                           uint32_t M, uint32_t S, float *ws, hipStream_t s)
 {
-    constexpr size_t lds = 2 * (size_t)(BM + BN) * (BK + 8) * 2;
+    constexpr size_t lds = 2 * (size_t)(BM + BN) * BK * 2;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
     const uint32_t tiles_n = N / BN, tiles = tiles_n * (M / BM);
     if (S > 1)
