@@ -72,16 +72,21 @@ __device__ __forceinline__ uint32_t byte_of(uint32_t w, uint32_t i) { return (w 
 __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2,
                                              uint32_t &sc, uint32_t &mn)
 {
-    // q[i] for i in 0..11 is byte (i & 3) of dword s[i >> 2].  Both cases are
-    // computed and one is selected (j often differs across the lanes of a
-    // wave, and a branch would run both sides anyway):
-    //   j < 4:  sc = q[j] & 63,                      mn = q[j+4] & 63
-    //   j >= 4: sc = (q[j+4] & 15) | (q[j-4] >> 6) << 4, mn = (q[j+4] >> 4) | (q[j] >> 6) << 4
-    const uint32_t i = j & 3u;
+    // q[i] for i in 0..11 is byte (i & 3) of dword s[i >> 2].  With i = j % 4
+    // and h = j / 4, q0 = q[i], q4 = q[4 + i], q8 = q[8 + i]:
+    //   h = 0: sc = q0 & 63,                     mn = q4 & 63
+    //   h = 1: sc = (q8 & 15) | (q0 >> 6) << 4,  mn = (q8 >> 4) | (q4 >> 6) << 4
+    // Both cases are a 4-bit and a 2-bit field of u = q8 | q0 << 8 (sc) or
+    // v = q8 | q4 << 8 (mn) at offsets that depend on h only:
+    //   sc = u[8 - 8h .. +3] | u[12 + 2h .. +1] << 4
+    //   mn = v[8 - 4h .. +3] | v[12 + 2h .. +1] << 4
+    // so there is no select (which the compiler turns into branches around
+    // the header loads when j is the same on every lane).
+    const uint32_t i = j & 3u, h = (j >> 2) & 1u;
     const uint32_t q0 = byte_of(s0, i), q4 = byte_of(s1, i), q8 = byte_of(s2, i);
-    const bool hi = j >= 4;
-    sc = hi ? (q8 & 0x0Fu) | ((q0 >> 2) & 0x30u) : q0 & 63u;
-    mn = hi ? (q8 >> 4) | ((q4 >> 2) & 0x30u) : q4 & 63u;
+    const uint32_t u = q8 | (q0 << 8), v = q8 | (q4 << 8);
+    sc = ((u >> (8u - 8u * h)) & 15u) | (((u >> (12u + 2u * h)) & 3u) << 4);
+    mn = ((v >> (8u - 4u * h)) & 15u) | (((v >> (12u + 2u * h)) & 3u) << 4);
 }
 
 // Deterministic full-wave sum: fixed butterfly order, identical on every call.
