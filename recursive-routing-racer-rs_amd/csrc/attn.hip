@@ -123,6 +123,24 @@ __device__ __forceinline__ void merge_pair(float &m, float &l, float (&o)[8])
     m = M;
 }
 
+// Maximum / sum of v over the lanes l, l ^ 16, l ^ 32, l ^ 48 by the lane
+// swaps (VALU, no LDS round trip); every lane of the four gets the same
+// value, and the sum is the one the xor-16 then xor-32 butterfly gives.
+__device__ __forceinline__ float lanes4_max(float v)
+{
+    float a, b;
+    lane_pair<16>(v, a, b);
+    lane_pair<32>(fmaxf(a, b), a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float lanes4_sum(float v)
+{
+    float a, b;
+    lane_pair<16>(v, a, b);
+    lane_pair<32>(a + b, a, b);
+    return a + b;
+}
+
 template <int HPK>
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, const uint16_t *__restrict__ kc,
                                                    const uint16_t *__restrict__ vc, float *part, uint32_t *counters,
@@ -518,8 +536,9 @@ struct AttmLds {
     static constexpr size_t ML = (size_t)ATTM_WAVES * HPK * 16 * 2 * 4;                // merge: max, sum
     static constexpr size_t Q = (size_t)HPK * 4 * 2 * 64 * 16;                        // Q^T operands, hi + lo
     // the loop's V^T and Q^T share their bytes with the merge's outputs
+    static constexpr size_t CW = (size_t)HPK * 16 * (ATTM_WAVES + 1) * 4;             // merge: weights, scale
     static constexpr size_t LOOP = VT + Q, MAIN = LOOP > O ? LOOP : O;
-    static constexpr size_t BYTES = MAIN + ML;
+    static constexpr size_t BYTES = MAIN + ML + CW;
 };
 
 template <int HPK, bool F16OUT>
@@ -538,12 +557,38 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
     _Float16 *vt = (_Float16 *)sm + (size_t)wv * ATT_HD * ATTM_LD;   // this wave's V^T
     float *mo = (float *)sm;                                        // merge outputs (after the loop)
     float *mml = (float *)(sm + LD::MAIN);                          // merge max / sum
+    float *mcw = (float *)(sm + LD::MAIN + LD::ML);                 // merge weights and scale per (head, token)
     h8 *qop = (h8 *)(sm + LD::VT);                                  // Q^T operands [h][kk][hi, lo][lane]
     const uint32_t g = blockIdx.x, tb = blockIdx.y, l = threadIdx.x & 63, n = l & 15, grp = l >> 4;
     const uint32_t tok = tb * 16 + n, tq = min(tok, rows - 1), tpos = pos0 + tq;
     const uint32_t last = pos0 + min(tb * 16 + 15, rows - 1);      // the last cache row the block's tokens see
     const uint32_t nblk = last / 32 + 1;
     const uint16_t *kbase = kc + (size_t)g * ATT_HD, *vbase = vc + (size_t)g * ATT_HD;
+
+    // K and V of block blk (rows past `last` repeat it): the next block of
+    // this wave is requested before the current one is multiplied
+    auto load_blk = [&](uint32_t blk, h8 (&ka)[2][4], h8 (&vr)[2][4]) {
+        const uint32_t c0 = 32 * blk;
+        // K A operands: key tile kt (rows c0 + 16 kt + n), dims 32 kk + 8 grp
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+            const uint32_t row = min(c0 + 16 * kt + n, last);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+                ka[kt][kk] = *(const h8 *)(kbase + (size_t)row * kv_stride + 32 * kk + 8 * grp);
+        }
+        // V rows c0 + 4 grp + {0..3} and c0 + 16 + 4 grp + {0..3}, dims 8 n .. 8 n + 7
+#pragma unroll
+        for (int half = 0; half < 2; half++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t row = min(c0 + 16 * half + 4 * grp + j, last);
+                vr[half][j] = *(const h8 *)(vbase + (size_t)row * kv_stride + 8 * n);
+            }
+    };
+    // this wave's first block is requested before the Q^T operands are built
+    h8 kaA[2][4], vrA[2][4];
+    if (wv < nblk) load_blk(wv, kaA, vrA);
 
     // Q^T operands of each head: token tq, dims 32 kk + 8 grp .. +7, scaled,
     // hi + lo; every wave computes them, wave 0 keeps them in LDS (the block
@@ -565,8 +610,7 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
                 mx = fmaxf(mx, fabsf(x[kk][i]));
             }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));   // the token's 128 dims sit in lanes n + 16 j
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = lanes4_max(mx);   // the token's 128 dims sit in lanes n + 16 j
         int e = 0;
         if (mx > 0.0f && __builtin_isfinite(mx)) (void)frexpf(mx, &e);
         const float up = ldexpf(1.0f, 14 - e);
@@ -597,27 +641,8 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) o[h][dt] = f4{0.f, 0.f, 0.f, 0.f};
     }
-    for (uint32_t blk = wv; blk < nblk; blk += ATTM_WAVES) {
+    auto process = [&](uint32_t blk, const h8 (&ka)[2][4], const h8 (&vr)[2][4]) {
         const uint32_t c0 = 32 * blk;
-        // K A operands: key tile kt (rows c0 + 16 kt + n), dims 32 kk + 8 grp
-        h8 ka[2][4];
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-            const uint32_t row = min(c0 + 16 * kt + n, last);
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-                ka[kt][kk] = *(const h8 *)(kbase + (size_t)row * kv_stride + 32 * kk + 8 * grp);
-        }
-        // V rows c0 + 4 grp + {0..3} and c0 + 16 + 4 grp + {0..3}, dims 8 n .. 8 n + 7,
-        // written to V^T[dim][key] four keys at a time
-        h8 vr[2][4];
-#pragma unroll
-        for (int half = 0; half < 2; half++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t row = min(c0 + 16 * half + 4 * grp + j, last);
-                vr[half][j] = *(const h8 *)(vbase + (size_t)row * kv_stride + 8 * n);
-            }
         // this wave's V^T (the wave's LDS operations run in order: the
         // previous block's reads come before these writes)
         wave_lds_order();
@@ -656,8 +681,7 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
                     if (c0 + 16 * kt + 4 * grp + r > tpos) sc[kt][r] = -__builtin_inff();
                     bm = fmaxf(bm, sc[kt][r]);
                 }
-            bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            bm = lanes4_max(bm);
             // Lazy reference max: it moves only when the block's max passes it
             // by more than 3 (so P <= 8 and P * 2^12 stays inside f16), which
             // after the first blocks is rare, and the accumulators are then
@@ -685,8 +709,7 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
                     pb[4 * kt + r] = hi;
                     pl[4 * kt + r] = (_Float16)(pp - (float)hi);
                 }
-            ps += __shfl_xor(ps, 16, 64);
-            ps += __shfl_xor(ps, 32, 64);
+            ps = lanes4_sum(ps);
             ls[h] = fmaf(ls[h], cf, ps);
             m[h] = mn;
 #pragma unroll
@@ -697,6 +720,26 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
                 o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[h][dt], 0, 0, 0);
                 o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[h][dt], 0, 0, 0);
             }
+        }
+    };
+    if constexpr (HPK <= 3) {
+        // two register sets (HPK = 4 would spill: its accumulators take 32
+        // registers more)
+        h8 kaB[2][4], vrB[2][4];
+        uint32_t blk = wv;
+        while (blk < nblk) {
+            load_blk(min(blk + ATTM_WAVES, nblk - 1), kaB, vrB);   // past the last block: a repeat, unused
+            process(blk, kaA, vrA);
+            blk += ATTM_WAVES;
+            if (blk >= nblk) break;
+            load_blk(min(blk + ATTM_WAVES, nblk - 1), kaA, vrA);
+            process(blk, kaB, vrB);
+            blk += ATTM_WAVES;
+        }
+    } else {
+        for (uint32_t blk = wv; blk < nblk; blk += ATTM_WAVES) {
+            if (blk != wv) load_blk(blk, kaA, vrA);
+            process(blk, kaA, vrA);
         }
     }
     // merge the waves: wave w's output rows (token, dims) and its max / sum
@@ -714,28 +757,48 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
         }
     }
     __syncthreads();
-    const size_t qd = (size_t)gridDim.x * HPK * ATT_HD;
-    for (uint32_t i = threadIdx.x; i < HPK * 16 * ATT_HD; i += 64 * ATTM_WAVES) {
-        const uint32_t d = i % ATT_HD, ht = i / ATT_HD, h = ht % HPK, t = ht / HPK;   // dims fastest
-        const uint32_t tk = tb * 16 + t;
+    // per (head, token): the waves' weights exp2(m_w - M) and the output
+    // scale 1 / (PS L), once (L summed over the waves in order)
+    if (threadIdx.x < HPK * 16) {
+        const uint32_t ht = threadIdx.x, h = ht % HPK, t = ht / HPK;
         float M = -__builtin_inff();
 #pragma unroll
         for (uint32_t w = 0; w < ATTM_WAVES; w++) M = fmaxf(M, mml[((w * HPK + h) * 16 + t) * 2]);
-        float L = 0.0f, O = 0.0f;
+        float L = 0.0f;
 #pragma unroll
         for (uint32_t w = 0; w < ATTM_WAVES; w++) {
-            const float c = safe_scale(mml[((w * HPK + h) * 16 + t) * 2], M);
+            const float c = safe_scale(mml[((w * HPK + h) * 16 + t) * 2], M);   // 0 for a wave without rows
             L = fmaf(mml[((w * HPK + h) * 16 + t) * 2 + 1], c, L);
-            O = fmaf(mo[((size_t)(w * HPK + h) * 16 + t) * ATTM_OLD + d], c, O);
+            mcw[ht * (ATTM_WAVES + 1) + w] = c;
+        }
+        mcw[ht * (ATTM_WAVES + 1) + ATTM_WAVES] = (1.0f / ATTM_PS) / L;
+    }
+    __syncthreads();
+    // four dims a thread: the waves' outputs weighted and added in wave order
+    const size_t qd = (size_t)gridDim.x * HPK * ATT_HD;
+    for (uint32_t i = threadIdx.x; i < HPK * 16 * ATT_HD / 4; i += 64 * ATTM_WAVES) {
+        const uint32_t d = 4 * (i % (ATT_HD / 4)), ht = i / (ATT_HD / 4), h = ht % HPK, t = ht / HPK;   // dims fastest
+        const uint32_t tk = tb * 16 + t;
+        const float *cw = mcw + ht * (ATTM_WAVES + 1);
+        f4 O = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t w = 0; w < ATTM_WAVES; w++) {
+            const float c = cw[w];
+            const f4 ow = *(const f4 *)(mo + ((size_t)(w * HPK + h) * 16 + t) * ATTM_OLD + d);
+#pragma unroll
+            for (int e = 0; e < 4; e++) O[e] = fmaf(ow[e], c, O[e]);
         }
         if (tk < rows) {
             const size_t oi = (size_t)tk * qd + (size_t)(g * HPK + h) * ATT_HD + d;
-            float v = O * ((1.0f / ATTM_PS) / L);
+            const float sc = cw[ATTM_WAVES];
+            f4 v;
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] = O[e] * sc;
             if constexpr (F16OUT) {
-                asm volatile("" : "+v"(v));   // the f32 result, then its rounding (no mixed-precision fold)
-                ((_Float16 *)out)[oi] = (_Float16)v;
+                asm volatile("" : "+v"(v));   // the f32 results, then their rounding (no mixed-precision fold)
+                *(h4 *)((_Float16 *)out + oi) = h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
             } else {
-                ((float *)out)[oi] = v;
+                *(f4 *)((float *)out + oi) = v;
             }
         }
     }
