@@ -712,14 +712,19 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
             ps = lanes4_sum(ps);
             ls[h] = fmaf(ls[h], cf, ps);
             m[h] = mn;
+            // V^T operands of the 8 dim tiles read first, then the 8 P-hi
+            // MFMAs and the 8 P-lo MFMAs (each accumulator takes hi then lo)
+            h8 av[8];
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
                 const _Float16 *vrow = vt + (16 * dt + n) * ATTM_LD;
                 const h4 a0 = *(const h4 *)(vrow + 4 * grp), a1 = *(const h4 *)(vrow + 16 + 4 * grp);
-                const h8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-                o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[h][dt], 0, 0, 0);
-                o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[h][dt], 0, 0, 0);
+                av[dt] = h8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
             }
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[dt], pb, o[h][dt], 0, 0, 0);
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) o[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[dt], pl, o[h][dt], 0, 0, 0);
         }
     };
     if constexpr (HPK <= 3) {
