@@ -184,33 +184,54 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
 #pragma unroll
         for (int d = 0; d < 8; d++) o[h][d] = 0.0f;
     }
+    // the lane group's ATT_ROWS_PER_GROUP rows at once: their scores (independent
+    // dot products and row sums), one update of the running max, then the
+    // sum and output; rows past the split add nothing (uniform in the row of
+    // 16 lanes)
+    constexpr int R = (int)ATT_ROWS_PER_GROUP;
+    float kf[R][8], v[R][8];
+    bool live[R];
 #pragma unroll
-    for (int k = 0; k < (int)ATT_ROWS_PER_GROUP; k++) {
-        // rows past the split leave the state as it is (uniform in the row of 16 lanes)
-        const bool live = r0 + grp + 16 * k < r1;
-        float kf[8], v[8];
+    for (int k = 0; k < R; k++) {
+        live[k] = r0 + grp + 16 * k < r1;
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            kf[2 * w] = h2f(kr[k][w] & 0xFFFFu);
-            kf[2 * w + 1] = h2f(kr[k][w] >> 16);
-            v[2 * w] = h2f(vr[k][w] & 0xFFFFu);
-            v[2 * w + 1] = h2f(vr[k][w] >> 16);
+            kf[k][2 * w] = h2f(kr[k][w] & 0xFFFFu);
+            kf[k][2 * w + 1] = h2f(kr[k][w] >> 16);
+            v[k][2 * w] = h2f(vr[k][w] & 0xFFFFu);
+            v[k][2 * w + 1] = h2f(vr[k][w] >> 16);
         }
+    }
 #pragma unroll
-        for (int h = 0; h < HPK; h++) {
+    for (int h = 0; h < HPK; h++) {
+        float sc[R];
+#pragma unroll
+        for (int k = 0; k < R; k++) {
             float s = 0.0f;
 #pragma unroll
-            for (int d = 0; d < 8; d++) s = fmaf(qv[h][d], kf[d], s);
-            s = row16_sum(s);
-            if (live) {
-                const float mn = fmaxf(m[h], s);
-                const float c = exp2f(m[h] - mn), p = exp2f(s - mn);
-                l[h] = fmaf(l[h], c, p);
-#pragma unroll
-                for (int d = 0; d < 8; d++) o[h][d] = fmaf(o[h][d], c, p * v[d]);
-                m[h] = mn;
-            }
+            for (int d = 0; d < 8; d++) s = fmaf(qv[h][d], kf[k][d], s);
+            sc[k] = row16_sum(s);
         }
+        float mn = m[h];
+#pragma unroll
+        for (int k = 0; k < R; k++)
+            if (live[k]) mn = fmaxf(mn, sc[k]);
+        const float c = safe_scale(m[h], mn);   // 0 while no row has been seen
+        float p[R], ps = 0.0f;
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+            p[k] = live[k] ? exp2f(sc[k] - mn) : 0.0f;
+            ps += p[k];
+        }
+        l[h] = fmaf(l[h], c, ps);
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            float od = o[h][d] * c;
+#pragma unroll
+            for (int k = 0; k < R; k++) od = fmaf(p[k], v[k][d], od);
+            o[h][d] = od;
+        }
+        m[h] = mn;
     }
     // the wave's 4 lane groups by lane swaps, then the workgroup's 4 waves in LDS
     const uint32_t wv = t >> 6;
