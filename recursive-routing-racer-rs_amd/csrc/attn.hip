@@ -351,17 +351,21 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
 
 uint64_t attention_scratch_bytes() { return ATT_SCRATCH_BYTES; }
 
-// Rows per split: enough splits for about two workgroups per CU, at least 16
-// rows (one per lane group) and at most 16 * ATT_ROWS_PER_GROUP rows each,
-// at most ATT_SPLITS_MAX splits and at most 256 / heads_per_kv (the merge
-// reads one split maximum and sum per thread).
+// Rows per split: as many as the 16 lane groups take (16 * ATT_ROWS_PER_GROUP),
+// so the fewest splits: below that the cross-workgroup merge (partials
+// through the coherent level, a counter, the last workgroup's loads, ~2.5 us)
+// costs more than the longer splits' load phase (64 rows: 4.3 us in one split
+// against 6.9 us in four; 512 rows 7.45 against 8.1 us in 32 splits).  At
+// most ATT_SPLITS_MAX splits, at most 256 / heads_per_kv (the merge reads one
+// split maximum and sum per thread): both hold for seq <= ATT_SEQ_MAX and
+// heads_per_kv <= 8.
 void attention_plan(uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t cus, uint32_t &splits,
                     uint32_t &per)
 {
+    (void)n_kv_heads;
+    (void)cus;
     const uint32_t cap = min(ATT_SPLITS_MAX, 256 / heads_per_kv);
-    const uint32_t want = max(1u, min(cap, (2 * cus + n_kv_heads - 1) / n_kv_heads));
-    const uint32_t least = (seq + 16 * ATT_ROWS_PER_GROUP - 1) / (16 * ATT_ROWS_PER_GROUP);
-    splits = max(least, max(1u, min(want, (seq + 15) / 16)));
+    splits = min(cap, max(1u, (seq + 16 * ATT_ROWS_PER_GROUP - 1) / (16 * ATT_ROWS_PER_GROUP)));
     per = (seq + splits - 1) / splits;
     splits = (seq + per - 1) / per;   // every split has at least one row
 }
