@@ -277,6 +277,17 @@ int rrr_gemm_f16(rrr_ctx *ctx, const rrr_buf *X_f16, const rrr_buf *row_scale, c
  * (nearest even), the input of rrr_gemm_f16 (|y| <= sqrt(d) * max|gamma|). */
 int rrr_rmsnorm_f16(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, rrr_buf *y_f16, uint32_t rows,
                     uint32_t d, float eps);
+/* rrr_gemm_f16 into Y, then rrr_rmsnorm_f16(Y, gamma, y_f16, M, N, eps) of the
+ * updated rows, as one call: the prefill layer's O-proj and FFN-down, whose
+ * residual rows feed the next norm (phi4.rs:1321-1339, :1396-1404 then the
+ * next layer's :1234-1246).  Results bitwise those of the two calls; when K
+ * is split over workgroups the norm is taken inside the split reduction, so
+ * the rows are not read again.  Needs N % 4 == 0 and N <= 8192 besides
+ * rrr_gemm_f16's shape rules.  No counterpart call in the reference (it
+ * runs these as separate dispatches). */
+int rrr_gemm_f16_rmsnorm(rrr_ctx *ctx, const rrr_buf *X_f16, const rrr_buf *row_scale, const rrr_buf *W,
+                         uint32_t type, rrr_buf *Y, uint32_t K, uint32_t N, uint32_t M, uint32_t accumulate,
+                         const rrr_buf *gamma, float eps, rrr_buf *y_f16);
 /* rrr_silu_gate (phi4.rs:1369-1373) in f16 block floating point: row r's f32
  * results v, with max|v| = f * 2^e (f in [0.5, 1)), stored as
  * f16(v * 2^(15 - e)) (nearest even; the scaling is exact) and

@@ -936,6 +936,42 @@ int rrr_gemm_f16(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *row_scale, const
                   what);
 }
 
+int rrr_gemm_f16_rmsnorm(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *row_scale, const rrr_buf *W, uint32_t type,
+                         rrr_buf *Y, uint32_t K, uint32_t N, uint32_t M, uint32_t accumulate, const rrr_buf *gamma,
+                         float eps, rrr_buf *y16)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_gemm_f16_rmsnorm";
+    TRY(check_buf(ctx, X, what));
+    if (row_scale) {
+        TRY(check_buf(ctx, row_scale, what));
+        TRY(need_f32(row_scale, M, what));
+    }
+    TRY(check_buf(ctx, W, what));
+    TRY(check_buf(ctx, Y, what));
+    TRY(check_buf(ctx, gamma, what));
+    TRY(check_buf(ctx, y16, what));
+    TRY(check_shape(type, K, N));
+    if (type == RRR_TYPE_F32) return fail(RRR_ERR_UNSUPPORTED, "%s: F32 weights are not a prefill shape", what);
+    if (M == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: M must be positive", what);
+    if (!(std::isfinite(eps) && eps >= 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: eps must be finite and >= 0", what);
+    TRY(need(W, rrr_tensor_bytes(type, K, N), what));
+    TRY(need(X, (uint64_t)M * K * 2, what));
+    TRY(need_f32(Y, (uint64_t)M * N, what));
+    TRY(need_f32(gamma, N, what));
+    TRY(need(y16, 2ull * M * N, what));
+    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2) || !splitk_reduce_rmsnorm_supported(N))
+        return fail(RRR_ERR_UNSUPPORTED, "%s: needs M %% 128 == 0, N %% 64 == 0 and N <= 8192 (M=%u N=%u)", what, M,
+                    N);
+    TRY(device_ready(ctx));
+    return finish(ctx,
+                  launch_gemm_f16_rmsnorm((const uint16_t *)X->ptr, row_scale ? (const float *)row_scale->ptr : nullptr,
+                                          (const uint8_t *)W->ptr, type, (float *)Y->ptr, K, N, M, accumulate != 0,
+                                          (const float *)gamma->ptr, eps, (uint16_t *)y16->ptr, (float *)ctx->gemm_ws,
+                                          GEMM_WS_BYTES, ctx->stream),
+                  what);
+}
+
 int rrr_rmsnorm_f16(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, rrr_buf *y, uint32_t rows, uint32_t d,
                     float eps)
 {

@@ -444,7 +444,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restric
 
 template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC>
 static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K, uint32_t N,
-                          uint32_t M, uint32_t S, float *ws, hipStream_t s)
+                          uint32_t M, uint32_t S, float *ws, const GemmNorm *nrm, hipStream_t s)
 {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * BK * 2;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
@@ -455,10 +455,21 @@ static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t 
     else
         hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC, false>), dim3(tiles), dim3(512), lds, s, X, W, Y, K,
                            N, M, tiles_n, rscale, K / BK, nullptr);
+    if (S > 1 && nrm) {
+        // the reduction also writes the rows' RMSNorm
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_splitk_reduce_rmsnorm(ws, S, M, N, Y, rscale, ACC, nrm->gamma, nrm->eps, nrm->out, s);
+    }
     if (S > 1) {
         const uint64_t quads = (uint64_t)M * N / 4;
         hipLaunchKernelGGL(gemm_splitk_reduce<ACC>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, ws, S, M,
                            N, Y, rscale);
+    }
+    if (nrm) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_rmsnorm_f16(Y, nrm->gamma, nrm->out, M, N, nrm->eps, s);
     }
     return hipGetLastError();
 }
@@ -479,7 +490,7 @@ static uint32_t gemm_splits(uint32_t tiles, uint32_t K, uint32_t M, uint32_t N, 
 
 template <template <int> class QT, bool XH, bool ACC>
 static hipError_t go_gemm_t(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K,
-                            uint32_t N, uint32_t M, float *ws, size_t ws_bytes, hipStream_t s)
+                            uint32_t N, uint32_t M, float *ws, size_t ws_bytes, const GemmNorm *nrm, hipStream_t s)
 {
     // 256 x 128 tiles when they cover at least half of the CUs, or with K
     // split to do so; else 128 x 64 (with K steps of 128 so each barrier
@@ -487,9 +498,9 @@ static hipError_t go_gemm_t(const uint16_t *X, const float *rscale, const uint8_
     if (M % 256 == 0 && N % 128 == 0) {
         const uint32_t tiles = (N / 128) * (M / 256);
         const uint32_t S = ws ? gemm_splits(tiles, K, M, N, ws_bytes) : 1u;
-        if (tiles * S >= 128) return go_gemm<QT, 256, 128, 64, XH, ACC>(X, rscale, W, Y, K, N, M, S, ws, s);
+        if (tiles * S >= 128) return go_gemm<QT, 256, 128, 64, XH, ACC>(X, rscale, W, Y, K, N, M, S, ws, nrm, s);
     }
-    return go_gemm<QT, 128, 64, 128, XH, ACC>(X, rscale, W, Y, K, N, M, 1, nullptr, s);
+    return go_gemm<QT, 128, 64, 128, XH, ACC>(X, rscale, W, Y, K, N, M, 1, nullptr, nrm, s);
 }
 
 bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t x_bytes)
@@ -500,13 +511,14 @@ bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t 
 
 template <bool XH, bool ACC>
 static hipError_t go_gemm_q(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
-                            uint32_t K, uint32_t N, uint32_t M, float *ws, size_t ws_bytes, hipStream_t s)
+                            uint32_t K, uint32_t N, uint32_t M, float *ws, size_t ws_bytes, hipStream_t s,
+                            const GemmNorm *nrm = nullptr)
 {
     if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2)) return hipErrorNotSupported;
     switch (type) {
-    case T_Q4_K: return go_gemm_t<GqQ4K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, s);
-    case T_Q5_K: return go_gemm_t<GqQ5K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, s);
-    case T_Q6_K: return go_gemm_t<GqQ6K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, s);
+    case T_Q4_K: return go_gemm_t<GqQ4K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, s);
+    case T_Q5_K: return go_gemm_t<GqQ5K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, s);
+    case T_Q6_K: return go_gemm_t<GqQ6K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, s);
     default: return hipErrorNotSupported;
     }
 }
@@ -551,6 +563,16 @@ hipError_t launch_gemm_f16(const uint16_t *X, const float *rscale, const uint8_t
 {
     return accumulate ? go_gemm_q<true, true>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s)
                       : go_gemm_q<true, false>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s);
+}
+
+hipError_t launch_gemm_f16_rmsnorm(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
+                                   uint32_t K, uint32_t N, uint32_t M, bool accumulate, const float *gamma, float eps,
+                                   uint16_t *out16, float *ws, size_t ws_bytes, hipStream_t s)
+{
+    if (!splitk_reduce_rmsnorm_supported(N)) return hipErrorNotSupported;
+    const GemmNorm nrm{gamma, eps, out16};
+    return accumulate ? go_gemm_q<true, true>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s, &nrm)
+                      : go_gemm_q<true, false>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s, &nrm);
 }
 
 }  // namespace rrr

@@ -142,6 +142,21 @@ hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint32_t type, 
 hipError_t launch_gemm_f16(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
                            uint32_t K, uint32_t N, uint32_t M, bool accumulate, float *ws, size_t ws_bytes,
                            hipStream_t s);
+// the same GEMM, then the RMSNorm (gamma, eps) of Y's rows in f16 into out16:
+// with K split, inside the split reduction (splitk_reduce_rmsnorm_kernel),
+// else the rmsnorm launch after the GEMM; N % 4 == 0, N <= 8192
+struct GemmNorm {
+    const float *gamma;
+    float eps;
+    uint16_t *out;
+};
+hipError_t launch_gemm_f16_rmsnorm(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
+                                   uint32_t K, uint32_t N, uint32_t M, bool accumulate, const float *gamma, float eps,
+                                   uint16_t *out16, float *ws, size_t ws_bytes, hipStream_t s);
+bool splitk_reduce_rmsnorm_supported(uint32_t d);
+hipError_t launch_splitk_reduce_rmsnorm(const float *ws, uint32_t S, uint32_t M, uint32_t d, float *Y,
+                                        const float *rscale, bool acc, const float *g, float eps, uint16_t *out,
+                                        hipStream_t s);
 // f16 (round to nearest even) outputs of RMSNorm rows and of silu_gate rows
 // (the latter scaled per row by a power of two, rscale undoing it), the
 // activations of the prefill GEMMs (ops.hip)

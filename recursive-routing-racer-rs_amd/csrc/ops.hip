@@ -149,6 +149,72 @@ hipError_t launch_rmsnorm_f16(const float *x, const float *g, uint16_t *y, uint3
     return hipGetLastError();
 }
 
+// The split-K reduction of a GEMM whose output feeds an RMSNorm (the prefill
+// layer's O-proj and FFN-down, each adding to the residual rows that the next
+// norm reads): one 256-thread workgroup per row m adds the S partials
+// ws[k][m][:] in split order, applies the row scale, adds the row of Y when
+// `acc`, stores it to Y (what gemm_splitk_reduce stores) and writes the
+// row's RMSNorm with gamma in f16, the arithmetic and canonical sum-of-squares
+// order of rmsnorm_kernel<_Float16> over the stored row, so both outputs are
+// bitwise the two launches'.  d % 4 == 0, d <= 8192.
+__global__ __launch_bounds__(256) void splitk_reduce_rmsnorm_kernel(const float *__restrict__ ws, uint32_t S,
+                                                                    uint32_t M, uint32_t d, float *__restrict__ Y,
+                                                                    const float *__restrict__ rscale, uint32_t acc,
+                                                                    const float *__restrict__ g, float eps,
+                                                                    _Float16 *__restrict__ out)
+{
+    __shared__ float red[16];
+    const uint32_t m = blockIdx.x, nf = d / 4;
+    const uint64_t mn = (uint64_t)M * d;
+    float4 *yr = (float4 *)(Y + (uint64_t)m * d);
+    const float4 *wr = (const float4 *)(ws + (uint64_t)m * d);
+    const float r = rscale ? rscale[m] : 1.0f;
+    uint32_t f[8], sl[8];
+    sumsq_slots<8>(sumsq_parts(d), f, sl);
+    float4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (f[j] < nf) {
+            float4 a = wr[f[j]];
+            for (uint32_t k = 1; k < S; k++) {
+                const float4 p = ((const float4 *)(ws + k * mn + (uint64_t)m * d))[f[j]];
+                a.x += p.x; a.y += p.y; a.z += p.z; a.w += p.w;
+            }
+            if (rscale) {
+                a.x *= r; a.y *= r; a.z *= r; a.w *= r;
+            }
+            if (acc) {
+                const float4 o = yr[f[j]];
+                a.x = o.x + a.x; a.y = o.y + a.y; a.z = o.z + a.z; a.w = o.w + a.w;
+            }
+            yr[f[j]] = a;
+            v[j] = a;
+        }
+    }
+    const float inv = rms_inv(sumsq_held_256<8>(v, f, sl, nf, red), d, eps);
+    _Float16 *orow = out + (uint64_t)m * d;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (f[j] < nf) {
+            const float4 w = ((const float4 *)g)[f[j]];
+            store4(orow, f[j], make_float4(__fmul_rn(__fmul_rn(w.x, v[j].x), inv), __fmul_rn(__fmul_rn(w.y, v[j].y), inv),
+                                           __fmul_rn(__fmul_rn(w.z, v[j].z), inv), __fmul_rn(__fmul_rn(w.w, v[j].w), inv)));
+        }
+    }
+}
+
+bool splitk_reduce_rmsnorm_supported(uint32_t d) { return d % 4 == 0 && d <= 8 * 4 * 256; }
+
+hipError_t launch_splitk_reduce_rmsnorm(const float *ws, uint32_t S, uint32_t M, uint32_t d, float *Y,
+                                        const float *rscale, bool acc, const float *g, float eps, uint16_t *out,
+                                        hipStream_t s)
+{
+    hipLaunchKernelGGL(splitk_reduce_rmsnorm_kernel, dim3(M), dim3(256), 0, s, ws, S, M, d, Y, rscale, acc ? 1u : 0u,
+                       g, eps, (_Float16 *)out);
+    return hipGetLastError();
+}
+
 // silu_gate (phi4.rs:1369-1373): rows of [gate(F) | up(F)] -> rows of F (f32,
 // or the same values rounded to f16).
 template <typename TO>

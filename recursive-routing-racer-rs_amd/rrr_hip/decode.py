@@ -242,6 +242,9 @@ class DecodeSweep:
         # one launch (rrr_gemv_rmsnorm_rope_kv); False: the two launches
         # (the same values bit for bit)
         self.rope_fused = True
+        # prefill: the O-proj and FFN-down GEMMs write the next RMSNorm's f16
+        # rows in the same call (rrr_gemm_f16_rmsnorm); False: separate calls
+        self.prefill_fused = True
         self.logits = ctx.alloc(shape.vocab * 4)
         self.token = ctx.alloc(4)
         self.attention = attention
@@ -472,22 +475,33 @@ class DecodeSweep:
         Mp, d, F = pf["Mp"], s.d_model, s.ffn_dim
         if M < Mp:   # rows past the prompt stay zero through every step
             c.fill_u32(pf["att16"], 0, M * d * 2, (Mp - M) * d * 2)
+        fused = self.prefill_fused
         for i, L in enumerate(self.layers):
             T = L["types"]
             kc, vc = self.kv[i]
-            c.rmsnorm_f16(pf["hid"], L["attn_norm"], pf["n16"], Mp, d, s.eps)
+            if i == 0 or not fused:   # else the previous layer's down GEMM wrote this norm
+                c.rmsnorm_f16(pf["hid"], L["attn_norm"], pf["n16"], Mp, d, s.eps)
             c.gemm_f16(pf["n16"], L["attn_qkv"], T["attn_qkv"], pf["qkv"], d, s.qkv_dim, Mp)
             c.rope_kv_store_rows(pf["qkv"], M, self.rope_factors, self.n_rope_factors, kc, vc, pos0, s.n_heads,
                                  s.n_kv_heads, s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta,
                                  s.rope_attn_factor)
             c.attention_prefill(pf["qkv"], M, kc, vc, pf["att16"], pos0, s.n_kv_heads, s.heads_per_kv, s.head_dim,
                                 out_type=E.F16)
-            c.gemm_f16(pf["att16"], L["attn_output"], T["attn_output"], pf["hid"], d, d, Mp, accumulate=True)
-            c.rmsnorm_f16(pf["hid"], L["ffn_norm"], pf["n16"], Mp, d, s.eps)
+            if fused:
+                c.gemm_f16_rmsnorm(pf["att16"], L["attn_output"], T["attn_output"], pf["hid"], d, d, Mp,
+                                   L["ffn_norm"], pf["n16"], s.eps, accumulate=True)
+            else:
+                c.gemm_f16(pf["att16"], L["attn_output"], T["attn_output"], pf["hid"], d, d, Mp, accumulate=True)
+                c.rmsnorm_f16(pf["hid"], L["ffn_norm"], pf["n16"], Mp, d, s.eps)
             c.gemm_f16(pf["n16"], L["ffn_up"], T["ffn_up"], pf["gu"], d, 2 * F, Mp)
             c.silu_gate_f16(pf["gu"], pf["mid16"], pf["mid_scale"], Mp, F)
-            c.gemm_f16(pf["mid16"], L["ffn_down"], T["ffn_down"], pf["hid"], F, d, Mp, accumulate=True,
-                       row_scale=pf["mid_scale"])
+            if fused and i + 1 < len(self.layers):   # the next layer's attention norm with it
+                c.gemm_f16_rmsnorm(pf["mid16"], L["ffn_down"], T["ffn_down"], pf["hid"], F, d, Mp,
+                                   self.layers[i + 1]["attn_norm"], pf["n16"], s.eps, accumulate=True,
+                                   row_scale=pf["mid_scale"])
+            else:
+                c.gemm_f16(pf["mid16"], L["ffn_down"], T["ffn_down"], pf["hid"], F, d, Mp, accumulate=True,
+                           row_scale=pf["mid_scale"])
         if M not in pf["last"]:
             pf["last"][M] = c.view(pf["hid"], (M - 1) * d * 4, d * 4)
         hidden, self.hidden = self.hidden, pf["last"][M]

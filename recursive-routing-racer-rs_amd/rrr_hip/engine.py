@@ -269,6 +269,10 @@ class Context:
         _check(self.lib.rrr_gemm_f16(self._h, X._h, row_scale._h if row_scale is not None else None, W._h, qtype,
                                      Y._h, K, N, M, 1 if accumulate else 0))
 
+    def gemm_f16_rmsnorm(self, X, W, qtype, Y, K, N, M, gamma, y16, eps=1e-5, accumulate=False, row_scale=None):
+        _check(self.lib.rrr_gemm_f16_rmsnorm(self._h, X._h, row_scale._h if row_scale is not None else None, W._h,
+                                             qtype, Y._h, K, N, M, 1 if accumulate else 0, gamma._h, eps, y16._h))
+
     def rmsnorm_f16(self, x, gamma, y, rows, d, eps=1e-5):
         _check(self.lib.rrr_rmsnorm_f16(self._h, x._h, gamma._h, y._h, rows, d, eps))
 

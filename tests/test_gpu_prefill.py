@@ -274,6 +274,34 @@ def test_gemm_f16_row_scale(ctx, M):
         b.free()
 
 
+# (K, N, M): split K (O-proj 4 ways, the down shape 4 ways, QKV 3 ways) and
+# a 128-row prompt on 128 x 64 tiles (no split: the norm is its own launch)
+@pytest.mark.parametrize("qtype,K,N,M,acc,scaled", [(rrr_hip.Q4_K, 3072, 3072, 512, True, False),
+                                                    (rrr_hip.Q6_K, 8192, 3072, 512, True, True),
+                                                    (rrr_hip.Q5_K, 3072, 5120, 512, False, False),
+                                                    (rrr_hip.Q4_K, 3072, 3072, 128, True, False)])
+def test_gemm_f16_rmsnorm_is_the_two_calls(ctx, qtype, K, N, M, acc, scaled):
+    """rrr_gemm_f16_rmsnorm = rrr_gemm_f16 then rrr_rmsnorm_f16 of the rows,
+    bit for bit: Y and the f16 norm rows."""
+    raw = synth.weight(7, 90, qtype, K, N)
+    X = f16r(synth.normal_f32(7, 91, M * K).reshape(M, K))
+    rs = np.ldexp(np.float32(1.0), np.random.default_rng(9).integers(-8, 8, M)).astype(np.float32)
+    Y0 = synth.normal_f32(7, 92, M * N, 0.0, 3.0)
+    g = synth.normal_f32(7, 93, N, 1.0, 0.1)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    xb, rb, gb = ctx.to_device(X.astype(np.float16).view(np.uint16)), ctx.to_device(rs), ctx.to_device(g)
+    ya, yb = ctx.to_device(Y0), ctx.to_device(Y0)
+    na, nb = ctx.alloc(M * N * 2), ctx.alloc(M * N * 2)
+    rsb = rb if scaled else None
+    ctx.gemm_f16(xb, W, qtype, ya, K, N, M, accumulate=acc, row_scale=rsb)
+    ctx.rmsnorm_f16(ya, gb, na, M, N, 1e-5)
+    ctx.gemm_f16_rmsnorm(xb, W, qtype, yb, K, N, M, gb, nb, 1e-5, accumulate=acc, row_scale=rsb)
+    assert np.array_equal(ctx.download(yb, np.uint32, M * N), ctx.download(ya, np.uint32, M * N))
+    assert np.array_equal(ctx.download(nb, np.uint16, M * N), ctx.download(na, np.uint16, M * N))
+    for b in (W, xb, rb, gb, ya, yb, na, nb):
+        b.free()
+
+
 def oracle_prefill(s, host, prompt, pos0, caches):
     """The prefill composed in the oracle: fp64 GEMMs and attention, the f32
     restatement of RoPE and the f16 cache store, the GEMM inputs rounded to
@@ -360,3 +388,26 @@ def test_prefill_graph_replay_matches_eager(ctx, sweep):
         assert np.array_equal(hid.view(np.uint32), hid0.view(np.uint32))
         assert np.array_equal(logits.view(np.uint32), logits0.view(np.uint32))
     g.destroy()
+
+
+def test_prefill_fused_norms_are_the_separate_calls(ctx, sweep):
+    """record_prefill with the O-proj / FFN-down GEMMs writing the next norm
+    (rrr_gemm_f16_rmsnorm) equals the separate GEMM and RMSNorm calls bit for
+    bit: hidden rows, logits and the cached K/V."""
+    s, M = SHAPE, 130
+    prompt = decode.prompt_host(5, s, M)
+    out = []
+    for fused in (False, True):
+        sweep.prefill_fused = fused
+        sweep.load_prompt(prompt)
+        sweep.record_prefill(M, 0)
+        ctx.sync()
+        logits, tok, hid = sweep.prefill_results(M)
+        kv = [ctx.download(kc, np.uint16, M * s.kv_stride) for kc, _ in sweep.kv]
+        out.append((logits, tok, hid, kv))
+    sweep.prefill_fused = True
+    (l0, t0, h0, kv0), (l1, t1, h1, kv1) = out
+    assert t0 == t1
+    assert np.array_equal(h0.view(np.uint32), h1.view(np.uint32))
+    assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
+    assert all(np.array_equal(a, b) for a, b in zip(kv0, kv1))
