@@ -369,13 +369,6 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int j = 0; j < BPW; j++) issue(j, 0);
-    // ROPE: the position's rotation coefficients, one pair per thread, while
-    // the weights are in flight (read after the final barrier)
-    float *coef = part + ntl * W * 16;
-    if constexpr (ROPE) {
-        if (t < a.rope.rope_dim / 2) rope_coef(t, a.rope.pos, a.rope, coef[2 * t], coef[2 * t + 1]);
-    }
-
     // 2. fused RMSNorm: the wave's slice of x is slice `wave` of the canonical
     // sum-of-squares split (BPW float4s per lane is its P = ceil(K / 4096)
     // for K <= 8192); the slice sums are added in wave order (waves without
@@ -448,6 +441,15 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         for (int j = 0; j < AJ; j++)
 #pragma unroll
             for (int u = 0; u < 4; u++) av[j][u] = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
+    }
+
+    // ROPE: the position's rotation coefficients, one pair per thread (read
+    // after the final barrier), here where the wave would wait for its first
+    // weight block anyway: computed before the RMSNorm barrier, they held
+    // every wave back by their latency
+    float *coef = part + ntl * W * 16;
+    if constexpr (ROPE) {
+        if (t < a.rope.rope_dim / 2) rope_coef(t, a.rope.pos, a.rope, coef[2 * t], coef[2 * t + 1]);
     }
 
     // 4. per tile, block by block: the block's units to LDS (its registers
