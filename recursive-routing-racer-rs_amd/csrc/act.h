@@ -28,7 +28,7 @@ __device__ __forceinline__ uint32_t f16_bits(float v) { return __builtin_bit_cas
 
 // apply_rope_cfg (phi4.rs:238-256) in f32, pair j of a head at position
 // pos: the coefficients (cos and sin of the angle, scaled by attn_factor)
-// and the rotation; rope_pair is the two in order.
+// and the rotation, applied in that order.
 __device__ __forceinline__ void rope_coef(uint32_t j, uint32_t pos, const RopeArgs &r, float &cs, float &ss)
 {
     const float base_freq = 1.0f / powf(r.theta, 2.0f * (float)j / (float)r.rope_dim);
@@ -46,13 +46,6 @@ __device__ __forceinline__ void rope_rotate(float &x0, float &x1, float cs, floa
     const float a = x0, b = x1;
     x0 = a * cs - b * ss;
     x1 = a * ss + b * cs;
-}
-
-__device__ __forceinline__ void rope_pair(float &x0, float &x1, uint32_t j, uint32_t pos, const RopeArgs &r)
-{
-    float cs, ss;
-    rope_coef(j, pos, r, cs, ss);
-    rope_rotate(x0, x1, cs, ss);
 }
 
 // rope_kv_store (rope_kv_store_kernel, attn.hip) of the qkv row pair (row,

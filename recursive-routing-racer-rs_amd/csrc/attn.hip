@@ -7,49 +7,74 @@
 namespace rrr {
 
 // Token blockIdx.y (position pos + blockIdx.y, its qkv row_stride floats
-// after the previous one's).  Threads [0, nq): the Q rotation pairs (head
-// i / (rope_dim/2), pair i % (rope_dim/2)), rotated in place.  Threads
-// [nq, nq + kv_stride/2): element pair 2p of K (rotated in place when it lies
-// in its head's first rope_dim dims) and of V, both stored as f16 into the
-// token's row of the caches.
+// after the previous one's).  Work items [0, nq): the Q rotation pairs (head
+// i / (rope_dim/2), pair i % (rope_dim/2)), rotated in place.  Items [nq, nq +
+// kv_stride/2): element pair 2p of K (rotated in place when it lies in its
+// head's first rope_dim dims) and of V, both stored as f16 into the token's
+// row of the caches.  The position's rope_dim/2 coefficient pairs (shared by
+// every Q and K head) are computed once per workgroup into LDS when `lds_coef`
+// (rope_coef, the same values), else per item.
 __global__ __launch_bounds__(256) void rope_kv_store_kernel(float *__restrict__ qkv, RopeArgs r, uint32_t *__restrict__ kc,
-                                                            uint32_t *__restrict__ vc)
+                                                            uint32_t *__restrict__ vc, uint32_t lds_coef)
 {
+    extern __shared__ float cf[];   // pair j at cf[2j], cf[2j + 1]
     const uint32_t half_rope = r.rope_dim / 2;
     const uint32_t nq = r.n_heads * half_rope, nkv = r.kv_stride / 2;
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x, pos = r.pos + blockIdx.y;
+    const uint32_t pos = r.pos + blockIdx.y;
     qkv += (size_t)blockIdx.y * r.row_stride;
-    if (i < nq) {
-        const uint32_t h = i / half_rope, j = i - h * half_rope;
-        float *p = qkv + (size_t)h * r.head_dim + 2 * j;
-        float x0 = p[0], x1 = p[1];
-        rope_pair(x0, x1, j, pos, r);
-        p[0] = x0;
-        p[1] = x1;
-    } else if (i < nq + nkv) {
-        const uint32_t e = 2 * (i - nq);
-        float *k = qkv + r.q_dim + e;
-        const float *v = qkv + r.q_dim + r.kv_stride + e;
-        float k0 = k[0], k1 = k[1];
-        const uint32_t d = r.rope_dim ? e % r.head_dim : 0u;   // head_dim is 0 in the kv_store form
-        if (d < r.rope_dim) {
-            rope_pair(k0, k1, d / 2, pos, r);
-            k[0] = k0;
-            k[1] = k1;
+    if (lds_coef) {
+        for (uint32_t j = threadIdx.x; j < half_rope; j += 256) rope_coef(j, pos, r, cf[2 * j], cf[2 * j + 1]);
+        __syncthreads();
+    }
+    auto coef = [&](uint32_t j, float &cs, float &ss) {
+        if (lds_coef) {
+            cs = cf[2 * j];
+            ss = cf[2 * j + 1];
+        } else {
+            rope_coef(j, pos, r, cs, ss);
         }
-        const size_t w = ((size_t)pos * r.kv_stride + e) / 2;
-        kc[w] = f16_bits(k0) | (f16_bits(k1) << 16);
-        vc[w] = f16_bits(v[0]) | (f16_bits(v[1]) << 16);
+    };
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < nq + nkv; i += gridDim.x * 256) {
+        if (i < nq) {
+            const uint32_t h = i / half_rope, j = i - h * half_rope;
+            float *p = qkv + (size_t)h * r.head_dim + 2 * j;
+            float x0 = p[0], x1 = p[1], cs, ss;
+            coef(j, cs, ss);
+            rope_rotate(x0, x1, cs, ss);
+            p[0] = x0;
+            p[1] = x1;
+        } else {
+            const uint32_t e = 2 * (i - nq);
+            float *k = qkv + r.q_dim + e;
+            const float *v = qkv + r.q_dim + r.kv_stride + e;
+            float k0 = k[0], k1 = k[1];
+            const uint32_t d = r.rope_dim ? e % r.head_dim : 0u;   // head_dim is 0 in the kv_store form
+            if (d < r.rope_dim) {
+                float cs, ss;
+                coef(d / 2, cs, ss);
+                rope_rotate(k0, k1, cs, ss);
+                k[0] = k0;
+                k[1] = k1;
+            }
+            const size_t w = ((size_t)pos * r.kv_stride + e) / 2;
+            kc[w] = f16_bits(k0) | (f16_bits(k1) << 16);
+            vc[w] = f16_bits(v[0]) | (f16_bits(v[1]) << 16);
+        }
     }
 }
 
+// Rows of many tokens: one workgroup per token walking its items (its
+// coefficients computed once); a few tokens: a workgroup per 256 items.
 hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uint16_t *vc, hipStream_t s,
                                 uint32_t rows)
 {
     const uint32_t n = r.n_heads * (r.rope_dim / 2) + r.kv_stride / 2;
     if (n == 0 || rows == 0) return hipSuccess;
-    hipLaunchKernelGGL(rope_kv_store_kernel, dim3((n + 255) / 256, rows), dim3(256), 0, s, qkv, r, (uint32_t *)kc,
-                       (uint32_t *)vc);
+    const size_t lds = (size_t)r.rope_dim * 4;
+    const uint32_t lds_coef = lds <= 32 * 1024 ? 1u : 0u;
+    const uint32_t bx = rows >= 64 ? 1u : (n + 255) / 256;
+    hipLaunchKernelGGL(rope_kv_store_kernel, dim3(bx, rows), dim3(256), lds_coef ? lds : 0, s, qkv, r, (uint32_t *)kc,
+                       (uint32_t *)vc, lds_coef);
     return hipGetLastError();
 }
 
