@@ -108,27 +108,6 @@ __device__ __forceinline__ float row16_sum(float v)
     return v;
 }
 
-// The values of v in lane (lane & ~X) and in lane (lane | X), X = 16 or 32,
-// by the gfx950 lane swaps (VALU, no LDS round trip): v_permlane16_swap
-// exchanges the odd 16-lane rows of its first operand with the even rows of
-// its second, v_permlane32_swap the upper half of the first with the lower
-// half of the second, so with both operands v the results are v of the
-// lower and of the upper partner.
-template <int X>
-__device__ __forceinline__ void lane_pair(float v, float &lo, float &hi)
-{
-    const uint32_t u = __float_as_uint(v);
-    if constexpr (X == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        lo = __uint_as_float(r[0]);
-        hi = __uint_as_float(r[1]);
-    } else {
-        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        lo = __uint_as_float(r[0]);
-        hi = __uint_as_float(r[1]);
-    }
-}
-
 // Online-softmax state {m, l, o[8]} of lanes (lane & ~X) and (lane | X)
 // merged, lower partner first: both lanes end with the same state.
 template <int X>
@@ -146,24 +125,6 @@ __device__ __forceinline__ void merge_pair(float &m, float &l, float (&o)[8])
         o[d] = o0 * c0 + o1 * c1;
     }
     m = M;
-}
-
-// Maximum / sum of v over the lanes l, l ^ 16, l ^ 32, l ^ 48 by the lane
-// swaps (VALU, no LDS round trip); every lane of the four gets the same
-// value, and the sum is the one the xor-16 then xor-32 butterfly gives.
-__device__ __forceinline__ float lanes4_max(float v)
-{
-    float a, b;
-    lane_pair<16>(v, a, b);
-    lane_pair<32>(fmaxf(a, b), a, b);
-    return fmaxf(a, b);
-}
-__device__ __forceinline__ float lanes4_sum(float v)
-{
-    float a, b;
-    lane_pair<16>(v, a, b);
-    lane_pair<32>(a + b, a, b);
-    return a + b;
 }
 
 template <int HPK>

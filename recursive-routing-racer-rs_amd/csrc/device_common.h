@@ -89,6 +89,45 @@ __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s
     mn = ((v >> (8u - 4u * h)) & 15u) | (((v >> (12u + 2u * h)) & 3u) << 4);
 }
 
+// The values of v in lane (lane & ~X) and in lane (lane | X), X = 16 or 32,
+// by the gfx950 lane swaps (VALU, no LDS round trip): v_permlane16_swap
+// exchanges the odd 16-lane rows of its first operand with the even rows of
+// its second, v_permlane32_swap the upper half of the first with the lower
+// half of the second, so with both operands v the results are v of the
+// lower and of the upper partner.
+template <int X>
+__device__ __forceinline__ void lane_pair(float v, float &lo, float &hi)
+{
+    const uint32_t u = __float_as_uint(v);
+    if constexpr (X == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        lo = __uint_as_float(r[0]);
+        hi = __uint_as_float(r[1]);
+    }
+}
+
+// Maximum / sum of v over the lanes l, l ^ 16, l ^ 32, l ^ 48 by the lane
+// swaps (VALU, no LDS round trip); every lane of the four gets the same
+// value, and the sum is the one the xor-16 then xor-32 butterfly gives.
+__device__ __forceinline__ float lanes4_max(float v)
+{
+    float a, b;
+    lane_pair<16>(v, a, b);
+    lane_pair<32>(fmaxf(a, b), a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float lanes4_sum(float v)
+{
+    float a, b;
+    lane_pair<16>(v, a, b);
+    lane_pair<32>(a + b, a, b);
+    return a + b;
+}
+
 // Deterministic full-wave sum: fixed butterfly order, identical on every call.
 __device__ __forceinline__ float wave_sum(float v)
 {

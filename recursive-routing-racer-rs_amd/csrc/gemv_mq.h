@@ -288,6 +288,20 @@ constexpr uint32_t MQ_OOB = 0x80000000u;
 // row's value is the sum a plain launch stores.  The rope_dim rotation
 // coefficients sit in LDS past the row partials (the launcher adds their
 // rope_dim floats).
+// Sum of the W <= 16 wave partials p[0], p[16], ..., p[16 (W - 1)] in wave
+// order, every one requested from LDS before the first add (one LDS wait
+// instead of one per wave).
+__device__ __forceinline__ float waves_sum(const float *p, uint32_t W)
+{
+    float q[16];
+#pragma unroll
+    for (uint32_t w = 0; w < 16; w++) q[w] = p[16 * min(w, W - 1)];
+    float v = q[0];
+#pragma unroll
+    for (uint32_t w = 1; w < 16; w++) v = w < W ? v + q[w] : v;
+    return v;
+}
+
 template <class Q, int BPW, int ACT, bool MULTI, int TR = 16, bool PAIR = false, bool ROPE = false>
 __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr)
 {
@@ -501,9 +515,8 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
                 if constexpr (Q::HAS_MIN) acc = fmaf(-dmin, acc_m, acc);
             }
         }
-        // the 4 k-groups of a row (lanes n, n+16, n+32, n+48)
-        acc = acc + __shfl_xor(acc, 16, 64);
-        acc = acc + __shfl_xor(acc, 32, 64);
+        // the 4 k-groups of a row (lanes n, n+16, n+32, n+48), by lane swaps
+        acc = lanes4_sum(acc);
         if (lane < 16) part[(tl * W + wave) * 16 + lane] = acc;
     };
     if constexpr (MULTI) {
@@ -519,12 +532,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
             const uint32_t q = i >> 4, r = i & 15, row = (tile0 + q * GR) * 16 + r;
             if (row < a.N) {
                 const float *pg = part + 2 * q * W * 16 + r, *pu = pg + W * 16;
-                float gv = pg[0], uv = pu[0];
-                for (uint32_t w = 1; w < W; w++) {
-                    gv += pg[w * 16];
-                    uv += pu[w * 16];
-                }
-                a.y[row] = silu_fast(gv) * uv;
+                a.y[row] = silu_fast(waves_sum(pg, W)) * waves_sum(pu, W);
             }
         }
         return;
@@ -534,12 +542,8 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         for (uint32_t i = t; i < ntl * 8; i += NT) {
             const uint32_t tl = i >> 3, r = 2 * (i & 7), row = (tile0 + tl * GR) * tr + r;
             if (r < tr && row < a.N) {
-                float v0 = part[tl * W * 16 + r], v1 = part[tl * W * 16 + r + 1];
-                for (uint32_t w = 1; w < W; w++) {
-                    v0 += part[(tl * W + w) * 16 + r];
-                    v1 += part[(tl * W + w) * 16 + r + 1];
-                }
-                rope_store_pair(a, row, v0, v1, coef);
+                rope_store_pair(a, row, waves_sum(part + tl * W * 16 + r, W), waves_sum(part + tl * W * 16 + r + 1, W),
+                                coef);
             }
         }
         return;
@@ -547,8 +551,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     for (uint32_t i = t; i < ntl * 16; i += NT) {
         const uint32_t tl = i >> 4, r = i & 15, row = (tile0 + tl * GR) * tr + r;
         if (r < tr && row < a.N) {
-            float v = part[tl * W * 16 + r];
-            for (uint32_t w = 1; w < W; w++) v += part[(tl * W + w) * 16 + r];
+            float v = waves_sum(part + tl * W * 16 + r, W);
             if (a.residual) v = (i == t ? yres : a.y[row]) + v;
             a.y[row] = v;
         }

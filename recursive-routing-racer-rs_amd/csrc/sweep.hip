@@ -369,8 +369,7 @@ __device__ __forceinline__ void sw_compute_op(const SwOpDev &o, uint32_t w, uint
                 acc = fmaf(d, acc_s, acc);
                 if constexpr (Q::HAS_MIN) acc = fmaf(-dmin, acc_m, acc);
             }
-            acc = acc + __shfl_xor(acc, 16, 64);
-            acc = acc + __shfl_xor(acc, 32, 64);
+            acc = lanes4_sum(acc);
             if (lane < 16) part[(tl * SW_CW + w) * 16 + lane] = acc;
         }
     }
