@@ -144,8 +144,8 @@ def batched_tol(qtype, K, M):
     return MFMA_TOL if qtype in (12, 13) and 16 < M <= 32 and K <= 3072 else TOL
 
 
-@pytest.mark.parametrize("qtype,K,N", [(12, 3072, 16384), (13, 3072, 5120), (14, 8192, 3072), (0, 3072, 2048),
-                                       (12, 512, 37), (13, 4096, 300)])
+@pytest.mark.parametrize("qtype,K,N", [(12, 3072, 16384), (13, 3072, 5120), (12, 3072, 3072), (14, 8192, 3072),
+                                       (0, 3072, 2048), (12, 512, 37), (13, 4096, 300)])
 @pytest.mark.parametrize("M", [2, 3, 4, 8, 13, 16, 17, 32])
 def test_batched_gemv_parity(ctx, qtype, K, N, M):
     raw = weights(qtype, K, N, seed=6, stream=qtype)
