@@ -288,6 +288,19 @@ int rrr_rmsnorm_f16(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, rrr_bu
 int rrr_gemm_f16_rmsnorm(rrr_ctx *ctx, const rrr_buf *X_f16, const rrr_buf *row_scale, const rrr_buf *W,
                          uint32_t type, rrr_buf *Y, uint32_t K, uint32_t N, uint32_t M, uint32_t accumulate,
                          const rrr_buf *gamma, float eps, rrr_buf *y_f16);
+/* The prompt's QKV step (phi4.rs:1257-1268 batched matmul, then the
+ * per-token rope_kv_store dispatches of :1285-1298): qkv = X . W^T as
+ * rrr_gemm_f16 (accumulate 0, no row scale; N = q_dim + 2 * kv_stride, M
+ * rows), then rrr_rope_kv_store_rows of its first `rows` rows at positions
+ * pos0 .. (same RoPE arguments and checks).  With K split over workgroups
+ * the split reduction and the RoPE + KV store are one launch.  qkv and the
+ * caches end bit for bit as after those two calls.  q_dim and kv_stride
+ * % 4 == 0, qkv 16-byte aligned.  No counterpart call in the reference. */
+int rrr_gemm_f16_rope_kv_rows(rrr_ctx *ctx, const rrr_buf *X_f16, const rrr_buf *W, uint32_t type, rrr_buf *qkv,
+                              uint32_t K, uint32_t M, uint32_t rows, const rrr_buf *rope_factors,
+                              uint32_t n_factors, rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos0,
+                              uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t rope_dim,
+                              uint32_t q_dim, uint32_t kv_stride, float theta, float attn_factor);
 /* rrr_silu_gate (phi4.rs:1369-1373) in f16 block floating point: row r's f32
  * results v, with max|v| = f * 2^e (f in [0.5, 1)), stored as
  * f16(v * 2^(15 - e)) (nearest even; the scaling is exact) and

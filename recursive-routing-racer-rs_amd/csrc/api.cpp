@@ -972,6 +972,38 @@ int rrr_gemm_f16_rmsnorm(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *row_scal
                   what);
 }
 
+int rrr_gemm_f16_rope_kv_rows(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t type, rrr_buf *qkv,
+                              uint32_t K, uint32_t M, uint32_t rows, const rrr_buf *rope_factors, uint32_t n_factors,
+                              rrr_buf *k_cache, rrr_buf *v_cache, uint32_t pos0, uint32_t n_heads,
+                              uint32_t n_kv_heads, uint32_t head_dim, uint32_t rope_dim, uint32_t q_dim,
+                              uint32_t kv_stride, float theta, float attn_factor)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_gemm_f16_rope_kv_rows";
+    if (rows > M) return fail(RRR_ERR_BAD_SHAPE, "%s: rows=%u exceeds M=%u", what, rows, M);
+    RopeArgs r;
+    TRY(rope_check(ctx, qkv, rows, rope_factors, n_factors, k_cache, v_cache, pos0, n_heads, n_kv_heads, head_dim,
+                   rope_dim, q_dim, kv_stride, theta, attn_factor, what, r));
+    const uint32_t N = r.row_stride;
+    TRY(check_buf(ctx, X, what));
+    TRY(check_buf(ctx, W, what));
+    TRY(check_shape(type, K, N));
+    if (type == RRR_TYPE_F32) return fail(RRR_ERR_UNSUPPORTED, "%s: F32 weights are not a prefill shape", what);
+    TRY(need(W, rrr_tensor_bytes(type, K, N), what));
+    TRY(need(X, (uint64_t)M * K * 2, what));
+    TRY(need_f32(qkv, (uint64_t)M * N, what));
+    if ((uintptr_t)qkv->ptr & 15) return fail(RRR_ERR_INVALID_ARG, "%s: qkv must be 16-byte aligned", what);
+    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2) || !splitk_rope_kv_store_supported(r))
+        return fail(RRR_ERR_UNSUPPORTED, "%s: needs M %% 128 == 0, N %% 64 == 0, q_dim and kv_stride %% 4 == 0 "
+                    "(M=%u N=%u)", what, M, N);
+    TRY(device_ready(ctx));
+    return finish(ctx,
+                  launch_gemm_f16_rope_kv((const uint16_t *)X->ptr, (const uint8_t *)W->ptr, type, (float *)qkv->ptr, K,
+                                          N, M, r, rows, (uint16_t *)k_cache->ptr, (uint16_t *)v_cache->ptr,
+                                          (float *)ctx->gemm_ws, GEMM_WS_BYTES, ctx->stream),
+                  what);
+}
+
 int rrr_rmsnorm_f16(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, rrr_buf *y, uint32_t rows, uint32_t d,
                     float eps)
 {

@@ -78,6 +78,104 @@ hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uin
     return hipGetLastError();
 }
 
+// The prompt's QKV rows from the K-split GEMM's partials: element (m, c) is
+// the sum of ws[k][m][c] over the S splits in split order (as
+// gemm_splitk_reduce adds them), then the rope_kv_store of the row: every
+// element of qkv, and the caches, end bit for bit as after the reduction
+// followed by rope_kv_store_kernel.  Rows m >= rows (the GEMM's padding rows)
+// get the plain sums.  Four elements (two pairs) a thread; the launcher
+// requires q_dim, kv_stride and row_stride (= the GEMM's N) % 4 == 0, so a
+// quad never straddles the Q, K and V parts.
+__global__ __launch_bounds__(256) void splitk_rope_kv_store_kernel(const float *__restrict__ ws, uint32_t S, uint32_t M,
+                                                                   float *__restrict__ qkv, RopeArgs r, uint32_t rows,
+                                                                   uint32_t *__restrict__ kc, uint32_t *__restrict__ vc,
+                                                                   uint32_t lds_coef)
+{
+    extern __shared__ float cf[];   // pair j at cf[2j], cf[2j + 1]
+    const uint32_t N = r.row_stride, m = blockIdx.y, half_rope = r.rope_dim / 2;
+    const uint32_t pos = r.pos + m, qh = r.n_heads * r.head_dim;
+    const bool live = m < rows;
+    const uint64_t mn = (uint64_t)M * N;
+    const float *src = ws + (uint64_t)m * N;
+    float *dst = qkv + (uint64_t)m * N;
+    if (lds_coef && live) {
+        for (uint32_t j = threadIdx.x; j < half_rope; j += 256) rope_coef(j, pos, r, cf[2 * j], cf[2 * j + 1]);
+        __syncthreads();
+    }
+    auto coef = [&](uint32_t j, float &cs, float &ss) {
+        if (lds_coef) {
+            cs = cf[2 * j];
+            ss = cf[2 * j + 1];
+        } else {
+            rope_coef(j, pos, r, cs, ss);
+        }
+    };
+    for (uint32_t c = 4 * (blockIdx.x * 256 + threadIdx.x); c < N; c += 4 * gridDim.x * 256) {
+        float4 v = *(const float4 *)(src + c);
+        for (uint32_t k = 1; k < S; k++) {
+            const float4 p = *(const float4 *)(src + k * mn + c);
+            v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+        }
+        if (live) {
+            float x[4] = {v.x, v.y, v.z, v.w};
+            if (c < r.q_dim) {
+                // Q: pair j of a head rotated for j < rope_dim / 2
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t e = c + 2 * h;
+                    if (e < qh) {
+                        const uint32_t j = (e % r.head_dim) / 2;
+                        if (j < half_rope) {
+                            float cs, ss;
+                            coef(j, cs, ss);
+                            rope_rotate(x[2 * h], x[2 * h + 1], cs, ss);
+                        }
+                    }
+                }
+            } else if (c < r.q_dim + r.kv_stride) {
+                // K: rotated dims below rope_dim of each head, stored in row pos
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t e = c - r.q_dim + 2 * h;
+                    const uint32_t d = r.rope_dim ? e % r.head_dim : 0u;
+                    if (d < r.rope_dim) {
+                        float cs, ss;
+                        coef(d / 2, cs, ss);
+                        rope_rotate(x[2 * h], x[2 * h + 1], cs, ss);
+                    }
+                    kc[((size_t)pos * r.kv_stride + e) / 2] = f16_bits(x[2 * h]) | (f16_bits(x[2 * h + 1]) << 16);
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t e = c - r.q_dim - r.kv_stride + 2 * h;
+                    vc[((size_t)pos * r.kv_stride + e) / 2] = f16_bits(x[2 * h]) | (f16_bits(x[2 * h + 1]) << 16);
+                }
+            }
+            v = make_float4(x[0], x[1], x[2], x[3]);
+        }
+        *(float4 *)(dst + c) = v;
+    }
+}
+
+bool splitk_rope_kv_store_supported(const RopeArgs &r)
+{
+    return r.q_dim % 4 == 0 && r.kv_stride % 4 == 0 && r.row_stride % 4 == 0 &&
+           r.row_stride == r.q_dim + 2 * r.kv_stride;
+}
+
+// One workgroup per row (M rows: the GEMM's, padding included).
+hipError_t launch_splitk_rope_kv_store(const float *ws, uint32_t S, uint32_t M, float *qkv, const RopeArgs &r,
+                                       uint32_t rows, uint16_t *kc, uint16_t *vc, hipStream_t s)
+{
+    if (!splitk_rope_kv_store_supported(r)) return hipErrorNotSupported;
+    const size_t lds = (size_t)r.rope_dim * 4;
+    const uint32_t lds_coef = lds <= 32 * 1024 ? 1u : 0u;
+    hipLaunchKernelGGL(splitk_rope_kv_store_kernel, dim3(1, M), dim3(256), lds_coef ? lds : 0, s, ws, S, M, qkv, r,
+                       rows, (uint32_t *)kc, (uint32_t *)vc, lds_coef);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Decode attention, split over the sequence (flash-decoding), one launch.
 // Workgroup (g, sp) takes KV head g and cache rows [sp * per, sp * per + per),

@@ -444,7 +444,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restric
 
 template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC>
 static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K, uint32_t N,
-                          uint32_t M, uint32_t S, float *ws, const GemmNorm *nrm, hipStream_t s)
+                          uint32_t M, uint32_t S, float *ws, const GemmNorm *nrm, const GemmRope *rp, hipStream_t s)
 {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * BK * 2;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
@@ -455,6 +455,17 @@ static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t 
     else
         hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC, false>), dim3(tiles), dim3(512), lds, s, X, W, Y, K,
                            N, M, tiles_n, rscale, K / BK, nullptr);
+    if (S > 1 && rp) {
+        // the reduction is the rope_kv_store's first step
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_splitk_rope_kv_store(ws, S, M, Y, rp->r, rp->rows, rp->kc, rp->vc, s);
+    }
+    if (rp) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_rope_kv_store(Y, rp->r, rp->kc, rp->vc, s, rp->rows);
+    }
     if (S > 1 && nrm) {
         // the reduction also writes the rows' RMSNorm
         const hipError_t e = hipGetLastError();
@@ -490,7 +501,8 @@ static uint32_t gemm_splits(uint32_t tiles, uint32_t K, uint32_t M, uint32_t N, 
 
 template <template <int> class QT, bool XH, bool ACC>
 static hipError_t go_gemm_t(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K,
-                            uint32_t N, uint32_t M, float *ws, size_t ws_bytes, const GemmNorm *nrm, hipStream_t s)
+                            uint32_t N, uint32_t M, float *ws, size_t ws_bytes, const GemmNorm *nrm,
+                            const GemmRope *rp, hipStream_t s)
 {
     // 256 x 128 tiles when they cover at least half of the CUs, or with K
     // split to do so; else 128 x 64 (with K steps of 128 so each barrier
@@ -498,9 +510,9 @@ static hipError_t go_gemm_t(const uint16_t *X, const float *rscale, const uint8_
     if (M % 256 == 0 && N % 128 == 0) {
         const uint32_t tiles = (N / 128) * (M / 256);
         const uint32_t S = ws ? gemm_splits(tiles, K, M, N, ws_bytes) : 1u;
-        if (tiles * S >= 128) return go_gemm<QT, 256, 128, 64, XH, ACC>(X, rscale, W, Y, K, N, M, S, ws, nrm, s);
+        if (tiles * S >= 128) return go_gemm<QT, 256, 128, 64, XH, ACC>(X, rscale, W, Y, K, N, M, S, ws, nrm, rp, s);
     }
-    return go_gemm<QT, 128, 64, 128, XH, ACC>(X, rscale, W, Y, K, N, M, 1, nullptr, nrm, s);
+    return go_gemm<QT, 128, 64, 128, XH, ACC>(X, rscale, W, Y, K, N, M, 1, nullptr, nrm, rp, s);
 }
 
 bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t x_bytes)
@@ -512,13 +524,13 @@ bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t 
 template <bool XH, bool ACC>
 static hipError_t go_gemm_q(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
                             uint32_t K, uint32_t N, uint32_t M, float *ws, size_t ws_bytes, hipStream_t s,
-                            const GemmNorm *nrm = nullptr)
+                            const GemmNorm *nrm = nullptr, const GemmRope *rp = nullptr)
 {
     if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2)) return hipErrorNotSupported;
     switch (type) {
-    case T_Q4_K: return go_gemm_t<GqQ4K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, s);
-    case T_Q5_K: return go_gemm_t<GqQ5K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, s);
-    case T_Q6_K: return go_gemm_t<GqQ6K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, s);
+    case T_Q4_K: return go_gemm_t<GqQ4K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, rp, s);
+    case T_Q5_K: return go_gemm_t<GqQ5K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, rp, s);
+    case T_Q6_K: return go_gemm_t<GqQ6K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, rp, s);
     default: return hipErrorNotSupported;
     }
 }
@@ -573,6 +585,15 @@ hipError_t launch_gemm_f16_rmsnorm(const uint16_t *X, const float *rscale, const
     const GemmNorm nrm{gamma, eps, out16};
     return accumulate ? go_gemm_q<true, true>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s, &nrm)
                       : go_gemm_q<true, false>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s, &nrm);
+}
+
+hipError_t launch_gemm_f16_rope_kv(const uint16_t *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K,
+                                   uint32_t N, uint32_t M, const RopeArgs &r, uint32_t rows, uint16_t *kc,
+                                   uint16_t *vc, float *ws, size_t ws_bytes, hipStream_t s)
+{
+    if (!splitk_rope_kv_store_supported(r) || r.row_stride != N || rows > M) return hipErrorNotSupported;
+    const GemmRope rp{r, rows, kc, vc};
+    return go_gemm_q<true, false>(X, nullptr, W, type, Y, K, N, M, ws, ws_bytes, s, nullptr, &rp);
 }
 
 }  // namespace rrr

@@ -153,6 +153,21 @@ struct GemmNorm {
 hipError_t launch_gemm_f16_rmsnorm(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
                                    uint32_t K, uint32_t N, uint32_t M, bool accumulate, const float *gamma, float eps,
                                    uint16_t *out16, float *ws, size_t ws_bytes, hipStream_t s);
+// the QKV GEMM (accumulate 0, no row scale) of the prompt's M rows into the
+// qkv rows Y, then the rope_kv_store of its first `rows` rows at positions
+// r.pos ..: with K split, inside the split reduction
+// (splitk_rope_kv_store_kernel), else the rope launch after the GEMM
+struct GemmRope {
+    RopeArgs r;
+    uint32_t rows;
+    uint16_t *kc, *vc;
+};
+hipError_t launch_gemm_f16_rope_kv(const uint16_t *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K,
+                                   uint32_t N, uint32_t M, const RopeArgs &r, uint32_t rows, uint16_t *kc,
+                                   uint16_t *vc, float *ws, size_t ws_bytes, hipStream_t s);
+bool splitk_rope_kv_store_supported(const RopeArgs &r);
+hipError_t launch_splitk_rope_kv_store(const float *ws, uint32_t S, uint32_t M, float *qkv, const RopeArgs &r,
+                                       uint32_t rows, uint16_t *kc, uint16_t *vc, hipStream_t s);
 bool splitk_reduce_rmsnorm_supported(uint32_t d);
 hipError_t launch_splitk_reduce_rmsnorm(const float *ws, uint32_t S, uint32_t M, uint32_t d, float *Y,
                                         const float *rscale, bool acc, const float *g, float eps, uint16_t *out,

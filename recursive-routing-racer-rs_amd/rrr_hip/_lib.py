@@ -121,6 +121,8 @@ SIGNATURES = {
     "rrr_gemm_f16": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, c_buf_p, u32, u32, u32, u32]),
     "rrr_gemm_f16_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, c_buf_p, u32, u32, u32, u32, c_buf_p, f32,
                                    c_buf_p]),
+    "rrr_gemm_f16_rope_kv_rows": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, c_buf_p, u32, u32, u32, c_buf_p, u32, c_buf_p,
+                                        c_buf_p, u32, u32, u32, u32, u32, u32, u32, f32, f32]),
     "rrr_rmsnorm_f16": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, u32, f32]),
     "rrr_silu_gate_f16": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, u32]),
     "rrr_dispatch": (i32, [c_ctx_p, ctypes.c_char_p, ctypes.POINTER(c_buf_p), u32, vp, u32,

@@ -481,10 +481,16 @@ class DecodeSweep:
             kc, vc = self.kv[i]
             if i == 0 or not fused:   # else the previous layer's down GEMM wrote this norm
                 c.rmsnorm_f16(pf["hid"], L["attn_norm"], pf["n16"], Mp, d, s.eps)
-            c.gemm_f16(pf["n16"], L["attn_qkv"], T["attn_qkv"], pf["qkv"], d, s.qkv_dim, Mp)
-            c.rope_kv_store_rows(pf["qkv"], M, self.rope_factors, self.n_rope_factors, kc, vc, pos0, s.n_heads,
-                                 s.n_kv_heads, s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta,
-                                 s.rope_attn_factor)
+            if fused:   # the QKV GEMM's split reduction is the RoPE + KV store's first step
+                c.gemm_f16_rope_kv_rows(pf["n16"], L["attn_qkv"], T["attn_qkv"], pf["qkv"], d, Mp, M,
+                                        self.rope_factors, self.n_rope_factors, kc, vc, pos0, s.n_heads,
+                                        s.n_kv_heads, s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta,
+                                        s.rope_attn_factor)
+            else:
+                c.gemm_f16(pf["n16"], L["attn_qkv"], T["attn_qkv"], pf["qkv"], d, s.qkv_dim, Mp)
+                c.rope_kv_store_rows(pf["qkv"], M, self.rope_factors, self.n_rope_factors, kc, vc, pos0, s.n_heads,
+                                     s.n_kv_heads, s.head_dim, s.rope_dim, d, s.kv_stride, s.rope_theta,
+                                     s.rope_attn_factor)
             c.attention_prefill(pf["qkv"], M, kc, vc, pf["att16"], pos0, s.n_kv_heads, s.heads_per_kv, s.head_dim,
                                 out_type=E.F16)
             if fused:

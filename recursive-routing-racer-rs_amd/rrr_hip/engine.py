@@ -273,6 +273,14 @@ class Context:
         _check(self.lib.rrr_gemm_f16_rmsnorm(self._h, X._h, row_scale._h if row_scale is not None else None, W._h,
                                              qtype, Y._h, K, N, M, 1 if accumulate else 0, gamma._h, eps, y16._h))
 
+    def gemm_f16_rope_kv_rows(self, X, W, qtype, qkv, K, M, rows, rope_factors, n_factors, k_cache, v_cache, pos0,
+                              n_heads, n_kv_heads, head_dim, rope_dim, q_dim, kv_stride, theta=10000.0,
+                              attn_factor=1.190238):
+        _check(self.lib.rrr_gemm_f16_rope_kv_rows(self._h, X._h, W._h, qtype, qkv._h, K, M, rows,
+                                                  rope_factors._h if rope_factors is not None else None, n_factors,
+                                                  k_cache._h, v_cache._h, pos0, n_heads, n_kv_heads, head_dim,
+                                                  rope_dim, q_dim, kv_stride, theta, attn_factor))
+
     def rmsnorm_f16(self, x, gamma, y, rows, d, eps=1e-5):
         _check(self.lib.rrr_rmsnorm_f16(self._h, x._h, gamma._h, y._h, rows, d, eps))
 

@@ -302,6 +302,42 @@ def test_gemm_f16_rmsnorm_is_the_two_calls(ctx, qtype, K, N, M, acc, scaled):
         b.free()
 
 
+# (type, K, n_heads, n_kv_heads, head_dim, rope_dim, M, rows, pos0): the
+# Phi-4-mini QKV (partial rotary) with K split 3 ways and padding rows, on
+# 128 x 64 tiles (no split) and on 256 x 128 tiles without a split; full
+# rotary with K split 8 ways; the kv_store form (rope_dim 0), K split 3 ways
+@pytest.mark.parametrize("qtype,K,nh,nkv,hd,rd,M,rows,pos0", [
+    (rrr_hip.Q5_K, 3072, 24, 8, 128, 96, 512, 500, 37),
+    (rrr_hip.Q5_K, 3072, 24, 8, 128, 96, 128, 128, 0),
+    (rrr_hip.Q4_K, 3072, 24, 8, 128, 96, 1024, 1000, 5),
+    (rrr_hip.Q4_K, 2048, 8, 4, 64, 64, 512, 300, 11),
+    (rrr_hip.Q6_K, 3072, 24, 8, 128, 0, 512, 512, 3)])
+def test_gemm_f16_rope_kv_rows_is_the_two_calls(ctx, qtype, K, nh, nkv, hd, rd, M, rows, pos0):
+    """rrr_gemm_f16_rope_kv_rows = rrr_gemm_f16 then rrr_rope_kv_store_rows,
+    bit for bit: every qkv row (padding rows included) and both caches."""
+    q_dim, kv = nh * hd, nkv * hd
+    N = q_dim + 2 * kv
+    raw = synth.weight(8, 40 + qtype, qtype, K, N)
+    X = f16r(synth.normal_f32(8, 41, M * K).reshape(M, K))
+    nf = rd // 2
+    fac = (1.0 + np.abs(synth.normal_f32(8, 42, max(nf, 1)))).astype(np.float32)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    xb, fb = ctx.to_device(X.astype(np.float16).view(np.uint16)), ctx.to_device(fac)
+    crow = (pos0 + rows) * kv
+    c0 = synth.normal_f32(8, 43, crow).astype(np.float16).view(np.uint16)
+    qa, qb = ctx.alloc(M * N * 4), ctx.alloc(M * N * 4)
+    ka, va, kb, vb = (ctx.to_device(c0) for _ in range(4))
+    args = (fb if nf else None, nf)
+    ctx.gemm_f16(xb, W, qtype, qa, K, N, M)
+    ctx.rope_kv_store_rows(qa, rows, *args, ka, va, pos0, nh, nkv, hd, rd, q_dim, kv)
+    ctx.gemm_f16_rope_kv_rows(xb, W, qtype, qb, K, M, rows, *args, kb, vb, pos0, nh, nkv, hd, rd, q_dim, kv)
+    assert np.array_equal(ctx.download(qb, np.uint32, M * N), ctx.download(qa, np.uint32, M * N))
+    assert np.array_equal(ctx.download(kb, np.uint16, crow), ctx.download(ka, np.uint16, crow))
+    assert np.array_equal(ctx.download(vb, np.uint16, crow), ctx.download(va, np.uint16, crow))
+    for b in (W, xb, fb, qa, qb, ka, va, kb, vb):
+        b.free()
+
+
 def oracle_prefill(s, host, prompt, pos0, caches):
     """The prefill composed in the oracle: fp64 GEMMs and attention, the f32
     restatement of RoPE and the f16 cache store, the GEMM inputs rounded to
