@@ -310,6 +310,19 @@ int rrr_gemm_f16_rope_kv_rows(rrr_ctx *ctx, const rrr_buf *X_f16, const rrr_buf 
 int rrr_silu_gate_f16(rrr_ctx *ctx, const rrr_buf *gate_up, rrr_buf *mid_f16, rrr_buf *row_scale,
                       uint32_t rows, uint32_t F);
 
+/* The prompt's gate/up step (phi4.rs:1346-1373: the batched ffn_up matmul
+ * into the 2F gate_up rows, then silu_gate): rrr_gemm_f16 of X (M x K f16)
+ * against W (N = 2F rows: F gate rows, then F up rows; accumulate 0, no row
+ * scale) followed by rrr_silu_gate_f16 of its rows, with silu(gate) * up
+ * taken in the GEMM's epilogue, so no M x 2F gate_up rows are written or
+ * read back.  mid_f16 and row_scale end bit for bit as after the two calls.
+ * Needs M % 256 == 0, F % 64 == 0, (F / 64) * (M / 256) >= 128 (the GEMM
+ * covers the CUs without a K split) and M * F * 4 bytes of the context's
+ * GEMM workspace (48 MiB); RRR_ERR_UNSUPPORTED otherwise, and the two calls
+ * do the step.  No counterpart call in the reference. */
+int rrr_gemm_f16_silu_gate_f16(rrr_ctx *ctx, const rrr_buf *X_f16, const rrr_buf *W, uint32_t type,
+                               rrr_buf *mid_f16, rrr_buf *row_scale, uint32_t K, uint32_t F, uint32_t M);
+
 /* ---- fused decode-sweep ops (the four launches per layer) ------------ */
 
 /* Y = W . rmsnorm(x, gamma, eps): RMSNorm folded into the GEMV's activation

@@ -1041,6 +1041,36 @@ int rrr_silu_gate_f16(rrr_ctx *ctx, const rrr_buf *gate_up, rrr_buf *mid, rrr_bu
                   what);
 }
 
+int rrr_gemm_f16_silu_gate_f16(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t type, rrr_buf *mid,
+                               rrr_buf *row_scale, uint32_t K, uint32_t F, uint32_t M)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_gemm_f16_silu_gate_f16";
+    TRY(check_buf(ctx, X, what));
+    TRY(check_buf(ctx, W, what));
+    TRY(check_buf(ctx, mid, what));
+    TRY(check_buf(ctx, row_scale, what));
+    if (M == 0 || F == 0 || F > 0x7FFFFFFFu) return fail(RRR_ERR_BAD_SHAPE, "%s: M and F must be positive", what);
+    const uint32_t N = 2 * F;
+    TRY(check_shape(type, K, N));
+    if (type == RRR_TYPE_F32) return fail(RRR_ERR_UNSUPPORTED, "%s: F32 weights are not a prefill shape", what);
+    TRY(need(W, rrr_tensor_bytes(type, K, N), what));
+    TRY(need(X, (uint64_t)M * K * 2, what));
+    TRY(need(mid, 2ull * M * F, what));
+    TRY(need_f32(row_scale, M, what));
+    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2) || M % 256 || F % 64 || (uint64_t)M * F * 4 > GEMM_WS_BYTES ||
+        (uint64_t)(N / 128) * (M / 256) < 128)
+        return fail(RRR_ERR_UNSUPPORTED, "%s: needs M %% 256 == 0, F %% 64 == 0, (F / 64) * (M / 256) >= 128 and "
+                    "M * F * 4 <= %llu (M=%u F=%u); use rrr_gemm_f16 and rrr_silu_gate_f16", what,
+                    (unsigned long long)GEMM_WS_BYTES, M, F);
+    TRY(device_ready(ctx));
+    return finish(ctx,
+                  launch_gemm_f16_silu_f16((const uint16_t *)X->ptr, (const uint8_t *)W->ptr, type,
+                                           (uint16_t *)mid->ptr, (float *)row_scale->ptr, K, F, M,
+                                           (float *)ctx->gemm_ws, GEMM_WS_BYTES, ctx->stream),
+                  what);
+}
+
 // ---- name-keyed dispatch shim ----------------------------------------------
 
 static int push_u32(const void *push, uint32_t push_bytes, uint32_t n, uint32_t *out, const char *name)

@@ -200,7 +200,30 @@ struct GqQ6K {
 // into the other LDS buffer, so every SIMD holds one wave of each kind and the
 // staging VALU fills the matrix core's gaps.  Both roles pass one barrier per
 // step (plus one after the prologue) on separate straight-line paths.
-template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC, bool SPLIT>
+// silu_f(gate) * up of row block i (32 rows) of MFMA wave cw's 32 outputs of
+// tile nt into Y (M x F), the D layout of the 32x32 MFMAs (lane l: column
+// l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4 in register r)
+template <int BM>
+__device__ __forceinline__ void silu_rows_store(float *Y, uint32_t F, uint32_t nt, uint32_t m0, uint32_t cw,
+                                                uint32_t lane, int i, const float *g, const float *u)
+{
+    const uint32_t wm = cw >> 1, wn = cw & 1, n = nt * 64 + wn * 32 + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const uint32_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        Y[(uint64_t)m * F + n] = silu_f(g[r]) * u[r];
+    }
+}
+
+// SILU (gate/up with silu(gate) * up in the epilogue): W holds N = 2F rows,
+// F gate rows then F up rows; tile nt takes outputs 64 nt .. 64 nt + 63, its
+// B rows 0-31 / 32-63 / 64-95 / 96-127 being gate / up / gate / up rows of
+// outputs 64 nt + 0-31, + 0-31, + 32-63, + 32-63, so an MFMA wave's two
+// 32-column accumulators hold the gate and the up sums of the same outputs;
+// Y (M x F) gets silu_f(gate) * up of the sums the plain GEMM stores.  The
+// MFMA waves hand row blocks 2 and 3 of their sums to the staging waves
+// through the (then idle) LDS, so the eight waves share the silu work.
+template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC, bool SPLIT, bool SILU = false>
 __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K,
                                                       uint32_t N, uint32_t M, uint32_t tiles_n, const float *rscale,
                                                       uint32_t ksteps, float *ws)
@@ -250,7 +273,8 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         // part wp of it (two parts a thread: the whole chunk, wp = 0)
         const uint32_t ur = tp / TPW, lb = 64 * ((tp % TPW) * NPW / 2), wp = (tp % TPW) * NPW % 2;
         const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, (uint64_t)N * B * Q::BS);
-        const uint32_t wvoff = (n0 + ur) * B * Q::BS;
+        const uint32_t wrow = SILU ? ((ur & 32u) ? N / 2 : 0u) + nt * (BN / 2) + (ur & 31u) + ((ur >> 6) << 5) : n0 + ur;
+        const uint32_t wvoff = wrow * B * Q::BS;
         // X: pass i covers rows XRS*i .. XRS*(i+1)-1 of the step, consecutive
         // threads on consecutive 16-byte chunks of a row (whole cache lines per
         // wave load)
@@ -323,6 +347,22 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
             issue(S0, s + 2 * NSET);
             __syncthreads();
         }
+        if constexpr (SILU) {
+            // row blocks 2, 3 of MFMA wave t / 64 - 4, once it has handed them over
+            __syncthreads();
+            const uint32_t cw = wave - 4;
+            const float *hs = (const float *)smem + cw * 64 * 64 + lane;
+#pragma unroll
+            for (int i = 2; i < 4; i++) {
+                float g[16], u[16];
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    g[r] = hs[((i - 2) * 32 + 2 * r) * 64];
+                    u[r] = hs[((i - 2) * 32 + 2 * r + 1) * 64];
+                }
+                silu_rows_store<BM>(Y, N / 2, nt, m0, cw, lane, i, g, u);
+            }
+        }
         return;
     }
 
@@ -394,6 +434,31 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         }
     }
 
+    if constexpr (SILU) {
+        static_assert(!SPLIT && !ACC && BN == 128 && BM == 256, "gate/up tiles of 64 outputs, whole K");
+        // row blocks 2, 3 to the staging wave t / 64 + 4 (LDS past the last
+        // step's barrier: only this wave's stale fragment read touches it)
+        float *hs = (float *)smem + wave * 64 * 64 + lane;
+#pragma unroll
+        for (int i = 2; i < 4; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                hs[((i - 2) * 32 + 2 * r) * 64] = acc[i][0][r];
+                hs[((i - 2) * 32 + 2 * r + 1) * 64] = acc[i][1][r];
+            }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            float g[16], u[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                g[r] = acc[i][0][r];
+                u[r] = acc[i][1][r];
+            }
+            silu_rows_store<BM>(Y, N / 2, nt, m0, wave, lane, i, g, u);
+        }
+        return;
+    }
     // the row scales (powers of two) are exact
 #pragma unroll
     for (int i = 0; i < UI; i++)
@@ -585,6 +650,34 @@ hipError_t launch_gemm_f16_rmsnorm(const uint16_t *X, const float *rscale, const
     const GemmNorm nrm{gamma, eps, out16};
     return accumulate ? go_gemm_q<true, true>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s, &nrm)
                       : go_gemm_q<true, false>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s, &nrm);
+}
+
+// The gate/up GEMM with silu(gate) * up in its epilogue into ws (M x F
+// f32), then the f16 block-floating-point rows of silu_gate_f16 from it:
+// whole K on 256 x 128 tiles that cover half of the CUs, else not supported.
+hipError_t launch_gemm_f16_silu_f16(const uint16_t *X, const uint8_t *W, uint32_t type, uint16_t *mid, float *rscale,
+                                    uint32_t K, uint32_t F, uint32_t M, float *ws, size_t ws_bytes, hipStream_t s)
+{
+    const uint32_t N = 2 * F;
+    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2) || M % 256 || N % 128) return hipErrorNotSupported;
+    const uint32_t tiles_n = N / 128, tiles = tiles_n * (M / 256);
+    if (tiles < 128 || (uint64_t)M * F * 4 > ws_bytes) return hipErrorNotSupported;
+    constexpr size_t lds = 2 * (size_t)(256 + 128) * 64 * 2;
+#define RRR_SILU_CASE(T, QT)                                                                                          \
+    case T:                                                                                                            \
+        hipLaunchKernelGGL((gemm_dq_kernel<QT, 256, 128, 64, true, false, false, true>), dim3(tiles), dim3(512), lds, \
+                           s, X, W, ws, K, N, M, tiles_n, nullptr, K / 64, nullptr);                                   \
+        break;
+    switch (type) {
+        RRR_SILU_CASE(T_Q4_K, GqQ4K)
+        RRR_SILU_CASE(T_Q5_K, GqQ5K)
+        RRR_SILU_CASE(T_Q6_K, GqQ6K)
+    default: return hipErrorNotSupported;
+    }
+#undef RRR_SILU_CASE
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_f16_rows_scaled(ws, mid, rscale, M, F, s);
 }
 
 hipError_t launch_gemm_f16_rope_kv(const uint16_t *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K,

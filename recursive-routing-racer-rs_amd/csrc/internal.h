@@ -165,6 +165,13 @@ struct GemmRope {
 hipError_t launch_gemm_f16_rope_kv(const uint16_t *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K,
                                    uint32_t N, uint32_t M, const RopeArgs &r, uint32_t rows, uint16_t *kc,
                                    uint16_t *vc, float *ws, size_t ws_bytes, hipStream_t s);
+// the gate/up GEMM (N = 2F: F gate rows, F up rows) with silu(gate) * up in
+// its epilogue into ws (M x F f32), then silu_gate_f16's block floating
+// point rows from those values (launch_f16_rows_scaled)
+hipError_t launch_gemm_f16_silu_f16(const uint16_t *X, const uint8_t *W, uint32_t type, uint16_t *mid, float *rscale,
+                                    uint32_t K, uint32_t F, uint32_t M, float *ws, size_t ws_bytes, hipStream_t s);
+hipError_t launch_f16_rows_scaled(const float *v, uint16_t *mid, float *rscale, uint32_t rows, uint32_t F,
+                                  hipStream_t s);
 bool splitk_rope_kv_store_supported(const RopeArgs &r);
 hipError_t launch_splitk_rope_kv_store(const float *ws, uint32_t S, uint32_t M, float *qkv, const RopeArgs &r,
                                        uint32_t rows, uint16_t *kc, uint16_t *vc, hipStream_t s);

@@ -244,14 +244,15 @@ hipError_t launch_silu_gate(const float *gu, float *mid, uint32_t rows, uint32_t
 // activations grow); rscale[row] = 2^(e - 15) undoes it.  A row with no
 // finite nonzero maximum is stored unscaled (rscale 1).
 // NV > 0: the row's values stay in registers (F <= 256 * NV, one read of
-// gate / up); NV == 0: any F, gate / up read twice.
-template <int NV>
+// gate / up); NV == 0: any F, gate / up read twice.  PRE: gu holds the
+// values v themselves (rows of F: the gate/up GEMM's silu epilogue).
+template <int NV, bool PRE = false>
 __global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__restrict__ gu,
                                                                  _Float16 *__restrict__ mid,
                                                                  float *__restrict__ rscale, uint32_t F)
 {
     __shared__ float red[4];
-    const float *row = gu + (uint64_t)blockIdx.x * 2 * F;
+    const float *row = gu + (uint64_t)blockIdx.x * (PRE ? 1 : 2) * F;
     _Float16 *out = mid + (uint64_t)blockIdx.x * F;
     const uint32_t t = threadIdx.x;
     float m = 0.0f;
@@ -262,19 +263,27 @@ __global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__
         for (int j = 0; j < NV / 4; j++) {
             const uint32_t i = 4 * (t + 256u * j);
             float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
-            if (i < F) {
-                g = *(const float4 *)(row + i);
-                u = *(const float4 *)(row + F + i);
+            if constexpr (PRE) {
+                if (i < F) g = *(const float4 *)(row + i);
+                v[4 * j] = g.x;
+                v[4 * j + 1] = g.y;
+                v[4 * j + 2] = g.z;
+                v[4 * j + 3] = g.w;
+            } else {
+                if (i < F) {
+                    g = *(const float4 *)(row + i);
+                    u = *(const float4 *)(row + F + i);
+                }
+                v[4 * j] = silu_f(g.x) * u.x;
+                v[4 * j + 1] = silu_f(g.y) * u.y;
+                v[4 * j + 2] = silu_f(g.z) * u.z;
+                v[4 * j + 3] = silu_f(g.w) * u.w;
             }
-            v[4 * j] = silu_f(g.x) * u.x;
-            v[4 * j + 1] = silu_f(g.y) * u.y;
-            v[4 * j + 2] = silu_f(g.z) * u.z;
-            v[4 * j + 3] = silu_f(g.w) * u.w;
 #pragma unroll
             for (int c = 0; c < 4; c++) m = fmaxf(m, fabsf(v[4 * j + c]));
         }
     } else {
-        for (uint32_t i = t; i < F; i += 256) m = fmaxf(m, fabsf(silu_f(row[i]) * row[F + i]));
+        for (uint32_t i = t; i < F; i += 256) m = fmaxf(m, fabsf(PRE ? row[i] : silu_f(row[i]) * row[F + i]));
     }
     m = wave_max(m);
     if ((t & 63) == 0) red[t >> 6] = m;
@@ -293,7 +302,7 @@ __global__ __launch_bounds__(256) void silu_gate_f16_rows_kernel(const float *__
                                       to_out<_Float16>(v[4 * j + 2] * sc), to_out<_Float16>(v[4 * j + 3] * sc)};
         }
     } else {
-        for (uint32_t i = t; i < F; i += 256) out[i] = to_out<_Float16>((silu_f(row[i]) * row[F + i]) * sc);
+        for (uint32_t i = t; i < F; i += 256) out[i] = to_out<_Float16>((PRE ? row[i] : silu_f(row[i]) * row[F + i]) * sc);
     }
     if (t == 0) rscale[blockIdx.x] = ldexpf(1.0f, e - 15);
 }
@@ -305,6 +314,19 @@ hipError_t launch_silu_gate_f16(const float *gu, uint16_t *mid, float *rscale, u
         hipLaunchKernelGGL(silu_gate_f16_rows_kernel<32>, dim3(rows), dim3(256), 0, s, gu, (_Float16 *)mid, rscale, F);
     else
         hipLaunchKernelGGL(silu_gate_f16_rows_kernel<0>, dim3(rows), dim3(256), 0, s, gu, (_Float16 *)mid, rscale, F);
+    return hipGetLastError();
+}
+
+// The same rows from precomputed values v (rows of F floats).
+hipError_t launch_f16_rows_scaled(const float *v, uint16_t *mid, float *rscale, uint32_t rows, uint32_t F,
+                                  hipStream_t s)
+{
+    if (F <= 256 * 32 && F % 4 == 0)
+        hipLaunchKernelGGL((silu_gate_f16_rows_kernel<32, true>), dim3(rows), dim3(256), 0, s, v, (_Float16 *)mid,
+                           rscale, F);
+    else
+        hipLaunchKernelGGL((silu_gate_f16_rows_kernel<0, true>), dim3(rows), dim3(256), 0, s, v, (_Float16 *)mid,
+                           rscale, F);
     return hipGetLastError();
 }
 

@@ -121,6 +121,7 @@ SIGNATURES = {
     "rrr_gemm_f16": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, c_buf_p, u32, u32, u32, u32]),
     "rrr_gemm_f16_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, c_buf_p, u32, u32, u32, u32, c_buf_p, f32,
                                    c_buf_p]),
+    "rrr_gemm_f16_silu_gate_f16": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, c_buf_p, c_buf_p, u32, u32, u32]),
     "rrr_gemm_f16_rope_kv_rows": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, c_buf_p, u32, u32, u32, c_buf_p, u32, c_buf_p,
                                         c_buf_p, u32, u32, u32, u32, u32, u32, u32, f32, f32]),
     "rrr_rmsnorm_f16": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, u32, u32, f32]),

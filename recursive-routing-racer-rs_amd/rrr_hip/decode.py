@@ -429,6 +429,11 @@ class DecodeSweep:
         c.argmax_f32(self.logits, s.vocab, self.token)
 
     # ---- prefill: the prompt's tokens through every layer at once ----------
+    @staticmethod
+    def _silu_gemm_ok(Mp, F):
+        """The shapes rrr_gemm_f16_silu_gate_f16 takes (else the two calls)."""
+        return Mp % 256 == 0 and F % 64 == 0 and (F // 64) * (Mp // 256) >= 128 and Mp * F * 4 <= (48 << 20)
+
     PREFILL_ROWS = 128   # the prefill GEMM's row block; prompts are padded to it with zero rows
 
     def prefill_buffers(self, M):
@@ -499,8 +504,11 @@ class DecodeSweep:
             else:
                 c.gemm_f16(pf["att16"], L["attn_output"], T["attn_output"], pf["hid"], d, d, Mp, accumulate=True)
                 c.rmsnorm_f16(pf["hid"], L["ffn_norm"], pf["n16"], Mp, d, s.eps)
-            c.gemm_f16(pf["n16"], L["ffn_up"], T["ffn_up"], pf["gu"], d, 2 * F, Mp)
-            c.silu_gate_f16(pf["gu"], pf["mid16"], pf["mid_scale"], Mp, F)
+            if fused and self._silu_gemm_ok(Mp, F):   # silu(gate) * up in the gate/up GEMM's epilogue
+                c.gemm_f16_silu_gate_f16(pf["n16"], L["ffn_up"], T["ffn_up"], pf["mid16"], pf["mid_scale"], d, F, Mp)
+            else:
+                c.gemm_f16(pf["n16"], L["ffn_up"], T["ffn_up"], pf["gu"], d, 2 * F, Mp)
+                c.silu_gate_f16(pf["gu"], pf["mid16"], pf["mid_scale"], Mp, F)
             if fused and i + 1 < len(self.layers):   # the next layer's attention norm with it
                 c.gemm_f16_rmsnorm(pf["mid16"], L["ffn_down"], T["ffn_down"], pf["hid"], F, d, Mp,
                                    self.layers[i + 1]["attn_norm"], pf["n16"], s.eps, accumulate=True,

@@ -281,6 +281,9 @@ class Context:
                                                   k_cache._h, v_cache._h, pos0, n_heads, n_kv_heads, head_dim,
                                                   rope_dim, q_dim, kv_stride, theta, attn_factor))
 
+    def gemm_f16_silu_gate_f16(self, X, W, qtype, mid, row_scale, K, F, M):
+        _check(self.lib.rrr_gemm_f16_silu_gate_f16(self._h, X._h, W._h, qtype, mid._h, row_scale._h, K, F, M))
+
     def rmsnorm_f16(self, x, gamma, y, rows, d, eps=1e-5):
         _check(self.lib.rrr_rmsnorm_f16(self._h, x._h, gamma._h, y._h, rows, d, eps))
 

@@ -338,6 +338,42 @@ def test_gemm_f16_rope_kv_rows_is_the_two_calls(ctx, qtype, K, nh, nkv, hd, rd, 
         b.free()
 
 
+# (type, K, F, M, scale): the Phi-4-mini gate/up at 512 and 1024 rows, Q5_K /
+# Q6_K weights, larger activations, 256 rows of a wider F
+@pytest.mark.parametrize("qtype,K,F,M,xs", [(rrr_hip.Q4_K, 3072, 8192, 512, 1.0),
+                                             (rrr_hip.Q4_K, 3072, 8192, 1024, 30.0),
+                                             (rrr_hip.Q5_K, 2048, 8192, 512, 1.0),
+                                             (rrr_hip.Q6_K, 1024, 16384, 256, 4.0)])
+def test_gemm_f16_silu_gate_f16_is_the_two_calls(ctx, qtype, K, F, M, xs):
+    """rrr_gemm_f16_silu_gate_f16 = rrr_gemm_f16 (N = 2F) then
+    rrr_silu_gate_f16, bit for bit: the f16 rows and the row scales."""
+    raw = synth.weight(9, 60 + qtype, qtype, K, 2 * F)
+    X = f16r(synth.normal_f32(9, 61, M * K).reshape(M, K) * np.float32(xs))
+    W = ctx.weight_upload(qtype, K, 2 * F, raw)
+    xb = ctx.to_device(X.astype(np.float16).view(np.uint16))
+    gu = ctx.alloc(M * 2 * F * 4)
+    ma, mb = ctx.alloc(M * F * 2), ctx.alloc(M * F * 2)
+    sa, sb = ctx.alloc(M * 4), ctx.alloc(M * 4)
+    ctx.gemm_f16(xb, W, qtype, gu, K, 2 * F, M)
+    ctx.silu_gate_f16(gu, ma, sa, M, F)
+    ctx.gemm_f16_silu_gate_f16(xb, W, qtype, mb, sb, K, F, M)
+    assert np.array_equal(ctx.download(mb, np.uint16, M * F), ctx.download(ma, np.uint16, M * F))
+    assert np.array_equal(ctx.download(sb, np.uint32, M), ctx.download(sa, np.uint32, M))
+    for b in (W, xb, gu, ma, mb, sa, sb):
+        b.free()
+
+
+def test_gemm_f16_silu_gate_f16_unsupported(ctx):
+    """Shapes whose GEMM would split K or leave CUs idle are refused (the two
+    calls do them)."""
+    W = ctx.weight_upload(rrr_hip.Q4_K, 256, 256, synth.weight(9, 70, rrr_hip.Q4_K, 256, 256))
+    xb, mb, sb = ctx.alloc(256 * 256 * 2), ctx.alloc(256 * 128 * 2), ctx.alloc(256 * 4)
+    with pytest.raises(rrr_hip.RrrError):
+        ctx.gemm_f16_silu_gate_f16(xb, W, rrr_hip.Q4_K, mb, sb, 256, 128, 256)
+    for b in (W, xb, mb, sb):
+        b.free()
+
+
 def oracle_prefill(s, host, prompt, pos0, caches):
     """The prefill composed in the oracle: fp64 GEMMs and attention, the f32
     restatement of RoPE and the f16 cache store, the GEMM inputs rounded to
