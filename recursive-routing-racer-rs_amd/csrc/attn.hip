@@ -601,8 +601,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
     }
 }
 
-// Causal prefill attention on the matrix cores.  Workgroup (g, tb): KV head
-// g, tokens tb*16 .. tb*16+15 (lane l's token is l % 16); its ATTM_WAVES
+// Causal prefill attention on the matrix cores.  Workgroup (g, tb): query
+// heads g*HPK .. g*HPK+HPK-1, of KV head g / hsplit (hsplit workgroups share
+// a KV group's heads_per_kv = hsplit * HPK heads; hsplit 1: all of them),
+// tokens tb*16 .. tb*16+15 (lane l's token is l % 16); its ATTM_WAVES
 // waves take every ATTM_WAVES-th block of 32 cache rows and merge their
 // (max, sum, output) at the end in a fixed order.  Per block and per query
 // head h of the group:
@@ -655,7 +657,7 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
                                                                const uint16_t *__restrict__ kc,
                                                                const uint16_t *__restrict__ vc,
                                                                void *__restrict__ out, uint32_t rows, uint32_t pos0,
-                                                               uint32_t kv_stride, float qscale)
+                                                               uint32_t kv_stride, float qscale, uint32_t hsplit)
 {
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
@@ -672,7 +674,7 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
     const uint32_t tok = tb * 16 + n, tq = min(tok, rows - 1), tpos = pos0 + tq;
     const uint32_t last = pos0 + min(tb * 16 + 15, rows - 1);      // the last cache row the block's tokens see
     const uint32_t nblk = last / 32 + 1;
-    const uint16_t *kbase = kc + (size_t)g * ATT_HD, *vbase = vc + (size_t)g * ATT_HD;
+    const uint16_t *kbase = kc + (size_t)(g / hsplit) * ATT_HD, *vbase = vc + (size_t)(g / hsplit) * ATT_HD;
 
     // K and V of block blk (rows past `last` repeat it): the next block of
     // this wave is requested before the current one is multiplied
@@ -921,18 +923,18 @@ __global__ __launch_bounds__(64 * ATTM_WAVES) void attn_prefill_mfma_kernel(cons
 template <int HPK>
 static void go_attn_prefill(const float *qkv, uint32_t row_stride, uint32_t rows, const uint16_t *kc,
                             const uint16_t *vc, void *out, bool out_f16, uint32_t pos0, uint32_t n_kv_heads,
-                            float qscale, hipStream_t s)
+                            float qscale, hipStream_t s, uint32_t hsplit = 1)
 {
     const uint32_t kv_stride = n_kv_heads * ATT_HD;
     if constexpr (HPK <= 4) {   // the matrix-core form (its accumulators take 32 registers per head)
-        const dim3 grid(n_kv_heads, (rows + 15) / 16);
+        const dim3 grid(n_kv_heads * hsplit, (rows + 15) / 16);
         static_assert(AttmLds<4>::BYTES <= 160 * 1024, "LDS per workgroup");
         if (out_f16)
             hipLaunchKernelGGL((attn_prefill_mfma_kernel<HPK, true>), grid, dim3(64 * ATTM_WAVES), 0, s, qkv,
-                               row_stride, kc, vc, out, rows, pos0, kv_stride, qscale);
+                               row_stride, kc, vc, out, rows, pos0, kv_stride, qscale, hsplit);
         else
             hipLaunchKernelGGL((attn_prefill_mfma_kernel<HPK, false>), grid, dim3(64 * ATTM_WAVES), 0, s, qkv,
-                               row_stride, kc, vc, out, rows, pos0, kv_stride, qscale);
+                               row_stride, kc, vc, out, rows, pos0, kv_stride, qscale, hsplit);
         return;
     }
     if (out_f16)
@@ -949,6 +951,16 @@ hipError_t launch_attention_prefill(const float *qkv, uint32_t row_stride, uint3
 {
     if (rows == 0) return hipSuccess;
     const float qscale = (float)(1.4426950408889634 / sqrt((double)ATT_HD));   // log2(e) / sqrt(head_dim)
+    // a short prompt's workgroups (KV head, 16 tokens) leave CUs idle: then
+    // one workgroup per query head (the same arithmetic per head, bitwise
+    // the grouped form; 128 rows x 8 x 3 heads: 7.6 instead of 12.2 us),
+    // else the KV group's heads share every K/V block in one workgroup
+    // (512 rows: 22.4 against 30.8 us split)
+    const uint64_t tgroups = (rows + 15) / 16;
+    if (heads_per_kv > 1 && heads_per_kv <= 4 && (uint64_t)n_kv_heads * heads_per_kv * tgroups <= sweep_cus()) {
+        go_attn_prefill<1>(qkv, row_stride, rows, kc, vc, out, out_f16, pos0, n_kv_heads, qscale, s, heads_per_kv);
+        return hipGetLastError();
+    }
 #define RRR_ATTP_CASE(H) \
     case H: go_attn_prefill<H>(qkv, row_stride, rows, kc, vc, out, out_f16, pos0, n_kv_heads, qscale, s); break;
     switch (heads_per_kv) {

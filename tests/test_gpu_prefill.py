@@ -114,9 +114,13 @@ def test_rope_kv_store_rows(ctx, caches, pos0, rows):
 
 
 # (9, 40) and (25, 70): blocks of 32 cache rows that start past some of a
-# workgroup's tokens (a wave whose first block holds none of a token's keys)
+# workgroup's tokens (a wave whose first block holds none of a token's keys).
+# Up to 256 workgroups of one query head each cover the short prompts; (0,
+# 200, 8, 3), (7, 400, 8, 2) and (0, 300, 4, 4) take the grouped form (a
+# workgroup per KV head's query heads)
 @pytest.mark.parametrize("pos0,rows,nkv,hpk", [(0, 1, 8, 3), (0, 130, 8, 3), (100, 37, 8, 3), (2000, 48, 8, 3),
-                                               (0, 64, 2, 8), (5, 20, 1, 1), (9, 40, 8, 3), (25, 70, 8, 3)])
+                                               (0, 64, 2, 8), (5, 20, 1, 1), (9, 40, 8, 3), (25, 70, 8, 3),
+                                               (0, 200, 8, 3), (7, 400, 8, 2), (0, 300, 4, 4)])
 def test_attention_prefill_parity(ctx, caches, pos0, rows, nkv, hpk):
     kc, vc = caches
     rng = np.random.default_rng(pos0 * 7 + rows + nkv * hpk)
