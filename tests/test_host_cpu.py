@@ -335,6 +335,28 @@ def test_prefill_validation(vctx):
     assert code_of(vctx.silu_gate_f16, x, y16, rs, 2 * M, K // 4) == ERR_SHORT_BUFFER     # row scales
     assert code_of(g, X, W, 12, Y, K, N, M, row_scale=rs) == ERR_NO_DEVICE
     assert code_of(g, X, W, 12, Y, K, N, M, row_scale=vctx.alloc(4)) == ERR_SHORT_BUFFER
+    # the gate/up GEMM with silu * up in its epilogue: shapes it takes reach
+    # the device check, the rest are refused before it
+    Ws = vctx.alloc(rrr_hip.tensor_bytes(12, K, 2 * 8192))
+    Xs, ms, rss = vctx.alloc(512 * K * 2), vctx.alloc(512 * 8192 * 2), vctx.alloc(512 * 4)
+    gs = vctx.gemm_f16_silu_gate_f16
+    assert code_of(gs, Xs, Ws, 12, ms, rss, K, 8192, 512) == ERR_NO_DEVICE
+    assert code_of(gs, Xs, Ws, 12, ms, rss, K, 8192, 256) == ERR_NO_DEVICE   # 128 tiles
+    assert code_of(gs, Xs, Ws, 12, ms, rss, K, 8192, 128) == ERR_UNSUPPORTED  # M % 256
+    assert code_of(gs, Xs, Ws, 12, ms, rss, K, 4096, 256) == ERR_UNSUPPORTED  # 64 tiles: K would split
+    assert code_of(gs, Xs, Ws, 12, ms, rss, K, 8192, 1024) == ERR_SHORT_BUFFER
+    assert code_of(gs, Xs, Ws, 0, ms, rss, K, 8192, 512) == ERR_UNSUPPORTED
+    # the QKV GEMM with the RoPE + KV store of its rows
+    qk = vctx.alloc(M * (qd + 2 * kvs) * 4)
+    rk = vctx.gemm_f16_rope_kv_rows
+    Wq = vctx.alloc(rrr_hip.tensor_bytes(12, 256, qd + 2 * kvs))
+    Xq = vctx.alloc(M * 256 * 2)
+    assert code_of(rk, Xq, Wq, 12, qk, 256, M, rows, fac, 48, kc, vc, 12, nh, nkv, hd, rd, qd, kvs) == ERR_NO_DEVICE
+    assert code_of(rk, Xq, Wq, 12, qk, 256, M, M + 1, fac, 48, kc, vc, 0, nh, nkv, hd, rd, qd, kvs) == ERR_BAD_SHAPE
+    assert code_of(rk, Xq, Wq, 12, qk, 256, M, rows, fac, 48, kc, vc, 13, nh, nkv, hd, rd, qd, kvs) == ERR_SHORT_BUFFER
+    assert code_of(rk, Xq, Wq, 12, qk, 256, 2 * M, rows, fac, 48, kc, vc, 12, nh, nkv, hd, rd, qd,
+                   kvs) == ERR_SHORT_BUFFER   # X and qkv hold M rows
+    assert code_of(rk, Xq, Wq, 12, qk, 256, 100, rows, fac, 48, kc, vc, 12, nh, nkv, hd, rd, qd, kvs) == ERR_UNSUPPORTED
 
 
 def test_graph_state_rules(vctx):
