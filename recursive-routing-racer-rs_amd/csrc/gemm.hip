@@ -25,9 +25,10 @@
 // so they run on the same XCD and the weight tile is fetched from HBM once.
 //
 // Split K: when the BM x BN tiles are too few to fill the CUs (a 512-token
-// prompt against N = 3072 or 5120), workgroup (tile, ks) takes the K range
-// [ks * ksteps * BK, (ks + 1) * ksteps * BK) and writes its fp32 partial to a
-// workspace; gemm_splitk_reduce then adds the S partials of each output in
+// prompt against N = 3072 or 5120), workgroup (tile, ks) of S splits takes
+// super-blocks [ks * q + min(ks, r), (ks + 1) * q + min(ks + 1, r)) of the
+// B = K / 256 (q = B / S, r = B % S: the first r splits one more) and
+// writes its fp32 partial to a workspace; gemm_splitk_reduce then adds the S partials of each output in
 // split order (deterministic), applies the row scale and stores or adds to Y.
 #include "device_common.h"
 #include "internal.h"
@@ -226,7 +227,7 @@ __device__ __forceinline__ void silu_rows_store(float *Y, uint32_t F, uint32_t n
 template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC, bool SPLIT, bool SILU = false>
 __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K,
                                                       uint32_t N, uint32_t M, uint32_t tiles_n, const float *rscale,
-                                                      uint32_t ksteps, float *ws)
+                                                      uint32_t S, float *ws)
 {
     // LDS rows of BK f16, unpadded; 16-byte chunk c of row r sits at chunk
     // c ^ swz(r), swz(r) = (r / RPL) % CPR with RPL rows per 64-bank line
@@ -264,7 +265,9 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     }
     const uint32_t m0 = mt * BM, n0 = nt * BN;
     // this split's K steps and its first step
-    const uint32_t nsteps = SPLIT ? ksteps : K / BK, s0 = ks * nsteps, B = K / 256;
+    const uint32_t B = K / 256, bq = B / S, br = B % S;
+    const uint32_t nsteps = SPLIT ? (bq + (ks < br ? 1u : 0u)) * (256 / BK) : K / BK;
+    const uint32_t s0 = SPLIT ? (ks * bq + min(ks, br)) * (256 / BK) : 0u;
 
     if (wave >= 4) {
         // ---- producer: loads, dequant, conversion --------------------------
@@ -516,10 +519,10 @@ static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t 
     const uint32_t tiles_n = N / BN, tiles = tiles_n * (M / BM);
     if (S > 1)
         hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC, true>), dim3(tiles * S), dim3(512), lds, s, X, W, Y,
-                           K, N, M, tiles_n, rscale, K / BK / S, ws);
+                           K, N, M, tiles_n, rscale, S, ws);
     else
         hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC, false>), dim3(tiles), dim3(512), lds, s, X, W, Y, K,
-                           N, M, tiles_n, rscale, K / BK, nullptr);
+                           N, M, tiles_n, rscale, 1u, nullptr);
     if (S > 1 && rp) {
         // the reduction is the rope_kv_store's first step
         const hipError_t e = hipGetLastError();
@@ -550,18 +553,24 @@ static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t 
     return hipGetLastError();
 }
 
-// Splits of K for a grid of `tiles` large tiles: as many as keep every
-// workgroup in the first round over the MI355X's 256 CUs (a second round
-// costs a whole tile's time), at most 8, each a whole number of
-// super-blocks, their partials within the workspace; 1 when the tiles
+// Splits of K for a grid of `tiles` large tiles: at most as many as keep
+// every workgroup in the first round over the MI355X's 256 CUs (a second
+// round costs a whole tile's time) and at most 8, each a whole number of
+// super-blocks (the first B % S splits one more), their partials within the
+// workspace; of those, the fewest that give the shortest longest split
+// (K = 8192, 48 tiles: 5 splits of 7/7/6/6/6 super-blocks rather than 4 of
+// 8; K = 3072: 4 splits of 3 rather than 5 of 3/3/2/2/2); 1 when the tiles
 // already fill half of the CUs.
 static uint32_t gemm_splits(uint32_t tiles, uint32_t K, uint32_t M, uint32_t N, size_t ws_bytes)
 {
-    const uint32_t cus = 256;
+    const uint32_t cus = 256, B = K / 256;
     if (tiles >= cus / 2 || tiles % 8) return 1;
-    uint32_t S = min(8u, cus / tiles);
-    while (S > 1 && ((K / 256) % S || (uint64_t)S * M * N * 4 > ws_bytes)) S--;
-    return S;
+    uint32_t best = 1;
+    for (uint32_t S = 2; S <= min(min(8u, cus / tiles), B); S++) {
+        if ((uint64_t)S * M * N * 4 > ws_bytes) break;
+        if ((B + S - 1) / S < (B + best - 1) / best) best = S;
+    }
+    return best;
 }
 
 template <template <int> class QT, bool XH, bool ACC>
@@ -666,7 +675,7 @@ hipError_t launch_gemm_f16_silu_f16(const uint16_t *X, const uint8_t *W, uint32_
 #define RRR_SILU_CASE(T, QT)                                                                                          \
     case T:                                                                                                            \
         hipLaunchKernelGGL((gemm_dq_kernel<QT, 256, 128, 64, true, false, false, true>), dim3(tiles), dim3(512), lds, \
-                           s, X, W, ws, K, N, M, tiles_n, nullptr, K / 64, nullptr);                                   \
+                           s, X, W, ws, K, N, M, tiles_n, nullptr, 1u, nullptr);                                       \
         break;
     switch (type) {
         RRR_SILU_CASE(T_Q4_K, GqQ4K)
