@@ -467,9 +467,13 @@ def test_prefill_graph_replay_matches_eager(ctx, sweep):
 
 
 def test_prefill_fused_norms_are_the_separate_calls(ctx, sweep):
-    """record_prefill with the O-proj / FFN-down GEMMs writing the next norm
-    (rrr_gemm_f16_rmsnorm) equals the separate GEMM and RMSNorm calls bit for
-    bit: hidden rows, logits and the cached K/V."""
+    """record_prefill with its fused steps equals the separate calls bit for
+    bit (hidden rows, logits and the cached K/V): the O-proj / FFN-down GEMMs
+    writing the next norm (rrr_gemm_f16_rmsnorm), the QKV GEMM's split
+    reduction doing the RoPE + KV store (rrr_gemm_f16_rope_kv_rows) and the
+    gate/up GEMM writing silu * up (rrr_gemm_f16_silu_gate_f16).  130 tokens
+    pad to 256 rows: every GEMM but gate/up splits K, and gate/up's 128 tiles
+    are the fewest its fused form takes."""
     s, M = SHAPE, 130
     prompt = decode.prompt_host(5, s, M)
     out = []
