@@ -83,10 +83,12 @@ hipError_t launch_rope_kv_store(float *qkv, const RopeArgs &r, uint16_t *kc, uin
 // gemm_splitk_reduce adds them), then the rope_kv_store of the row: every
 // element of qkv, and the caches, end bit for bit as after the reduction
 // followed by rope_kv_store_kernel.  Rows m >= rows (the GEMM's padding rows)
-// get the plain sums.  Four elements (two pairs) a thread; the launcher
+// get the plain sums (SS = S, 2..8: a quad's partials are all requested
+// before the first add).  Four elements (two pairs) a thread; the launcher
 // requires q_dim, kv_stride and row_stride (= the GEMM's N) % 4 == 0, so a
 // quad never straddles the Q, K and V parts.
-__global__ __launch_bounds__(256) void splitk_rope_kv_store_kernel(const float *__restrict__ ws, uint32_t S, uint32_t M,
+template <int SS>
+__global__ __launch_bounds__(256) void splitk_rope_kv_store_kernel(const float *__restrict__ ws, uint32_t M,
                                                                    float *__restrict__ qkv, RopeArgs r, uint32_t rows,
                                                                    uint32_t *__restrict__ kc, uint32_t *__restrict__ vc,
                                                                    uint32_t lds_coef)
@@ -111,10 +113,13 @@ __global__ __launch_bounds__(256) void splitk_rope_kv_store_kernel(const float *
         }
     };
     for (uint32_t c = 4 * (blockIdx.x * 256 + threadIdx.x); c < N; c += 4 * gridDim.x * 256) {
-        float4 v = *(const float4 *)(src + c);
-        for (uint32_t k = 1; k < S; k++) {
-            const float4 p = *(const float4 *)(src + k * mn + c);
-            v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+        float4 p[SS];
+#pragma unroll
+        for (int k = 0; k < SS; k++) p[k] = *(const float4 *)(src + k * mn + c);
+        float4 v = p[0];
+#pragma unroll
+        for (int k = 1; k < SS; k++) {
+            v.x += p[k].x; v.y += p[k].y; v.z += p[k].z; v.w += p[k].w;
         }
         if (live) {
             float x[4] = {v.x, v.y, v.z, v.w};
@@ -171,8 +176,17 @@ hipError_t launch_splitk_rope_kv_store(const float *ws, uint32_t S, uint32_t M, 
     if (!splitk_rope_kv_store_supported(r)) return hipErrorNotSupported;
     const size_t lds = (size_t)r.rope_dim * 4;
     const uint32_t lds_coef = lds <= 32 * 1024 ? 1u : 0u;
-    hipLaunchKernelGGL(splitk_rope_kv_store_kernel, dim3(1, M), dim3(256), lds_coef ? lds : 0, s, ws, S, M, qkv, r,
-                       rows, (uint32_t *)kc, (uint32_t *)vc, lds_coef);
+#define RRR_SRK_CASE(K)                                                                                          \
+    case K:                                                                                                       \
+        hipLaunchKernelGGL(splitk_rope_kv_store_kernel<K>, dim3(1, M), dim3(256), lds_coef ? lds : 0, s, ws, M, qkv, \
+                           r, rows, (uint32_t *)kc, (uint32_t *)vc, lds_coef);                                      \
+        break;
+    switch (S) {
+        RRR_SRK_CASE(2) RRR_SRK_CASE(3) RRR_SRK_CASE(4) RRR_SRK_CASE(5)
+        RRR_SRK_CASE(6) RRR_SRK_CASE(7) RRR_SRK_CASE(8)
+    default: return hipErrorInvalidValue;
+    }
+#undef RRR_SRK_CASE
     return hipGetLastError();
 }
 

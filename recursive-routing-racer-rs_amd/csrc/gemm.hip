@@ -484,19 +484,21 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         }
 }
 
-// Y (+)= rscale[m] * sum over the S partials of ws (in split order), four
-// outputs per thread (N % 4 == 0)
-template <bool ACC>
-__global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restrict__ ws, uint32_t S, uint32_t M,
-                                                          uint32_t N, float *__restrict__ Y,
-                                                          const float *__restrict__ rscale)
+// Y (+)= rscale[m] * sum over the SS partials of ws (in split order, all
+// requested before the first add), four outputs per thread (N % 4 == 0)
+template <bool ACC, int SS>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restrict__ ws, uint32_t M, uint32_t N,
+                                                          float *__restrict__ Y, const float *__restrict__ rscale)
 {
     const uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x, mn = (uint64_t)M * N;
     if (4 * q >= mn) return;
-    float4 v = ((const float4 *)ws)[q];
-    for (uint32_t k = 1; k < S; k++) {
-        const float4 p = ((const float4 *)(ws + k * mn))[q];
-        v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+    float4 p[SS];
+#pragma unroll
+    for (int k = 0; k < SS; k++) p[k] = ((const float4 *)(ws + k * mn))[q];
+    float4 v = p[0];
+#pragma unroll
+    for (int k = 1; k < SS; k++) {
+        v.x += p[k].x; v.y += p[k].y; v.z += p[k].z; v.w += p[k].w;
     }
     if (rscale) {
         const float r = rscale[(4 * q) / N];
@@ -542,8 +544,15 @@ static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t 
     }
     if (S > 1) {
         const uint64_t quads = (uint64_t)M * N / 4;
-        hipLaunchKernelGGL(gemm_splitk_reduce<ACC>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, ws, S, M,
-                           N, Y, rscale);
+        const dim3 grid((unsigned)((quads + 255) / 256));
+#define RRR_SKR_CASE(K)                                                                                         \
+    case K: hipLaunchKernelGGL((gemm_splitk_reduce<ACC, K>), grid, dim3(256), 0, s, ws, M, N, Y, rscale); break;
+        switch (S) {
+            RRR_SKR_CASE(2) RRR_SKR_CASE(3) RRR_SKR_CASE(4) RRR_SKR_CASE(5)
+            RRR_SKR_CASE(6) RRR_SKR_CASE(7) RRR_SKR_CASE(8)
+        default: return hipErrorInvalidValue;
+        }
+#undef RRR_SKR_CASE
     }
     if (nrm) {
         const hipError_t e = hipGetLastError();

@@ -157,8 +157,11 @@ hipError_t launch_rmsnorm_f16(const float *x, const float *g, uint16_t *y, uint3
 // row's RMSNorm with gamma in f16, the arithmetic and canonical sum-of-squares
 // order of rmsnorm_kernel<_Float16> over the stored row, so both outputs are
 // bitwise the two launches'.  d % 4 == 0, d <= 8192.
-__global__ __launch_bounds__(256) void splitk_reduce_rmsnorm_kernel(const float *__restrict__ ws, uint32_t S,
-                                                                    uint32_t M, uint32_t d, float *__restrict__ Y,
+// SS: the split count (2..8), so a slot's partials are all requested before
+// the first add
+template <int SS>
+__global__ __launch_bounds__(256) void splitk_reduce_rmsnorm_kernel(const float *__restrict__ ws, uint32_t M,
+                                                                    uint32_t d, float *__restrict__ Y,
                                                                     const float *__restrict__ rscale, uint32_t acc,
                                                                     const float *__restrict__ g, float eps,
                                                                     _Float16 *__restrict__ out)
@@ -167,7 +170,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_rmsnorm_kernel(const float 
     const uint32_t m = blockIdx.x, nf = d / 4;
     const uint64_t mn = (uint64_t)M * d;
     float4 *yr = (float4 *)(Y + (uint64_t)m * d);
-    const float4 *wr = (const float4 *)(ws + (uint64_t)m * d);
     const float r = rscale ? rscale[m] : 1.0f;
     uint32_t f[8], sl[8];
     sumsq_slots<8>(sumsq_parts(d), f, sl);
@@ -176,10 +178,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_rmsnorm_kernel(const float 
     for (int j = 0; j < 8; j++) {
         v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (f[j] < nf) {
-            float4 a = wr[f[j]];
-            for (uint32_t k = 1; k < S; k++) {
-                const float4 p = ((const float4 *)(ws + k * mn + (uint64_t)m * d))[f[j]];
-                a.x += p.x; a.y += p.y; a.z += p.z; a.w += p.w;
+            float4 p[SS];
+#pragma unroll
+            for (int k = 0; k < SS; k++) p[k] = ((const float4 *)(ws + k * mn + (uint64_t)m * d))[f[j]];
+            float4 a = p[0];
+#pragma unroll
+            for (int k = 1; k < SS; k++) {
+                a.x += p[k].x; a.y += p[k].y; a.z += p[k].z; a.w += p[k].w;
             }
             if (rscale) {
                 a.x *= r; a.y *= r; a.z *= r; a.w *= r;
@@ -210,8 +215,17 @@ hipError_t launch_splitk_reduce_rmsnorm(const float *ws, uint32_t S, uint32_t M,
                                         const float *rscale, bool acc, const float *g, float eps, uint16_t *out,
                                         hipStream_t s)
 {
-    hipLaunchKernelGGL(splitk_reduce_rmsnorm_kernel, dim3(M), dim3(256), 0, s, ws, S, M, d, Y, rscale, acc ? 1u : 0u,
-                       g, eps, (_Float16 *)out);
+#define RRR_SRR_CASE(N)                                                                                          \
+    case N:                                                                                                       \
+        hipLaunchKernelGGL(splitk_reduce_rmsnorm_kernel<N>, dim3(M), dim3(256), 0, s, ws, M, d, Y, rscale,         \
+                           acc ? 1u : 0u, g, eps, (_Float16 *)out);                                                \
+        break;
+    switch (S) {
+        RRR_SRR_CASE(2) RRR_SRR_CASE(3) RRR_SRR_CASE(4) RRR_SRR_CASE(5)
+        RRR_SRR_CASE(6) RRR_SRR_CASE(7) RRR_SRR_CASE(8)
+    default: return hipErrorInvalidValue;
+    }
+#undef RRR_SRR_CASE
     return hipGetLastError();
 }
 
