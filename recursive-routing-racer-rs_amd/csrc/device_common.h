@@ -128,6 +128,21 @@ __device__ __forceinline__ float lanes4_sum(float v)
     return a + b;
 }
 
+// Sum of the n <= NMAX values p[0], p[stride], ..., p[(n - 1) stride] (LDS)
+// in index order, every one requested before the first add (one LDS wait
+// instead of one per value); n >= 1.
+template <int NMAX>
+__device__ __forceinline__ float ordered_sum(const float *p, uint32_t n, uint32_t stride)
+{
+    float q[NMAX];
+#pragma unroll
+    for (uint32_t k = 0; k < NMAX; k++) q[k] = p[stride * min(k, n - 1)];
+    float v = q[0];
+#pragma unroll
+    for (uint32_t k = 1; k < NMAX; k++) v = k < n ? v + q[k] : v;
+    return v;
+}
+
 // Deterministic full-wave sum: fixed butterfly order, identical on every call.
 __device__ __forceinline__ float wave_sum(float v)
 {

@@ -289,18 +289,8 @@ constexpr uint32_t MQ_OOB = 0x80000000u;
 // coefficients sit in LDS past the row partials (the launcher adds their
 // rope_dim floats).
 // Sum of the W <= 16 wave partials p[0], p[16], ..., p[16 (W - 1)] in wave
-// order, every one requested from LDS before the first add (one LDS wait
-// instead of one per wave).
-__device__ __forceinline__ float waves_sum(const float *p, uint32_t W)
-{
-    float q[16];
-#pragma unroll
-    for (uint32_t w = 0; w < 16; w++) q[w] = p[16 * min(w, W - 1)];
-    float v = q[0];
-#pragma unroll
-    for (uint32_t w = 1; w < 16; w++) v = w < W ? v + q[w] : v;
-    return v;
-}
+// order (all requested before the first add).
+__device__ __forceinline__ float waves_sum(const float *p, uint32_t W) { return ordered_sum<16>(p, W, 16); }
 
 template <class Q, int BPW, int ACT, bool MULTI, int TR = 16, bool PAIR = false, bool ROPE = false>
 __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr)

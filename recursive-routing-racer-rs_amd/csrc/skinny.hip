@@ -378,9 +378,8 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
         for (uint32_t i = t; i < MP * 16; i += blockDim.x) {
             const uint32_t m = i >> 4, c = i & 15, row = (tile0 + tl * GR) * 16 + c;
             if (m < M && row < N) {
-                const float *q = part + (size_t)buf * W * MP * 16 + i;
-                float v = q[0];
-                for (uint32_t w2 = 1; w2 < W; w2++) v = v + q[w2 * MP * 16];
+                // the W <= 16 waves' partials in wave order
+                float v = ordered_sum<16>(part + (size_t)buf * W * MP * 16 + i, W, MP * 16);
                 float *yp = a.y + (uint64_t)m * N + row;
                 if (a.residual) v = *yp + v;
                 *yp = v;
