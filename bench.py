@@ -533,8 +533,8 @@ def main():
     ap.add_argument("--no-skinny", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the decode path is single-device; see DESIGN.md for how it would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the decode path runs on a single device)", file=sys.stderr)
         sys.exit(2)
 
     ctx = rrr_hip.Context(0)
