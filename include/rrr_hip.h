@@ -43,7 +43,7 @@ typedef enum rrr_status {
     RRR_ERR_SHORT_BUFFER = -4, /* a buffer is smaller than the op reads/writes */
     RRR_ERR_NULL = -5,         /* null handle or pointer */
     RRR_ERR_HIP = -6,          /* a HIP runtime call failed */
-    RRR_ERR_UNSUPPORTED = -7,  /* pipeline name or shape this build does not run */
+    RRR_ERR_UNSUPPORTED = -7,  /* pipeline name or shape the library does not run */
     RRR_ERR_NO_DEVICE = -8,    /* no such HIP device */
     RRR_ERR_STATE = -9,        /* call not allowed in the context's state */
     RRR_ERR_STALE = -10        /* handle already destroyed */

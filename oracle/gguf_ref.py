@@ -6,7 +6,7 @@ included, so that tests can show (a) that the product reader
 every file the reference reads correctly, and (b) where the two part: the
 reference reads UINT8 and INT8 values as 4 bytes (gguf.rs:100-101) and skips
 one byte for an unknown value type (gguf.rs:119).  Only tests/ may import it,
-and only as the checker.
+and only to check the library's results against.
 
 Panics of the Rust code (slice out of range, failed assert, from_utf8
 unwrap, unknown quant type) raise RefPanic here.

@@ -3,7 +3,8 @@
 The CPU oracle restates the reference's CPU formulas (src/model/phi4.rs);
 see rrr_oracle.h for the function-by-function citations and the checks that
 pin each function.  Only tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg may import this module, and only as the checker.
+cpu_baseline leg may import this module, and only to check results against
+(or, for the cpu_baseline, to time the CPU formulas).
 """
 import ctypes
 import os

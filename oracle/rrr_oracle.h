@@ -3,8 +3,9 @@
  *
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference's
  * CPU formulas (src/model/phi4.rs, src/model/gguf.rs) and is used exclusively
- * as the checker by tests/, __graft_entry__.smoke() and the cpu_baseline leg of
- * bench.py.  Nothing in the product library links or calls it.
+ * to check results against, by tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py.  Nothing in the product library links or calls
+ * it.
  *
  * Build: oracle/Makefile, with -O2 -ffp-contract=off and no -ffast-math, so
  * that every `a * b + c` below rounds twice exactly as the Rust code does.

@@ -600,7 +600,7 @@ int rrr_gemm_bf16(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t typ
     TRY(device_ready(ctx));
     hipError_t e = launch_gemm_bf16((const uint16_t *)X->ptr, (const uint8_t *)W->ptr, type, (float *)Y->ptr, K, N, M,
                                     (float *)ctx->gemm_ws, GEMM_WS_BYTES, ctx->stream);
-    if (e == hipErrorNotSupported) return fail(RRR_ERR_UNSUPPORTED, "%s: shape not supported by this build", what);
+    if (e == hipErrorNotSupported) return fail(RRR_ERR_UNSUPPORTED, "%s: shape not supported by the kernels", what);
     return finish(ctx, e, what);
 }
 
