@@ -440,8 +440,8 @@ def bf16_to_f32(bits):
                                          # 256 x 128 workgroup tiles
                                          (12, 512, 16384, 256), (14, 768, 16384, 256), (13, 256, 16384, 256),
                                          # config 5 as benchmarked (512-token prompt): gate+up in one round of
-                                         # 256 x 128 tiles; down (48 tiles) with K split 4 ways, 8 super-blocks
-                                         # a split; Q4_K down and Q5_K QKV (80 tiles, split 3 ways)
+                                         # 256 x 128 tiles; down (48 tiles) with K split 5 ways, 7/7/6/6/6
+                                         # super-blocks a split; Q4_K down and Q5_K QKV (80 tiles, split 3 ways)
                                          (12, 3072, 16384, 512), (14, 8192, 3072, 512), (12, 8192, 3072, 512),
                                          (13, 3072, 5120, 512)])
 def test_gemm_bf16_parity(ctx, qtype, K, N, M):
