@@ -202,22 +202,36 @@ def platform(ctx):
     out["hbm_read_1GiB"] = {"us": round(ms * 1e3, 2), "GBs": round((1 << 30) / (ms * 1e-3) / 1e9, 1),
                             "frac_hbm": round((1 << 30) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     log(f"[bench] platform: streaming read of 1 GiB {out['hbm_read_1GiB']['GBs']} GB/s")
+    # per-launch read floors at the GEMVs' byte counts, each a graph of
+    # back-to-back launches over distinct regions (600 MB+ a pass): the
+    # size-matched form (one workgroup per CU, each lane's whole share in
+    # flight at once) and the streaming form (4 workgroups of 1024 a CU)
     floors = {}
     for name, nbytes in (("q4k_3072x3072", rrr_hip.tensor_bytes(rrr_hip.Q4_K, 3072, 3072)),
                          ("q5k_5120x3072", rrr_hip.tensor_bytes(rrr_hip.Q5_K, 3072, 5120)),
+                         ("q4k_3072x8192", rrr_hip.tensor_bytes(rrr_hip.Q4_K, 8192, 3072)),
                          ("q6k_3072x8192", rrr_hip.tensor_bytes(rrr_hip.Q6_K, 8192, 3072)),
                          ("q4k_16384x3072", rrr_hip.tensor_bytes(rrr_hip.Q4_K, 3072, 16384))):
         nb = (nbytes + 255) // 256 * 256
         regions = max(8, (600 << 20) // nb)
         views = [ctx.view(big, (r * nb) % ((1 << 30) - nb), nb) for r in range(regions)]
-        ms = timed_graph(ctx, lambda i: ctx.probe_read(views[i % regions], nb, sink), 4 * regions) / (4 * regions)
-        floors[name] = {"bytes": nb, "us": round(ms * 1e3, 3), "GBs": round(nb / (ms * 1e-3) / 1e9, 1),
-                        "frac_hbm": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        f = {"bytes": nb}
+        for form, fn in (("shares", ctx.probe_read_shares), ("streaming", ctx.probe_read)):
+            ms = timed_graph(ctx, lambda i: fn(views[i % regions], nb, sink), 4 * regions) / (4 * regions)
+            f[form] = {"us": round(ms * 1e3, 3), "GBs": round(nb / (ms * 1e-3) / 1e9, 1),
+                       "frac_hbm": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        best = min(f["shares"]["us"], f["streaming"]["us"])
+        f["floor_us"] = best
+        f["floor_frac_hbm"] = round(nb / (best * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        floors[name] = f
         log(f"[bench] platform: one launch reading {nb / 1e6:.1f} MB (the {name} GEMV's bytes): "
-            f"{ms * 1e3:.2f} us ({floors[name]['GBs']} GB/s)")
+            f"{f['shares']['us']:.2f} us one share per CU, {f['streaming']['us']:.2f} us streaming "
+            f"(floor {best:.2f} us = {100 * f['floor_frac_hbm']:.1f} % of 8 TB/s)")
         for v in views:
             v.free()
     out["read_floor_per_launch"] = floors
+    big.free()
+    out["decode_layer_read_chain"] = read_chain(ctx, sink)
     cus = ctx.probe_cus()
     mf = {}
     for name, kind, ops in (("f16_16x16x32", rrr_hip.engine.PROBE_MFMA_F16_16X16X32, 2 * 16 * 16 * 32),
@@ -231,8 +245,33 @@ def platform(ctx):
     out["mfma_dense"] = mf
     out["note"] = ("HBM peak 8.0 TB/s and dense fp16 2.5 PF/s are AMD's published figures; these are measured on "
                    "this device the way the kernels are timed (graphs of back-to-back launches, cache flushed)")
-    big.free(); sink.free()
+    sink.free()
     return out
+
+
+def read_chain(ctx, sink):
+    """The floor of the decode token's layer launches: 128 launches of the
+    size-matched read probe at the 32 layers' GEMV byte counts (QKV Q5_K,
+    O-proj Q4_K, gate/up Q4_K, down Q6_K / Q4_K alternating), each over its
+    own region of one 2 GB buffer, in layer order, as one graph behind the
+    cache flush: what a graph of one kernel per GEMV costs when the kernels
+    only read their weights (no activations, no arithmetic)."""
+    shape = decode.Phi4Shape()
+    sizes = [(rrr_hip.tensor_bytes(qt, K, N) + 255) // 256 * 256
+             for i in range(shape.n_layers) for _, qt, K, N in shape.layer_tensors(i)]
+    total = sum(sizes)
+    buf = ctx.alloc(total)
+    ctx.fill_u32(buf, 0x3F800000)
+    offs = np.cumsum([0] + sizes[:-1])
+    views = [ctx.view(buf, int(o), n) for o, n in zip(offs, sizes)]
+    ms = timed_graph(ctx, lambda i: ctx.probe_read_shares(views[i], sizes[i], sink), len(sizes))
+    for v in views:
+        v.free()
+    buf.free()
+    log(f"[bench] platform: {len(sizes)} launches reading the 32 layers' GEMV bytes ({total / 1e9:.2f} GB) "
+        f"back to back: {ms * 1e3:.1f} us ({ms * 1e3 / len(sizes):.2f} us a launch, {total / (ms * 1e-3) / 1e9:.0f} GB/s)")
+    return {"launches": len(sizes), "bytes": total, "us": round(ms * 1e3, 2),
+            "us_per_launch": round(ms * 1e3 / len(sizes), 3), "GBs": round(total / (ms * 1e-3) / 1e9, 1)}
 
 
 def prefill(ctx, reps=20):
@@ -255,9 +294,10 @@ def prefill(ctx, reps=20):
     return out
 
 
-def gemv_q4k_config1(ctx, reps=256, copies=64):
+def gemv_q4k_config1(ctx, reps=256, copies=104):
     """Single Q4_K GEMV 3072x3072, batch 1, rotating `copies` weight copies
-    (64 x 5.3 MB: one pass exceeds the 256 MB Infinity Cache)."""
+    (104 x 5.3 MB = 552 MB: one pass is over twice the 256 MB Infinity
+    Cache)."""
     K = N = 3072
     ws = [ctx.weight_upload(rrr_hip.Q4_K, K, N, synth.weight(1, 200 + c, rrr_hip.Q4_K, K, N)) for c in range(copies)]
     x, y = ctx.to_device(synth.normal_f32(1, 1, K)), ctx.alloc(N * 4)
@@ -273,11 +313,12 @@ def gemv_q4k_config1(ctx, reps=256, copies=64):
 
 def skinny(ctx, reps=64):
     """Batched GEMV / skinny GEMM, M in {4, 8, 32} token rows of f32 X:
-    gate+up Q4_K 16384x3072 (10 copies, 283 MB) and QKV Q5_K 5120x3072
-    (26 copies, 281 MB), rotated so the weights stream from HBM."""
+    gate+up Q4_K 16384x3072 (20 copies, 566 MB) and QKV Q5_K 5120x3072
+    (52 copies, 562 MB), rotated so the weights stream from HBM (a pass is
+    over twice the 256 MB Infinity Cache)."""
     out = {}
-    for name, qt, K, N, copies in (("gateup_q4k_16384x3072", rrr_hip.Q4_K, 3072, 16384, 10),
-                                   ("qkv_q5k_5120x3072", rrr_hip.Q5_K, 3072, 5120, 26)):
+    for name, qt, K, N, copies in (("gateup_q4k_16384x3072", rrr_hip.Q4_K, 3072, 16384, 20),
+                                   ("qkv_q5k_5120x3072", rrr_hip.Q5_K, 3072, 5120, 52)):
         ws = [ctx.weight_upload(qt, K, N, synth.weight(4, 300 + c, qt, K, N)) for c in range(copies)]
         for M in (4, 8, 32):
             x, y = ctx.to_device(synth.normal_f32(4, 40 + M, M * K)), ctx.alloc(M * N * 4)
@@ -292,6 +333,28 @@ def skinny(ctx, reps=64):
             x.free(); y.free()
         for w in ws:
             w.free()
+    return out
+
+
+def batched_prompt(ctx, reps=8, M=512):
+    """The reference's batch pipelines at a prompt's row count, M = 512, as
+    its prefill dispatches them (matmul_gpuq*_batch, push [K, N, M], grid
+    [N, M, 1], phi4.rs:1257-1268, :1346-1391): f32 X rows through the name
+    shim onto the fp16 matrix cores (f16 block-floating-point rows, 2e-3
+    bar); QKV Q5_K 5120x3072, gate/up Q4_K 16384x3072, down Q6_K 3072x8192."""
+    out = {}
+    for name, pipe, qt, K, N in (("qkv_q5k_5120x3072", "matmul_gpuq5_batch", rrr_hip.Q5_K, 3072, 5120),
+                                 ("gateup_q4k_16384x3072", "matmul_gpuq4_batch", rrr_hip.Q4_K, 3072, 16384),
+                                 ("down_q6k_3072x8192", "matmul_gpuq6_batch", rrr_hip.Q6_K, 8192, 3072)):
+        W = ctx.weight_upload(qt, K, N, synth.weight(5, 70 + qt, qt, K, N))
+        X, Y = ctx.to_device(synth.normal_f32(5, 71 + qt, M * K)), ctx.alloc(M * N * 4)
+        ms = timed_graph(ctx, lambda i: ctx.dispatch(pipe, [X, W, Y], [K, N, M], [N, M, 1]), reps) / reps
+        tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        log(f"[bench] {pipe} M={M} ({name}): {ms * 1e3:.2f} us, {tf:.0f} TFLOP/s")
+        out[f"batched_{name}_m{M}"] = {"us": round(ms * 1e3, 3), "TFLOPs": round(tf, 1),
+                                       "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4), "pipeline": pipe,
+                                       "flops": 2 * M * N * K}
+        W.free(); X.free(); Y.free()
     return out
 
 
@@ -364,29 +427,6 @@ def decode_sweep(ctx, tokens):
     b = shape.bytes_per_token()
     log(f"[bench] decode sweep (graph of per-op launches): {ms:.4f} ms/token ({b / (ms * 1e-3) / 1e9:.0f} GB/s), "
         f"argmax {tok}")
-    # the 128 layer GEMVs as one persistent launch per token, the token as
-    # one graph (input row, sweep, RMSNorm + logits, argmax)
-    per = sw.ctx.sweep(sw.sweep_ops())
-    ctx.graph_begin()
-    sw.run_token_sweep(per)
-    gpt = ctx.graph_end()
-    for _ in range(3):
-        gpt.launch()
-    per.check()
-    FLUSH()
-    ctx.timer_start()
-    for _ in range(tokens):
-        gpt.launch()
-    ms_p = ctx.timer_stop() / tokens
-    per.check()
-    gpt.destroy()
-    logits_p, tok_p, _ = sw.results()
-    per.destroy()
-    # the sweep sums in another order than the per-op kernels: same 1e-4 bar,
-    # not bitwise equal; reported as the max deviation over the max |logit|
-    dev = float(np.max(np.abs(logits_p.astype(np.float64) - logits)) / max(np.max(np.abs(logits)), 1e-30))
-    log(f"[bench] decode sweep (persistent layer sweep): {ms_p:.4f} ms/token ({b / (ms_p * 1e-3) / 1e9:.0f} GB/s), "
-        f"argmax {tok_p}, logits within {dev:.2e} of the per-op run")
     # the full decode step at the last cache position: RoPE + f16 KV store and
     # attention over 2048 rows per layer on top of the sweep
     pos = shape.max_seq - 1
@@ -449,8 +489,7 @@ def decode_sweep(ctx, tokens):
     log(f"[bench] prefill of {M} tokens through 32 layers + logits: {ms_pf:.3f} ms ({M / (ms_pf * 1e-3):.0f} tokens/s, "
         f"{fl / (ms_pf * 1e-3) / 1e12:.0f} TFLOP/s in the layer GEMMs), argmax {tok_pf}")
     gg = gguf_load(ctx, sw, shape)
-    best = min(ms, ms_p)
-    return {"ms_per_token": round(best, 5), "tokens": tokens, "bytes_per_token": b, "gguf_load": gg,
+    return {"ms_per_token": round(ms, 5), "tokens": tokens, "bytes_per_token": b, "gguf_load": gg,
             "prefill_512": {"ms": round(ms_pf, 4), "tokens_per_s": round(M / (ms_pf * 1e-3), 1),
                             "gemm_flops": fl, "TFLOPs": round(fl / (ms_pf * 1e-3) / 1e12, 1),
                             "frac_fp16_peak": round(fl / (ms_pf * 1e-3) / 2.5e15, 4), "argmax": tok_pf,
@@ -465,9 +504,8 @@ def decode_sweep(ctx, tokens):
             "attention_2048_rows": {"us_per_layer": round(us_att, 3), "kv_bytes": kv_bytes,
                                     "GBs": round(kv_bytes / (us_att * 1e-6) / 1e9, 1),
                                     "frac_hbm": round(kv_bytes / (us_att * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
-            "GBs": round(b / (best * 1e-3) / 1e9, 1), "frac_hbm": round(b / (best * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "ms_per_token_per_op_graph": round(ms, 5), "ms_per_token_persistent": round(ms_p, 5),
-            "persistent_logits_rel_dev": dev, "persistent_argmax": tok_p,
+            "GBs": round(b / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "ms_per_token_per_op_graph": round(ms, 5),
             "argmax": tok, "logits_finite": bool(np.all(np.isfinite(logits))),
             "workload": "32 layers (RMSNorm+QKV Q5_K 5120x3072, O Q4_K 3072x3072 +res, RMSNorm+gate/up Q4_K "
                         "16384x3072, silu+down Q6_K/Q4_K 3072x8192 +res) + RMSNorm + F32 logits 200064x3072 "
@@ -614,6 +652,7 @@ def main():
         extra.update(skinny(ctx))
     if not args.no_prefill:
         extra.update(prefill(ctx))
+        extra.update(batched_prompt(ctx))
 
     if not args.no_decode:
         extra["decode_sweep"] = decode_sweep(ctx, args.tokens)
@@ -635,6 +674,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "dtype_detail": ("f32 activations in and f32 outputs; the batch-1 GEMVs feed the int8 matrix cores "
+                         "with each 16-element group of x in 20-bit block fixed point (three int8 digits, "
+                         "encoding error below 2^-20 of the group maximum), raw K-quant weights, int32 / f32 "
+                         "accumulation; 1e-4 normwise of the fp64 oracle"),
         "data": "synthetic (seeded splitmix64: K-quant blocks per the config recipe, N(0,1) activations)",
         "config": {"workload": "rmsnorm_3072 + q5k_gemv_5120x3072 + q6k_gemv_3072x8192, batch 1 "
                                "(RMSNorm fused into the QKV GEMV)",

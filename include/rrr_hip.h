@@ -72,7 +72,6 @@ typedef enum rrr_logits_layout {
 typedef struct rrr_ctx rrr_ctx;
 typedef struct rrr_buf rrr_buf;
 typedef struct rrr_graph rrr_graph;
-typedef struct rrr_sweep rrr_sweep;
 
 /* ---- engine lifetime ------------------------------------------------- */
 
@@ -139,14 +138,24 @@ int rrr_dequant(rrr_ctx *ctx, uint32_t type, const rrr_buf *W, rrr_buf *out, uin
  * M == 1 replaces matmul_q{4,5,6}k / matmul_gpuq{4,5,6} (push [K, N], grid
  * [N,1,1]; phi4.rs:631-658, :1081-1096) and matmul_tiled for F32 weights
  * (phi4.rs:641-646).  M > 1 replaces matmul_gpuq*_batch (push [K, N, M],
- * grid [N, M, 1]; phi4.rs:1257-1268, :1346-1391).  type 0 means F32 W stored
- * row-major N x K. */
+ * grid [N, M, 1]; phi4.rs:1257-1268, :1346-1391), which the reference's
+ * prefill calls with M = the prompt length.  type 0 means F32 W stored
+ * row-major N x K.  Accuracy: within 1e-4 normwise of the exact product per
+ * row up to M = 16; above 16 rows the K-quant rows run on the fp16 matrix
+ * cores (Q4_K / Q5_K with K <= 3072 up to 32 rows, every K-quant shape with
+ * N % 64 == 0, X and Y 16-byte aligned, beyond: X as f16 rows with a
+ * power-of-two scale per row, zero-padded to 128 rows in the context
+ * workspace) within 2e-3. */
 int rrr_gemv(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t type, rrr_buf *Y,
              uint32_t K, uint32_t N, uint32_t M);
 
 /* Y[m][n] = sum_k float(X_bf16[m][k]) * W[n][k]: the prefill dequant-GEMM
  * (MFMA, fp16 tiles, fp32 accumulate).  No reference counterpart exists for the
- * MFMA kernel; its call shape is the batched one above with X in bf16. */
+ * MFMA kernel; its call shape is the batched one above with X in bf16.  Any
+ * M >= 1: X is converted to f16 (exact in f16's normal range) in row chunks
+ * inside the context workspace, each padded with zero rows to a multiple of
+ * 128.  K-quant W with N % 64 == 0 (else RRR_ERR_UNSUPPORTED); X and Y
+ * 16-byte aligned. */
 int rrr_gemm_bf16(rrr_ctx *ctx, const rrr_buf *X_bf16, const rrr_buf *W, uint32_t type,
                   rrr_buf *Y, uint32_t K, uint32_t N, uint32_t M);
 
@@ -412,52 +421,6 @@ int rrr_graph_begin(rrr_ctx *ctx);
 int rrr_graph_end(rrr_ctx *ctx, rrr_graph **out);
 int rrr_graph_launch(rrr_ctx *ctx, rrr_graph *g);
 int rrr_graph_destroy(rrr_ctx *ctx, rrr_graph *g);
-
-/* ---- persistent decode sweep -------------------------------------------- */
-
-/* One op of a sweep: exactly the arguments of rrr_gemv_rmsnorm (kind
- * RRR_SWEEP_GEMV_RMSNORM; act_kind / act_param unused) or of
- * rrr_gemv_residual (kind RRR_SWEEP_GEMV_RESIDUAL; gamma / eps unused). */
-enum { RRR_SWEEP_GEMV_RMSNORM = 0, RRR_SWEEP_GEMV_RESIDUAL = 1 };
-typedef struct rrr_sweep_op {
-    uint32_t kind;
-    const rrr_buf *x;
-    const rrr_buf *gamma;
-    float eps;
-    uint32_t act_kind;
-    uint32_t act_param;
-    const rrr_buf *W;
-    uint32_t type;
-    rrr_buf *y;
-    uint32_t K;
-    uint32_t N;
-} rrr_sweep_op;
-
-/* A list of fused decode GEMVs run in order by ONE persistent launch (one
- * workgroup per CU): the MI355X counterpart of replaying the layer dispatches
- * through dispatch_batch_persistent_v2 with a barrier between dependent
- * dispatches (engine.rs:317-370, phi4.rs:1163-1168).  Each op starts once
- * every row of the previous op is written; its weights stream into LDS while
- * the previous op runs.  Results meet the same 1e-4 bar as the ops issued one
- * by one (not the same bits: the down GEMVs split K three ways per wave and
- * an RMSNorm takes its sum of squares from the previous op's workgroups in
- * workgroup order) and are the same bits on every run.  Supported: the decode
- * layer's sequence -- RMSNorm + Q5_K (QKV), GQA-V + Q4_K (O-proj),
- * RMSNorm + Q4_K (gate/up), SiLU-gate + Q6_K or Q4_K (down), K <= 3072 for
- * the first three and 3072 < K <= 9216 for the down GEMV -- where an RMSNorm
- * op past the first follows the residual op that writes its input;
- * RRR_ERR_UNSUPPORTED otherwise.  The buffers are referenced, not copied:
- * they must outlive the sweep and stay at their size. */
-int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_sweep **out);
-/* Runs the sweep on the context stream; may be recorded between
- * rrr_graph_begin and rrr_graph_end and replayed (its epochs live in device
- * memory).  Runs of one sweep must not overlap. */
-int rrr_sweep_run(rrr_ctx *ctx, rrr_sweep *sw);
-/* Waits for the stream; RRR_ERR_HIP if a run gave up waiting for an op (a
- * bounded wait of about 2 s expired: its outputs are invalid), else RRR_OK.
- * Clears the condition. */
-int rrr_sweep_check(rrr_ctx *ctx, rrr_sweep *sw);
-int rrr_sweep_destroy(rrr_ctx *ctx, rrr_sweep *sw);
 
 /* ---- synchronisation and timing -------------------------------------- */
 

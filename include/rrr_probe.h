@@ -21,6 +21,15 @@ extern "C" {
  * reaches; a read of twice the Infinity Cache's 256 MB evicts it. */
 int rrr_probe_read(rrr_ctx *ctx, const rrr_buf *buf, uint64_t bytes, rrr_buf *sink);
 
+/* Per-launch read floor of a GEMV's byte count: one workgroup of 1024
+ * threads per CU reads a contiguous share of ceil(bytes / CUs) bytes (rounded
+ * up to 16 KB), every lane issuing all of its 16-byte non-temporal loads
+ * (at most 16) before using any.  bytes a positive multiple of 16, at most
+ * CUs * 256 KB (RRR_ERR_UNSUPPORTED beyond).  bytes / time is what one launch
+ * that only reads those bytes, spread over every CU as the GEMVs spread their
+ * rows, reaches. */
+int rrr_probe_read_shares(rrr_ctx *ctx, const rrr_buf *buf, uint64_t bytes, rrr_buf *sink);
+
 /* Matrix-core rate: `waves_per_cu` waves on every CU (a multiple of 4, at most
  * 32) each run `iters` rounds of 4 independent MFMAs of `kind`.  Operations per
  * launch = CUs * waves_per_cu * iters * 4 * ops_per_mfma, ops_per_mfma

@@ -138,18 +138,25 @@ def residual_add(a, b):
     return out
 
 
+MAX_M = 1024   # token rows of one rrr_o_gemv call (rrr_oracle.c)
+
+
 def gemv(qtype, W, X, K, N, M=1, threads=1, f64=False):
-    """Y[M, N] from raw W (N x K of qtype) and X[M, K]."""
+    """Y[M, N] from raw W (N x K of qtype) and X[M, K]; more than MAX_M rows
+    go through in calls of MAX_M (every row is computed on its own)."""
     W = np.ascontiguousarray(W).view(np.uint8)
-    X = np.ascontiguousarray(X, dtype=np.float32)
-    if f64:
-        Y = np.empty(M * N, dtype=np.float64)
-        rc = lib().rrr_o_gemv_f64(qtype, _p(W, _u8p), _p(X, _f32p), _p(Y, _f64p), K, N, M, threads)
-    else:
-        Y = np.empty(M * N, dtype=np.float32)
-        rc = lib().rrr_o_gemv(qtype, _p(W, _u8p), _p(X, _f32p), _p(Y, _f32p), K, N, M, threads)
-    if rc != 0:
-        raise ValueError("oracle gemv rejected its arguments")
+    X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1)
+    Y = np.empty(M * N, dtype=np.float64 if f64 else np.float32)
+    for m0 in range(0, M, MAX_M):
+        mc = min(MAX_M, M - m0)
+        x = X[m0 * K:(m0 + mc) * K]
+        y = Y[m0 * N:(m0 + mc) * N]
+        if f64:
+            rc = lib().rrr_o_gemv_f64(qtype, _p(W, _u8p), _p(x, _f32p), _p(y, _f64p), K, N, mc, threads)
+        else:
+            rc = lib().rrr_o_gemv(qtype, _p(W, _u8p), _p(x, _f32p), _p(y, _f32p), K, N, mc, threads)
+        if rc != 0:
+            raise ValueError("oracle gemv rejected its arguments")
     return Y.reshape(M, N)
 
 

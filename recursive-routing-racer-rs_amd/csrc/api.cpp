@@ -66,14 +66,6 @@ struct rrr_buf {
     rrr_buf *parent;  // non-null for views
 };
 
-struct rrr_sweep {
-    uint32_t magic;
-    void *ops;          // device SwOpDev[nops]
-    uint32_t *state;    // device: completion records, run counters, error word
-    uint32_t *err;      // device, inside the state
-    uint32_t nops, grid;
-};
-
 struct rrr_graph {
     uint32_t magic;
     rrr_ctx *ctx;
@@ -97,7 +89,6 @@ struct rrr_ctx {
     void *logits_cnt;   // split-K logits: per-slab counters (zero between calls)
     std::unordered_set<rrr_buf *> bufs;
     std::unordered_set<rrr_graph *> graphs;
-    std::unordered_set<rrr_sweep *> sweeps;
 };
 
 namespace {
@@ -260,12 +251,6 @@ int rrr_destroy(rrr_ctx *ctx)
             g->magic = 0;
             delete g;
         }
-        for (rrr_sweep *sw : ctx->sweeps) {
-            (void)hipFree(sw->ops);
-            (void)hipFree(sw->state);
-            sw->magic = 0;
-            delete sw;
-        }
         for (rrr_buf *b : ctx->bufs)
             if (!b->parent && b->ptr) (void)hipFree(b->ptr);
         (void)hipFree(ctx->scratch);
@@ -277,7 +262,6 @@ int rrr_destroy(rrr_ctx *ctx)
         (void)hipStreamDestroy(ctx->stream);
     } else {
         for (rrr_graph *g : ctx->graphs) delete g;
-        for (rrr_sweep *sw : ctx->sweeps) delete sw;
     }
     for (rrr_buf *b : ctx->bufs) {
         b->magic = 0;
@@ -597,6 +581,10 @@ int rrr_gemm_bf16(rrr_ctx *ctx, const rrr_buf *X, const rrr_buf *W, uint32_t typ
     TRY(need(W, rrr_tensor_bytes(type, K, N), what));
     TRY(need(X, (uint64_t)M * K * 2, what));
     TRY(need_f32(Y, (uint64_t)M * N, what));
+    if (!gemm_rows_supported(type, K, N, M, GEMM_WS_BYTES))
+        return fail(RRR_ERR_UNSUPPORTED, "%s: needs N %% 64 == 0 (N=%u)", what, N);
+    if (((uintptr_t)X->ptr | (uintptr_t)Y->ptr) & 15)
+        return fail(RRR_ERR_INVALID_ARG, "%s: X and Y must be 16-byte aligned", what);
     TRY(device_ready(ctx));
     hipError_t e = launch_gemm_bf16((const uint16_t *)X->ptr, (const uint8_t *)W->ptr, type, (float *)Y->ptr, K, N, M,
                                     (float *)ctx->gemm_ws, GEMM_WS_BYTES, ctx->stream);
@@ -862,12 +850,12 @@ int rrr_attention(rrr_ctx *ctx, const rrr_buf *q, const rrr_buf *k_cache, const 
     TRY(need_f32(out, nq, what));
     TRY(need(k_cache, 2 * kv, what));
     TRY(need(v_cache, 2 * kv, what));
-    if (((uintptr_t)k_cache->ptr | (uintptr_t)v_cache->ptr) & 15)
-        return fail(RRR_ERR_INVALID_ARG, "%s: caches must be 16-byte aligned", what);
+    if (((uintptr_t)q->ptr | (uintptr_t)out->ptr | (uintptr_t)k_cache->ptr | (uintptr_t)v_cache->ptr) & 15)
+        return fail(RRR_ERR_INVALID_ARG, "%s: q, out and the caches must be 16-byte aligned", what);
     TRY(device_ready(ctx));
     return finish(ctx, launch_attention((const float *)q->ptr, (const uint16_t *)k_cache->ptr,
                                         (const uint16_t *)v_cache->ptr, (float *)out->ptr, ctx->att_scratch, seq_len,
-                                        n_kv_heads, heads_per_kv, sweep_cus(), ctx->stream),
+                                        n_kv_heads, heads_per_kv, device_cu_count(), ctx->stream),
                   what);
 }
 
@@ -1293,134 +1281,6 @@ int rrr_graph_destroy(rrr_ctx *ctx, rrr_graph *g)
 
 // ---- sync and timing ----------------------------------------------------------
 
-// ---- persistent decode sweep --------------------------------------------
-
-static constexpr uint32_t SWEEP_MAGIC = 0x53574550u;
-
-static int check_sweep(rrr_ctx *ctx, rrr_sweep *sw, const char *what)
-{
-    if (!sw) return fail(RRR_ERR_NULL, "%s: null sweep", what);
-    if (!ctx->sweeps.count(sw) || sw->magic != SWEEP_MAGIC)
-        return fail(RRR_ERR_STALE, "%s: sweep already destroyed or not owned by this context", what);
-    return RRR_OK;
-}
-
-int rrr_sweep_create(rrr_ctx *ctx, const rrr_sweep_op *ops, uint32_t n, rrr_sweep **out)
-{
-    TRY(check_ctx(ctx));
-    const char *what = "rrr_sweep_create";
-    if (!out || (!ops && n)) return fail(RRR_ERR_NULL, "%s: null argument", what);
-    *out = nullptr;
-    if (n == 0) return fail(RRR_ERR_INVALID_ARG, "%s: no ops", what);
-    if (ctx->capturing) return fail(RRR_ERR_INVALID_ARG, "%s: not inside rrr_graph_begin/end", what);
-    TRY(device_ready(ctx));
-    const uint32_t grid = sweep_grid(0);
-    if (grid == 0) return fail(RRR_ERR_UNSUPPORTED, "%s: the sweep's workgroup does not fit a CU", what);
-    std::vector<GemvArgs> args(n);
-    std::vector<uint32_t> acts(n), variants(n), ntiles(n), trs(n);
-    for (uint32_t i = 0; i < n; i++) {
-        const rrr_sweep_op &o = ops[i];
-        GemvArgs &a = args[i];
-        if (o.kind == RRR_SWEEP_GEMV_RMSNORM) {
-            if (!o.gamma) return fail(RRR_ERR_NULL, "%s: op %u: null gamma", what, i);
-            TRY(gemv_prepare(ctx, o.x, o.K, o.gamma, o.eps, ACT_RMSNORM, 0, 0, o.W, o.type, o.y, o.K, o.N, 1, 0,
-                             what, a));
-            acts[i] = ACT_RMSNORM;
-        } else if (o.kind == RRR_SWEEP_GEMV_RESIDUAL) {
-            uint64_t x_floats;
-            uint32_t act, hd, hpk;
-            TRY(residual_act(o.act_kind, o.act_param, o.K, x_floats, act, hd, hpk, what));
-            TRY(gemv_prepare(ctx, o.x, x_floats, nullptr, 0.0f, act, hd, hpk, o.W, o.type, o.y, o.K, o.N, 1, 1,
-                             what, a));
-            acts[i] = act;
-        } else {
-            return fail(RRR_ERR_INVALID_ARG, "%s: op %u: kind %u", what, i, o.kind);
-        }
-        size_t l;
-        if (!sweep_plan_op(a, acts[i], grid, variants[i], ntiles[i], trs[i], l))
-            return fail(RRR_ERR_UNSUPPORTED, "%s: op %u (type %u, K=%u, N=%u) is not a sweep shape", what, i, o.type,
-                        o.K, o.N);
-        // an RMSNorm op past the first takes its input's sum of squares from
-        // the previous op's completion records: that op must write its input
-        if (i > 0 && acts[i] == ACT_RMSNORM &&
-            (ops[i - 1].kind != RRR_SWEEP_GEMV_RESIDUAL || ops[i - 1].y != o.x || ops[i - 1].N != o.K))
-            return fail(RRR_ERR_UNSUPPORTED, "%s: op %u: an RMSNorm op must follow the residual op that writes its input",
-                        what, i);
-        if (i > 0 && !sweep_pair_ok(variants[i - 1], ntiles[i - 1], trs[i - 1], variants[i], ntiles[i], trs[i], grid))
-            return fail(RRR_ERR_UNSUPPORTED, "%s: op %u cannot follow op %u in one sweep (not a decode-layer sequence)",
-                        what, i, i - 1);
-    }
-    std::vector<uint8_t> packed((size_t)n * sweep_op_bytes());
-    for (uint32_t i = 0; i < n; i++)
-        sweep_pack_op(packed.data() + (size_t)i * sweep_op_bytes(), args[i], variants[i], ntiles[i], trs[i], grid);
-    rrr_sweep *sw = new rrr_sweep{};
-    sw->magic = SWEEP_MAGIC;
-    sw->nops = n;
-    sw->grid = grid;
-    hipError_t e = hipMalloc(&sw->ops, packed.size());
-    const size_t sbytes = 4 * sweep_state_words();
-    if (e == hipSuccess) e = hipMalloc((void **)&sw->state, sbytes);
-    if (e == hipSuccess) {
-        sw->err = sw->state + sweep_err_word();
-        e = hipMemcpyAsync(sw->ops, packed.data(), packed.size(), hipMemcpyHostToDevice, ctx->stream);
-    }
-    if (e == hipSuccess) e = hipMemsetAsync(sw->state, 0, sbytes, ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) {
-        (void)hipFree(sw->ops);
-        (void)hipFree(sw->state);
-        delete sw;
-        return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-    }
-    ctx->sweeps.insert(sw);
-    *out = sw;
-    return ok();
-}
-
-int rrr_sweep_run(rrr_ctx *ctx, rrr_sweep *sw)
-{
-    TRY(check_ctx(ctx));
-    const char *what = "rrr_sweep_run";
-    TRY(check_sweep(ctx, sw, what));
-    TRY(device_ready(ctx));
-    // the epochs come from run counters in device memory: the launch may be
-    // recorded into a graph and replayed
-    return finish(ctx, launch_sweep(sw->ops, sw->nops, sw->state, sw->grid, ctx->stream), what);
-}
-
-int rrr_sweep_check(rrr_ctx *ctx, rrr_sweep *sw)
-{
-    TRY(check_ctx(ctx));
-    const char *what = "rrr_sweep_check";
-    TRY(check_sweep(ctx, sw, what));
-    TRY(device_ready(ctx));
-    uint32_t err = 0;
-    hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e == hipSuccess) e = hipMemcpy(&err, sw->err, 4, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-    if (err) {
-        // start over: records, run counters and the error word back to zero
-        e = hipMemset(sw->state, 0, 4 * sweep_state_words());
-        if (e != hipSuccess) return fail(RRR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-        return fail(RRR_ERR_HIP, "%s: a sweep run gave up waiting for an op; its outputs are invalid", what);
-    }
-    return ok();
-}
-
-int rrr_sweep_destroy(rrr_ctx *ctx, rrr_sweep *sw)
-{
-    TRY(check_ctx(ctx));
-    TRY(check_sweep(ctx, sw, "rrr_sweep_destroy"));
-    (void)hipSetDevice(ctx->device);
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(sw->ops);
-    (void)hipFree(sw->state);
-    ctx->sweeps.erase(sw);
-    sw->magic = 0;
-    delete sw;
-    return ok();
-}
-
 int rrr_set_async(rrr_ctx *ctx, int async)
 {
     TRY(check_ctx(ctx));
@@ -1478,6 +1338,21 @@ int rrr_probe_read(rrr_ctx *ctx, const rrr_buf *buf, uint64_t bytes, rrr_buf *si
     return finish(ctx, launch_probe_read(buf->ptr, bytes, (uint32_t *)sink->ptr, ctx->stream), what);
 }
 
+int rrr_probe_read_shares(rrr_ctx *ctx, const rrr_buf *buf, uint64_t bytes, rrr_buf *sink)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_probe_read_shares";
+    TRY(check_buf(ctx, buf, what));
+    TRY(check_buf(ctx, sink, what));
+    if (bytes == 0 || bytes % 16) return fail(RRR_ERR_INVALID_ARG, "%s: bytes must be a positive multiple of 16", what);
+    TRY(need(buf, bytes, what));
+    TRY(need(sink, 4, what));
+    TRY(device_ready(ctx));
+    if (!probe_shares_supported(bytes))
+        return fail(RRR_ERR_UNSUPPORTED, "%s: %llu bytes exceed 256 KB per CU", what, (unsigned long long)bytes);
+    return finish(ctx, launch_probe_shares(buf->ptr, bytes, (uint32_t *)sink->ptr, ctx->stream), what);
+}
+
 int rrr_probe_mfma(rrr_ctx *ctx, uint32_t kind, uint32_t waves_per_cu, uint32_t iters, rrr_buf *sink)
 {
     TRY(check_ctx(ctx));
@@ -1495,7 +1370,7 @@ int rrr_probe_mfma(rrr_ctx *ctx, uint32_t kind, uint32_t waves_per_cu, uint32_t 
 uint32_t rrr_probe_cus(rrr_ctx *ctx)
 {
     if (check_ctx(ctx) != RRR_OK || ctx->nodevice || device_ready(ctx) != RRR_OK) return 0;
-    return sweep_cus();
+    return device_cu_count();
 }
 
 // ---- one-call helper ------------------------------------------------------------

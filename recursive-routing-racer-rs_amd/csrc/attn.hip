@@ -971,7 +971,7 @@ hipError_t launch_attention_prefill(const float *qkv, uint32_t row_stride, uint3
     // else the KV group's heads share every K/V block in one workgroup
     // (512 rows: 22.4 against 30.8 us split)
     const uint64_t tgroups = (rows + 15) / 16;
-    if (heads_per_kv > 1 && heads_per_kv <= 4 && (uint64_t)n_kv_heads * heads_per_kv * tgroups <= sweep_cus()) {
+    if (heads_per_kv > 1 && heads_per_kv <= 4 && (uint64_t)n_kv_heads * heads_per_kv * tgroups <= device_cu_count()) {
         go_attn_prefill<1>(qkv, row_stride, rows, kc, vc, out, out_f16, pos0, n_kv_heads, qscale, s, heads_per_kv);
         return hipGetLastError();
     }

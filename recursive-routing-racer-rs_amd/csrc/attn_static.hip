@@ -74,7 +74,7 @@ extern "C" int rrr_attention_noalloc(const float *q, const uint16_t *k_cache, co
     // node, so the call may be captured into a graph)
     hipError_t e = launch_fill_u32((uint32_t *)ptr, ATT_COUNTER_BYTES / 4, 0u, s);
     if (e == hipSuccess)
-        e = launch_attention(q, k_cache, v_cache, out, ptr, seq_len, n_kv_heads, heads_per_kv, sweep_cus(), s);
+        e = launch_attention(q, k_cache, v_cache, out, ptr, seq_len, n_kv_heads, heads_per_kv, device_cu_count(), s);
     if (e != hipSuccess) return set_error(RRR_ERR_HIP, hipGetErrorString(e));
     return set_error(RRR_OK, "");
 }

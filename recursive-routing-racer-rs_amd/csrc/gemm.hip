@@ -224,10 +224,10 @@ __device__ __forceinline__ void silu_rows_store(float *Y, uint32_t F, uint32_t n
 // Y (M x F) gets silu_f(gate) * up of the sums the plain GEMM stores.  The
 // MFMA waves hand row blocks 2 and 3 of their sums to the staging waves
 // through the (then idle) LDS, so the eight waves share the silu work.
-template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC, bool SPLIT, bool SILU = false>
+template <template <int> class QT, int BM, int BN, int BK, bool ACC, bool SPLIT, bool SILU = false>
 __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const uint8_t *W, float *Y, uint32_t K,
                                                       uint32_t N, uint32_t M, uint32_t tiles_n, const float *rscale,
-                                                      uint32_t S, float *ws)
+                                                      uint32_t S, float *ws, uint32_t mrows)
 {
     // LDS rows of BK f16, unpadded; 16-byte chunk c of row r sits at chunk
     // c ^ swz(r), swz(r) = (r / RPL) % CPR with RPL rows per 64-bank line
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     using Q = QT<NPW>;
     // register sets of the producer's load ring: four (loads issued four
     // steps ahead) where the registers allow it, else three
-    constexpr int NSET = (XH && BK == 64 && Q::BS != 210) ? 4 : 3;
+    constexpr int NSET = (BK == 64 && Q::BS != 210) ? 4 : 3;
     extern __shared__ float smem[];
     _Float16 *As = (_Float16 *)smem;                       // [2][BM][LDK]
     _Float16 *Bs = As + 2 * BM * LDK;                      // [2][BN][LDK]
@@ -312,18 +312,7 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
                     u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
             _Float16 *xd = As + (buf * BM + xr) * LDK + 8 * ((xk / 8) ^ swz(xr));   // pass i: + XRS*i rows
 #pragma unroll
-            for (int i = 0; i < XE / 8; i++) {
-                const u32x4 v = st.xv[i];
-                u32x4 h;
-                if constexpr (XH) {
-                    h = v;
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; c++)
-                        h[c] = pk_f16(__uint_as_float(v[c] << 16), __uint_as_float(v[c] & 0xFFFF0000u));
-                }
-                *(u32x4 *)(xd + XRS * i * LDK) = h;
-            }
+            for (int i = 0; i < XE / 8; i++) *(u32x4 *)(xd + XRS * i * LDK) = st.xv[i];
         };
         issue(S0, 0);
         issue(S1, 1);
@@ -475,6 +464,7 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
                     ws[((uint64_t)ks * M + m) * N + n] = acc[i][j][r];
                     continue;
                 }
+                if (m >= mrows) continue;   // zero padding rows of a row chunk: not the caller's
                 const float v = rscale ? acc[i][j][r] * rscale[m] : acc[i][j][r];
                 if constexpr (ACC)
                     Y[(uint64_t)m * N + n] += v;
@@ -485,13 +475,15 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
 }
 
 // Y (+)= rscale[m] * sum over the SS partials of ws (in split order, all
-// requested before the first add), four outputs per thread (N % 4 == 0)
+// requested before the first add), four outputs per thread (N % 4 == 0), for
+// the first mrows of the M partial rows
 template <bool ACC, int SS>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restrict__ ws, uint32_t M, uint32_t N,
-                                                          float *__restrict__ Y, const float *__restrict__ rscale)
+                                                          float *__restrict__ Y, const float *__restrict__ rscale,
+                                                          uint32_t mrows)
 {
     const uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x, mn = (uint64_t)M * N;
-    if (4 * q >= mn) return;
+    if (4 * q >= (uint64_t)mrows * N) return;
     float4 p[SS];
 #pragma unroll
     for (int k = 0; k < SS; k++) p[k] = ((const float4 *)(ws + k * mn))[q];
@@ -512,19 +504,22 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restric
     *y = v;
 }
 
-template <template <int> class QT, int BM, int BN, int BK, bool XH, bool ACC>
+template <template <int> class QT, int BM, int BN, int BK, bool ACC>
 static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K, uint32_t N,
-                          uint32_t M, uint32_t S, float *ws, const GemmNorm *nrm, const GemmRope *rp, hipStream_t s)
+                          uint32_t M, uint32_t mrows, uint32_t S, float *ws, const GemmNorm *nrm, const GemmRope *rp,
+                          hipStream_t s)
 {
     constexpr size_t lds = 2 * (size_t)(BM + BN) * BK * 2;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
+    // the fused reductions take every one of the M rows
+    if ((nrm || rp) && mrows != M) return hipErrorInvalidValue;
     const uint32_t tiles_n = N / BN, tiles = tiles_n * (M / BM);
     if (S > 1)
-        hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC, true>), dim3(tiles * S), dim3(512), lds, s, X, W, Y,
-                           K, N, M, tiles_n, rscale, S, ws);
+        hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, ACC, true>), dim3(tiles * S), dim3(512), lds, s, X, W, Y, K,
+                           N, M, tiles_n, rscale, S, ws, mrows);
     else
-        hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, XH, ACC, false>), dim3(tiles), dim3(512), lds, s, X, W, Y, K,
-                           N, M, tiles_n, rscale, 1u, nullptr);
+        hipLaunchKernelGGL((gemm_dq_kernel<QT, BM, BN, BK, ACC, false>), dim3(tiles), dim3(512), lds, s, X, W, Y, K,
+                           N, M, tiles_n, rscale, 1u, nullptr, mrows);
     if (S > 1 && rp) {
         // the reduction is the rope_kv_store's first step
         const hipError_t e = hipGetLastError();
@@ -543,10 +538,12 @@ static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t 
         return launch_splitk_reduce_rmsnorm(ws, S, M, N, Y, rscale, ACC, nrm->gamma, nrm->eps, nrm->out, s);
     }
     if (S > 1) {
-        const uint64_t quads = (uint64_t)M * N / 4;
+        const uint64_t quads = (uint64_t)mrows * N / 4;
         const dim3 grid((unsigned)((quads + 255) / 256));
 #define RRR_SKR_CASE(K)                                                                                         \
-    case K: hipLaunchKernelGGL((gemm_splitk_reduce<ACC, K>), grid, dim3(256), 0, s, ws, M, N, Y, rscale); break;
+    case K:                                                                                                     \
+        hipLaunchKernelGGL((gemm_splitk_reduce<ACC, K>), grid, dim3(256), 0, s, ws, M, N, Y, rscale, mrows); \
+        break;
         switch (S) {
             RRR_SKR_CASE(2) RRR_SKR_CASE(3) RRR_SKR_CASE(4) RRR_SKR_CASE(5)
             RRR_SKR_CASE(6) RRR_SKR_CASE(7) RRR_SKR_CASE(8)
@@ -562,9 +559,9 @@ static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t 
     return hipGetLastError();
 }
 
-// Splits of K for a grid of `tiles` large tiles: at most as many as keep
-// every workgroup in the first round over the MI355X's 256 CUs (a second
-// round costs a whole tile's time) and at most 8, each a whole number of
+// Splits of K for a grid of `tiles` tiles: at most as many as keep every
+// workgroup in the first round over the MI355X's 256 CUs (a second round
+// costs a whole tile's time) and at most 8, each a whole number of
 // super-blocks (the first B % S splits one more), their partials within the
 // workspace; of those, the fewest that give the shortest longest split
 // (K = 8192, 48 tiles: 5 splits of 7/7/6/6/6 super-blocks rather than 4 of
@@ -582,20 +579,22 @@ static uint32_t gemm_splits(uint32_t tiles, uint32_t K, uint32_t M, uint32_t N, 
     return best;
 }
 
-template <template <int> class QT, bool XH, bool ACC>
+template <template <int> class QT, bool ACC>
 static hipError_t go_gemm_t(const uint16_t *X, const float *rscale, const uint8_t *W, float *Y, uint32_t K,
-                            uint32_t N, uint32_t M, float *ws, size_t ws_bytes, const GemmNorm *nrm,
+                            uint32_t N, uint32_t M, uint32_t mrows, float *ws, size_t ws_bytes, const GemmNorm *nrm,
                             const GemmRope *rp, hipStream_t s)
 {
     // 256 x 128 tiles when they cover at least half of the CUs, or with K
     // split to do so; else 128 x 64 (with K steps of 128 so each barrier
-    // covers as much MFMA work)
+    // covers as much MFMA work), K split the same way when those tiles are few
     if (M % 256 == 0 && N % 128 == 0) {
         const uint32_t tiles = (N / 128) * (M / 256);
         const uint32_t S = ws ? gemm_splits(tiles, K, M, N, ws_bytes) : 1u;
-        if (tiles * S >= 128) return go_gemm<QT, 256, 128, 64, XH, ACC>(X, rscale, W, Y, K, N, M, S, ws, nrm, rp, s);
+        if (tiles * S >= 128)
+            return go_gemm<QT, 256, 128, 64, ACC>(X, rscale, W, Y, K, N, M, mrows, S, ws, nrm, rp, s);
     }
-    return go_gemm<QT, 128, 64, 128, XH, ACC>(X, rscale, W, Y, K, N, M, 1, nullptr, nrm, rp, s);
+    const uint32_t S = ws ? gemm_splits((N / 64) * (M / 128), K, M, N, ws_bytes) : 1u;
+    return go_gemm<QT, 128, 64, 128, ACC>(X, rscale, W, Y, K, N, M, mrows, S, ws, nrm, rp, s);
 }
 
 bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t x_bytes)
@@ -604,60 +603,150 @@ bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t 
            (uint64_t)N * (K / 256) * 210 + RRR_READ_SLACK < GM_OOB && x_bytes + RRR_READ_SLACK < GM_OOB;
 }
 
-template <bool XH, bool ACC>
+template <bool ACC>
 static hipError_t go_gemm_q(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
-                            uint32_t K, uint32_t N, uint32_t M, float *ws, size_t ws_bytes, hipStream_t s,
-                            const GemmNorm *nrm = nullptr, const GemmRope *rp = nullptr)
+                            uint32_t K, uint32_t N, uint32_t M, uint32_t mrows, float *ws, size_t ws_bytes,
+                            hipStream_t s, const GemmNorm *nrm = nullptr, const GemmRope *rp = nullptr)
 {
-    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2)) return hipErrorNotSupported;
+    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2) || mrows == 0 || mrows > M) return hipErrorNotSupported;
     switch (type) {
-    case T_Q4_K: return go_gemm_t<GqQ4K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, rp, s);
-    case T_Q5_K: return go_gemm_t<GqQ5K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, rp, s);
-    case T_Q6_K: return go_gemm_t<GqQ6K, XH, ACC>(X, rscale, W, Y, K, N, M, ws, ws_bytes, nrm, rp, s);
+    case T_Q4_K: return go_gemm_t<GqQ4K, ACC>(X, rscale, W, Y, K, N, M, mrows, ws, ws_bytes, nrm, rp, s);
+    case T_Q5_K: return go_gemm_t<GqQ5K, ACC>(X, rscale, W, Y, K, N, M, mrows, ws, ws_bytes, nrm, rp, s);
+    case T_Q6_K: return go_gemm_t<GqQ6K, ACC>(X, rscale, W, Y, K, N, M, mrows, ws, ws_bytes, nrm, rp, s);
     default: return hipErrorNotSupported;
     }
 }
 
-// bf16 -> f16 of the whole activation matrix once, 8 elements a thread, with
-// the conversion the staging waves apply (pk_f16: exact for |x| in f16's
-// normal range), so the f16-activation GEMM on the result is bitwise the
-// bf16 GEMM while the N/BN column tiles no longer convert X again each.
-__global__ __launch_bounds__(256) void bf16_to_f16_kernel(const u32x4 *__restrict__ X, u32x4 *__restrict__ Xh,
-                                                          uint64_t n8)
+// The activations of rrr_gemm_bf16 and of the batched GEMV above 16 rows,
+// converted to f16 rows once per call (so the N / BN column tiles read them
+// as they are), into the context workspace, a chunk of rows at a time; a
+// chunk is padded with zero rows to a multiple of 128 (which the GEMM computes
+// and does not store).
+//
+// bf16 -> f16, 8 elements a thread: exact for |x| in f16's normal range.
+__global__ __launch_bounds__(256) void bf16_rows_to_f16_kernel(const uint16_t *__restrict__ X, uint32_t K,
+                                                               uint32_t rows, u32x4 *__restrict__ Xh, uint64_t n8)
 {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n8) return;
-    const u32x4 v = X[i];
-    u32x4 h;
+    const uint64_t e = 8 * i;   // K % 256 == 0: a thread's 8 elements sit in one row
+    u32x4 h = {0u, 0u, 0u, 0u};
+    if (e / K < rows) {
+        const u32x4 v = *(const u32x4 *)(X + e);
 #pragma unroll
-    for (int c = 0; c < 4; c++) h[c] = pk_f16(__uint_as_float(v[c] << 16), __uint_as_float(v[c] & 0xFFFF0000u));
+        for (int c = 0; c < 4; c++) h[c] = pk_f16(__uint_as_float(v[c] << 16), __uint_as_float(v[c] & 0xFFFF0000u));
+    }
     Xh[i] = h;
+}
+
+// f32 rows -> f16 block floating point, one workgroup per row: row m is
+// scaled by 2^(15 - e) (max|x_m| = f * 2^e, f in [0.5, 1); exact in f32), so
+// its largest value lands in [2^14, 2^15), rounded to nearest even, and
+// rscale[m] = 2^(e - 15) undoes the scale on the GEMM's output (exact).
+// A zero row keeps scale 1; a row holding inf or NaN is converted unscaled,
+// so the non-finite values reach the products.  Rows past `rows` are zeros.
+__global__ __launch_bounds__(256) void f32_rows_to_f16_kernel(const float *__restrict__ X, uint32_t K, uint32_t rows,
+                                                              uint16_t *__restrict__ Xh, float *__restrict__ rscale)
+{
+    __shared__ float wmax[4];
+    const uint32_t m = blockIdx.x, t = threadIdx.x;
+    uint16_t *out = Xh + (uint64_t)m * K;
+    if (m >= rows) {
+        for (uint32_t k = 8 * t; k < K; k += 8 * 256) *(u32x4 *)(out + k) = u32x4{0u, 0u, 0u, 0u};
+        if (t == 0) rscale[m] = 1.0f;
+        return;
+    }
+    const float *row = X + (uint64_t)m * K;
+    float mx = 0.0f;
+    for (uint32_t k = 4 * t; k < K; k += 4 * 256) {
+        const float4 v = *(const float4 *)(row + k);
+        // fmaxf drops NaN: a NaN anywhere is kept by the isnan test below
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        if (__builtin_isnan(v.x + v.y + v.z + v.w)) mx = __builtin_inff();
+    }
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((t & 63) == 0) wmax[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int e = 15;
+    if (mx > 0.0f && __builtin_isfinite(mx)) (void)frexpf(mx, &e);
+    e = max(e, -110);   // 2^(15 - e) stays a normal f32
+    const float sc = ldexpf(1.0f, 15 - e);
+    if (t == 0) rscale[m] = ldexpf(1.0f, e - 15);
+    for (uint32_t k = 8 * t; k < K; k += 8 * 256) {
+        const float4 a = *(const float4 *)(row + k), b = *(const float4 *)(row + k + 4);
+        *(u32x4 *)(out + k) = u32x4{pk_f16_rn(a.x * sc, a.y * sc), pk_f16_rn(a.z * sc, a.w * sc),
+                                    pk_f16_rn(b.x * sc, b.y * sc), pk_f16_rn(b.z * sc, b.w * sc)};
+    }
+}
+
+// Rows per chunk: all M rows (rounded up to 128) when their f16 copy and
+// row scales take at most half of the workspace (the other half holds split
+// partials), else the most multiples of 256 that do; 0 when not even 128 do.
+static uint32_t gemm_chunk_rows(uint32_t M, uint32_t K, size_t ws_bytes)
+{
+    const uint64_t per_row = 2ull * K + 4, cap = (uint64_t)(ws_bytes / 2) / per_row;
+    const uint64_t mp = (M + 127ull) / 128 * 128;
+    if (mp <= cap) return (uint32_t)mp;
+    if (cap >= 256) return (uint32_t)(cap / 256 * 256);
+    return cap >= 128 ? 128u : 0u;
+}
+
+// X (bf16 or f32, M x K) . W^T in row chunks through the f16 GEMM.
+static hipError_t gemm_rows(const void *X, bool f32, const uint8_t *W, uint32_t type, float *Y, uint32_t K,
+                            uint32_t N, uint32_t M, void *ws, size_t ws_bytes, hipStream_t s)
+{
+    const uint32_t mc = ws ? gemm_chunk_rows(M, K, ws_bytes) : 0u;
+    if (!mc || !gemm_supported(type, K, N, mc, (uint64_t)mc * K * 2)) return hipErrorNotSupported;
+    // workspace: f16 rows | row scales | split partials (256-byte aligned)
+    const uint64_t xh_bytes = ((uint64_t)mc * K * 2 + 255) & ~255ull, rs_bytes = ((uint64_t)mc * 4 + 255) & ~255ull;
+    uint16_t *Xh = (uint16_t *)ws;
+    float *rscale = (float *)((uint8_t *)ws + xh_bytes);
+    float *part = (float *)((uint8_t *)ws + xh_bytes + rs_bytes);
+    const size_t part_bytes = ws_bytes - xh_bytes - rs_bytes;
+    for (uint32_t m0 = 0; m0 < M; m0 += mc) {
+        const uint32_t rows = min(mc, M - m0), mp = (rows + 127) / 128 * 128;
+        if (f32) {
+            hipLaunchKernelGGL(f32_rows_to_f16_kernel, dim3(mp), dim3(256), 0, s, (const float *)X + (uint64_t)m0 * K,
+                               K, rows, Xh, rscale);
+        } else {
+            const uint64_t n8 = (uint64_t)mp * K / 8;
+            hipLaunchKernelGGL(bf16_rows_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s,
+                               (const uint16_t *)X + (uint64_t)m0 * K, K, rows, (u32x4 *)Xh, n8);
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        e = go_gemm_q<false>(Xh, f32 ? rscale : nullptr, W, type, Y + (uint64_t)m0 * N, K, N, mp, rows, part,
+                             part_bytes, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K, uint32_t N,
                             uint32_t M, float *ws, size_t ws_bytes, hipStream_t s)
 {
-    if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2)) return hipErrorNotSupported;
-    // the f16 copy of X at the start of the workspace (256-byte aligned
-    // remainder for the split-K partials), when it fits
-    const uint64_t xh_bytes = ((uint64_t)M * K * 2 + 255) & ~255ull;
-    if (ws && (uint64_t)M * K % 8 == 0 && xh_bytes + (ws_bytes / 2) <= ws_bytes && xh_bytes <= ws_bytes / 2) {
-        const uint64_t n8 = (uint64_t)M * K / 8;
-        uint16_t *Xh = (uint16_t *)ws;
-        hipLaunchKernelGGL(bf16_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const u32x4 *)X,
-                           (u32x4 *)Xh, n8);
-        return go_gemm_q<true, false>(Xh, nullptr, W, type, Y, K, N, M, (float *)((uint8_t *)ws + xh_bytes),
-                                      ws_bytes - xh_bytes, s);
-    }
-    return go_gemm_q<false, false>(X, nullptr, W, type, Y, K, N, M, ws, ws_bytes, s);
+    return gemm_rows(X, false, W, type, Y, K, N, M, ws, ws_bytes, s);
+}
+
+bool gemm_rows_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, size_t ws_bytes)
+{
+    const uint32_t mc = gemm_chunk_rows(M, K, ws_bytes);
+    return M > 0 && mc && gemm_supported(type, K, N, mc, (uint64_t)mc * K * 2);
+}
+
+hipError_t launch_gemm_f32_rows(const float *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K, uint32_t N,
+                                uint32_t M, void *ws, size_t ws_bytes, hipStream_t s)
+{
+    return gemm_rows(X, true, W, type, Y, K, N, M, ws, ws_bytes, s);
 }
 
 hipError_t launch_gemm_f16(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
                            uint32_t K, uint32_t N, uint32_t M, bool accumulate, float *ws, size_t ws_bytes,
                            hipStream_t s)
 {
-    return accumulate ? go_gemm_q<true, true>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s)
-                      : go_gemm_q<true, false>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s);
+    return accumulate ? go_gemm_q<true>(X, rscale, W, type, Y, K, N, M, M, ws, ws_bytes, s)
+                      : go_gemm_q<false>(X, rscale, W, type, Y, K, N, M, M, ws, ws_bytes, s);
 }
 
 hipError_t launch_gemm_f16_rmsnorm(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
@@ -666,8 +755,8 @@ hipError_t launch_gemm_f16_rmsnorm(const uint16_t *X, const float *rscale, const
 {
     if (!splitk_reduce_rmsnorm_supported(N)) return hipErrorNotSupported;
     const GemmNorm nrm{gamma, eps, out16};
-    return accumulate ? go_gemm_q<true, true>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s, &nrm)
-                      : go_gemm_q<true, false>(X, rscale, W, type, Y, K, N, M, ws, ws_bytes, s, &nrm);
+    return accumulate ? go_gemm_q<true>(X, rscale, W, type, Y, K, N, M, M, ws, ws_bytes, s, &nrm)
+                      : go_gemm_q<false>(X, rscale, W, type, Y, K, N, M, M, ws, ws_bytes, s, &nrm);
 }
 
 // The gate/up GEMM with silu(gate) * up in its epilogue into ws (M x F
@@ -683,8 +772,8 @@ hipError_t launch_gemm_f16_silu_f16(const uint16_t *X, const uint8_t *W, uint32_
     constexpr size_t lds = 2 * (size_t)(256 + 128) * 64 * 2;
 #define RRR_SILU_CASE(T, QT)                                                                                          \
     case T:                                                                                                            \
-        hipLaunchKernelGGL((gemm_dq_kernel<QT, 256, 128, 64, true, false, false, true>), dim3(tiles), dim3(512), lds, \
-                           s, X, W, ws, K, N, M, tiles_n, nullptr, 1u, nullptr);                                       \
+        hipLaunchKernelGGL((gemm_dq_kernel<QT, 256, 128, 64, false, false, true>), dim3(tiles), dim3(512), lds, s, X, \
+                           W, ws, K, N, M, tiles_n, nullptr, 1u, nullptr, M);                                          \
         break;
     switch (type) {
         RRR_SILU_CASE(T_Q4_K, GqQ4K)
@@ -704,7 +793,7 @@ hipError_t launch_gemm_f16_rope_kv(const uint16_t *X, const uint8_t *W, uint32_t
 {
     if (!splitk_rope_kv_store_supported(r) || r.row_stride != N || rows > M) return hipErrorNotSupported;
     const GemmRope rp{r, rows, kc, vc};
-    return go_gemm_q<true, false>(X, nullptr, W, type, Y, K, N, M, ws, ws_bytes, s, nullptr, &rp);
+    return go_gemm_q<false>(X, nullptr, W, type, Y, K, N, M, M, ws, ws_bytes, s, nullptr, &rp);
 }
 
 }  // namespace rrr

@@ -589,10 +589,22 @@ static hipError_t go_type(const GemvArgs &a, uint32_t act, hipStream_t s)
     }
 }
 
+// Batched K-quant rows above 16 tokens that the skinny kernel does not take
+// (more than 32 rows, Q6_K, K > 3072) run on the prefill GEMM's fp16 matrix
+// cores: the f32 rows become f16 block floating point (a power-of-two scale
+// per row, undone exactly on the output), zero-padded to a multiple of 128
+// rows inside the context workspace.
+static bool batched_gemm_route(const GemvArgs &a, uint32_t act)
+{
+    return a.M > 16 && act == ACT_PLAIN && !a.residual && a.type != T_F32 && a.ws &&
+           (((uintptr_t)a.x | (uintptr_t)a.y) & 15) == 0 && gemm_rows_supported(a.type, a.K, a.N, a.M, a.ws_bytes);
+}
+
 hipError_t launch_gemv(const GemvArgs &a, uint32_t act, hipStream_t s)
 {
     if (gemv_mfma_supported(a)) return launch_gemv_mfma(a, act, s);
     if (a.M > 1 && act == ACT_PLAIN && skinny_supported(a)) return launch_skinny(a, s);
+    if (batched_gemm_route(a, act)) return launch_gemm_f32_rows(a.x, a.W, a.type, a.y, a.K, a.N, a.M, a.ws, a.ws_bytes, s);
     switch (a.type) {
     case T_Q4_K: return go_type<DecQ4K>(a, act, s);
     case T_Q5_K: return go_type<DecQ5K>(a, act, s);

@@ -127,6 +127,8 @@ static hipError_t go_mq_act(const GemvArgs &a, uint32_t act, hipStream_t s)
     }
 }
 
+uint32_t device_cu_count() { return device_cus(); }
+
 bool gemv_mfma_supported(const GemvArgs &a)
 {
     if (a.M != 1 || (a.type != T_Q4_K && a.type != T_Q5_K && a.type != T_Q6_K) || a.K > 8192) return false;

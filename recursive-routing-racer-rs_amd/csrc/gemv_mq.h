@@ -1,6 +1,5 @@
 // gemv_mq.h -- batch-1 K-quant GEMV on the int8 matrix cores: quant unit
-// decoders and activation encoding (shared with the persistent decode sweep,
-// sweep.hip) and the per-workgroup body of the standalone launch
+// decoders, activation encoding and the per-workgroup body of the launch
 // (gemv_mfma.hip).
 //
 // y[n] = sum_k x[k] * W[n][k] for Q4_K / Q5_K / Q6_K rows (phi4.rs:628-630),
@@ -447,13 +446,13 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
             for (int u = 0; u < 4; u++) av[j][u] = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
     }
 
-    // ROPE: the position's rotation coefficients, one pair per thread (read
-    // after the final barrier), here where the wave would wait for its first
-    // weight block anyway: computed before the RMSNorm barrier, they held
-    // every wave back by their latency
+    // ROPE: the position's rotation coefficients (pair j by thread j, j + NT,
+    // ...; read after the final barrier), here where the wave would wait for
+    // its first weight block anyway: computed before the RMSNorm barrier, they
+    // held every wave back by their latency
     float *coef = part + ntl * W * 16;
     if constexpr (ROPE) {
-        if (t < a.rope.rope_dim / 2) rope_coef(t, a.rope.pos, a.rope, coef[2 * t], coef[2 * t + 1]);
+        for (uint32_t j = t; j < a.rope.rope_dim / 2; j += NT) rope_coef(j, a.rope.pos, a.rope, coef[2 * j], coef[2 * j + 1]);
     }
 
     // 4. per tile, block by block: the block's units to LDS (its registers

@@ -61,21 +61,8 @@ hipError_t launch_gemv_mfma(const GemvArgs &a, uint32_t act, hipStream_t s);
 // fp16-MFMA batched GEMV for 2 <= M <= 32, Q4_K / Q5_K (skinny.hip)
 bool skinny_supported(const GemvArgs &a);
 hipError_t launch_skinny(const GemvArgs &a, hipStream_t s);
-// Persistent decode sweep (sweep.hip): per-op plan, packing and the launch
-bool sweep_plan_op(const GemvArgs &a, uint32_t act, uint32_t grid, uint32_t &variant, uint32_t &ntiles, uint32_t &tr,
-                   size_t &lds);
-// whether op `next` may follow op `cur` in one sweep (forms and LDS)
-bool sweep_pair_ok(uint32_t cur, uint32_t cur_ntiles, uint32_t cur_tr, uint32_t next, uint32_t next_ntiles,
-                   uint32_t next_tr, uint32_t grid);
-size_t sweep_op_bytes();
-void sweep_pack_op(void *dst, const GemvArgs &a, uint32_t variant, uint32_t ntiles, uint32_t tr, uint32_t grid);
-uint32_t sweep_cus();
-uint32_t sweep_grid(size_t lds);
-// u32 words of a sweep's device state (completion records, run counters,
-// error word) and the index of the error word in it
-size_t sweep_state_words();
-size_t sweep_err_word();
-hipError_t launch_sweep(const void *ops, uint32_t nops, uint32_t *state, uint32_t grid, hipStream_t s);
+// CUs of the current device (cached per device)
+uint32_t device_cu_count();
 hipError_t launch_dequant(uint32_t type, const uint8_t *W, uint64_t w_bytes, float *out,
                           uint64_t n_elements, hipStream_t s);
 hipError_t launch_rmsnorm(const float *x, const float *g, float *y, uint32_t rows, uint32_t d,
@@ -137,8 +124,15 @@ hipError_t launch_attention_prefill(const float *qkv, uint32_t row_stride, uint3
 // be null) holds the fp32 partials when K is split.
 constexpr size_t GEMM_WS_BYTES = 48ull << 20;
 bool gemm_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, uint64_t x_bytes);
+// bf16 X (any M >= 1, X and Y 16-byte aligned): converted to f16 in row
+// chunks inside ws, each chunk zero-padded to a multiple of 128 rows
 hipError_t launch_gemm_bf16(const uint16_t *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K, uint32_t N,
                             uint32_t M, float *ws, size_t ws_bytes, hipStream_t s);
+// f32 X (the batched GEMV above 16 rows): each row chunk as f16 block floating
+// point (row m scaled by a power of two, undone exactly on Y's row) in ws
+bool gemm_rows_supported(uint32_t type, uint32_t K, uint32_t N, uint32_t M, size_t ws_bytes);
+hipError_t launch_gemm_f32_rows(const float *X, const uint8_t *W, uint32_t type, float *Y, uint32_t K, uint32_t N,
+                                uint32_t M, void *ws, size_t ws_bytes, hipStream_t s);
 hipError_t launch_gemm_f16(const uint16_t *X, const float *rscale, const uint8_t *W, uint32_t type, float *Y,
                            uint32_t K, uint32_t N, uint32_t M, bool accumulate, float *ws, size_t ws_bytes,
                            hipStream_t s);
@@ -189,6 +183,8 @@ hipError_t launch_silu_gate_f16(const float *gu, uint16_t *mid, float *rscale, u
 
 // Platform probes (probe.hip)
 hipError_t launch_probe_read(const void *p, uint64_t bytes, uint32_t *out, hipStream_t s);
+bool probe_shares_supported(uint64_t bytes);
+hipError_t launch_probe_shares(const void *p, uint64_t bytes, uint32_t *out, hipStream_t s);
 hipError_t launch_probe_mfma(uint32_t kind, uint32_t waves_per_cu, uint32_t iters, uint32_t *out, hipStream_t s);
 
 }  // namespace rrr

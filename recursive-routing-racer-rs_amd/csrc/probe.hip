@@ -1,7 +1,8 @@
 // probe.hip -- platform probes for the measurements: a streaming read of a
-// device buffer (the HBM rate one launch of a given size reaches, and the
-// read that flushes the Infinity Cache before a timed region) and loops of
-// independent MFMAs (the matrix cores' dense rate).
+// device buffer (the read that flushes the Infinity Cache before a timed
+// region), a read of one share per CU with every load in flight (the floor
+// one launch of a GEMV's byte count can reach) and loops of independent MFMAs
+// (the matrix cores' dense rate).
 #include "rrr_probe.h"
 
 #include <hip/hip_runtime.h>
@@ -29,6 +30,25 @@ __global__ __launch_bounds__(1024) void probe_read_kernel(const u32x4 *p, uint64
         const u32x4 a = __builtin_nontemporal_load(p + i);
         acc ^= a.x ^ a.y ^ a.z ^ a.w;
     }
+    if (acc == 0x9E3779B9u) out[0] = acc;
+}
+
+// One workgroup of 1024 threads per CU reads a contiguous share of NL * 16 KB
+// (a GEMV's per-CU share of its weight bytes): lane t of workgroup b loads
+// the 16-byte units b * NL * 1024 + t + 1024 j, j < NL, all NL loads issued
+// before the first is used (a wave load covers 1 KB of whole cache lines),
+// non-temporal; buffer loads past `bytes` return zeros and move no data.
+template <int NL>
+__global__ __launch_bounds__(1024) void probe_share_kernel(const void *p, uint32_t bytes, uint32_t *out)
+{
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p, bytes);
+    const uint32_t base = blockIdx.x * (uint32_t)(NL * 16384) + 16u * threadIdx.x;
+    u32x4 v[NL];
+#pragma unroll
+    for (int j = 0; j < NL; j++) v[j] = bload16_nt(rs, base + 16384u * j);
+    uint32_t acc = 0;
+#pragma unroll
+    for (int j = 0; j < NL; j++) acc ^= (v[j].x ^ v[j].y) ^ (v[j].z ^ v[j].w);
     if (acc == 0x9E3779B9u) out[0] = acc;
 }
 
@@ -101,15 +121,32 @@ __global__ __launch_bounds__(256) void probe_mfma_kernel(uint32_t iters, uint32_
 
 hipError_t launch_probe_read(const void *p, uint64_t bytes, uint32_t *out, hipStream_t s)
 {
-    const uint32_t grid = 4 * sweep_cus();
+    const uint32_t grid = 4 * device_cu_count();
     hipLaunchKernelGGL(probe_read_kernel, dim3(grid), dim3(1024), 0, s, (const u32x4 *)p, bytes / 16, out);
     return hipGetLastError();
+}
+
+bool probe_shares_supported(uint64_t bytes) { return bytes > 0 && bytes <= (uint64_t)device_cu_count() * 16 * 16384; }
+
+hipError_t launch_probe_shares(const void *p, uint64_t bytes, uint32_t *out, hipStream_t s)
+{
+    const uint32_t cus = device_cu_count();
+    const uint64_t per = (bytes + cus - 1) / cus, nl = (per + 16383) / 16384;
+#define RRR_SHARE_CASE(N)                                                                                         \
+    if (nl <= N) {                                                                                                \
+        hipLaunchKernelGGL(probe_share_kernel<N>, dim3(cus), dim3(1024), 0, s, p, (uint32_t)bytes, out);         \
+        return hipGetLastError();                                                                                 \
+    }
+    RRR_SHARE_CASE(1) RRR_SHARE_CASE(2) RRR_SHARE_CASE(3) RRR_SHARE_CASE(4) RRR_SHARE_CASE(5) RRR_SHARE_CASE(6)
+    RRR_SHARE_CASE(7) RRR_SHARE_CASE(8) RRR_SHARE_CASE(10) RRR_SHARE_CASE(12) RRR_SHARE_CASE(16)
+#undef RRR_SHARE_CASE
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_probe_mfma(uint32_t kind, uint32_t waves_per_cu, uint32_t iters, uint32_t *out, hipStream_t s)
 {
     // 4 waves a workgroup, waves_per_cu / 4 workgroups per CU
-    const uint32_t grid = sweep_cus() * (waves_per_cu / 4);
+    const uint32_t grid = device_cu_count() * (waves_per_cu / 4);
     switch (kind) {
     case RRR_PROBE_MFMA_F16_16X16X32:
         hipLaunchKernelGGL(probe_mfma_kernel<RRR_PROBE_MFMA_F16_16X16X32>, dim3(grid), dim3(256), 0, s, iters, out);

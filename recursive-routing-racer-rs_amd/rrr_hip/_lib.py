@@ -33,23 +33,6 @@ class DispatchDesc(ctypes.Structure):
     ]
 
 
-class SweepOp(ctypes.Structure):
-    """rrr_sweep_op (include/rrr_hip.h)."""
-    _fields_ = [
-        ("kind", u32),
-        ("x", c_buf_p),
-        ("gamma", c_buf_p),
-        ("eps", f32),
-        ("act_kind", u32),
-        ("act_param", u32),
-        ("W", c_buf_p),
-        ("type", u32),
-        ("y", c_buf_p),
-        ("K", u32),
-        ("N", u32),
-    ]
-
-
 class GgufKv(ctypes.Structure):
     """rrr_gguf_kv (include/rrr_gguf.h)."""
     _fields_ = [
@@ -113,6 +96,7 @@ SIGNATURES = {
     "rrr_attention": (i32, [c_ctx_p, c_buf_p, c_buf_p, c_buf_p, c_buf_p, u32, u32, u32, u32]),
     "rrr_attention_noalloc": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
     "rrr_probe_read": (i32, [c_ctx_p, c_buf_p, u64, c_buf_p]),
+    "rrr_probe_read_shares": (i32, [c_ctx_p, c_buf_p, u64, c_buf_p]),
     "rrr_probe_mfma": (i32, [c_ctx_p, u32, u32, u32, c_buf_p]),
     "rrr_probe_cus": (u32, [c_ctx_p]),
     "rrr_rope_kv_store_rows": (i32, [c_ctx_p, c_buf_p, u32, c_buf_p, u32, c_buf_p, c_buf_p, u32, u32, u32, u32, u32,
@@ -133,10 +117,6 @@ SIGNATURES = {
     "rrr_graph_end": (i32, [c_ctx_p, ctypes.POINTER(vp)]),
     "rrr_graph_launch": (i32, [c_ctx_p, vp]),
     "rrr_graph_destroy": (i32, [c_ctx_p, vp]),
-    "rrr_sweep_create": (i32, [c_ctx_p, ctypes.POINTER(SweepOp), u32, ctypes.POINTER(vp)]),
-    "rrr_sweep_run": (i32, [c_ctx_p, vp]),
-    "rrr_sweep_check": (i32, [c_ctx_p, vp]),
-    "rrr_sweep_destroy": (i32, [c_ctx_p, vp]),
     "rrr_set_async": (i32, [c_ctx_p, i32]),
     "rrr_sync": (i32, [c_ctx_p]),
     "rrr_timer_start": (i32, [c_ctx_p]),

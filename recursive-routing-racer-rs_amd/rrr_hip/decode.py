@@ -541,32 +541,6 @@ class DecodeSweep:
         hid = c.download(self._pf["hid"], np.float32, M * s.d_model).reshape(M, s.d_model)
         return (c.download(self.logits, np.float32, s.vocab), int(c.download(self.token, np.uint32, 1)[0]), hid)
 
-    def sweep_ops(self):
-        """The 4 fused GEMVs of every layer as one persistent sweep's op list
-        (the same calls record_token issues one by one)."""
-        s = self.shape
-        d = s.d_model
-        gqa = s.head_dim | (s.heads_per_kv << 16)
-        ops = []
-        for i, L in enumerate(self.layers):
-            T = L["types"]
-            ops += [("rmsnorm", self.hidden, L["attn_norm"], s.eps, L["attn_qkv"], T["attn_qkv"], self.qkv, d,
-                     s.qkv_dim),
-                    ("residual", self.qkv, E.ACT_GQA_V, gqa, L["attn_output"], T["attn_output"], self.hidden, d, d),
-                    ("rmsnorm", self.hidden, L["ffn_norm"], s.eps, L["ffn_up"], T["ffn_up"], self.gate_up, d,
-                     2 * s.ffn_dim),
-                    ("residual", self.gate_up, E.ACT_SILU_GATE, 0, L["ffn_down"], T["ffn_down"], self.hidden,
-                     s.ffn_dim, d)]
-        return ops
-
-    def run_token_sweep(self, sweep):
-        """One token with the layers as one persistent launch (`sweep` from
-        ctx.sweep(self.sweep_ops())), the logits and argmax as before."""
-        c, s = self.ctx, self.shape
-        c.residual_add(self.x_in, self.zero, self.hidden, s.d_model)
-        sweep.run()
-        self.record_logits()
-
     def graph(self, pos=None, logits=None):
         """One token as a HIP graph; logits ("f32" / "q6k") overrides
         logits_mode for it."""

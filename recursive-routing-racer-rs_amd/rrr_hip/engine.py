@@ -35,7 +35,6 @@ F32, F16, Q4_K, Q5_K, Q6_K = 0, 1, 12, 13, 14
 LOGITS_ROWS, LOGITS_CHUNKED, LOGITS_Q6K = 0, 1, 2
 ACT_IDENTITY, ACT_SILU_GATE, ACT_GQA_V = 0, 1, 2
 PROBE_MFMA_F16_16X16X32, PROBE_MFMA_F16_32X32X16, PROBE_MFMA_I8_16X16X64 = 0, 1, 2
-SWEEP_GEMV_RMSNORM, SWEEP_GEMV_RESIDUAL = 0, 1
 DEVICE_NONE = -1
 BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, F32: 1024}
 
@@ -94,41 +93,6 @@ class Graph:
     def destroy(self):
         if self.handle:
             _check(_lib.hip().rrr_graph_destroy(self.ctx._h, ctypes.c_void_p(self.handle)))
-            self.handle = None
-
-
-class Sweep:
-    """A list of fused decode GEMVs run by one persistent launch
-    (rrr_sweep_*).  Ops are ("rmsnorm", x, gamma, eps, W, qtype, y, K, N) or
-    ("residual", x, act_kind, act_param, W, qtype, hidden, K, N)."""
-
-    def __init__(self, ctx, ops):
-        self.ctx = ctx
-        self._keep = ops
-        arr = (_lib.SweepOp * len(ops))()
-        for o, op in zip(arr, ops):
-            if op[0] == "rmsnorm":
-                _, x, gamma, eps, W, qt, y, K, N = op
-                o.kind, o.gamma, o.eps = SWEEP_GEMV_RMSNORM, gamma._h, eps
-            elif op[0] == "residual":
-                _, x, act_kind, act_param, W, qt, y, K, N = op
-                o.kind, o.act_kind, o.act_param = SWEEP_GEMV_RESIDUAL, act_kind, act_param
-            else:
-                raise ValueError(f"sweep op kind {op[0]!r}")
-            o.x, o.W, o.type, o.y, o.K, o.N = x._h, W._h, qt, y._h, K, N
-        h = ctypes.c_void_p()
-        _check(_lib.hip().rrr_sweep_create(ctx._h, arr, len(ops), ctypes.byref(h)))
-        self.handle = h.value
-
-    def run(self):
-        _check(_lib.hip().rrr_sweep_run(self.ctx._h, ctypes.c_void_p(self.handle)))
-
-    def check(self):
-        _check(_lib.hip().rrr_sweep_check(self.ctx._h, ctypes.c_void_p(self.handle)))
-
-    def destroy(self):
-        if self.handle:
-            _check(_lib.hip().rrr_sweep_destroy(self.ctx._h, ctypes.c_void_p(self.handle)))
             self.handle = None
 
 
@@ -323,15 +287,15 @@ class Context:
         _check(self.lib.rrr_graph_end(self._h, ctypes.byref(h)))
         return Graph(self, h.value)
 
-    def sweep(self, ops):
-        return Sweep(self, ops)
-
     def set_async(self, flag):
         _check(self.lib.rrr_set_async(self._h, 1 if flag else 0))
 
     # ---- platform probes (include/rrr_probe.h) ---------------------------
     def probe_read(self, buf, nbytes, sink):
         _check(self.lib.rrr_probe_read(self._h, buf._h, nbytes, sink._h))
+
+    def probe_read_shares(self, buf, nbytes, sink):
+        _check(self.lib.rrr_probe_read_shares(self._h, buf._h, nbytes, sink._h))
 
     def probe_mfma(self, kind, waves_per_cu, iters, sink):
         _check(self.lib.rrr_probe_mfma(self._h, kind, waves_per_cu, iters, sink._h))

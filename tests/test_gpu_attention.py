@@ -238,3 +238,47 @@ def test_gemv_rmsnorm_rope_kv_is_the_two_launches(ctx, caches, pos, with_factors
     assert not np.all(rows[1][2] == 0x5A5A)   # the V row was written
     for b in (W, x, g, q1, q2) + ((fac,) if fac is not None else ()):
         b.free()
+
+
+@pytest.mark.parametrize("qtype,K,nh,nkv,hd,rd,pos", [
+    (rrr_hip.Q4_K, 3072, 24, 8, 128, 96, 5),       # Q4_K rows, tiles of 10
+    (rrr_hip.Q6_K, 3072, 24, 8, 128, 96, 300),     # Q6_K rows
+    (rrr_hip.Q5_K, 3072, 16, 8, 128, 128, 9),      # N = 4096: one tile of 16 rows per workgroup
+    (rrr_hip.Q5_K, 3072, 64, 64, 128, 64, 33),     # N = 24,576: several tiles per workgroup
+    (rrr_hip.Q4_K, 8192, 24, 8, 128, 96, 2),       # K = 8192: two super-blocks a wave
+    (rrr_hip.Q5_K, 3072, 24, 8, 128, 0, 7),        # rope_dim 0: the kv_store form
+    (rrr_hip.Q4_K, 512, 1, 1, 1024, 1024, 11),     # 512 rotation pairs on a 256-thread workgroup
+])
+def test_gemv_rope_kv_forms_are_the_two_launches(ctx, qtype, K, nh, nkv, hd, rd, pos):
+    """The fused QKV + RoPE + KV-store GEMV on every tile plan and weight
+    type it takes leaves qkv and both cache rows bit for bit as the GEMV
+    followed by rrr_rope_kv_store."""
+    from rrr_hip import synth
+    qd, kvs = nh * hd, nkv * hd
+    N = qd + 2 * kvs
+    raw = synth.weight(8, 10 + qtype, qtype, K, N)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    x = ctx.to_device(synth.normal_f32(8, 11, K))
+    g = ctx.to_device(synth.normal_f32(8, 12, K, 1.0, 0.1))
+    nf = rd // 2
+    fac = ctx.to_device((1.0 + np.random.default_rng(rd).uniform(0.0, 3.0, nf)).astype(np.float32)) if nf else None
+    kc, vc = ctx.alloc((pos + 1) * kvs * 2), ctx.alloc((pos + 1) * kvs * 2)
+    q1, q2 = ctx.alloc(N * 4), ctx.alloc(N * 4)
+    rows = []
+    for fused, q in ((False, q1), (True, q2)):
+        ctx.fill_u32(kc, 0x5A5A5A5A)
+        ctx.fill_u32(vc, 0x5A5A5A5A)
+        if fused:
+            ctx.gemv_rmsnorm_rope_kv(x, g, 1e-5, W, qtype, q, K, fac, nf, kc, vc, pos, nh, nkv, hd, rd, qd, kvs)
+        else:
+            ctx.gemv_rmsnorm(x, g, 1e-5, W, qtype, q, K, N)
+            ctx.rope_kv_store(q, fac, nf, kc, vc, pos, nh, nkv, hd, rd, qd, kvs)
+        rows.append((ctx.download(q, np.uint32, N), ctx.download(kc, np.uint16, (pos + 1) * kvs),
+                     ctx.download(vc, np.uint16, (pos + 1) * kvs)))
+    for a, b in zip(rows[0], rows[1]):
+        assert np.array_equal(a, b)
+    assert not np.all(rows[1][2][pos * kvs:] == 0x5A5A)   # row pos of V was written
+    assert np.all(rows[1][1][:pos * kvs] == 0x5A5A)       # and no other row
+    for b in (W, x, g, kc, vc, q1, q2) + ((fac,) if fac is not None else ()):
+        b.free()
+

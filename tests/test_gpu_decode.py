@@ -17,41 +17,13 @@ import pytest
 import oracle.oracle as orc
 import rrr_hip
 from rrr_hip import decode, synth
-from decode_ref import oracle_step
+from decode_ref import gqa_gather, oracle_step, oracle_token
 
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
 THREADS = 16
 SHAPE = dataclasses.replace(decode.Phi4Shape(), n_layers=2, vocab=20000)
-
-
-def gqa_gather(qkv, s):
-    """Attention output at position 0: head h reads V of kv head h / hpk
-    (phi4.rs attention with a single cached position)."""
-    v = qkv[s.d_model + s.n_kv_heads * s.head_dim:].reshape(s.n_kv_heads, s.head_dim)
-    return np.repeat(v, s.heads_per_kv, axis=0).reshape(-1)
-
-
-def oracle_token(s, host, logits="f32"):
-    d, F = s.d_model, s.ffn_dim
-    h = host["x"].astype(np.float64)
-    for i in range(s.n_layers):
-        L = host[i]
-        normed = orc.rms_norm(h.astype(np.float32), L["attn_norm"], s.eps)
-        qkv = orc.gemv(rrr_hip.Q5_K, L["attn_qkv"], normed, d, s.qkv_dim, 1, THREADS, f64=True)[0]
-        v = gqa_gather(qkv.astype(np.float32), s)
-        h = h + orc.gemv(rrr_hip.Q4_K, L["attn_output"], v, d, d, 1, THREADS, f64=True)[0]
-        normed = orc.rms_norm(h.astype(np.float32), L["ffn_norm"], s.eps)
-        gu = orc.gemv(rrr_hip.Q4_K, L["ffn_up"], normed, d, 2 * F, 1, THREADS, f64=True)[0]
-        mid = orc.silu_gate(gu.astype(np.float32), F)
-        h = h + orc.gemv(s.down_type(i), L["ffn_down"], mid, F, d, 1, THREADS, f64=True)[0]
-    normed = orc.rms_norm(h.astype(np.float32), host["out_norm"], s.eps)
-    if logits == "q6k":
-        out = orc.gemv(rrr_hip.Q6_K, host["emb_q6k"], normed, d, s.vocab, 1, THREADS, f64=True)[0]
-    else:
-        out = orc.logits(normed, host["emb"], d, s.vocab, 1, s.chunk, THREADS, f64=True)
-    return out, h
 
 
 @pytest.fixture(scope="module")
@@ -128,81 +100,6 @@ def test_decode_graph_replay_matches_eager(ctx, sweep):
         assert np.array_equal(logits.view(np.uint32), logits0.view(np.uint32))
         assert np.array_equal(hidden.view(np.uint32), hidden0.view(np.uint32))
     g.destroy()
-
-
-def test_decode_sweep_persistent_matches_oracle(ctx, sweep):
-    """The layers as one persistent launch (its own K split for the down
-    GEMVs and its RMSNorm sums from the workgroups' completion records) are
-    within the bar of the fp64 composition, the same bits on every run (the
-    records' epochs carry over from run to run) and agree with the per-op
-    token within the bar."""
-    logits0, tok0, hidden0 = sweep.results()
-    ref_logits, ref_h = oracle_token(SHAPE, sweep.host)
-    sw = ctx.sweep(sweep.sweep_ops())
-    try:
-        first = None
-        for _ in range(3):
-            sweep.run_token_sweep(sw)
-            sw.check()
-            logits, tok, hidden = sweep.results()
-            assert np.all(np.isfinite(logits))
-            assert orc.normwise_err(hidden, ref_h) < TOL
-            assert orc.normwise_err(logits, ref_logits) < TOL
-            assert orc.normwise_err(hidden, hidden0.astype(np.float64)) < TOL
-            assert tok == int(np.argmax(logits))
-            if first is None:
-                first = (logits, hidden)
-            else:
-                assert np.array_equal(logits.view(np.uint32), first[0].view(np.uint32))
-                assert np.array_equal(hidden.view(np.uint32), first[1].view(np.uint32))
-        # the token with the persistent sweep recorded as a graph: replays
-        # (with eager work between them) give the eager bits
-        ctx.graph_begin()
-        sweep.run_token_sweep(sw)
-        g = ctx.graph_end()
-        for _ in range(3):
-            ctx.fill_u32(sweep.logits, 0)
-            ctx.fill_u32(sweep.hidden, 0x7FC00000)
-            g.launch()
-            ctx.sync()
-            logits, tok, hidden = sweep.results()
-            assert np.array_equal(logits.view(np.uint32), first[0].view(np.uint32))
-            assert np.array_equal(hidden.view(np.uint32), first[1].view(np.uint32))
-        g.destroy()
-        sw.check()
-    finally:
-        sw.destroy()
-
-
-def test_sweep_rejects_other_forms_and_runs_small_shapes(ctx):
-    K, N = 3072, 64
-    W = ctx.weight_upload(rrr_hip.Q6_K, K, N, synth.weight(1, 1, rrr_hip.Q6_K, K, N))
-    W4 = ctx.weight_upload(rrr_hip.Q4_K, K, N, synth.weight(1, 2, rrr_hip.Q4_K, K, N))
-    x, g, y = ctx.to_device(synth.normal_f32(1, 3, K)), ctx.to_device(synth.normal_f32(1, 4, K)), ctx.alloc(N * 4)
-    try:
-        # RMSNorm + Q6_K is not one of the decode layer's forms
-        with pytest.raises(rrr_hip.RrrError) as e:
-            ctx.sweep([("rmsnorm", x, g, 1e-5, W, rrr_hip.Q6_K, y, K, N)])
-        assert e.value.code == rrr_hip.engine.ERR_UNSUPPORTED
-        # an RMSNorm op that does not follow the op writing its input
-        with pytest.raises(rrr_hip.RrrError) as e:
-            ctx.sweep([("rmsnorm", x, g, 1e-5, W4, rrr_hip.Q4_K, y, K, N),
-                       ("rmsnorm", x, g, 1e-5, W4, rrr_hip.Q4_K, y, K, N)])
-        assert e.value.code == rrr_hip.engine.ERR_UNSUPPORTED
-        # one op of 64 rows: one row on each of 64 workgroups, the rest idle
-        sw = ctx.sweep([("rmsnorm", x, g, 1e-5, W4, rrr_hip.Q4_K, y, K, N)])
-        ref = orc.gemv(rrr_hip.Q4_K, synth.weight(1, 2, rrr_hip.Q4_K, K, N),
-                       orc.rms_norm(synth.normal_f32(1, 3, K), synth.normal_f32(1, 4, K), 1e-5), K, N, 1, THREADS,
-                       f64=True)[0]
-        for _ in range(2):
-            ctx.fill_u32(y, 0x7FC00000)
-            sw.run()
-            sw.check()
-            assert orc.normwise_err(ctx.download(y), ref) < TOL
-        sw.destroy()
-    finally:
-        for b in (W, W4, x, g, y):
-            b.free()
 
 
 # ---- the full decode step with RoPE, the f16 KV caches and attention ----------

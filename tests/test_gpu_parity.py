@@ -135,34 +135,94 @@ def test_matmul_kquant_helper_and_dispatch_names(ctx):
 
 # ---- batched GEMV / skinny ----------------------------------------------------------
 
-# Q4_K / Q5_K at 2 <= M <= 32 run on the fp16 matrix cores: up to 16 rows
-# with hi/lo-split activations (the GEMV bar), above that hi only (the MFMA bar)
+# Batched K-quant rows on the matrix cores: Q4_K / Q5_K at 2 <= M <= 32 with
+# K <= 3072 on the skinny kernel (up to 16 rows with hi/lo-split activations,
+# the GEMV bar; above that hi only, the MFMA bar), and every K-quant shape
+# above 16 rows that the skinny kernel does not take (more than 32 rows,
+# Q6_K, K > 3072) on the prefill GEMM with f16 block-floating-point rows
+# (N % 64 == 0; the MFMA bar).  The rest runs on the VALU kernels (GEMV bar).
 MFMA_TOL = 2e-3
 
 
-def batched_tol(qtype, K, M):
-    return MFMA_TOL if qtype in (12, 13) and 16 < M <= 32 and K <= 3072 else TOL
+def batched_tol(qtype, K, N, M):
+    if qtype == 0 or M <= 16:
+        return TOL
+    if qtype in (12, 13) and M <= 32 and K <= 3072:
+        return MFMA_TOL
+    return MFMA_TOL if N % 64 == 0 else TOL
+
+
+BATCH_NAME = {12: "matmul_gpuq4_batch", 13: "matmul_gpuq5_batch", 14: "matmul_gpuq6_batch"}
+
+
+def check_batched(ctx, qtype, K, N, M, seed=6):
+    raw = weights(qtype, K, N, seed=seed, stream=qtype)
+    X = synth.normal_f32(seed, 50 + M, M * K)
+    W = ctx.weight_upload(qtype, K, N, raw)
+    Xb, Yb = ctx.to_device(X), ctx.alloc(M * N * 4)
+    ctx.gemv(Xb, W, qtype, Yb, K, N, M)
+    Y = ctx.download(Yb).reshape(M, N)
+    ref = orc.gemv(qtype, raw, X, K, N, M, THREADS, f64=True)
+    tol = batched_tol(qtype, K, N, M)
+    assert np.all(np.isfinite(Y))
+    for m in range(M):
+        assert err(Y[m], ref[m]) < tol, m
+    if qtype:
+        # the reference's batch pipeline (push [K, N, M], grid [N, M, 1]) is the same call
+        ctx.fill_u32(Yb, 0)
+        ctx.dispatch(BATCH_NAME[qtype], [Xb, W, Yb], [K, N, M], [N, M, 1])
+        assert np.array_equal(ctx.download(Yb).reshape(M, N), Y)
+    W.free(); Xb.free(); Yb.free()
 
 
 @pytest.mark.parametrize("qtype,K,N", [(12, 3072, 16384), (13, 3072, 5120), (12, 3072, 3072), (14, 8192, 3072),
                                        (0, 3072, 2048), (12, 512, 37), (13, 4096, 300)])
 @pytest.mark.parametrize("M", [2, 3, 4, 8, 13, 16, 17, 32])
 def test_batched_gemv_parity(ctx, qtype, K, N, M):
-    raw = weights(qtype, K, N, seed=6, stream=qtype)
-    X = synth.normal_f32(6, 50 + M, M * K)
+    check_batched(ctx, qtype, K, N, M)
+
+
+# The reference's prefill calls these pipelines with M = the prompt length
+# (forward_prefill_batched: QKV phi4.rs:1257-1268, gate/up :1346-1357, down
+# :1380-1391): QKV Q5_K 5120x3072, gate/up Q4_K 16384x3072, down Q6_K and
+# Q4_K 3072x8192, at prompt lengths that are and are not multiples of 128.
+@pytest.mark.parametrize("qtype,K,N", [(13, 3072, 5120), (12, 3072, 16384), (14, 8192, 3072), (12, 8192, 3072)])
+@pytest.mark.parametrize("M", [33, 100, 130, 512])
+def test_batched_prompt_rows_parity(ctx, qtype, K, N, M):
+    check_batched(ctx, qtype, K, N, M, seed=16)
+
+
+def test_batched_rows_in_chunks(ctx):
+    """1,600 rows of K = 8192: their f16 copy (26 MB) exceeds half of the
+    48 MB workspace, so the rows go through in chunks of 1,536 and 64 (the
+    last padded to 128 rows, which are computed and not stored)."""
+    check_batched(ctx, 14, 8192, 512, 1600, seed=17)
+
+
+def test_batched_rows_extreme_scales(ctx):
+    """Rows of the f16 route are scaled by powers of two: a row of ~1e30, a
+    row of ~1e-30 and a zero row come out as the unscaled rows would, a row
+    holding inf or NaN makes only its own outputs non-finite."""
+    qtype, K, N, M = 12, 3072, 1024, 40
+    raw = weights(qtype, K, N, seed=18, stream=1)
+    X = synth.normal_f32(18, 2, M * K).reshape(M, K)
+    X[3] *= np.float32(1e30)
+    X[4] *= np.float32(1e-30)
+    X[5] = 0.0
+    X[6, 17] = np.inf
+    X[7, 1000] = np.nan
     W = ctx.weight_upload(qtype, K, N, raw)
-    Xb, Yb = ctx.to_device(X), ctx.alloc(M * N * 4)
+    Xb, Yb = ctx.to_device(X.reshape(-1)), ctx.alloc(M * N * 4)
     ctx.gemv(Xb, W, qtype, Yb, K, N, M)
     Y = ctx.download(Yb).reshape(M, N)
-    ref = orc.gemv(qtype, raw, X, K, N, M, THREADS, f64=True)
-    tol = batched_tol(qtype, K, M)
-    for m in range(M):
-        assert err(Y[m], ref[m]) < tol, m
-    if qtype:
-        name = {12: "matmul_gpuq4_batch", 13: "matmul_gpuq5_batch", 14: "matmul_gpuq6_batch"}[qtype]
-        ctx.fill_u32(Yb, 0)
-        ctx.dispatch(name, [Xb, W, Yb], [K, N, M], [N, M, 1])
-        assert np.array_equal(ctx.download(Yb).reshape(M, N), Y)
+    fin = [m for m in range(M) if m not in (6, 7)]
+    ref = orc.gemv(qtype, raw, np.ascontiguousarray(X[fin]).reshape(-1), K, N, len(fin), THREADS, f64=True)
+    for i, m in enumerate(fin):
+        if m == 5:
+            assert np.all(Y[m] == 0.0)
+        else:
+            assert err(Y[m], ref[i]) < MFMA_TOL, m
+    assert not np.any(np.isfinite(Y[6])) and not np.any(np.isfinite(Y[7]))
     W.free(); Xb.free(); Yb.free()
 
 
@@ -437,6 +497,10 @@ def bf16_to_f32(bits):
 
 @pytest.mark.parametrize("qtype,K,N,M", [(12, 3072, 16384, 128), (14, 8192, 192, 128), (13, 3072, 256, 256),
                                          (12, 512, 128, 384), (14, 256, 64, 128),
+                                         # rows padded inside the library: M not a multiple of 128, and
+                                         # 2,048 rows of K = 8192 whose f16 copy goes through the
+                                         # workspace in chunks of 1,536 and 512 rows
+                                         (12, 3072, 3072, 100), (13, 512, 320, 1), (14, 8192, 1024, 2048),
                                          # 256 x 128 workgroup tiles
                                          (12, 512, 16384, 256), (14, 768, 16384, 256), (13, 256, 16384, 256),
                                          # config 5 as benchmarked (512-token prompt): gate+up in one round of
@@ -461,9 +525,9 @@ def test_gemm_bf16_parity(ctx, qtype, K, N, M):
 
 
 def test_gemm_bf16_unsupported_shapes(ctx):
-    W = ctx.weight_upload(12, 256, 64, weights(12, 256, 64))
-    X, Y = ctx.alloc(100 * 256 * 2), ctx.alloc(100 * 64 * 4)
+    W = ctx.weight_upload(12, 256, 96, weights(12, 256, 96))
+    X, Y = ctx.alloc(100 * 256 * 2), ctx.alloc(100 * 96 * 4)
     with pytest.raises(rrr_hip.RrrError) as ei:
-        ctx.gemm_bf16(X, W, 12, Y, 256, 64, 100)      # M not a multiple of 128
+        ctx.gemm_bf16(X, W, 12, Y, 256, 96, 100)      # N not a multiple of 64
     assert ei.value.code == rrr_hip.engine.ERR_UNSUPPORTED
     W.free(); X.free(); Y.free()

@@ -7,9 +7,12 @@ on two calls in a row, the second on a smaller problem (fewer rows and
 heads, so stale partials of the first call would show), and within 1e-4
 normwise of the fp64 oracle.  The entry point takes plain device pointers
 and a stream: the test allocates them with the HIP runtime the library
-itself is linked against (libamdhip64.so.7) and passes the null stream.
+itself has loaded (found in the process's memory map) and passes the null
+stream.
 """
 import ctypes
+import ctypes.util
+import os
 
 import numpy as np
 import pytest
@@ -24,9 +27,19 @@ HD = 128
 H2D, D2H = 1, 2   # hipMemcpyHostToDevice, hipMemcpyDeviceToHost
 
 
+def _runtime_path():
+    """The libamdhip64 that librrr_hip.so brought into this process."""
+    with open("/proc/self/maps") as f:
+        for line in f:
+            path = line.split()[-1]
+            if os.path.basename(path).startswith("libamdhip64.so"):
+                return path
+    return ctypes.util.find_library("amdhip64") or "libamdhip64.so"
+
+
 def _hip():
     _lib.hip()   # the library first: it loads the runtime this binds to
-    rt = ctypes.CDLL("libamdhip64.so.7")
+    rt = ctypes.CDLL(_runtime_path())
     rt.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
     rt.hipFree.argtypes = [ctypes.c_void_p]
     rt.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
