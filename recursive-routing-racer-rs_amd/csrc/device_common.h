@@ -143,11 +143,31 @@ __device__ __forceinline__ float ordered_sum(const float *p, uint32_t n, uint32_
     return v;
 }
 
-// Deterministic full-wave sum: fixed butterfly order, identical on every call.
+// Deterministic full-wave sum: the xor butterfly over lane distances 32, 16,
+// 8, 4, 2, 1 in that order (each step adds a lane's value and its partner's,
+// so every lane ends with the same bits), entirely in VALU: the 32 and 16
+// steps by the gfx950 lane swaps, 8 by a row rotation, 4 by two row shifts
+// each writing the banks (groups of 4 lanes) whose partner it reaches, 2 and
+// 1 by quad permutes.  No LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, RRR_WAVE);
+    float a, b;
+    lane_pair<32>(v, a, b);
+    v = a + b;
+    lane_pair<16>(v, a, b);
+    v = a + b;
+    v = v + dpp_f<0x128>(v);                                             // row_ror:8 = lane ^ 8
+    const int u = __float_as_int(v);
+    int p = __builtin_amdgcn_update_dpp(u, u, 0x104, 0xF, 0x5, false);   // row_shl:4 on lanes with bit 2 clear
+    p = __builtin_amdgcn_update_dpp(p, u, 0x114, 0xF, 0xA, false);       // row_shr:4 on lanes with bit 2 set
+    v = v + __int_as_float(p);
+    v = v + dpp_f<0x4E>(v);                                              // quad_perm [2,3,0,1] = lane ^ 2
+    v = v + dpp_f<0xB1>(v);                                              // quad_perm [1,0,3,2] = lane ^ 1
     return v;
 }
 
