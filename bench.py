@@ -569,6 +569,9 @@ def main():
     ap.add_argument("--traffic", action="store_true")
     ap.add_argument("--decode-only", action="store_true")
     ap.add_argument("--no-skinny", action="store_true")
+    ap.add_argument("--only", default="",
+                    help="profiling aid: run only these sections (comma list of platform, config1, skinny, prefill, "
+                         "batched, decode) and print their figures as JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -585,6 +588,20 @@ def main():
         return
     if args.decode_only:  # profiling aid: the sweep alone, its figures as JSON
         print(json.dumps({"decode_sweep": decode_sweep(ctx, args.tokens)}), flush=True)
+        ctx.close()
+        return
+    if args.only:  # profiling aid: the named sections alone, their figures as JSON
+        sections = {"platform": lambda: {"platform": platform(ctx)}, "config1": lambda: {"q4k_gemv_3072x3072":
+                    gemv_q4k_config1(ctx)}, "skinny": lambda: skinny(ctx), "prefill": lambda: prefill(ctx),
+                    "batched": lambda: batched_prompt(ctx), "decode": lambda: {"decode_sweep": decode_sweep(ctx,
+                                                                                                      args.tokens)}}
+        res = {}
+        for name in args.only.split(","):
+            if name not in sections:
+                print(f"--only: unknown section {name!r} (one of {', '.join(sections)})", file=sys.stderr)
+                sys.exit(2)
+            res.update(sections[name]())
+        print(json.dumps(res), flush=True)
         ctx.close()
         return
     log(f"[bench] generating config-2 inputs, {args.copies} weight copies")

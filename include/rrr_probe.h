@@ -30,6 +30,24 @@ int rrr_probe_read(rrr_ctx *ctx, const rrr_buf *buf, uint64_t bytes, rrr_buf *si
  * rows, reaches. */
 int rrr_probe_read_shares(rrr_ctx *ctx, const rrr_buf *buf, uint64_t bytes, rrr_buf *sink);
 
+/* Phase timestamps of one batch-1 K-quant GEMV launch: the launch the named
+ * entry point makes for these arguments (op RRR_PHASES_PLAIN = rrr_gemv with
+ * M = 1, _RMSNORM = rrr_gemv_rmsnorm, _RESIDUAL = rrr_gemv_residual with
+ * act_kind / act_param, _RMSNORM_SILU = rrr_gemv_rmsnorm_silu with N = F),
+ * the same kernel instantiated to read the 100 MHz constant clock at its
+ * phases.  Outputs are those of the entry point.  stamps: at least
+ * CUs * 16 * 16 * 8 bytes; wave w of workgroup b writes 16 u64 at
+ * (b * waves + w) * 16: 0 start, 1 activations landed, 2 after the fused
+ * RMSNorm scale, 3 activations encoded, 4 / 6 the first tile's super-block
+ * 0 / 1 staged and 5 / 7 multiplied, 8-11 the same for the last tile, 12 the
+ * wave's row partials written, 13 past the final workgroup barrier, 14 end
+ * (its stores complete); 0 where a phase does not occur.  *grid_out and
+ * *waves_out give the launch shape. */
+enum { RRR_PHASES_PLAIN = 0, RRR_PHASES_RMSNORM = 1, RRR_PHASES_RESIDUAL = 2, RRR_PHASES_RMSNORM_SILU = 3 };
+int rrr_probe_gemv_phases(rrr_ctx *ctx, uint32_t op, uint32_t act_kind, uint32_t act_param, const rrr_buf *x,
+                          const rrr_buf *gamma, float eps, const rrr_buf *W, uint32_t type, rrr_buf *y, uint32_t K,
+                          uint32_t N, rrr_buf *stamps, uint32_t *grid_out, uint32_t *waves_out);
+
 /* Matrix-core rate: `waves_per_cu` waves on every CU (a multiple of 4, at most
  * 32) each run `iters` rounds of 4 independent MFMAs of `kind`.  Operations per
  * launch = CUs * waves_per_cu * iters * 4 * ops_per_mfma, ops_per_mfma

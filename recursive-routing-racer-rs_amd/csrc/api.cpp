@@ -1353,6 +1353,55 @@ int rrr_probe_read_shares(rrr_ctx *ctx, const rrr_buf *buf, uint64_t bytes, rrr_
     return finish(ctx, launch_probe_shares(buf->ptr, bytes, (uint32_t *)sink->ptr, ctx->stream), what);
 }
 
+int rrr_probe_gemv_phases(rrr_ctx *ctx, uint32_t op, uint32_t act_kind, uint32_t act_param, const rrr_buf *x,
+                          const rrr_buf *gamma, float eps, const rrr_buf *W, uint32_t type, rrr_buf *y, uint32_t K,
+                          uint32_t N, rrr_buf *stamps, uint32_t *grid_out, uint32_t *waves_out)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_probe_gemv_phases";
+    if (!grid_out || !waves_out) return fail(RRR_ERR_NULL, "%s: null grid / waves output", what);
+    TRY(check_buf(ctx, stamps, what));
+    GemvArgs a;
+    uint32_t act = ACT_PLAIN;
+    switch (op) {
+    case RRR_PHASES_PLAIN:
+        TRY(gemv_prepare(ctx, x, K, nullptr, 0.0f, ACT_PLAIN, 0, 0, W, type, y, K, N, 1, 0, what, a));
+        break;
+    case RRR_PHASES_RMSNORM:
+        if (!gamma) return fail(RRR_ERR_NULL, "%s: null gamma", what);
+        act = ACT_RMSNORM;
+        TRY(gemv_prepare(ctx, x, K, gamma, eps, ACT_RMSNORM, 0, 0, W, type, y, K, N, 1, 0, what, a));
+        break;
+    case RRR_PHASES_RESIDUAL: {
+        uint64_t x_floats;
+        uint32_t hd, hpk;
+        TRY(residual_act(act_kind, act_param, K, x_floats, act, hd, hpk, what));
+        TRY(gemv_prepare(ctx, x, x_floats, nullptr, 0.0f, act, hd, hpk, W, type, y, K, N, 1, 1, what, a));
+        break;
+    }
+    case RRR_PHASES_RMSNORM_SILU:
+        if (!gamma) return fail(RRR_ERR_NULL, "%s: null gamma", what);
+        if (N == 0 || N > 0x7FFFFFFFu) return fail(RRR_ERR_BAD_SHAPE, "%s: F=%u", what, N);
+        act = ACT_RMSNORM;
+        TRY(gemv_prepare(ctx, x, K, gamma, eps, ACT_RMSNORM, 0, 0, W, type, y, K, 2 * N, 1, 0, what, a, N));
+        a.N = N;
+        a.pair = 1;
+        break;
+    default:
+        return fail(RRR_ERR_INVALID_ARG, "%s: op %u", what, op);
+    }
+    if (!gemv_mfma_supported(a))
+        return fail(RRR_ERR_UNSUPPORTED, "%s: not a shape of the int8-MFMA GEMV (Q4_K/Q5_K/Q6_K, K <= 8192)", what);
+    TRY(device_ready(ctx));
+    TRY(need(stamps, (uint64_t)device_cu_count() * 16 * 16 * 8, what));
+    a.stamps = (uint64_t *)stamps->ptr;
+    uint32_t grid = 0, waves = 0;
+    const hipError_t e = launch_gemv_mfma_stamped(a, act, ctx->stream, grid, waves);
+    *grid_out = grid;
+    *waves_out = waves;
+    return finish(ctx, e, what);
+}
+
 int rrr_probe_mfma(rrr_ctx *ctx, uint32_t kind, uint32_t waves_per_cu, uint32_t iters, rrr_buf *sink)
 {
     TRY(check_ctx(ctx));

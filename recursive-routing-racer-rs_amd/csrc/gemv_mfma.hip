@@ -5,11 +5,16 @@
 
 namespace rrr {
 
-template <class Q, int BPW, int ACT, bool MULTI, int TR, bool PAIR = false, bool ROPE = false>
+template <class Q, int BPW, int ACT, bool MULTI, int TR, bool PAIR = false, bool ROPE = false, bool ST = false>
 __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntiles, uint32_t tr)
 {
-    mq_body<Q, BPW, ACT, MULTI, TR, PAIR, ROPE>(a, ntiles, tr);
+    mq_body<Q, BPW, ACT, MULTI, TR, PAIR, ROPE, ST>(a, ntiles, tr);
 }
+
+// The launch's grid and waves per workgroup (reported to the stamped launch).
+struct MqShape {
+    uint32_t grid, waves;
+};
 
 // Super-blocks per wave and waves per workgroup (at least 4; waves past the
 // last super-block only encode).
@@ -30,21 +35,23 @@ static void mq_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds,
     lds = fixed + (size_t)per * W * 64;
 }
 
-template <class Q, int BPW, int ACT, int TR>
+template <class Q, int BPW, int ACT, int TR, bool ST>
 static void launch_mq(const GemvArgs &a, uint32_t W, uint32_t grid, size_t lds, uint32_t tr, uint32_t ntiles,
                       hipStream_t s)
 {
     if (grid == ntiles)
-        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, false, TR>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
+        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, false, TR, false, false, ST>), dim3(grid), dim3(64 * W), lds, s,
+                           a, ntiles, tr);
     else
-        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, true, TR>), dim3(grid), dim3(64 * W), lds, s, a, ntiles, tr);
+        hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT, true, TR, false, false, ST>), dim3(grid), dim3(64 * W), lds, s,
+                           a, ntiles, tr);
 }
 
 // The silu pair form (a.pair): per 16 output rows a gate tile and its up
 // tile, fused RMSNorm; always the persistent form (a workgroup holds both
 // tiles of a pair).
-template <class Q, int BPW>
-static hipError_t go_mq_pair(const GemvArgs &a, hipStream_t s)
+template <class Q, int BPW, bool ST = false>
+static hipError_t go_mq_pair(const GemvArgs &a, hipStream_t s, MqShape *sh = nullptr)
 {
     using G = MwGeom<Q, BPW>;
     const uint32_t B = a.K / 256;
@@ -56,13 +63,14 @@ static hipError_t go_mq_pair(const GemvArgs &a, hipStream_t s)
     const uint32_t per = min((npairs + cus - 1) / cus, per_max);
     const uint32_t grid = (npairs + per - 1) / per;
     const size_t lds = fixed + (size_t)2 * per * W * 64;
-    hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT_RMSNORM, true, 16, true>), dim3(grid), dim3(64 * W), lds, s, a,
-                       npairs, 16u);
+    hipLaunchKernelGGL((gemv_mq_kernel<Q, BPW, ACT_RMSNORM, true, 16, true, false, ST>), dim3(grid), dim3(64 * W), lds,
+                       s, a, npairs, 16u);
+    if (sh) *sh = MqShape{grid, W};
     return hipGetLastError();
 }
 
-template <class Q, int BPW, int ACT>
-static hipError_t go_mq(const GemvArgs &a, hipStream_t s)
+template <class Q, int BPW, int ACT, bool ST = false>
+static hipError_t go_mq(const GemvArgs &a, hipStream_t s, MqShape *sh = nullptr)
 {
     static_assert(16 * MwGeom<Q, BPW>::BYTES + 64 + 16 * 64 <= 160 * 1024, "LDS per workgroup");
     uint32_t W, grid, tr, ntiles;
@@ -71,11 +79,12 @@ static hipError_t go_mq(const GemvArgs &a, hipStream_t s)
     // slot sets for the tile heights of the decode shapes (N = 5120: 10 rows,
     // N = 3072: 12 rows, larger N: 16 rows)
     if (tr <= 10)
-        launch_mq<Q, BPW, ACT, 10>(a, W, grid, lds, tr, ntiles, s);
+        launch_mq<Q, BPW, ACT, 10, ST>(a, W, grid, lds, tr, ntiles, s);
     else if (tr <= 12)
-        launch_mq<Q, BPW, ACT, 12>(a, W, grid, lds, tr, ntiles, s);
+        launch_mq<Q, BPW, ACT, 12, ST>(a, W, grid, lds, tr, ntiles, s);
     else
-        launch_mq<Q, BPW, ACT, 16>(a, W, grid, lds, tr, ntiles, s);
+        launch_mq<Q, BPW, ACT, 16, ST>(a, W, grid, lds, tr, ntiles, s);
+    if (sh) *sh = MqShape{grid, W};
     return hipGetLastError();
 }
 
@@ -109,20 +118,20 @@ static hipError_t go_mq_rope(const GemvArgs &a, hipStream_t s)
     return hipGetLastError();
 }
 
-template <class Q, int ACT>
-static hipError_t go_mq_k(const GemvArgs &a, hipStream_t s)
+template <class Q, int ACT, bool ST>
+static hipError_t go_mq_k(const GemvArgs &a, hipStream_t s, MqShape *sh)
 {
-    return a.K <= 16 * 256 ? go_mq<Q, 1, ACT>(a, s) : go_mq<Q, 2, ACT>(a, s);
+    return a.K <= 16 * 256 ? go_mq<Q, 1, ACT, ST>(a, s, sh) : go_mq<Q, 2, ACT, ST>(a, s, sh);
 }
 
-template <class Q>
-static hipError_t go_mq_act(const GemvArgs &a, uint32_t act, hipStream_t s)
+template <class Q, bool ST = false>
+static hipError_t go_mq_act(const GemvArgs &a, uint32_t act, hipStream_t s, MqShape *sh = nullptr)
 {
     switch (act) {
-    case ACT_PLAIN: return go_mq_k<Q, ACT_PLAIN>(a, s);
-    case ACT_SILU: return go_mq_k<Q, ACT_SILU>(a, s);
-    case ACT_GQA_V: return go_mq_k<Q, ACT_GQA_V>(a, s);
-    case ACT_RMSNORM: return go_mq_k<Q, ACT_RMSNORM>(a, s);
+    case ACT_PLAIN: return go_mq_k<Q, ACT_PLAIN, ST>(a, s, sh);
+    case ACT_SILU: return go_mq_k<Q, ACT_SILU, ST>(a, s, sh);
+    case ACT_GQA_V: return go_mq_k<Q, ACT_GQA_V, ST>(a, s, sh);
+    case ACT_RMSNORM: return go_mq_k<Q, ACT_RMSNORM, ST>(a, s, sh);
     default: return hipErrorInvalidValue;
     }
 }
@@ -163,6 +172,35 @@ hipError_t launch_gemv_mfma(const GemvArgs &a, uint32_t act, hipStream_t s)
     case T_Q6_K: return go_mq_act<MqQ6K>(a, act, s);
     default: return hipErrorInvalidValue;
     }
+}
+
+// The launch launch_gemv_mfma makes for `a` (plain and pair forms; not the
+// RoPE epilogue), instantiated with phase timestamps into a.stamps.
+hipError_t launch_gemv_mfma_stamped(const GemvArgs &a, uint32_t act, hipStream_t s, uint32_t &grid, uint32_t &waves)
+{
+    if (a.rope_on || !a.stamps) return hipErrorNotSupported;
+    MqShape sh{0, 0};
+    hipError_t e;
+    if (a.pair) {
+        if (act != ACT_RMSNORM || a.residual) return hipErrorInvalidValue;
+        const bool one = a.K <= 16 * 256;
+        switch (a.type) {
+        case T_Q4_K: e = one ? go_mq_pair<MqQ4K, 1, true>(a, s, &sh) : go_mq_pair<MqQ4K, 2, true>(a, s, &sh); break;
+        case T_Q5_K: e = one ? go_mq_pair<MqQ5K, 1, true>(a, s, &sh) : go_mq_pair<MqQ5K, 2, true>(a, s, &sh); break;
+        case T_Q6_K: e = one ? go_mq_pair<MqQ6K, 1, true>(a, s, &sh) : go_mq_pair<MqQ6K, 2, true>(a, s, &sh); break;
+        default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (a.type) {
+        case T_Q4_K: e = go_mq_act<MqQ4K, true>(a, act, s, &sh); break;
+        case T_Q5_K: e = go_mq_act<MqQ5K, true>(a, act, s, &sh); break;
+        case T_Q6_K: e = go_mq_act<MqQ6K, true>(a, act, s, &sh); break;
+        default: return hipErrorInvalidValue;
+        }
+    }
+    grid = sh.grid;
+    waves = sh.waves;
+    return e;
 }
 
 }  // namespace rrr

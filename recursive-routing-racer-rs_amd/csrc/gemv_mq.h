@@ -291,7 +291,23 @@ constexpr uint32_t MQ_OOB = 0x80000000u;
 // order (all requested before the first add).
 __device__ __forceinline__ float waves_sum(const float *p, uint32_t W) { return ordered_sum<16>(p, W, 16); }
 
-template <class Q, int BPW, int ACT, bool MULTI, int TR = 16, bool PAIR = false, bool ROPE = false>
+// Phase timestamps (the STAMPS instantiation only, rrr_probe_gemv_phases):
+// the 100 MHz constant clock read once `dep` is available, kept in scalar
+// registers and stored at the end, so that no store enters the memory queue
+// between the phases.  Slot k of a wave (a.stamps[(block * W + wave) * 16 + k]):
+// 0 start, 1 activations landed, 2 after the fused RMSNorm scale, 3
+// activations encoded, 4 / 6 first tile's block 0 / 1 staged, 5 / 7 its
+// MFMAs done, 8-11 the same for the last tile (several tiles per workgroup),
+// 12 the wave's partials written, 13 past the final barrier, 14 end.
+__device__ __forceinline__ uint64_t phase_stamp(float dep)
+{
+    uint64_t t;
+    asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t) : "v"(dep) : "memory");
+    return t;
+}
+
+template <class Q, int BPW, int ACT, bool MULTI, int TR = 16, bool PAIR = false, bool ROPE = false,
+          bool STAMPS = false>
 __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr)
 {
     extern __shared__ float smem[];
@@ -307,6 +323,17 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     const uint32_t W = blockDim.x >> 6, NT = blockDim.x;
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t n = lane & 15, g = lane >> 4;
+    uint64_t stamp[15] = {};
+    auto mark = [&](int k, float dep) {
+        if constexpr (STAMPS) stamp[k] = phase_stamp(dep);
+    };
+    auto mark_flush = [&]() {
+        if constexpr (STAMPS) {
+            if (lane == 0)
+                for (int k = 0; k < 15; k++) a.stamps[((size_t)blockIdx.x * W + wave) * 16 + k] = stamp[k];
+        }
+    };
+    mark(0, 0.0f);
     const uint32_t GR = gridDim.x, tile0 = blockIdx.x;
     static_assert(!PAIR || (MULTI && TR == 16), "a pair is a gate tile and an up tile of 16 rows");
     const uint32_t nown = tile0 < ntiles ? (ntiles - tile0 + GR - 1) / GR : 0u;   // tiles (PAIR: pairs) of this workgroup
@@ -377,6 +404,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     // for K <= 8192); the slice sums are added in wave order (waves without
     // a super-block add +0)
     float inv = 1.0f;
+    mark(1, xa[0].x);
     if constexpr (ACT == ACT_RMSNORM) {
         float sq = 0.0f;
 #pragma unroll
@@ -390,6 +418,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         inv = rms_inv(s, K, a.eps);
     }
 
+    mark(2, xa[0].x + inv);
     // 3. activation staging of this wave's slice
 #pragma unroll
     for (int j = 0; j < BPW; j++) {
@@ -421,6 +450,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         if ((lane & 3) == 0) *(i32x4 *)(L + G::A_OFF + 4 * f) = ax;
     }
     wave_lds_sync();
+    mark(3, 0.0f);
 
     // A operands (zero in the non-live lanes), accumulator inputs and group
     // sums of the slice, into registers while the weights are in flight; lane
@@ -472,6 +502,8 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
             }
             if constexpr (MULTI) issue(j, tl + 1);
             wave_lds_sync();
+            if (tl == 0) mark(4 + 2 * j, 0.0f);
+            else if (tl + 1 == ntl) mark(8 + 2 * j, 0.0f);
             if (j < (int)nb) {
                 typename Q::Raw raw;
                 Q::load(raw, L, n * G::RS + j * G::LB, g);
@@ -503,10 +535,13 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
                 acc = fmaf(d, acc_s, acc);
                 if constexpr (Q::HAS_MIN) acc = fmaf(-dmin, acc_m, acc);
             }
+            if (tl == 0) mark(5 + 2 * j, acc);
+            else if (tl + 1 == ntl) mark(9 + 2 * j, acc);
         }
         // the 4 k-groups of a row (lanes n, n+16, n+32, n+48), by lane swaps
         acc = lanes4_sum(acc);
         if (lane < 16) part[(tl * W + wave) * 16 + lane] = acc;
+        if (tl + 1 == ntl) mark(12, acc);
     };
     if constexpr (MULTI) {
         for (uint32_t tl = 0; tl < ntl; tl++) process(tl);
@@ -516,6 +551,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
 
     // 5. rows of every tile of this workgroup: the W waves' partials in order
     __syncthreads();
+    mark(13, 0.0f);
     if constexpr (PAIR) {
         for (uint32_t i = t; i < nown * 16; i += NT) {
             const uint32_t q = i >> 4, r = i & 15, row = (tile0 + q * GR) * 16 + r;
@@ -523,6 +559,11 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
                 const float *pg = part + 2 * q * W * 16 + r, *pu = pg + W * 16;
                 a.y[row] = silu_fast(waves_sum(pg, W)) * waves_sum(pu, W);
             }
+        }
+        if constexpr (STAMPS) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            mark(14, 0.0f);
+            mark_flush();
         }
         return;
     }
@@ -535,6 +576,11 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
                                 coef);
             }
         }
+        if constexpr (STAMPS) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            mark(14, 0.0f);
+            mark_flush();
+        }
         return;
     }
     for (uint32_t i = t; i < ntl * 16; i += NT) {
@@ -544,6 +590,11 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
             if (a.residual) v = (i == t ? yres : a.y[row]) + v;
             a.y[row] = v;
         }
+    }
+    if constexpr (STAMPS) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        mark(14, 0.0f);
+        mark_flush();
     }
 }
 

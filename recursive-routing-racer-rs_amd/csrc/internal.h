@@ -44,6 +44,7 @@ struct GemvArgs {
     uint32_t rope_on;
     RopeArgs rope;
     uint32_t *kc, *vc;
+    uint64_t *stamps;     // phase timestamps of the stamped launch (rrr_probe_gemv_phases), else unused
 };
 
 // Every device buffer is allocated with at least this many bytes past its
@@ -58,6 +59,9 @@ hipError_t launch_gemv(const GemvArgs &a, uint32_t act, hipStream_t s);
 // int8-MFMA batch-1 K-quant GEMV (gemv_mfma.hip)
 bool gemv_mfma_supported(const GemvArgs &a);
 hipError_t launch_gemv_mfma(const GemvArgs &a, uint32_t act, hipStream_t s);
+// the same launch with phase timestamps into a.stamps (16 u64 per wave of
+// each workgroup); returns the grid and the waves per workgroup
+hipError_t launch_gemv_mfma_stamped(const GemvArgs &a, uint32_t act, hipStream_t s, uint32_t &grid, uint32_t &waves);
 // fp16-MFMA batched GEMV for 2 <= M <= 32, Q4_K / Q5_K (skinny.hip)
 bool skinny_supported(const GemvArgs &a);
 hipError_t launch_skinny(const GemvArgs &a, hipStream_t s);

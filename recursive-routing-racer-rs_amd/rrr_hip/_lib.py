@@ -97,6 +97,8 @@ SIGNATURES = {
     "rrr_attention_noalloc": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
     "rrr_probe_read": (i32, [c_ctx_p, c_buf_p, u64, c_buf_p]),
     "rrr_probe_read_shares": (i32, [c_ctx_p, c_buf_p, u64, c_buf_p]),
+    "rrr_probe_gemv_phases": (i32, [c_ctx_p, u32, u32, u32, c_buf_p, c_buf_p, f32, c_buf_p, u32, c_buf_p, u32, u32,
+                                    c_buf_p, ctypes.POINTER(u32), ctypes.POINTER(u32)]),
     "rrr_probe_mfma": (i32, [c_ctx_p, u32, u32, u32, c_buf_p]),
     "rrr_probe_cus": (u32, [c_ctx_p]),
     "rrr_rope_kv_store_rows": (i32, [c_ctx_p, c_buf_p, u32, c_buf_p, u32, c_buf_p, c_buf_p, u32, u32, u32, u32, u32,

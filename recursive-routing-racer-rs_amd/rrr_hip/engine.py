@@ -35,6 +35,7 @@ F32, F16, Q4_K, Q5_K, Q6_K = 0, 1, 12, 13, 14
 LOGITS_ROWS, LOGITS_CHUNKED, LOGITS_Q6K = 0, 1, 2
 ACT_IDENTITY, ACT_SILU_GATE, ACT_GQA_V = 0, 1, 2
 PROBE_MFMA_F16_16X16X32, PROBE_MFMA_F16_32X32X16, PROBE_MFMA_I8_16X16X64 = 0, 1, 2
+PHASES_PLAIN, PHASES_RMSNORM, PHASES_RESIDUAL, PHASES_RMSNORM_SILU = 0, 1, 2, 3
 DEVICE_NONE = -1
 BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, F32: 1024}
 
@@ -296,6 +297,14 @@ class Context:
 
     def probe_read_shares(self, buf, nbytes, sink):
         _check(self.lib.rrr_probe_read_shares(self._h, buf._h, nbytes, sink._h))
+
+    def probe_gemv_phases(self, op, x, W, qtype, y, K, N, stamps, gamma=None, eps=1e-5, act_kind=0, act_param=0):
+        """One stamped GEMV launch (include/rrr_probe.h); returns (grid, waves)."""
+        g, w = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(self.lib.rrr_probe_gemv_phases(self._h, op, act_kind, act_param, x._h,
+                                              gamma._h if gamma is not None else None, eps, W._h, qtype, y._h, K, N,
+                                              stamps._h, ctypes.byref(g), ctypes.byref(w)))
+        return g.value, w.value
 
     def probe_mfma(self, kind, waves_per_cu, iters, sink):
         _check(self.lib.rrr_probe_mfma(self._h, kind, waves_per_cu, iters, sink._h))
