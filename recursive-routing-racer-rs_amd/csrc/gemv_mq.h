@@ -413,9 +413,9 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         sq = wave_sum(sq);
         if (lane == 0) red[wave] = sq;
         __syncthreads();
-        float s = red[0];
-        for (uint32_t w = 1; w < W; w++) s = s + red[w];
-        inv = rms_inv(s, K, a.eps);
+        // the W slice sums in order, all requested before the first add (a
+        // runtime-length loop waits out one LDS round trip per wave)
+        inv = rms_inv(ordered_sum<16>(red, W, 1), K, a.eps);
     }
 
     mark(2, xa[0].x + inv);
