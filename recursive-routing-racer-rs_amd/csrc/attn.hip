@@ -198,16 +198,24 @@ hipError_t launch_splitk_rope_kv_store(const float *ws, uint32_t S, uint32_t M, 
 // owning dims 8 li .. 8 li + 7 of a row (one 16-byte f16 load of K and one of
 // V; a score is one DPP row sum).  The HPK query heads of the KV group share
 // every K/V load.  Scores go through exp2 with the queries pre-scaled by
-// log2(e) / sqrt(head_dim); each lane group keeps a running max, sum and
-// output (online softmax).  The 4 lane groups of a wave are merged by lane
-// swaps (rows 0+1 and 2+3, then the two halves, lower partner first), the 4
-// waves in LDS, and the workgroup's {output, max, sum}
-// per query head is written through the coherent level; the last workgroup of
-// KV head g to arrive (an agent-scope counter) merges the splits and writes
-// the output, then resets the counter for the next call.  Every merge runs in
-// a fixed order, so the result depends on seq_len only.
+// log2(e) / sqrt(head_dim).  A wave's 4 lane groups take one maximum per head
+// (lane swaps), so their sums and outputs add without rescaling; the 4 waves
+// are merged in LDS, and the workgroup's {output, max, sum} per query head is
+// written through the coherent level; the last workgroup of KV head g to
+// arrive (an agent-scope counter) merges the splits and writes the output,
+// then resets the counter for the next call.  Every merge runs in a fixed
+// order, so the result depends on seq_len only.
 
 __device__ __forceinline__ float safe_scale(float m, float M) { return m == -__builtin_inff() ? 0.0f : exp2f(m - M); }
+
+// exp2(m - M), 0 for m = -inf (a part without rows), without a branch: the
+// hardware exp2 runs for every lane and the select follows (results below
+// 2^-126 flush to zero, against a largest weight of 1).
+__device__ __forceinline__ float scale_exp2(float m, float M)
+{
+    const float e = __builtin_amdgcn_exp2f(m - M);
+    return m == -__builtin_inff() ? 0.0f : e;
+}
 
 // Sum over the 16 lanes of a DPP row (butterfly: xor 1, xor 2, then the
 // half-row and row mirrors); every lane of the row gets the sum.
@@ -247,9 +255,6 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
 {
     __shared__ float gml[4][HPK][2];
     __shared__ __attribute__((aligned(16))) float go[4][HPK][ATT_HD];
-    __shared__ float sw[HPK][ATT_SPLITS_MAX];   // split weights exp2(m_s - M)
-    __shared__ float sL[HPK];                   // the heads' merged sums
-    __shared__ __attribute__((aligned(16))) float so[HPK][8][ATT_HD];    // sums over split subsets
     __shared__ uint32_t last;
     const uint32_t g = blockIdx.x, sp = blockIdx.y, splits = gridDim.y;
     const uint32_t t = threadIdx.x, grp = t >> 4, li = t & 15;
@@ -274,18 +279,10 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
         qv[h][0] = a.x * qscale; qv[h][1] = a.y * qscale; qv[h][2] = a.z * qscale; qv[h][3] = a.w * qscale;
         qv[h][4] = b.x * qscale; qv[h][5] = b.y * qscale; qv[h][6] = b.z * qscale; qv[h][7] = b.w * qscale;
     }
-    float m[HPK], l[HPK], o[HPK][8];
-#pragma unroll
-    for (int h = 0; h < HPK; h++) {
-        m[h] = -__builtin_inff();
-        l[h] = 0.0f;
-#pragma unroll
-        for (int d = 0; d < 8; d++) o[h][d] = 0.0f;
-    }
-    // the lane group's ATT_ROWS_PER_GROUP rows at once: their scores (independent
-    // dot products and row sums), one update of the running max, then the
-    // sum and output; rows past the split add nothing (uniform in the row of
-    // 16 lanes)
+    // the lane group's ATT_ROWS_PER_GROUP rows at once: their scores
+    // (independent dot products and row sums), the wave's maximum per head,
+    // then the sum and output; rows past the split add nothing (uniform in the
+    // row of 16 lanes)
     constexpr int R = (int)ATT_ROWS_PER_GROUP;
     float kf[R][8], v[R][8];
     bool live[R];
@@ -300,6 +297,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
             v[k][2 * w + 1] = h2f(vr[k][w] >> 16);
         }
     }
+    const uint32_t wv = t >> 6;
 #pragma unroll
     for (int h = 0; h < HPK; h++) {
         float sc[R];
@@ -310,41 +308,35 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
             for (int d = 0; d < 8; d++) s = fmaf(qv[h][d], kf[k][d], s);
             sc[k] = row16_sum(s);
         }
-        float mn = m[h];
+        float mx = -__builtin_inff();
 #pragma unroll
         for (int k = 0; k < R; k++)
-            if (live[k]) mn = fmaxf(mn, sc[k]);
-        const float c = safe_scale(m[h], mn);   // 0 while no row has been seen
-        float p[R], ps = 0.0f;
+            if (live[k]) mx = fmaxf(mx, sc[k]);
+        mx = lanes4_max(mx);   // the wave's maximum: -inf only for a wave without rows
+        float ps = 0.0f, p[R];
 #pragma unroll
         for (int k = 0; k < R; k++) {
-            p[k] = live[k] ? exp2f(sc[k] - mn) : 0.0f;
+            const float e = __builtin_amdgcn_exp2f(sc[k] - mx);
+            p[k] = live[k] ? e : 0.0f;
             ps += p[k];
         }
-        l[h] = fmaf(l[h], c, ps);
+        float od[8];
 #pragma unroll
         for (int d = 0; d < 8; d++) {
-            float od = o[h][d] * c;
+            float acc = 0.0f;
 #pragma unroll
-            for (int k = 0; k < R; k++) od = fmaf(p[k], v[k][d], od);
-            o[h][d] = od;
+            for (int k = 0; k < R; k++) acc = fmaf(p[k], v[k][d], acc);
+            od[d] = lanes4_sum(acc);
         }
-        m[h] = mn;
-    }
-    // the wave's 4 lane groups by lane swaps, then the workgroup's 4 waves in LDS
-    const uint32_t wv = t >> 6;
-#pragma unroll
-    for (int h = 0; h < HPK; h++) {
-        merge_pair<16>(m[h], l[h], o[h]);
-        merge_pair<32>(m[h], l[h], o[h]);
+        ps = lanes4_sum(ps);
         if ((t & 63) < 16) {
             if (li == 0) {
-                gml[wv][h][0] = m[h];
-                gml[wv][h][1] = l[h];
+                gml[wv][h][0] = mx;
+                gml[wv][h][1] = ps;
             }
             float4 *dst = (float4 *)&go[wv][h][8 * li];
-            dst[0] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-            dst[1] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+            dst[0] = make_float4(od[0], od[1], od[2], od[3]);
+            dst[1] = make_float4(od[4], od[5], od[6], od[7]);
         }
     }
     __syncthreads();
@@ -355,7 +347,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
         float L = 0.0f, O = 0.0f;
 #pragma unroll
         for (int wi = 0; wi < 4; wi++) {
-            const float c = safe_scale(gml[wi][h][0], M);   // 0 for a wave without rows
+            const float c = scale_exp2(gml[wi][h][0], M);   // 0 for a wave without rows
             L = fmaf(gml[wi][h][1], c, L);
             O = fmaf(go[wi][h][d], c, O);
         }
@@ -380,70 +372,57 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q, 
                                       __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
     __syncthreads();
     if (!last) return;
-    // the last workgroup of KV head g merges its splits.  Thread t takes dims
-    // 4 (t % 32) .. +3 of split subset ss = t / 32 (splits ss, ss + 8, ...):
-    // all of its output quads and the splits' maxima and sums are requested
-    // at once, then everything is added in a fixed order.
-    const uint32_t dq = t & 31, ss = t >> 5;
-    u32x4 ov[HPK][ATT_SPLITS_MAX / 8];
+    // the last workgroup of KV head g merges its splits: wave w takes query
+    // heads w, w + 4, ...; lane (dq, hf) = (lane % 32, lane / 32) takes dims
+    // 4 dq .. 4 dq + 3 of splits 16 hf .. 16 hf + 15.  All of a head's loads
+    // (output quads, maxima and sums) are in flight at once; the two halves
+    // meet by lane swaps (both lanes compute the same max and the same
+    // lower + upper sum), and everything is added in split order.
+    static_assert(ATT_SPLITS_MAX <= 32, "two halves of at most 16 splits");
+    const uint32_t lane = t & 63, dq = lane & 31, hf = lane >> 5;
+    for (uint32_t h = wv; h < (uint32_t)HPK; h += 4) {
+        u32x4 ov[16];
+        float ms[16], ls[16];
 #pragma unroll
-    for (int h = 0; h < HPK; h++)
-#pragma unroll
-        for (uint32_t j = 0; j < ATT_SPLITS_MAX / 8; j++) {
-            const uint32_t s = ss + 8 * j;
-            ov[h][j] = s < splits ? __builtin_amdgcn_raw_buffer_load_b128(
-                                        rp, (((g * splits + s) * HPK + h) * ATT_PART + 4 * dq) * 4, 0, RRR_CPOL_SC1)
-                                  : u32x4{0u, 0u, 0u, 0u};
+        for (int j = 0; j < 16; j++) {
+            const uint32_t s = min(16 * hf + j, splits - 1);   // past the last split: a valid record, weight 0
+            const uint32_t base = (((g * splits + s) * HPK + h) * ATT_PART) * 4;
+            ov[j] = __builtin_amdgcn_raw_buffer_load_b128(rp, base + 16 * dq, 0, RRR_CPOL_SC1);
+            const auto u = __builtin_amdgcn_raw_buffer_load_b64(rp, base + 4 * ATT_HD, 0, RRR_CPOL_SC1);
+            ms[j] = __uint_as_float(u[0]);
+            ls[j] = __uint_as_float(u[1]);
         }
-    // thread t: split t % 32 of head t / 32; the 32 lanes of a head reduce
-    // its maximum and sum by butterflies (both partners of a step compute
-    // the same a + b, so every lane gets the same value, every run)
-    {
-        const uint32_t hh = t >> 5, sh = t & 31;
-        float ms = -__builtin_inff(), ls = 0.0f;
-        if (hh < HPK && sh < splits) {
-            const uint32_t base = (((g * splits + sh) * HPK + hh) * ATT_PART) * 4;
-            ms = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, base + 4 * ATT_HD, 0, RRR_CPOL_SC1));
-            ls = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, base + 4 * ATT_HD + 4, 0, RRR_CPOL_SC1));
-        }
-        float M = ms;
+        __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the first use
+        float M = -__builtin_inff();
 #pragma unroll
-        for (int x = 16; x >= 1; x >>= 1) M = fmaxf(M, __shfl_xor(M, x, 64));
-        const float w = safe_scale(ms, M);
-        float L = ls * w;
+        for (int j = 0; j < 16; j++)
+            if (16 * hf + j < splits) M = fmaxf(M, ms[j]);
+        float lo, hi;
+        lane_pair<32>(M, lo, hi);
+        M = fmaxf(lo, hi);
+        float L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int x = 16; x >= 1; x >>= 1) L = L + __shfl_xor(L, x, 64);
-        if (hh < HPK) {
-            sw[hh][sh] = w;
-            if (sh == 0) sL[hh] = L;
+        for (int j = 0; j < 16; j++) {
+            const float e = scale_exp2(ms[j], M);
+            const float w = 16 * hf + j < splits ? e : 0.0f;
+            L = fmaf(ls[j], w, L);
+            O[0] = fmaf(__uint_as_float(ov[j].x), w, O[0]);
+            O[1] = fmaf(__uint_as_float(ov[j].y), w, O[1]);
+            O[2] = fmaf(__uint_as_float(ov[j].z), w, O[2]);
+            O[3] = fmaf(__uint_as_float(ov[j].w), w, O[3]);
         }
+        lane_pair<32>(L, lo, hi);
+        L = lo + hi;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            lane_pair<32>(O[c], lo, hi);
+            O[c] = lo + hi;
+        }
+        if (hf == 0)
+            *(float4 *)(out + (size_t)(g * HPK + h) * ATT_HD + 4 * dq) =
+                make_float4(O[0] / L, O[1] / L, O[2] / L, O[3] / L);
     }
     __syncthreads();
-    // its own splits' output quads, weighted and added in split order
-#pragma unroll
-    for (int h = 0; h < HPK; h++) {
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-        for (uint32_t j = 0; j < ATT_SPLITS_MAX / 8; j++) {
-            const uint32_t s = ss + 8 * j;
-            if (s < splits) {
-                const float c = sw[h][s];
-                acc.x = fmaf(__uint_as_float(ov[h][j].x), c, acc.x);
-                acc.y = fmaf(__uint_as_float(ov[h][j].y), c, acc.y);
-                acc.z = fmaf(__uint_as_float(ov[h][j].z), c, acc.z);
-                acc.w = fmaf(__uint_as_float(ov[h][j].w), c, acc.w);
-            }
-        }
-        *(float4 *)&so[h][ss][4 * dq] = acc;
-    }
-    __syncthreads();
-    for (uint32_t i = t; i < HPK * ATT_HD; i += 256) {
-        const uint32_t h = i / ATT_HD, d = i % ATT_HD;
-        float O = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; k++) O += so[h][k][d];
-        out[(size_t)(g * HPK + h) * ATT_HD + d] = O / sL[h];
-    }
     if (t == 0) __hip_atomic_store(counters + g * ATT_COUNTER_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -454,16 +433,14 @@ uint64_t attention_scratch_bytes() { return ATT_SCRATCH_BYTES; }
 // through the coherent level, a counter, the last workgroup's loads, ~2.5 us)
 // costs more than the longer splits' load phase (64 rows: 4.3 us in one split
 // against 6.9 us in four; 512 rows 7.45 against 8.1 us in 32 splits).  At
-// most ATT_SPLITS_MAX splits, at most 256 / heads_per_kv (the merge reads one
-// split maximum and sum per thread): both hold for seq <= ATT_SEQ_MAX and
-// heads_per_kv <= 8.
+// most ATT_SPLITS_MAX splits, which holds for seq <= ATT_SEQ_MAX.
 void attention_plan(uint32_t seq, uint32_t n_kv_heads, uint32_t heads_per_kv, uint32_t cus, uint32_t &splits,
                     uint32_t &per)
 {
     (void)n_kv_heads;
+    (void)heads_per_kv;
     (void)cus;
-    const uint32_t cap = min(ATT_SPLITS_MAX, 256 / heads_per_kv);
-    splits = min(cap, max(1u, (seq + 16 * ATT_ROWS_PER_GROUP - 1) / (16 * ATT_ROWS_PER_GROUP)));
+    splits = min(ATT_SPLITS_MAX, max(1u, (seq + 16 * ATT_ROWS_PER_GROUP - 1) / (16 * ATT_ROWS_PER_GROUP)));
     per = (seq + splits - 1) / splits;
     splits = (seq + per - 1) / per;   // every split has at least one row
 }
