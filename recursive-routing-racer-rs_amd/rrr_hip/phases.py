@@ -1,6 +1,6 @@
 """Phase timestamps of the decode-path batch-1 GEMVs (rrr_probe_gemv_phases).
 
-    python -m rrr_hip.phases [--launches 40]
+    python -m rrr_hip.phases [--launches 40] [--resident-x]
 
 For each of the decode token's GEMV launches (RMSNorm + QKV Q5_K 5120x3072,
 GQA-V + O-proj Q4_K 3072x3072 + residual, RMSNorm + gate/up Q4_K 16384x3072
@@ -8,7 +8,10 @@ with silu * up, down Q6_K / Q4_K 3072x8192 + residual) and the single Q4_K
 3072x3072 GEMV, the stamped twin of the kernel runs `--launches` times over
 rotating weight copies (over 600 MB a pass, so the weights stream from HBM),
 each launch right after a kernel that writes its activation vector (as in
-the decode token, where the previous op writes it).  Per phase it prints the
+the decode token, where the previous op writes it), or with --resident-x
+after a kernel that writes another buffer, so the activation vector stays
+as the previous launch left it (as in the per-kernel bench lines).  Per
+phase it prints the
 median over launches of the median, 90th percentile and maximum over the
 launch's waves of the phase's time after the launch's first wave started, in
 microseconds (the device's 100 MHz constant clock), as a markdown table.
@@ -39,7 +42,7 @@ CASES = [
 ]
 
 
-def measure(ctx, case, launches, warm=8):
+def measure(ctx, case, launches, warm=8, resident_x=False):
     name, op, qt, K, N, xlen, act_kind, act_param = case
     rows = 2 * N if op == E.PHASES_RMSNORM_SILU else N
     wbytes = E.tensor_bytes(qt, K, rows)
@@ -55,14 +58,17 @@ def measure(ctx, case, launches, warm=8):
     st = ctx.alloc(per)
     ts = []
     grid = waves = 0
+    other = ctx.alloc(xlen * 4)
+    ctx.residual_add(src, zero, x, xlen)
     for r in range(warm + launches):
-        ctx.residual_add(src, zero, x, xlen)   # the activations, written by the previous kernel
+        # the previous kernel writes the activations, or (resident) another buffer
+        ctx.residual_add(src, zero, other if resident_x else x, xlen)
         grid, waves = ctx.probe_gemv_phases(op, x, Ws[r % copies], qt, y, K, N, st, gamma=gamma,
                                             act_kind=act_kind, act_param=act_param)
         ctx.sync()
         if r >= warm:
             ts.append(ctx.download(st, np.uint64, grid * waves * 16).reshape(grid * waves, 16).astype(np.int64))
-    for b in Ws + [src, zero, x, gamma, y, st]:
+    for b in Ws + [src, zero, x, other, gamma, y, st]:
         b.free()
     stats = {}
     for k in range(len(PHASES)):
@@ -81,10 +87,12 @@ def measure(ctx, case, launches, warm=8):
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--launches", type=int, default=40)
+    ap.add_argument("--resident-x", action="store_true",
+                    help="no kernel writes the activations between launches")
     args = ap.parse_args(argv)
     with Context(0) as ctx:
         for case in CASES:
-            wbytes, grid, waves, st = measure(ctx, case, args.launches)
+            wbytes, grid, waves, st = measure(ctx, case, args.launches, resident_x=args.resident_x)
             print(f"\n### {case[0]} ({wbytes / 1e6:.1f} MB of weights; {grid} workgroups of {waves} waves)\n")
             print("| phase | median us | p90 us | max us |")
             print("|---|---|---|---|")
