@@ -67,6 +67,19 @@ __device__ __forceinline__ void sk_scale4(uint32_t v, f16x2s sc2, f16x2s nb2, ui
     o23 = sk_u32(__builtin_elementwise_fma(sk_bits(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u)), sc2, nb2));
 }
 
+// The 6-bit scales (sc) and mins (mn) of sub-blocks 0..3 and 4..7 as four
+// bytes each, from the 12 packed bytes in y, z, w (bytes 4..15 of a Q4_K /
+// Q5_K block; the get_scale_min step of phi4.rs:492-498 for all j at once):
+// j < 4: sc = q[j] & 63, mn = q[j+4] & 63; j >= 4: sc = (q[j+4] & 15) |
+// (q[j-4] >> 6) << 4, mn = (q[j+4] >> 4) | (q[j] >> 6) << 4.
+__device__ __forceinline__ void sk_scale_bytes(uint32_t y, uint32_t z, uint32_t w, uint32_t (&sc)[2], uint32_t (&mn)[2])
+{
+    sc[0] = y & 0x3F3F3F3Fu;
+    mn[0] = z & 0x3F3F3F3Fu;
+    sc[1] = (w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u);
+    mn[1] = ((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u);
+}
+
 // Q4_K (phi4.rs:481-510): element 32s + e of a block is nibble (s & 1) of
 // qs[32 (s/2) + e].  Lane k-group kg takes e = 8kg .. 8kg+7 of every s.
 struct SkQ4K {
@@ -322,6 +335,12 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
         }
     }
 
+    // 2^E of the lane's D-layout tokens (the same for every tile)
+    float pe[TOK][DPT];
+#pragma unroll
+    for (int tt = 0; tt < TOK; tt++)
+#pragma unroll
+        for (int j = 0; j < DPT; j++) pe[tt][j] = ldexpf(1.0f, eexp[tt][j]);
     // 2. tiles: tile tl + NB - 1 into the buffer tile tl - 1 used, wait for
     // tile tl, MFMAs, row partials
     uint32_t buf = 0;
@@ -332,23 +351,22 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
         typename Q::Raw raw;
         Q::load(raw, L + (tl % NB) * G::BUF, roff, kg);
         const float d = h2f(raw.hdr.x), dmin = h2f(raw.hdr.x >> 16);
+        uint32_t scb[2], mnb[2];
+        sk_scale_bytes(raw.hdr.y, raw.hdr.z, raw.hdr.w, scb, mnb);
         // min term B operand: mn of sub-blocks 4 kg .. 4 kg + 3 (k-groups 2, 3 padding)
-        f16x4s bmin;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t sc_, mn_;
-            scale_min_k4(min(4 * kg + i, 7u), raw.hdr.y, raw.hdr.z, raw.hdr.w, sc_, mn_);
-            bmin[i] = kg < 2 ? (_Float16)(float)mn_ : (_Float16)0.0f;
-        }
+        const uint32_t mk = kg == 0 ? mnb[0] : mnb[1];
+        const f16x2s m01 = sk_bits(__builtin_amdgcn_perm(0x64646464u, mk, 0x04010400u)) - f16x2s{(_Float16)1024.0f, (_Float16)1024.0f};
+        const f16x2s m23 = sk_bits(__builtin_amdgcn_perm(0x64646464u, mk, 0x04030402u)) - f16x2s{(_Float16)1024.0f, (_Float16)1024.0f};
+        const f16x4s bmin = kg < 2 ? f16x4s{m01[0], m01[1], m23[0], m23[1]} : f16x4s{(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
         f32x4 acc[TOK], accm[TOK];
 #pragma unroll
         for (int tt = 0; tt < TOK; tt++) acc[tt] = accm[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 8; s++) {
-            uint32_t sc, mn;
-            scale_min_k4(s, raw.hdr.y, raw.hdr.z, raw.hdr.w, sc, mn);
-            const _Float16 sch = (_Float16)(float)sc;
-            const f16x2s sc2 = {sch, sch}, nb2 = {(_Float16)(-1024.0f * (float)sc), (_Float16)(-1024.0f * (float)sc)};
+            // {sc_s, sc_s} exactly: byte s under the exponent of 1024, minus 1024
+            const f16x2s sc2 = sk_bits(__builtin_amdgcn_perm(0x64646464u, scb[s >> 2], 0x04000400u + 0x00010001u * (s & 3))) -
+                               f16x2s{(_Float16)1024.0f, (_Float16)1024.0f};
+            const f16x2s nb2 = sc2 * f16x2s{(_Float16)-1024.0f, (_Float16)-1024.0f};
             uint32_t v0, v1, b[4];
             Q::quants(raw, s, v0, v1);
             sk_scale4(v0, sc2, nb2, b[0], b[1]);
@@ -368,7 +386,7 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
             for (int j = 0; j < DPT; j++) {
                 const float sv = HILO ? acc[tt][2 * j] + acc[tt][2 * j + 1] : acc[tt][j];
                 const float sm = HILO ? accm[tt][2 * j] + accm[tt][2 * j + 1] : accm[tt][j];
-                const float v = ldexpf(d, eexp[tt][j]) * sv - ldexpf(dmin, eexp[tt][j] + 5) * sm;
+                const float v = pe[tt][j] * fmaf(d, sv, -(32.0f * dmin) * sm);
                 const uint32_t tok = tt * TPT + (HILO ? 2 * kg + j : 4 * kg + j);
                 pp[tok * 16] = v;
             }
