@@ -89,6 +89,38 @@ __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s
     mn = ((v >> (8u - 4u * h)) & 15u) | (((v >> (12u + 2u * h)) & 3u) << 4);
 }
 
+// The 6-bit scales (sc) and mins (mn) of sub-blocks 0..3 (index 0) and 4..7
+// (index 1) as the four bytes of a dword each, from the 12 packed bytes in y,
+// z, w (bytes 4..15 of a Q4_K / Q5_K block): the get_scale_min step of
+// phi4.rs:492-498 for every j at once.  j < 4: sc = q[j] & 63, mn = q[j+4] &
+// 63; j >= 4: sc = (q[j+4] & 15) | (q[j-4] >> 6) << 4, mn = (q[j+4] >> 4) |
+// (q[j] >> 6) << 4.  The shifts by 2 move bits 6..7 of each byte to bits 4..5;
+// the 0x30 mask drops what the next byte shifts in.
+__device__ __forceinline__ void scale_min_bytes_k4(uint32_t y, uint32_t z, uint32_t w, uint32_t (&sc)[2],
+                                                   uint32_t (&mn)[2])
+{
+    sc[0] = y & 0x3F3F3F3Fu;
+    mn[0] = z & 0x3F3F3F3Fu;
+    sc[1] = (w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u);
+    mn[1] = ((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u);
+}
+
+// Scale / min pairs of sub-blocks 2g and 2g + 1 (g = 0..3) from the packed
+// bytes: the four 6-bit scales (mins) of sub-blocks 0..3 are the bytes of
+// y & 0x3F3F3F3F (z & ...), those of 4..7 the low nibbles of w (its high
+// nibbles) with bits 6..7 of the bytes of y (z) on top.
+__device__ __forceinline__ void scale_min_pair_k4(uint32_t g, uint32_t y, uint32_t z, uint32_t w, uint32_t &s0,
+                                                  uint32_t &m0, uint32_t &s1, uint32_t &m1)
+{
+    const uint32_t scw = g < 2 ? y & 0x3F3F3F3Fu : (w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u);
+    const uint32_t mnw = g < 2 ? z & 0x3F3F3F3Fu : ((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u);
+    const uint32_t sh = 16u * (g & 1u);
+    s0 = (scw >> sh) & 0xFFu;
+    s1 = (scw >> (sh + 8u)) & 0xFFu;
+    m0 = (mnw >> sh) & 0xFFu;
+    m1 = (mnw >> (sh + 8u)) & 0xFFu;
+}
+
 // The values of v in lane (lane & ~X) and in lane (lane | X), X = 16 or 32,
 // by the gfx950 lane swaps (VALU, no LDS round trip): v_permlane16_swap
 // exchanges the odd 16-lane rows of its first operand with the even rows of

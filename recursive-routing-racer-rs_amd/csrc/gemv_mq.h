@@ -75,8 +75,7 @@ struct MqQ4K {
         d = h2f(w.hdr.x);
         dmin = h2f(w.hdr.x >> 16);
         uint32_t s0, m0, s1, m1;
-        scale_min_k4(2 * g, w.hdr.y, w.hdr.z, w.hdr.w, s0, m0);
-        scale_min_k4(2 * g + 1, w.hdr.y, w.hdr.z, w.hdr.w, s1, m1);
+        scale_min_pair_k4(g, w.hdr.y, w.hdr.z, w.hdr.w, s0, m0, s1, m1);
         sc[0] = sc[1] = (float)s0;
         sc[2] = sc[3] = (float)s1;
         mn[0] = mn[1] = (float)m0;
@@ -110,8 +109,7 @@ struct MqQ5K {
         d = h2f(w.hdr.x);
         dmin = h2f(w.hdr.x >> 16);
         uint32_t s0, m0, s1, m1;
-        scale_min_k4(2 * g, w.hdr.y, w.hdr.z, w.hdr.w, s0, m0);
-        scale_min_k4(2 * g + 1, w.hdr.y, w.hdr.z, w.hdr.w, s1, m1);
+        scale_min_pair_k4(g, w.hdr.y, w.hdr.z, w.hdr.w, s0, m0, s1, m1);
         sc[0] = sc[1] = (float)s0;
         sc[2] = sc[3] = (float)s1;
         mn[0] = mn[1] = (float)m0;

@@ -67,19 +67,6 @@ __device__ __forceinline__ void sk_scale4(uint32_t v, f16x2s sc2, f16x2s nb2, ui
     o23 = sk_u32(__builtin_elementwise_fma(sk_bits(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u)), sc2, nb2));
 }
 
-// The 6-bit scales (sc) and mins (mn) of sub-blocks 0..3 and 4..7 as four
-// bytes each, from the 12 packed bytes in y, z, w (bytes 4..15 of a Q4_K /
-// Q5_K block; the get_scale_min step of phi4.rs:492-498 for all j at once):
-// j < 4: sc = q[j] & 63, mn = q[j+4] & 63; j >= 4: sc = (q[j+4] & 15) |
-// (q[j-4] >> 6) << 4, mn = (q[j+4] >> 4) | (q[j] >> 6) << 4.
-__device__ __forceinline__ void sk_scale_bytes(uint32_t y, uint32_t z, uint32_t w, uint32_t (&sc)[2], uint32_t (&mn)[2])
-{
-    sc[0] = y & 0x3F3F3F3Fu;
-    mn[0] = z & 0x3F3F3F3Fu;
-    sc[1] = (w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u);
-    mn[1] = ((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u);
-}
-
 // Q4_K (phi4.rs:481-510): element 32s + e of a block is nibble (s & 1) of
 // qs[32 (s/2) + e].  Lane k-group kg takes e = 8kg .. 8kg+7 of every s.
 struct SkQ4K {
@@ -352,7 +339,7 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
         Q::load(raw, L + (tl % NB) * G::BUF, roff, kg);
         const float d = h2f(raw.hdr.x), dmin = h2f(raw.hdr.x >> 16);
         uint32_t scb[2], mnb[2];
-        sk_scale_bytes(raw.hdr.y, raw.hdr.z, raw.hdr.w, scb, mnb);
+        scale_min_bytes_k4(raw.hdr.y, raw.hdr.z, raw.hdr.w, scb, mnb);
         // min term B operand: mn of sub-blocks 4 kg .. 4 kg + 3 (k-groups 2, 3 padding)
         const uint32_t mk = kg == 0 ? mnb[0] : mnb[1];
         const f16x2s m01 = sk_bits(__builtin_amdgcn_perm(0x64646464u, mk, 0x04010400u)) - f16x2s{(_Float16)1024.0f, (_Float16)1024.0f};
