@@ -366,6 +366,16 @@ int rrr_gemv_residual(rrr_ctx *ctx, const rrr_buf *x, uint32_t act_kind, uint32_
 int rrr_logits_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps,
                        const rrr_buf *E, rrr_buf *logits, uint32_t K, uint32_t V, uint32_t layout,
                        uint32_t chunk);
+/* rrr_logits_rmsnorm, then the index of the largest logit as rrr_argmax_f32
+ * defines it (first on ties, NaN never wins), written as a u32 to out_index:
+ * the final logits dispatches (phi4.rs:1049-1064) and the host argmax over
+ * the mapped chunks (phi4.rs:1172-1183) in one call.  On the transposed-chunk
+ * layout the argmax runs inside the logits launch (the last workgroup of each
+ * 256-entry slab reduces the slab, the last slab reduces the slabs); the
+ * logits are bit-identical to rrr_logits_rmsnorm's. */
+int rrr_logits_rmsnorm_argmax(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps,
+                              const rrr_buf *E, rrr_buf *logits, uint32_t K, uint32_t V,
+                              uint32_t layout, uint32_t chunk, rrr_buf *out_index);
 
 /* ---- name-keyed dispatch shim ---------------------------------------- */
 

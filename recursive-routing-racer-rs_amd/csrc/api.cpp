@@ -640,12 +640,23 @@ int rrr_residual_add(rrr_ctx *ctx, const rrr_buf *a, const rrr_buf *b, rrr_buf *
 }
 
 static int logits_common(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps, const rrr_buf *E,
-                         rrr_buf *y, uint32_t K, uint32_t V, uint32_t layout, uint32_t chunk, const char *what)
+                         rrr_buf *y, uint32_t K, uint32_t V, uint32_t layout, uint32_t chunk, const char *what,
+                         rrr_buf *index = nullptr)
 {
     TRY(check_buf(ctx, x, what));
     TRY(check_buf(ctx, E, what));
     TRY(check_buf(ctx, y, what));
     if (gamma) TRY(check_buf(ctx, gamma, what));
+    if (index) {
+        TRY(check_buf(ctx, index, what));
+        TRY(need(index, 4, what));
+    }
+    uint32_t *token = index ? (uint32_t *)index->ptr : nullptr;
+    // the logits, then (forms without the fused argmax) the argmax launch
+    auto then_argmax = [&](hipError_t e) {
+        if (e == hipSuccess && token) e = launch_argmax((const float *)y->ptr, V, ctx->scratch, token, ctx->stream);
+        return e;
+    };
     if (K == 0 || V == 0) return fail(RRR_ERR_BAD_SHAPE, "%s: K and V must be positive", what);
     if (layout > RRR_LOGITS_Q6K) return fail(RRR_ERR_INVALID_ARG, "%s: layout %u", what, layout);
     if (gamma && !(std::isfinite(eps) && eps >= 0.0f)) return fail(RRR_ERR_INVALID_ARG, "%s: eps", what);
@@ -672,7 +683,7 @@ static int logits_common(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, f
         a.K = K;
         a.N = V;
         a.M = 1;
-        return finish(ctx, launch_gemv(a, gamma ? ACT_RMSNORM : ACT_PLAIN, ctx->stream), what);
+        return finish(ctx, then_argmax(launch_gemv(a, gamma ? ACT_RMSNORM : ACT_PLAIN, ctx->stream)), what);
     }
     if (chunk == 0) return fail(RRR_ERR_INVALID_ARG, "%s: chunk must be positive", what);
     if (chunk % 256 && chunk < V) return fail(RRR_ERR_UNSUPPORTED, "%s: chunk=%u must be a multiple of 256", what, chunk);
@@ -684,11 +695,11 @@ static int logits_common(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, f
     const float *g = gamma ? (const float *)gamma->ptr : nullptr;
     if (logits_split_supported(K, V, (uint32_t)cn, GEMM_WS_BYTES))
         return finish(ctx, launch_logits_split((const float *)x->ptr, g, eps, (const float *)E->ptr, (float *)y->ptr, K, V,
-                                               (uint32_t)cn, (float *)ctx->gemm_ws, (uint32_t *)ctx->logits_cnt,
+                                               (uint32_t)cn, (float *)ctx->gemm_ws, (uint32_t *)ctx->logits_cnt, token,
                                                ctx->stream),
                       what);
-    return finish(ctx, launch_logits_chunked((const float *)x->ptr, g, eps, (const float *)E->ptr, (float *)y->ptr, K, V,
-                                             (uint32_t)cn, ctx->stream),
+    return finish(ctx, then_argmax(launch_logits_chunked((const float *)x->ptr, g, eps, (const float *)E->ptr,
+                                                         (float *)y->ptr, K, V, (uint32_t)cn, ctx->stream)),
                   what);
 }
 
@@ -705,6 +716,17 @@ int rrr_logits_rmsnorm(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, flo
     TRY(check_ctx(ctx));
     if (!gamma) return fail(RRR_ERR_NULL, "rrr_logits_rmsnorm: null gamma");
     return logits_common(ctx, x, gamma, eps, E, logits, K, V, layout, chunk, "rrr_logits_rmsnorm");
+}
+
+int rrr_logits_rmsnorm_argmax(rrr_ctx *ctx, const rrr_buf *x, const rrr_buf *gamma, float eps, const rrr_buf *E,
+                              rrr_buf *logits, uint32_t K, uint32_t V, uint32_t layout, uint32_t chunk,
+                              rrr_buf *out_index)
+{
+    TRY(check_ctx(ctx));
+    const char *what = "rrr_logits_rmsnorm_argmax";
+    if (!gamma) return fail(RRR_ERR_NULL, "%s: null gamma", what);
+    if (!out_index) return fail(RRR_ERR_NULL, "%s: null out_index", what);
+    return logits_common(ctx, x, gamma, eps, E, logits, K, V, layout, chunk, what, out_index);
 }
 
 int rrr_argmax_f32(rrr_ctx *ctx, const rrr_buf *logits, uint32_t V, rrr_buf *out_index)

@@ -78,14 +78,16 @@ hipError_t launch_fill_u32(uint32_t *p, uint64_t n_words, uint32_t v, hipStream_
 hipError_t launch_logits_chunked(const float *x, const float *gamma, float eps, const float *E,
                                  float *y, uint32_t K, uint32_t V, uint32_t chunk, hipStream_t s);
 // Split-K transposed-chunk logits (K % 32 == 0, chunk % 256 == 0): `part`
-// holds 8 V floats, `counters` logits_counter_bytes() zeroed once before the
-// first call (they return to zero after every call; calls on one counter area
-// must not overlap).
+// holds 8 V floats and the slab candidates of the argmax, `counters`
+// logits_counter_bytes() zeroed once before the first call (they return to
+// zero after every call; calls on one counter area must not overlap).
+// token != nullptr: the argmax of the logits is written there too.
 constexpr uint32_t LOGITS_MAX_SLABS = 4096;
 uint64_t logits_counter_bytes();
 bool logits_split_supported(uint32_t K, uint32_t V, uint32_t chunk, uint64_t ws_bytes);
 hipError_t launch_logits_split(const float *x, const float *gamma, float eps, const float *E, float *y, uint32_t K,
-                               uint32_t V, uint32_t chunk, float *part, uint32_t *counters, hipStream_t s);
+                               uint32_t V, uint32_t chunk, float *part, uint32_t *counters, uint32_t *token,
+                               hipStream_t s);
 // Argmax: `partials` holds at least argmax_partials_bytes() bytes.
 uint64_t argmax_partials_bytes();
 hipError_t launch_argmax(const float *v, uint32_t n, void *partials, uint32_t *out, hipStream_t s);

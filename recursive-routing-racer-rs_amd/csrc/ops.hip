@@ -462,6 +462,42 @@ hipError_t launch_logits_chunked(const float *x, const float *gamma, float eps, 
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Argmax with the semantics of the sequential loop at phi4.rs:1172-1183:
+// start from (value -inf, index 0), replace only on strictly greater, so the
+// first maximal index wins and NaN never wins.  Pass 1: one candidate per
+// workgroup; pass 2: one workgroup reduces the candidates in index order.
+struct Cand { float v; uint32_t i; };
+
+__device__ __forceinline__ Cand better(Cand a, Cand b)
+{
+    // a precedes b in index order whenever both are live candidates
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+
+__device__ __forceinline__ Cand wave_best(Cand c)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        Cand d;
+        d.v = __shfl_xor(c.v, o, 64);
+        d.i = __shfl_xor(c.i, o, 64);
+        c = better(c, d);
+    }
+    return c;
+}
+
+__device__ Cand block_best(Cand c, Cand *sm)
+{
+    c = wave_best(c);
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = c;
+    __syncthreads();
+    Cand r = sm[0];
+    for (int w = 1; w < 4; w++) r = better(r, sm[w]);
+    return r;
+}
+
 // Split-K form of the transposed-chunk logits.  Workgroup (slab, h) takes
 // the 256 vocab entries of one slab of a chunk and rows [h*K/NS, (h+1)*K/NS)
 // of the chunk's [d][n] matrix, i.e. row pieces of 1 KB: lane l of a wave
@@ -473,16 +509,20 @@ hipError_t launch_logits_chunked(const float *x, const float *gamma, float eps, 
 // written through to the coherent level; the last workgroup of the slab to
 // arrive (an agent-scope counter, reset by that workgroup for the next call)
 // adds them in order h = 0, 1, ..., NS-1 and writes the logits.
+// AM: that workgroup also reduces its 256 logits to the slab's (max, first
+// index), writes it through to the coherent level and counts on one more
+// counter; the last slab to arrive reduces the slabs' candidates in index
+// order (the argmax rule above) and writes the token.
 constexpr uint32_t LOGITS_SPLITS = 8, LOGITS_SLAB = 256, LOGITS_COUNTER_STRIDE = 64, LOGITS_U = 8;
 // scalar+vector offset past every chunk byte (a chunk is below 2 GiB on this
 // path): such loads return zeros and move no data
 constexpr uint32_t MQ_OOB_LOGITS = 0x80000000u;
 
-template <int U>
+template <int U, bool AM>
 __global__ __launch_bounds__(256) void logits_split_kernel(const float *__restrict__ x, const float *__restrict__ gamma,
                                                            float eps, const float *__restrict__ E, float *__restrict__ y,
                                                            uint32_t K, uint32_t V, uint32_t chunk, float *part,
-                                                           uint32_t *counters)
+                                                           uint32_t *counters, Cand *cand, uint32_t *token)
 {
     constexpr uint32_t NS = LOGITS_SPLITS;
     extern __shared__ float sm[];
@@ -491,6 +531,7 @@ __global__ __launch_bounds__(256) void logits_split_kernel(const float *__restri
     float *wsum = xs + Dr;          // 4 waves x 256 entries
     float *red = wsum + 4 * 256;    // 16
     __shared__ uint32_t last;
+    __shared__ Cand amsm[4];
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t sb = blockIdx.x / NS, h = blockIdx.x % NS;
     const uint32_t spc = chunk / LOGITS_SLAB;                 // slabs per full chunk
@@ -550,20 +591,51 @@ __global__ __launch_bounds__(256) void logits_split_kernel(const float *__restri
                                       __HIP_MEMORY_SCOPE_AGENT) == NS - 1;
     __syncthreads();
     if (!last) return;
+    float r = -__builtin_inff();
     if (live) {
         float q[NS];
 #pragma unroll
         for (uint32_t k = 0; k < NS; k++)
             q[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, 4 * (k * V + v), 0, RRR_CPOL_SC1));
-        float r = q[0];
+        r = q[0];
 #pragma unroll
         for (uint32_t k = 1; k < NS; k++) r = r + q[k];
         y[v] = r;
     }
     if (t == 0) __hip_atomic_store(counters + sb * LOGITS_COUNTER_STRIDE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (AM) {
+        const uint32_t slabs = gridDim.x / NS;
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(cand, (uint64_t)slabs * sizeof(Cand));
+        Cand c = {-__builtin_inff(), 0u};
+        if (live && r > c.v) c = Cand{r, v};   // NaN and -inf never win
+        c = block_best(c, amsm);
+        if (t == 0) {
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(c.v), c.i}, rc, 8 * sb, 0, RRR_CPOL_SC1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            last = __hip_atomic_fetch_add(counters + LOGITS_MAX_SLABS * LOGITS_COUNTER_STRIDE, 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == slabs - 1;
+        }
+        __syncthreads();
+        if (!last) return;
+        Cand b = {-__builtin_inff(), 0u};
+        for (uint32_t i = t; i < slabs; i += 256) {
+            const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(rc, 8 * i, 0, RRR_CPOL_SC1);
+            b = better(b, Cand{__uint_as_float(u.x), u.y});
+        }
+        b = block_best(b, amsm);
+        if (t == 0) {
+            token[0] = b.i;
+            __hip_atomic_store(counters + LOGITS_MAX_SLABS * LOGITS_COUNTER_STRIDE, 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
-uint64_t logits_counter_bytes() { return (uint64_t)LOGITS_MAX_SLABS * LOGITS_COUNTER_STRIDE * 4; }
+// one counter line per slab, then the argmax counter's line
+uint64_t logits_counter_bytes() { return (uint64_t)(LOGITS_MAX_SLABS + 1) * LOGITS_COUNTER_STRIDE * 4; }
+
+// the slab candidates follow the split partials in the workspace
+static uint64_t logits_cand_offset(uint32_t V) { return ((uint64_t)LOGITS_SPLITS * V * 4 + 255) & ~255ull; }
 
 bool logits_split_supported(uint32_t K, uint32_t V, uint32_t chunk, uint64_t ws_bytes)
 {
@@ -571,54 +643,24 @@ bool logits_split_supported(uint32_t K, uint32_t V, uint32_t chunk, uint64_t ws_
     if ((uint64_t)(chunk < V ? chunk : V) * K * 4 >= MQ_OOB_LOGITS) return false;
     uint64_t slabs = 0;
     for (uint64_t c0 = 0; c0 < V; c0 += chunk) slabs += ((V - c0 < chunk ? V - c0 : chunk) + LOGITS_SLAB - 1) / LOGITS_SLAB;
-    return slabs <= LOGITS_MAX_SLABS && (uint64_t)LOGITS_SPLITS * V * 4 <= ws_bytes;
+    return slabs <= LOGITS_MAX_SLABS && logits_cand_offset(V) + slabs * sizeof(Cand) <= ws_bytes;
 }
 
 hipError_t launch_logits_split(const float *x, const float *gamma, float eps, const float *E, float *y, uint32_t K,
-                               uint32_t V, uint32_t chunk, float *part, uint32_t *counters, hipStream_t s)
+                               uint32_t V, uint32_t chunk, float *part, uint32_t *counters, uint32_t *token,
+                               hipStream_t s)
 {
     uint32_t slabs = 0;
     for (uint32_t c0 = 0; c0 < V; c0 += chunk) slabs += ((V - c0 < chunk ? V - c0 : chunk) + LOGITS_SLAB - 1) / LOGITS_SLAB;
     const size_t lds = ((size_t)K / LOGITS_SPLITS + 4 * 256 + 16) * sizeof(float);
-    hipLaunchKernelGGL(logits_split_kernel<LOGITS_U>, dim3(slabs * LOGITS_SPLITS), dim3(256), lds, s, x, gamma, eps, E, y, K, V,
-                       chunk, part, counters);
+    Cand *cand = (Cand *)((uint8_t *)part + logits_cand_offset(V));
+    if (token)
+        hipLaunchKernelGGL((logits_split_kernel<LOGITS_U, true>), dim3(slabs * LOGITS_SPLITS), dim3(256), lds, s, x, gamma,
+                           eps, E, y, K, V, chunk, part, counters, cand, token);
+    else
+        hipLaunchKernelGGL((logits_split_kernel<LOGITS_U, false>), dim3(slabs * LOGITS_SPLITS), dim3(256), lds, s, x,
+                           gamma, eps, E, y, K, V, chunk, part, counters, cand, token);
     return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// Argmax with the semantics of the sequential loop at phi4.rs:1172-1183:
-// start from (value -inf, index 0), replace only on strictly greater, so the
-// first maximal index wins and NaN never wins.  Pass 1: one candidate per
-// workgroup; pass 2: one workgroup reduces the candidates in index order.
-struct Cand { float v; uint32_t i; };
-
-__device__ __forceinline__ Cand better(Cand a, Cand b)
-{
-    // a precedes b in index order whenever both are live candidates
-    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
-    return a;
-}
-
-__device__ __forceinline__ Cand wave_best(Cand c)
-{
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        Cand d;
-        d.v = __shfl_xor(c.v, o, 64);
-        d.i = __shfl_xor(c.i, o, 64);
-        c = better(c, d);
-    }
-    return c;
-}
-
-__device__ Cand block_best(Cand c, Cand *sm)
-{
-    c = wave_best(c);
-    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = c;
-    __syncthreads();
-    Cand r = sm[0];
-    for (int w = 1; w < 4; w++) r = better(r, sm[w]);
-    return r;
 }
 
 constexpr uint32_t ARGMAX_WG = 1024;

@@ -89,6 +89,7 @@ SIGNATURES = {
     "rrr_gemv_rmsnorm_silu": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, u32, c_buf_p, u32, u32]),
     "rrr_gemv_residual": (i32, [c_ctx_p, c_buf_p, u32, u32, c_buf_p, u32, c_buf_p, u32, u32]),
     "rrr_logits_rmsnorm": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, c_buf_p, u32, u32, u32, u32]),
+    "rrr_logits_rmsnorm_argmax": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, c_buf_p, u32, u32, u32, u32, c_buf_p]),
     "rrr_rope_kv_store": (i32, [c_ctx_p, c_buf_p, c_buf_p, u32, c_buf_p, c_buf_p, u32, u32, u32, u32, u32, u32, u32,
                                 f32, f32]),
     "rrr_gemv_rmsnorm_rope_kv": (i32, [c_ctx_p, c_buf_p, c_buf_p, f32, c_buf_p, u32, c_buf_p, u32, c_buf_p, u32,

@@ -418,15 +418,15 @@ class DecodeSweep:
 
     def record_logits(self):
         """Final RMSNorm + logits (F32 chunks or raw Q6_K rows, by
-        logits_mode) + argmax."""
+        logits_mode) + argmax, one call (on the F32 chunks the argmax runs
+        inside the logits launch)."""
         c, s = self.ctx, self.shape
         if self.logits_mode == "q6k":
-            c.logits_rmsnorm(self.hidden, self.out_norm, s.eps, self.emb_q6k, self.logits, s.d_model, s.vocab,
-                             E.LOGITS_Q6K, 0)
+            c.logits_rmsnorm_argmax(self.hidden, self.out_norm, s.eps, self.emb_q6k, self.logits, s.d_model, s.vocab,
+                                    self.token, E.LOGITS_Q6K, 0)
         else:
-            c.logits_rmsnorm(self.hidden, self.out_norm, s.eps, self.emb, self.logits, s.d_model, s.vocab,
-                             E.LOGITS_CHUNKED, s.chunk)
-        c.argmax_f32(self.logits, s.vocab, self.token)
+            c.logits_rmsnorm_argmax(self.hidden, self.out_norm, s.eps, self.emb, self.logits, s.d_model, s.vocab,
+                                    self.token, E.LOGITS_CHUNKED, s.chunk)
 
     # ---- prefill: the prompt's tokens through every layer at once ----------
     @staticmethod

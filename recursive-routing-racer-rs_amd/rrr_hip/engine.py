@@ -199,6 +199,11 @@ class Context:
     def logits_rmsnorm(self, x, gamma, eps, E, y, K, V, layout=LOGITS_ROWS, chunk=8192):
         _check(self.lib.rrr_logits_rmsnorm(self._h, x._h, gamma._h, eps, E._h, y._h, K, V, layout, chunk))
 
+    def logits_rmsnorm_argmax(self, x, gamma, eps, E, y, K, V, index, layout=LOGITS_ROWS, chunk=8192):
+        """rrr_logits_rmsnorm plus the argmax of the logits into `index` (u32)."""
+        _check(self.lib.rrr_logits_rmsnorm_argmax(self._h, x._h, gamma._h, eps, E._h, y._h, K, V, layout, chunk,
+                                                   index._h))
+
     def rope_kv_store(self, qkv, rope_factors, n_factors, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim,
                       rope_dim, q_dim, kv_stride, theta=10000.0, attn_factor=1.190238):
         _check(self.lib.rrr_rope_kv_store(self._h, qkv._h, rope_factors._h if rope_factors is not None else None,

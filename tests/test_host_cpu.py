@@ -198,6 +198,19 @@ def test_elementwise_and_logits_validation(vctx):
     out = vctx.alloc(4)
     assert code_of(vctx.argmax_f32, lg, V, out) == ERR_NO_DEVICE
     assert code_of(vctx.argmax_f32, lg, V + 1, out) == ERR_SHORT_BUFFER
+    # the logits with their argmax in one call: the logits' checks plus the index buffer
+    gk = vctx.alloc(K * 4)
+    assert code_of(vctx.logits_rmsnorm_argmax, xk, gk, 1e-5, E, lg, K, V, out, rrr_hip.LOGITS_ROWS) == ERR_NO_DEVICE
+    assert code_of(vctx.logits_rmsnorm_argmax, xk, gk, 1e-5, E, lg, K, V, out, rrr_hip.LOGITS_CHUNKED, 256) == \
+        ERR_NO_DEVICE
+    assert code_of(vctx.logits_rmsnorm_argmax, xk, gk, 1e-5, E, lg, K, V + 1, out, rrr_hip.LOGITS_ROWS) == \
+        ERR_SHORT_BUFFER
+    short = vctx.alloc(2)
+    assert code_of(vctx.logits_rmsnorm_argmax, xk, gk, 1e-5, E, lg, K, V, short, rrr_hip.LOGITS_ROWS) == \
+        ERR_SHORT_BUFFER
+    lib = _lib.hip()
+    assert lib.rrr_logits_rmsnorm_argmax(vctx._h, xk._h, gk._h, 1e-5, E._h, lg._h, K, V, rrr_hip.LOGITS_ROWS, 0,
+                                         None) == ERR_NULL
 
 
 def test_fused_validation(vctx):
