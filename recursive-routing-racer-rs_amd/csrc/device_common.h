@@ -54,6 +54,40 @@ __device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t of
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }
 
+// 16-byte LDS DMA load: lane l's 16 bytes at `voff + soff` go to LDS
+// dst + 16 l (dst wave-uniform; out-of-range lanes write zeros).  Only the
+// device pass sees the builtin (the host pass would otherwise drop the
+// kernels' launch stubs).
+template <int CPOL>
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, void *dst, uint32_t voff, uint32_t soff)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16, voff, soff, 0,
+                                             CPOL);
+#endif
+}
+
+// Wait until at most N vector memory operations of this wave are in flight
+// (they retire in order).  The compiler does not track LDS DMA, so LDS reads
+// of DMA-written data wait here (and, for other waves, behind a barrier
+// after it); the memory clobber keeps them after the wait.
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier that waits for this wave's LDS (and scalar) operations
+// only.  __syncthreads' release fence also waits for every vector memory
+// operation once LDS DMA is in flight, which would wait out DMA issued for a
+// later step; the memory clobber keeps the compiler's memory accesses on
+// their side of the barrier.
+__device__ __forceinline__ void barrier_lds()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // IEEE binary16 -> binary32 (exact; v_cvt_f32_f16).
 __device__ __forceinline__ float h2f(uint32_t bits16)
 {

@@ -1,25 +1,24 @@
 // gemm.hip -- prefill dequant-GEMM: Y[M][N] = X[M][K] . W[N][K]^T (or Y +=, the
-// residual of the layer folded in) with X in bf16 or f16 and W in raw Q4_K /
-// Q5_K / Q6_K super-blocks (the batched shape of phi4.rs:1257-1268 at prompt
-// length; the reference has no MFMA kernel for it).
+// residual of the layer folded in) with X in f16 (bf16 activations are
+// converted to f16 rows once per call, below) and W in raw Q4_K / Q5_K / Q6_K
+// super-blocks (the batched shape of phi4.rs:1257-1268 at prompt length; the
+// reference has no MFMA kernel for it).
 //
 // Workgroup: 512 threads.  Waves 0-3 (2 x 2) each own a (BM/2) x (BN/2)
-// block of 16x16 v_mfma_f32_16x16x32_f16 tiles with fp32 accumulators (lane
-// l: A row l%16 and B column l%16 at k-group l/16, 8 f16 each; D rows
-// 4*(l/16)+r of column l%16 in register r).  Waves 4-7 stage the operands.
+// block of 32x32 v_mfma_f32_32x32x16_f16 tiles with fp32 accumulators, and
+// load X: 16-byte LDS DMA straight from global memory, GEMM_NA - 1 steps
+// ahead, into a ring of GEMM_NA X buffers.  Waves 4-7 stage the weights.
 //
-// K steps of BK elements.  Per step each staging thread dequantizes
-// 32 elements (two runs of 16) of one weight row into an fp16 LDS tile
-// and converts BM*BK/256 elements of X from bf16 to fp16 (exact for |x| in
-// f16's normal range; f16 X is copied as it is).  The dequant runs in packed fp16: v_perm places
-// each quant byte q under the exponent of 1024 (f16 0x64qq = 1024 + q), an
-// exact v_pk_add removes the 1024 (1056 for Q6_K's offset), and one
-// v_pk_fma / v_pk_mul applies the sub-block scale and min (phi4.rs:444-542:
-// w = d*sc*q - dmin*m, w = d*sc*(q - 32)) with one rounding to fp16; fp16
-// weights keep the product error near 2^-11 per weight (bf16 would be 2^-8).
-// LDS is double-buffered: step s+1 is staged while the MFMA waves work on
-// step s; a ring of three register sets keeps the loads of steps s+2 .. s+4
-// in flight.
+// K steps of BK elements.  Per step each staging thread dequantizes 32
+// elements (two runs of 16) of one weight row into an fp16 LDS tile.  The
+// dequant runs in packed fp16: v_perm places each quant byte q under the
+// exponent of 1024 (f16 0x64qq = 1024 + q), an exact v_pk_add removes the 1024
+// (1056 for Q6_K's offset), and one v_pk_fma / v_pk_mul applies the sub-block
+// scale and min (phi4.rs:444-542: w = d*sc*q - dmin*m, w = d*sc*(q - 32)) with
+// one rounding to fp16; fp16 weights keep the product error near 2^-11 per
+// weight (bf16 would be 2^-8).  The weight tile is double-buffered in LDS:
+// step s+1 is staged while the MFMA waves work on step s; a ring of four
+// register sets keeps the weight loads of the next three steps in flight.
 //
 // Tile order: the M/BM tiles of one N tile get workgroup ids congruent mod 8,
 // so they run on the same XCD and the weight tile is fetched from HBM once.
@@ -41,6 +40,14 @@ typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
 // Scalar offset past every input byte (the launcher requires smaller buffers):
 // loads of the step after the last return zeros and move no data.
 constexpr uint32_t GM_OOB = 0x80000000u;
+
+// X (A) buffers of the ring the MFMA waves load X into, GEMM_NA - 1 steps
+// ahead
+constexpr int GEMM_NA = 3;
+// LDS of a BM x BN tile with K steps of BK: GEMM_NA X buffers and two weight
+// (B) buffers, fp16
+template <int BM, int BN, int BK>
+constexpr size_t gemm_lds_bytes = (GEMM_NA * (size_t)BM + 2 * BN) * BK * 2;
 
 __device__ __forceinline__ uint32_t pk_f16(float a, float b)
 {
@@ -156,6 +163,8 @@ struct GqQ5K {
 template <int NP>
 struct GqQ6K {
     static constexpr uint32_t BS = 210;
+    // d: the block's last dword (scales 14, 15 and the f16 d in its high
+    // half), a 32-bit register with no 16-bit value to widen in the loop
     struct Raw { u32x4 ql[NP][2], qh[NP]; uint32_t sc, d; };
     __device__ static void load(Raw &r, __amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t blk, uint32_t c, uint32_t p0)
     {
@@ -168,12 +177,12 @@ struct GqQ6K {
             r.qh[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 128 + 32 * h6 + 16 * (p0 + k), blk, 0);
         }
         r.sc = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 192 + 4 * c, blk, 0);
-        r.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, voff + 208, blk, 0);
+        r.d = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + 206, blk, 0);
     }
     __device__ static void dequant(const Raw &r, uint32_t c, uint32_t p0, uint32_t *out)
     {
         const uint32_t hi = c & 1;
-        const float d = h2f(r.d);
+        const float d = h2f(r.d >> 16);
         const f16x2v K2 = {(_Float16)1056.0f, (_Float16)1056.0f};
 #pragma unroll
         for (int k = 0; k < NP; k++)
@@ -196,11 +205,30 @@ struct GqQ6K {
     }
 };
 
+// Every dword of v counts as used here, so the registers a load fills stay
+// reserved until this point.  Otherwise a dword the dequant never reads (a
+// Q4_K header's last word when the chunk's scales sit in the first two) is
+// dead from the load on, and the register allocator reuses its register for
+// a temporary right after the load issues: a write that must first wait for
+// that load to land.
+template <class T>
+__device__ __forceinline__ void keep_live(const T &v)
+{
+    constexpr int N = sizeof(T) / 4;
+    struct A {
+        uint32_t w[N];
+    };
+    const A a = __builtin_bit_cast(A, v);
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" ::"v"(a.w[i]));
+}
+
 // Warp-specialised form: waves 0-3 run the MFMAs of a BM x BN tile (2 x 2,
-// each (BM/2) x (BN/2)), waves 4-7 load, dequantize and convert the next step
-// into the other LDS buffer, so every SIMD holds one wave of each kind and the
-// staging VALU fills the matrix core's gaps.  Both roles pass one barrier per
-// step (plus one after the prologue) on separate straight-line paths.
+// each (BM/2) x (BN/2)) and send X into LDS by DMA, waves 4-7 load and
+// dequantize the next step's weights into the other LDS buffer, so every SIMD
+// holds one wave of each kind and the staging VALU fills the matrix core's
+// gaps.  Both roles pass one barrier per step (plus one after the prologue)
+// on separate straight-line paths.
 // silu_f(gate) * up of row block i (32 rows) of MFMA wave cw's 32 outputs of
 // tile nt into Y (M x F), the D layout of the 32x32 MFMAs (lane l: column
 // l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4 in register r)
@@ -239,16 +267,14 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     auto swz = [](uint32_t r) { return (r / RPL) % CPR; };
     constexpr int UE = BN * BK / 256, TPW = BK / UE;       // weight elements per producer thread, threads per row
     constexpr int NPW = UE / 32;                           // 32-element parts per producer thread
-    constexpr int XE = BM * BK / 256;                      // X elements per producer thread
-    constexpr int XC = BK / 8, XRS = 256 / XC;             // 16-byte chunks per X row and step, rows per pass
-    static_assert((UE == 32 || UE == 64) && XE % 8 == 0 && BK % 64 == 0, "tile shape");
+    static_assert((UE == 32 || UE == 64) && BK % 64 == 0, "tile shape");
     using Q = QT<NPW>;
-    // register sets of the producer's load ring: four (loads issued four
-    // steps ahead) where the registers allow it, else three
-    constexpr int NSET = (BK == 64 && Q::BS != 210) ? 4 : 3;
+    // register sets of the producer's load ring (loads issued four steps
+    // ahead, three sets in flight while one is staged)
+    constexpr int NSET = 4;
     extern __shared__ float smem[];
-    _Float16 *As = (_Float16 *)smem;                       // [2][BM][LDK]
-    _Float16 *Bs = As + 2 * BM * LDK;                      // [2][BN][LDK]
+    _Float16 *As = (_Float16 *)smem;                       // [GEMM_NA][BM][LDK]
+    _Float16 *Bs = As + GEMM_NA * BM * LDK;                // [2][BN][LDK]
 
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     // tile of this workgroup (same XCD for the M tiles of one N tile) and its
@@ -278,31 +304,22 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W, (uint64_t)N * B * Q::BS);
         const uint32_t wrow = SILU ? ((ur & 32u) ? N / 2 : 0u) + nt * (BN / 2) + (ur & 31u) + ((ur >> 6) << 5) : n0 + ur;
         const uint32_t wvoff = wrow * B * Q::BS;
-        // X: pass i covers rows XRS*i .. XRS*(i+1)-1 of the step, consecutive
-        // threads on consecutive 16-byte chunks of a row (whole cache lines per
-        // wave load)
-        const uint32_t xr = tp / XC, xk = 8 * (tp % XC);
-        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X, (uint64_t)M * K * 2);
-        const uint32_t xvoff = ((m0 + xr) * K + xk) * 2;
-        struct Set {
-            typename Q::Raw raw;
-            u32x4 xv[XE / 8];
-        };
-        Set S0, S1, S2, S3;
+        typename Q::Raw S0, S1, S2, S3;
         // element e0 of the step's unit inside its super-block: chunk e0/64, lane part e0%64
-        auto issue = [&](Set &st, uint32_t s) {
+        auto issue = [&](typename Q::Raw &st, uint32_t s) {
             const bool ok = s < nsteps;   // past the end: out-of-range offsets, zeros
             const uint32_t sg = s0 + s, e0 = (sg * BK) % 256 + lb;
-            Q::load(st.raw, wrs, wvoff, ok ? (sg * BK / 256) * Q::BS : GM_OOB, e0 >> 6, wp);
-            const uint32_t so = ok ? sg * BK * 2 : GM_OOB;
-#pragma unroll
-            for (int i = 0; i < XE / 8; i++)
-                st.xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvoff + XRS * i * K * 2, so, 0);
+            Q::load(st, wrs, wvoff, ok ? (sg * BK / 256) * Q::BS : GM_OOB, e0 >> 6, wp);
+            __builtin_amdgcn_sched_barrier(0);   // the sets' loads in program order
         };
-        auto stage = [&](const Set &st, uint32_t s) {
+        auto stage = [&](const typename Q::Raw &st, uint32_t s) {
+            // the dequant stays after the previous barrier: hoisted above
+            // it, it would wait for loads issued only a step earlier
+            __builtin_amdgcn_sched_barrier(0);
+            keep_live(st);
             const uint32_t buf = s & 1, e0 = ((s0 + s) * BK) % 256 + lb;
             uint32_t o[16 * NPW];
-            Q::dequant(st.raw, e0 >> 6, wp, o);
+            Q::dequant(st, e0 >> 6, wp, o);
             // part k: runs at chunks c0 + 2k + (0, 1) and c0 + 2k + (4, 5)
             _Float16 *dst = Bs + (buf * BN + ur) * LDK;
             const uint32_t c0 = (lb + 16 * wp) / 8, gu = swz(ur);
@@ -310,35 +327,34 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
             for (int i = 0; i < 4 * NPW; i++)
                 *(u32x4 *)(dst + 8 * ((c0 + 2 * (i >> 2) + (i & 1) + 4 * ((i >> 1) & 1)) ^ gu)) =
                     u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
-            _Float16 *xd = As + (buf * BM + xr) * LDK + 8 * ((xk / 8) ^ swz(xr));   // pass i: + XRS*i rows
-#pragma unroll
-            for (int i = 0; i < XE / 8; i++) *(u32x4 *)(xd + XRS * i * LDK) = st.xv[i];
         };
+        // Each stage finds the loads of the other NSET - 1 sets issued after
+        // its own, on the first pass as on every later one, so the compiler's
+        // wait before it lets those stay in flight (a prologue that staged
+        // step 0 and re-issued its set first would leave the loop-entry state
+        // differently ordered, and the merged wait covers nearly every load).
         issue(S0, 0);
         issue(S1, 1);
         issue(S2, 2);
-        if constexpr (NSET == 4) issue(S3, 3);
-        stage(S0, 0);
-        issue(S0, NSET);
-        __syncthreads();
-        // step s: stage s+1 (its set then takes the loads of s+1+NSET); steps
-        // past the end (nsteps rounded up to NSET) stage zeros
+        issue(S3, 3);
+        // stage s (its set then takes the loads of s+NSET) before barrier s;
+        // steps past the end (nsteps rounded up to NSET) stage zeros
         for (uint32_t s = 0; s < nsteps; s += NSET) {
+            stage(S0, s);
+            issue(S0, s + NSET);
+            __syncthreads();
             stage(S1, s + 1);
             issue(S1, s + 1 + NSET);
             __syncthreads();
             stage(S2, s + 2);
             issue(S2, s + 2 + NSET);
             __syncthreads();
-            if constexpr (NSET == 4) {
-                stage(S3, s + 3);
-                issue(S3, s + 3 + NSET);
-                __syncthreads();
-            }
-            stage(S0, s + NSET);
-            issue(S0, s + 2 * NSET);
+            stage(S3, s + 3);
+            issue(S3, s + 3 + NSET);
             __syncthreads();
         }
+        // the barrier that ends the MFMA waves' last step
+        __syncthreads();
         if constexpr (SILU) {
             // row blocks 2, 3 of MFMA wave t / 64 - 4, once it has handed them over
             __syncthreads();
@@ -381,10 +397,10 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     struct Frag {
         f16x8v a[UI], b[UJ];
     };
-    auto frag_load = [&](Frag &f, uint32_t buf, int kq) {
+    auto frag_load = [&](Frag &f, uint32_t abuf, uint32_t bbuf, int kq) {
         const uint32_t ch = 8 * (((fk / 8) + 2 * kq) ^ swz(fr));
-        const _Float16 *Ab = As + (buf * BM + wm * (BM / 2) + fr) * LDK + ch;
-        const _Float16 *Bb = Bs + (buf * BN + wn * (BN / 2) + fr) * LDK + ch;
+        const _Float16 *Ab = As + (abuf * BM + wm * (BM / 2) + fr) * LDK + ch;
+        const _Float16 *Bb = Bs + (bbuf * BN + wn * (BN / 2) + fr) * LDK + ch;
 #pragma unroll
         for (int i = 0; i < UI; i++) f.a[i] = *(const f16x8v *)(Ab + 32 * i * LDK);
 #pragma unroll
@@ -398,32 +414,70 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
     };
     constexpr int KQ = BK / 16;   // even
+    // X goes from global memory straight into LDS, issued by these waves
+    // (whose vector memory path is otherwise idle) NA - 1 steps ahead into a
+    // ring of NA A buffers: 16-byte LDS DMA, lane l of a load writing
+    // base + 16 l, so load i of wave w covers tile rows XRP (XI w + i) ..
+    // + XRP - 1, lane l row l / CPR and the chunk whose swizzled place is
+    // l % CPR.  Steps past nsteps load zeros (out-of-range offsets).
+    constexpr int NA = GEMM_NA, XRP = 512 / BK, XI = BM / (4 * XRP), XPQ = XI / (KQ / 2);
+    static_assert(XI * 4 * XRP == BM && XPQ * (KQ / 2) == XI && (NA - 2) * XI < 32 && NA >= 3 && NA <= 4,
+                  "X loads per wave and step");
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(X, (uint64_t)M * K * 2);
+    const uint32_t wu = __builtin_amdgcn_readfirstlane(wave);   // wave-uniform: LDS bases in scalar registers
+    auto x_dma = [&](uint32_t s, uint32_t abuf, int i) {
+        const uint32_t rb = XRP * (XI * wu + i), r = rb + lane / CPR;
+        const uint32_t voff = ((m0 + r) * K + 8 * ((lane % CPR) ^ swz(r))) * 2;
+        lds_dma16<0>(xrs, As + (abuf * BM + rb) * LDK, voff, s < nsteps ? (s0 + s) * BK * 2 : GM_OOB);
+    };
     // one barrier per step, as many steps as the producer stages (nsteps
-    // rounded up to NSET); the barrier of step s comes once this wave's reads
-    // of buffer s & 1 have landed, and the first slice of step s + 1 is read
-    // from the other buffer while the last slice of step s multiplies
+    // rounded up to NSET, at least NA - 1); the barrier of step s comes once this
+    // wave's reads of step s have landed and its X loads of step s + 1 have
+    // (those of the later steps stay in flight), and the first slice of step
+    // s + 1 is read while the last slice of step s multiplies
+    static_assert(NSET >= NA - 1, "the prologue's X steps exist");
     const uint32_t steps3 = (nsteps + NSET - 1) / NSET * NSET;
+#pragma unroll
+    for (int p = 0; p < NA - 1; p++)
+#pragma unroll
+        for (int i = 0; i < XI; i++) x_dma(p, p, i);
+    wait_vm<(NA - 2) * XI>();
     Frag f0, f1;
-    __syncthreads();
-    frag_load(f0, 0, 0);
+    barrier_lds();
+    frag_load(f0, 0, 0, 0);
+    uint32_t ca = 0;   // A buffer of step s (s % NA)
     for (uint32_t s = 0; s < steps3; s++) {
-        const uint32_t cur = s & 1;
+        const uint32_t cb = s & 1, na = ca == NA - 1 ? 0u : ca + 1, pa = ca == 0 ? NA - 1 : ca - 1;
+        const bool more = s + NA - 1 < steps3;
 #pragma unroll
         for (int kq = 0; kq < KQ; kq += 2) {
-            frag_load(f1, cur, kq + 1);
+            frag_load(f1, ca, cb, kq + 1);
             __builtin_amdgcn_sched_barrier(0);
             frag_mfma(f0);
             __builtin_amdgcn_sched_barrier(0);
+            // X of step s + NA - 1 into the buffer step s - 1 used
+            if (more) {
+#pragma unroll
+                for (int i = 0; i < XPQ; i++) x_dma(s + NA - 1, pa, XPQ * (kq / 2) + i);
+            }
             if (kq + 2 < KQ) {
-                frag_load(f0, cur, kq + 2);
+                frag_load(f0, ca, cb, kq + 2);
             } else {
-                __syncthreads();
-                frag_load(f0, cur ^ 1u, 0);   // past the last step: stale, unused
+                // X of steps s + 2 .. s + NA - 1 (those below steps3) stay in flight
+                if (more)
+                    wait_vm<(NA - 2) * XI>();
+                else if (NA == 4 && s + 2 < steps3)
+                    wait_vm<XI>();
+                else
+                    wait_vm<0>();
+                barrier_lds();
+                frag_load(f0, na, cb ^ 1u, 0);   // past the last step: stale, unused
             }
             __builtin_amdgcn_sched_barrier(0);
             frag_mfma(f1);
             __builtin_amdgcn_sched_barrier(0);
         }
+        ca = na;
     }
 
     if constexpr (SILU) {
@@ -509,7 +563,7 @@ static hipError_t go_gemm(const uint16_t *X, const float *rscale, const uint8_t 
                           uint32_t M, uint32_t mrows, uint32_t S, float *ws, const GemmNorm *nrm, const GemmRope *rp,
                           hipStream_t s)
 {
-    constexpr size_t lds = 2 * (size_t)(BM + BN) * BK * 2;
+    constexpr size_t lds = gemm_lds_bytes<BM, BN, BK>;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
     // the fused reductions take every one of the M rows
     if ((nrm || rp) && mrows != M) return hipErrorInvalidValue;
@@ -769,7 +823,7 @@ hipError_t launch_gemm_f16_silu_f16(const uint16_t *X, const uint8_t *W, uint32_
     if (!gemm_supported(type, K, N, M, (uint64_t)M * K * 2) || M % 256 || N % 128) return hipErrorNotSupported;
     const uint32_t tiles_n = N / 128, tiles = tiles_n * (M / 256);
     if (tiles < 128 || (uint64_t)M * F * 4 > ws_bytes) return hipErrorNotSupported;
-    constexpr size_t lds = 2 * (size_t)(256 + 128) * 64 * 2;
+    constexpr size_t lds = gemm_lds_bytes<256, 128, 64>;
 #define RRR_SILU_CASE(T, QT)                                                                                          \
     case T:                                                                                                            \
         hipLaunchKernelGGL((gemm_dq_kernel<QT, 256, 128, 64, false, false, true>), dim3(tiles), dim3(512), lds, s, X, \

@@ -119,27 +119,6 @@ struct SkGeom {
     __device__ static uint32_t row_off(uint32_t r) { return (r / RPS) * 1024 + (r % RPS) * Q::BS; }
 };
 
-// 16-byte LDS DMA load: lane l's 16 bytes at `voff + soff` go to LDS
-// dst + 16 l.  Only the device pass sees the builtin (the host pass would
-// otherwise drop the kernels' launch stubs).
-__device__ __forceinline__ void sk_dma16(__amdgpu_buffer_rsrc_t rs, uint8_t *dst, uint32_t voff, uint32_t soff)
-{
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16, voff, soff, 0,
-                                             RRR_CPOL_NT);
-#endif
-}
-
-// Wait until at most N vector memory operations of this wave are in flight
-// (they retire in order).  The compiler does not track LDS DMA, so the LDS
-// reads of a tile wait here; the memory clobber keeps them after the wait.
-template <int N>
-__device__ __forceinline__ void sk_wait_vm()
-{
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // Workspace layout of the encoded activations (see the top of this file).
 constexpr uint32_t SK_AV_UNIT = 8 * 64 * 16, SK_AMIN_UNIT = 64 * 8, SK_EX_UNIT = 16 * 4;
 __host__ __device__ constexpr uint64_t sk_ws_bytes(uint32_t tok, uint32_t W)
@@ -285,7 +264,7 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
         uint8_t *dst = L + (tl % NB) * G::BUF;
 #pragma unroll
         for (int s = 0; s < G::S; s++)
-            sk_dma16(rs, dst + 1024 * s, s == G::S - 1 ? voff_last : voff, tb + s * G::RPS * row_bytes);
+            lds_dma16<RRR_CPOL_NT>(rs, dst + 1024 * s, s == G::S - 1 ? voff_last : voff, tb + s * G::RPS * row_bytes);
     };
 
     // 1. A operands, the first tiles' weights streaming in meanwhile (queued
@@ -334,7 +313,7 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
     const uint32_t roff = G::row_off(r16);
     for (uint32_t tl = 0; tl < ntl; tl++) {
         dma(tl + NB - 1);
-        sk_wait_vm<(NB - 1) * G::S>();
+        wait_vm<(NB - 1) * G::S>();
         typename Q::Raw raw;
         Q::load(raw, L + (tl % NB) * G::BUF, roff, kg);
         const float d = h2f(raw.hdr.x), dmin = h2f(raw.hdr.x >> 16);
