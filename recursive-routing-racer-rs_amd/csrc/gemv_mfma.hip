@@ -26,7 +26,7 @@ static void mq_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds,
 {
     using G = MwGeom<Q, BPW>;
     const uint32_t B = a.K / 256;
-    W = max(4u, (B + BPW - 1) / BPW);
+    W = mq_waves(a.K, BPW);
     const size_t fixed = W * G::BYTES + 64;
     const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64));
     uint32_t per;
@@ -55,7 +55,7 @@ static hipError_t go_mq_pair(const GemvArgs &a, hipStream_t s, MqShape *sh = nul
 {
     using G = MwGeom<Q, BPW>;
     const uint32_t B = a.K / 256;
-    const uint32_t W = max(4u, (B + BPW - 1) / BPW);
+    const uint32_t W = mq_waves(a.K, BPW);
     const size_t fixed = W * G::BYTES + 64;
     const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64)) / 2;   // pairs: two tiles each
     if (per_max == 0) return hipErrorInvalidValue;

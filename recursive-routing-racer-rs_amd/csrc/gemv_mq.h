@@ -218,6 +218,15 @@ __device__ __forceinline__ uint32_t quad_sum_u32(uint32_t v)
 //   aux:     per 16-element group 16 bytes = MFMA accumulator input
 //            {-32 * sum Q (Q6_K only, else 0), 0, 0, bits of 2^(E-14)}
 //   gsum:    per group the f32 sum of x (Q4_K / Q5_K min term)
+// Waves of a workgroup for K columns at BPW super-blocks per wave (at least
+// 4, one per SIMD).  The launchers size the workgroup with it and the kernel
+// derives its wave count from it: reading blockDim.x would cost a dependent
+// load of the dispatch's hidden arguments at kernel entry.
+__host__ __device__ constexpr uint32_t mq_waves(uint32_t K, uint32_t BPW)
+{
+    return (K / 256 + BPW - 1) / BPW > 4u ? (K / 256 + BPW - 1) / BPW : 4u;
+}
+
 template <class Q, int BPW>
 struct MwGeom {
     static constexpr uint32_t UPB = (Q::BS + 15) / 16;            // 16-byte units per block piece
@@ -318,7 +327,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     constexpr bool AREG = BPW == 1 || !MULTI;
     constexpr int AJ = AREG ? BPW : 1;
     const uint32_t K = a.K, B = K / 256;
-    const uint32_t W = blockDim.x >> 6, NT = blockDim.x;
+    const uint32_t W = mq_waves(K, BPW), NT = 64 * W;   // the launch's workgroup
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t n = lane & 15, g = lane >> 4;
     uint64_t stamp[15] = {};
@@ -397,6 +406,10 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int j = 0; j < BPW; j++) issue(j, 0);
+    // the weight loads leave before any use of the activations: the
+    // scheduler would otherwise hoist the sum of squares (or the encoding)
+    // above them, behind a wait for the activation loads to land
+    __builtin_amdgcn_sched_barrier(0);
     // 2. fused RMSNorm: the wave's slice of x is slice `wave` of the canonical
     // sum-of-squares split (BPW float4s per lane is its P = ceil(K / 4096)
     // for K <= 8192); the slice sums are added in wave order (waves without

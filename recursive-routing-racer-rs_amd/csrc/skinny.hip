@@ -359,7 +359,7 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
         }
         __syncthreads();
         // the waves' partials in order
-        for (uint32_t i = t; i < MP * 16; i += blockDim.x) {
+        for (uint32_t i = t; i < MP * 16; i += 64 * W) {   // the launch's 64 W threads
             const uint32_t m = i >> 4, c = i & 15, row = (tile0 + tl * GR) * 16 + c;
             if (m < M && row < N) {
                 // the W <= 16 waves' partials in wave order
