@@ -356,9 +356,40 @@ __device__ __forceinline__ float sumsq_held_256(const float4 *v, const uint32_t 
 
 // Canonical sum of squares of x[0..d) by a 256-thread workgroup, read from
 // memory.  `red` is 16 floats of LDS.
+// The canonical sum of squares of block_sumsq_256 in two halves, for
+// d % 4 == 0 and d <= 4096 (one float4 per slice and thread): the loads, all
+// issued at once and unconditionally (clamped addresses; past d the value is
+// not used), then the sums.  A load under a branch makes the compiler wait
+// for every load in flight at the join -- also for loads issued before the
+// call, such as a weight stream -- and it serialises the x loads.
+struct SumsqX {
+    float4 v[4];
+};
+__device__ __forceinline__ SumsqX sumsq_load_256(const float *__restrict__ x, uint32_t d)
+{
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nf = d / 4;
+    const float4 *p = (const float4 *)x;
+    SumsqX r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.v[i] = p[min(64 * (wave + 4 * i) + lane, nf - 1)];
+    return r;
+}
+__device__ __forceinline__ float sumsq_finish_256(const SumsqX &xv, uint32_t d, float *red)
+{
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nf = d / 4;
+    float sq[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float acc = 64 * (wave + 4 * i) + lane < nf ? sumsq4(xv.v[i], 0.0f) : 0.0f;
+        sq[i] = wave_sum(acc);
+    }
+    return slices_total_256(sq, red);
+}
+
 __device__ __forceinline__ float block_sumsq_256(const float *__restrict__ x, uint32_t d, float *red)
 {
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (d % 4 == 0 && d > 0 && d <= 4096) return sumsq_finish_256(sumsq_load_256(x, d), d, red);
     if (d % 4 != 0) {
         float acc = 0.0f;
         for (uint32_t i = t; i < d; i += 256) acc = __builtin_fmaf(x[i], x[i], acc);

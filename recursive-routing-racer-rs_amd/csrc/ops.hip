@@ -532,7 +532,9 @@ __global__ __launch_bounds__(256) void logits_split_kernel(const float *__restri
     float *red = wsum + 4 * 256;    // 16
     __shared__ uint32_t last;
     __shared__ Cand amsm[4];
-    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // wave-uniform: the weight loads' scalar offsets derive from it (else each
+    // load is wrapped in a readfirstlane loop)
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t sb = blockIdx.x / NS, h = blockIdx.x % NS;
     const uint32_t spc = chunk / LOGITS_SLAB;                 // slabs per full chunk
     const uint32_t c = sb / spc, j = sb - c * spc;
