@@ -268,15 +268,16 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
     };
 
     // 1. A operands, the first tiles' weights streaming in meanwhile (queued
-    // before the loads of encoded operands, after those of f32 activations,
-    // which the encoding needs first)
+    // after the loads of the encoded operands, and after those of f32
+    // activations, which the encoding needs first: loads return in order, so
+    // tile 0 waits for the A operands and its own weights only, while the
+    // next tiles' weights arrive under its MFMAs)
     f16x8s av[TOK][8];
     f16x4s amin[TOK];
     int eexp[TOK][DPT];   // E of the lane's D-layout tokens
     // D row 4 kg + j holds A row 4 kg + j: the token of A row 4 kg + 2 j
     // (HILO: rows 2t, 2t+1 are token t's hi and lo) or 4 kg + j
     if constexpr (PRE) {
-        for (uint32_t i = 0; i + 1 < NB; i++) dma(i);
         const SkWs o(a.ws, TOK, W);
 #pragma unroll
         for (int tt = 0; tt < TOK; tt++) {
@@ -288,6 +289,8 @@ __global__ __launch_bounds__(TOK == 1 ? 1024 : 768) void skinny_kernel(GemvArgs 
             for (int j = 0; j < DPT; j++)
                 eexp[tt][j] = o.ex[(tt * W + wave) * 16 + (HILO ? 4 * kg + 2 * j : 4 * kg + j)];
         }
+        __builtin_amdgcn_sched_barrier(0);
+        for (uint32_t i = 0; i + 1 < NB; i++) dma(i);
     } else {
 #pragma unroll
         for (int tt = 0; tt < TOK; tt++) {
