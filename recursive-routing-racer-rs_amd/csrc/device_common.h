@@ -45,6 +45,19 @@ __device__ __forceinline__ u32x4 bload16_nt_so(__amdgpu_buffer_rsrc_t r, uint32_
 {
     return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, RRR_CPOL_NT);
 }
+// ... plain policy, with a wave-uniform part of the offset in the scalar operand
+__device__ __forceinline__ u32x4 bload16_so(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+// An offset past every buffer a kernel addresses this way (each below 2 GB):
+// a buffer load there moves no data and returns zeros, so a load can be
+// issued unconditionally instead of under a branch.
+constexpr uint32_t RRR_OOB = 0x80000000u;
+__device__ __forceinline__ float4 u2f4(const u32x4 &v)
+{
+    return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
 __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off)
 {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);

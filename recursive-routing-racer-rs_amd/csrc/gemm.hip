@@ -505,27 +505,56 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         }
         return;
     }
-    // the row scales (powers of two) are exact
+    if constexpr (SPLIT) {
 #pragma unroll
-    for (int i = 0; i < UI; i++)
+        for (int i = 0; i < UI; i++)
+#pragma unroll
+            for (int j = 0; j < UJ; j++) {
+                const uint32_t n = n0 + wn * (BN / 2) + 32 * j + fr;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    ws[((uint64_t)ks * M + m) * N + n] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+    // The row scales (powers of two) are exact.  Per row tile, its rows'
+    // scales and (ACC) the Y values it adds to are requested at once, rows
+    // past mrows (zero padding of a row chunk, not the caller's: never
+    // stored) reading row mrows - 1: loaded under the row test, each would
+    // wait for the one before.
+    // (no row scale: a resource of no bytes, whose loads return zeros
+    // without a memory request, and the product is not taken)
+    const __amdgpu_buffer_rsrc_t rsr = make_rsrc(rscale, rscale ? (uint64_t)mrows * 4 : 0u);
+#pragma unroll
+    for (int i = 0; i < UI; i++) {
+        float sc[16], yo[UJ][16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const uint32_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const uint32_t mc = min(m, mrows - 1);
+            sc[r] = __uint_as_float(bload4(rsr, 4 * mc));
+            if constexpr (ACC) {
+#pragma unroll
+                for (int j = 0; j < UJ; j++) yo[j][r] = Y[(uint64_t)mc * N + n0 + wn * (BN / 2) + 32 * j + fr];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < UJ; j++) {
             const uint32_t n = n0 + wn * (BN / 2) + 32 * j + fr;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const uint32_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if constexpr (SPLIT) {
-                    ws[((uint64_t)ks * M + m) * N + n] = acc[i][j][r];
-                    continue;
-                }
-                if (m >= mrows) continue;   // zero padding rows of a row chunk: not the caller's
-                const float v = rscale ? acc[i][j][r] * rscale[m] : acc[i][j][r];
+                if (m >= mrows) continue;
+                const float v = rscale ? acc[i][j][r] * sc[r] : acc[i][j][r];
                 if constexpr (ACC)
-                    Y[(uint64_t)m * N + n] += v;
+                    Y[(uint64_t)m * N + n] = yo[j][r] + v;
                 else
                     Y[(uint64_t)m * N + n] = v;
             }
         }
+    }
 }
 
 // Y (+)= rscale[m] * sum over the SS partials of ws (in split order, all

@@ -114,17 +114,27 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     if (d % 4 == 0 && d <= 8 * 4 * 256) {
         // the row stays in registers (one pass over x); the thread holds its
         // float4s of the canonical sum-of-squares split
+        // x and gamma requested at once (buffer loads; a slot past the row
+        // takes an out-of-range offset: no request, zeros), not each under
+        // its slot test, which would wait for the one before
         const uint32_t nf = d / 4;
         uint32_t f[8], sl[8];
         sumsq_slots<8>(sumsq_parts(d), f, sl);
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(xr, (uint64_t)d * 4), rg = make_rsrc(g, (uint64_t)d * 4);
         float4 v[8];
+        u32x4 gw[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = f[j] < nf ? ((const float4 *)xr)[f[j]] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < 8; j++) {
+            const uint32_t off = f[j] < nf ? 16 * f[j] : RRR_OOB;
+            v[j] = u2f4(bload16_so(rx, off, 0));
+            gw[j] = bload16_so(rg, off, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         const float inv = rms_inv(sumsq_held_256<8>(v, f, sl, nf, red), d, eps);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             if (f[j] < nf) {
-                const float4 w = ((const float4 *)g)[f[j]];
+                const float4 w = u2f4(gw[j]);
                 store4(yr, f[j], make_float4(__fmul_rn(__fmul_rn(w.x, v[j].x), inv), __fmul_rn(__fmul_rn(w.y, v[j].y), inv),
                                           __fmul_rn(__fmul_rn(w.z, v[j].z), inv), __fmul_rn(__fmul_rn(w.w, v[j].w), inv)));
             }
@@ -157,40 +167,57 @@ hipError_t launch_rmsnorm_f16(const float *x, const float *g, uint16_t *y, uint3
 // row's RMSNorm with gamma in f16, the arithmetic and canonical sum-of-squares
 // order of rmsnorm_kernel<_Float16> over the stored row, so both outputs are
 // bitwise the two launches'.  d % 4 == 0, d <= 8192.
-// SS: the split count (2..8), so a slot's partials are all requested before
-// the first add
-template <int SS>
+// SS: the split count (2..8); P = ceil(d / 4096), the slots a thread holds
+// being 4 P.  Every slot's partials, residual and gamma are requested at once
+// (buffer loads; a slot past the row, or the residual without acc, takes an
+// out-of-range offset: no request, zeros), before the first add: a load under
+// a branch would make the compiler wait for it at the join, one round trip
+// per slot.
+template <int SS, int P>
 __global__ __launch_bounds__(256) void splitk_reduce_rmsnorm_kernel(const float *__restrict__ ws, uint32_t M,
                                                                     uint32_t d, float *__restrict__ Y,
                                                                     const float *__restrict__ rscale, uint32_t acc,
                                                                     const float *__restrict__ g, float eps,
                                                                     _Float16 *__restrict__ out)
 {
+    constexpr int NS = 4 * P;
     __shared__ float red[16];
     const uint32_t m = blockIdx.x, nf = d / 4;
-    const uint64_t mn = (uint64_t)M * d;
+    const uint32_t mn4 = M * d * 4;                               // bytes of one split's partials
     float4 *yr = (float4 *)(Y + (uint64_t)m * d);
     const float r = rscale ? rscale[m] : 1.0f;
     uint32_t f[8], sl[8];
-    sumsq_slots<8>(sumsq_parts(d), f, sl);
+    sumsq_slots<8>(P, f, sl);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(ws, (uint64_t)SS * mn4);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(Y, (uint64_t)mn4);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(g, (uint64_t)d * 4);
+    u32x4 pw[NS][SS], py[NS], pg[NS];
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+        const bool ok = f[j] < nf;
+        const uint32_t off = ok ? (m * d + 4 * f[j]) * 4 : RRR_OOB;
+#pragma unroll
+        for (int k = 0; k < SS; k++) pw[j][k] = bload16_so(rw, off, k * mn4);
+        py[j] = bload16_so(ry, acc ? off : RRR_OOB, 0);
+        pg[j] = bload16_so(rg, ok ? 16 * f[j] : RRR_OOB, 0);
+    }
     float4 v[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (f[j] < nf) {
-            float4 p[SS];
+    for (int j = 0; j < 8; j++) v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int k = 0; k < SS; k++) p[k] = ((const float4 *)(ws + k * mn + (uint64_t)m * d))[f[j]];
-            float4 a = p[0];
+    for (int j = 0; j < NS; j++) {
+        if (f[j] < nf) {
+            float4 a = u2f4(pw[j][0]);
 #pragma unroll
             for (int k = 1; k < SS; k++) {
-                a.x += p[k].x; a.y += p[k].y; a.z += p[k].z; a.w += p[k].w;
+                const float4 q = u2f4(pw[j][k]);
+                a.x += q.x; a.y += q.y; a.z += q.z; a.w += q.w;
             }
             if (rscale) {
                 a.x *= r; a.y *= r; a.z *= r; a.w *= r;
             }
             if (acc) {
-                const float4 o = yr[f[j]];
+                const float4 o = u2f4(py[j]);
                 a.x = o.x + a.x; a.y = o.y + a.y; a.z = o.z + a.z; a.w = o.w + a.w;
             }
             yr[f[j]] = a;
@@ -200,9 +227,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_rmsnorm_kernel(const float 
     const float inv = rms_inv(sumsq_held_256<8>(v, f, sl, nf, red), d, eps);
     _Float16 *orow = out + (uint64_t)m * d;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < NS; j++) {
         if (f[j] < nf) {
-            const float4 w = ((const float4 *)g)[f[j]];
+            const float4 w = u2f4(pg[j]);
             store4(orow, f[j], make_float4(__fmul_rn(__fmul_rn(w.x, v[j].x), inv), __fmul_rn(__fmul_rn(w.y, v[j].y), inv),
                                            __fmul_rn(__fmul_rn(w.z, v[j].z), inv), __fmul_rn(__fmul_rn(w.w, v[j].w), inv)));
         }
@@ -217,8 +244,12 @@ hipError_t launch_splitk_reduce_rmsnorm(const float *ws, uint32_t S, uint32_t M,
 {
 #define RRR_SRR_CASE(N)                                                                                          \
     case N:                                                                                                       \
-        hipLaunchKernelGGL(splitk_reduce_rmsnorm_kernel<N>, dim3(M), dim3(256), 0, s, ws, M, d, Y, rscale,         \
-                           acc ? 1u : 0u, g, eps, (_Float16 *)out);                                                \
+        if (d <= 4096)                                                                                            \
+            hipLaunchKernelGGL((splitk_reduce_rmsnorm_kernel<N, 1>), dim3(M), dim3(256), 0, s, ws, M, d, Y, rscale, \
+                               acc ? 1u : 0u, g, eps, (_Float16 *)out);                                            \
+        else                                                                                                      \
+            hipLaunchKernelGGL((splitk_reduce_rmsnorm_kernel<N, 2>), dim3(M), dim3(256), 0, s, ws, M, d, Y, rscale, \
+                               acc ? 1u : 0u, g, eps, (_Float16 *)out);                                            \
         break;
     switch (S) {
         RRR_SRR_CASE(2) RRR_SRR_CASE(3) RRR_SRR_CASE(4) RRR_SRR_CASE(5)
