@@ -98,6 +98,7 @@ __global__ __launch_bounds__(256) void splitk_rope_kv_store_kernel(const float *
     const uint32_t pos = r.pos + m, qh = r.n_heads * r.head_dim;
     const bool live = m < rows;
     const uint64_t mn = (uint64_t)M * N;
+    const float *src = ws + (uint64_t)m * N;
     float *dst = qkv + (uint64_t)m * N;
     if (lds_coef && live) {
         for (uint32_t j = threadIdx.x; j < half_rope; j += 256) rope_coef(j, pos, r, cf[2 * j], cf[2 * j + 1]);
@@ -111,28 +112,14 @@ __global__ __launch_bounds__(256) void splitk_rope_kv_store_kernel(const float *
             rope_coef(j, pos, r, cs, ss);
         }
     };
-    // the partials of four strides requested at once (buffer loads; past N
-    // an out-of-range offset: no request), so one round trip covers them
-    const uint32_t step = 4 * gridDim.x * 256, mn4 = (uint32_t)(mn * 4);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(ws, (uint64_t)SS * mn4);
-    for (uint32_t c0 = 4 * (blockIdx.x * 256 + threadIdx.x); c0 < N; c0 += 4 * step) {
-        u32x4 pb[4][SS];
+    for (uint32_t c = 4 * (blockIdx.x * 256 + threadIdx.x); c < N; c += 4 * gridDim.x * 256) {
+        float4 p[SS];
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const uint32_t c = c0 + b * step;
-            const uint32_t off = c < N ? (uint32_t)(((uint64_t)m * N + c) * 4) : RRR_OOB;
-#pragma unroll
-            for (int k = 0; k < SS; k++) pb[b][k] = bload16_so(rw, off, k * mn4);
-        }
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-        const uint32_t c = c0 + b * step;
-        if (c >= N) continue;
-        float4 v = u2f4(pb[b][0]);
+        for (int k = 0; k < SS; k++) p[k] = *(const float4 *)(src + k * mn + c);
+        float4 v = p[0];
 #pragma unroll
         for (int k = 1; k < SS; k++) {
-            const float4 q = u2f4(pb[b][k]);
-            v.x += q.x; v.y += q.y; v.z += q.z; v.w += q.w;
+            v.x += p[k].x; v.y += p[k].y; v.z += p[k].z; v.w += p[k].w;
         }
         if (live) {
             float x[4] = {v.x, v.y, v.z, v.w};
@@ -173,7 +160,6 @@ __global__ __launch_bounds__(256) void splitk_rope_kv_store_kernel(const float *
             v = make_float4(x[0], x[1], x[2], x[3]);
         }
         *(float4 *)(dst + c) = v;
-        }
     }
 }
 
