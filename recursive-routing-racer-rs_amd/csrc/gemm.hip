@@ -356,7 +356,9 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         // the barrier that ends the MFMA waves' last step
         __syncthreads();
         if constexpr (SILU) {
-            // row blocks 2, 3 of MFMA wave t / 64 - 4, once it has handed them over
+            // the MFMA waves' zeros past the end have landed; then row blocks
+            // 2, 3 of MFMA wave t / 64 - 4, once it has handed them over
+            __syncthreads();
             __syncthreads();
             const uint32_t cw = wave - 4;
             const float *hs = (const float *)smem + cw * 64 * 64 + lane;
@@ -448,28 +450,23 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
     uint32_t ca = 0;   // A buffer of step s (s % NA)
     for (uint32_t s = 0; s < steps3; s++) {
         const uint32_t cb = s & 1, na = ca == NA - 1 ? 0u : ca + 1, pa = ca == 0 ? NA - 1 : ca - 1;
-        const bool more = s + NA - 1 < steps3;
 #pragma unroll
         for (int kq = 0; kq < KQ; kq += 2) {
             frag_load(f1, ca, cb, kq + 1);
             __builtin_amdgcn_sched_barrier(0);
             frag_mfma(f0);
             __builtin_amdgcn_sched_barrier(0);
-            // X of step s + NA - 1 into the buffer step s - 1 used
-            if (more) {
+            // X of step s + NA - 1 into the buffer step s - 1 used, issued on
+            // every step (one straight-line loop body with no branch): in the
+            // last NA - 1 steps it is a step past nsteps, whose zeros land in
+            // a buffer no later step reads
 #pragma unroll
-                for (int i = 0; i < XPQ; i++) x_dma(s + NA - 1, pa, XPQ * (kq / 2) + i);
-            }
+            for (int i = 0; i < XPQ; i++) x_dma(s + NA - 1, pa, XPQ * (kq / 2) + i);
             if (kq + 2 < KQ) {
                 frag_load(f0, ca, cb, kq + 2);
             } else {
-                // X of steps s + 2 .. s + NA - 1 (those below steps3) stay in flight
-                if (more)
-                    wait_vm<(NA - 2) * XI>();
-                else if (NA == 4 && s + 2 < steps3)
-                    wait_vm<XI>();
-                else
-                    wait_vm<0>();
+                // X of steps s + 2 .. s + NA - 1 stay in flight
+                wait_vm<(NA - 2) * XI>();
                 barrier_lds();
                 frag_load(f0, na, cb ^ 1u, 0);   // past the last step: stale, unused
             }
@@ -479,11 +476,16 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
         }
         ca = na;
     }
+    // the zeros of the steps past the end have landed before the epilogue
+    // reuses the LDS (SILU: every wave's, a barrier later)
+    wait_vm<0>();
 
     if constexpr (SILU) {
         static_assert(!SPLIT && !ACC && BN == 128 && BM == 256, "gate/up tiles of 64 outputs, whole K");
         // row blocks 2, 3 to the staging wave t / 64 + 4 (LDS past the last
-        // step's barrier: only this wave's stale fragment read touches it)
+        // step's barrier and the zeros' landing: only this wave's stale
+        // fragment read touches it)
+        __syncthreads();
         float *hs = (float *)smem + wave * 64 * 64 + lane;
 #pragma unroll
         for (int i = 2; i < 4; i++)
