@@ -240,7 +240,7 @@ __device__ __forceinline__ void silu_rows_store(float *Y, uint32_t F, uint32_t n
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const uint32_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        Y[(uint64_t)m * F + n] = silu_f(g[r]) * u[r];
+        __builtin_nontemporal_store(silu_f(g[r]) * u[r], Y + (uint64_t)m * F + n);
     }
 }
 
@@ -524,11 +524,15 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const uint32_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    ws[((uint64_t)ks * M + m) * N + n] = acc[i][j][r];
+                    __builtin_nontemporal_store(acc[i][j][r], ws + ((uint64_t)ks * M + m) * N + n);
                 }
             }
         return;
     }
+    // Outputs (here, the split partials above and the silu * up rows) leave
+    // as non-temporal stores: every CU writes its whole tile at the end at
+    // once, and the stream gets through faster without allocating in the
+    // caches on its way (gate+up at 512 rows: 33.5 MB of f32).
     // The row scales (powers of two) are exact.  Per row tile, its rows'
     // scales and (ACC) the Y values it adds to are requested at once, rows
     // past mrows (zero padding of a row chunk, not the caller's: never
@@ -561,7 +565,7 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
                 if constexpr (ACC)
                     Y[(uint64_t)m * N + n] = yo[j][r] + v;
                 else
-                    Y[(uint64_t)m * N + n] = v;
+                    __builtin_nontemporal_store(v, Y + (uint64_t)m * N + n);
             }
         }
     }
