@@ -259,13 +259,13 @@ __global__ __launch_bounds__(512) void gemm_dq_kernel(const uint16_t *X, const u
 {
     // LDS rows of BK f16, unpadded; 16-byte chunk c of row r sits at chunk
     // c ^ swz(r), swz(r) = g((r / RPL) % CPR) with RPL rows per 64-bank line,
-    // CPR chunks per row and g swapping bits 1 and 2.  The 16 lanes the LDS
-    // serves at once then hit 64 distinct banks both when they read one
-    // chunk of 16 consecutive rows (g is a bijection) and when the staging
-    // waves write chunks c and c ^ 2 of each of 16 / TPW consecutive rows
-    // (those rows' g values fall in distinct classes {x, x ^ 2}, bit 3
-    // aside); with g the identity those writes were two-way conflicts.  swz
-    // depends on r % 16 only; every tile base and row stride below is a
+    // CPR chunks per row and g swapping bits 1 and 2.  Any 16 consecutive
+    // lanes then hit 64 distinct banks both when they read one chunk of 16
+    // consecutive rows (g is a bijection) and when the staging waves write
+    // chunks c and c ^ 2 of each of 16 / TPW consecutive rows (those rows'
+    // g values fall in distinct classes {x, x ^ 2}, bit 3 aside); with g
+    // the identity, those writes pair up two to a bank within 16 lanes.
+    // swz depends on r % 16 only; every tile base and row stride below is a
     // multiple of 16.
     constexpr int LDK = BK, CPR = BK / 8, RPL = 128 / BK;
     static_assert(RPL * CPR == 16, "swizzle period");
