@@ -603,6 +603,7 @@ static bool batched_gemm_route(const GemvArgs &a, uint32_t act)
 hipError_t launch_gemv(const GemvArgs &a, uint32_t act, hipStream_t s)
 {
     if (gemv_mfma_supported(a)) return launch_gemv_mfma(a, act, s);
+    if (a.M > 1 && act == ACT_PLAIN && gemv_mq_tokens_supported(a)) return launch_gemv_mq_tokens(a, s);
     if (a.M > 1 && act == ACT_PLAIN && skinny_supported(a)) return launch_skinny(a, s);
     if (batched_gemm_route(a, act)) return launch_gemm_f32_rows(a.x, a.W, a.type, a.y, a.K, a.N, a.M, a.ws, a.ws_bytes, s);
     switch (a.type) {

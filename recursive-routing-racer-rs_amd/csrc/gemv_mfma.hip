@@ -11,6 +11,15 @@ __global__ __launch_bounds__(1024) void gemv_mq_kernel(GemvArgs a, uint32_t ntil
     mq_body<Q, BPW, ACT, MULTI, TR, PAIR, ROPE, ST>(a, ntiles, tr);
 }
 
+// The multi-token form, MT rows of x per weight stream, in workgroups of at
+// most NTH threads (768 = 12 waves leaves 168 registers a lane where 1024
+// threads leave 128, which MT = 4 and 8 exceed).
+template <class Q, int BPW, bool MULTI, int MT, int NTH>
+__global__ __launch_bounds__(NTH) void gemv_mq_tokens_kernel(GemvArgs a, uint32_t ntiles, uint32_t tr)
+{
+    mq_body<Q, BPW, ACT_PLAIN, MULTI, 16, false, false, false, MT>(a, ntiles, tr);
+}
+
 // The launch's grid and waves per workgroup (reported to the stamped launch).
 struct MqShape {
     uint32_t grid, waves;
@@ -135,6 +144,69 @@ static hipError_t go_mq_act(const GemvArgs &a, uint32_t act, hipStream_t s, MqSh
     default: return hipErrorInvalidValue;
     }
 }
+
+// The multi-token form: a.M <= MT rows of x through the same weight stream
+// (plain activations, optional residual).  Tiles of up to 16 rows; each
+// workgroup's LDS holds MT encoded slices and MT row partials per tile.
+template <class Q, int BPW, int MT>
+static bool mq_tokens_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds, uint32_t &tr,
+                           uint32_t &ntiles)
+{
+    using G = MwGeom<Q, BPW, MT>;
+    W = mq_waves(a.K, BPW);
+    const size_t fixed = W * G::BYTES + 64, per_tile = (size_t)W * 64 * MT;
+    if (fixed + per_tile > 160 * 1024) return false;
+    const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / per_tile);
+    uint32_t per;
+    mq_tiles(a.N, device_cus(), per_max, 1u, tr, ntiles, per);
+    grid = (ntiles + per - 1) / per;
+    lds = fixed + (size_t)per * per_tile;
+    return true;
+}
+
+template <class Q, int BPW, int MT, int NTH>
+static hipError_t go_mq_tokens_b(const GemvArgs &a, hipStream_t s, bool launch)
+{
+    uint32_t W, grid, tr, ntiles;
+    size_t lds;
+    if (!mq_tokens_plan<Q, BPW, MT>(a, W, grid, lds, tr, ntiles) || 64 * W > NTH) return hipErrorNotSupported;
+    if (!launch) return hipSuccess;
+    if (grid == ntiles)
+        hipLaunchKernelGGL((gemv_mq_tokens_kernel<Q, BPW, false, MT, NTH>), dim3(grid), dim3(64 * W), lds, s, a, ntiles,
+                           tr);
+    else
+        hipLaunchKernelGGL((gemv_mq_tokens_kernel<Q, BPW, true, MT, NTH>), dim3(grid), dim3(64 * W), lds, s, a, ntiles,
+                           tr);
+    return hipGetLastError();
+}
+
+// K <= 3072 (at most 12 waves): 2 or 4 tokens a launch; K <= 8192 (16
+// waves of two super-blocks): 2 (more tokens would spill at 128 registers)
+template <class Q>
+static hipError_t go_mq_tokens(const GemvArgs &a, hipStream_t s, bool launch)
+{
+    if (a.K <= 12 * 256) {
+        if (a.M <= 2) return go_mq_tokens_b<Q, 1, 2, 768>(a, s, launch);
+        return go_mq_tokens_b<Q, 1, 4, 768>(a, s, launch);
+    }
+    if (a.M <= 2) return go_mq_tokens_b<Q, 2, 2, 1024>(a, s, launch);
+    return hipErrorNotSupported;
+}
+
+static hipError_t mq_tokens(const GemvArgs &a, hipStream_t s, bool launch)
+{
+    if (a.M < 2 || a.M > MQ_TOKENS_MAX || a.K > 8192 || a.w_bytes + RRR_READ_SLACK >= MQ_OOB) return hipErrorNotSupported;
+    switch (a.type) {
+    case T_Q4_K: return go_mq_tokens<MqQ4K>(a, s, launch);
+    case T_Q5_K: return go_mq_tokens<MqQ5K>(a, s, launch);
+    case T_Q6_K: return go_mq_tokens<MqQ6K>(a, s, launch);
+    default: return hipErrorNotSupported;
+    }
+}
+
+bool gemv_mq_tokens_supported(const GemvArgs &a) { return mq_tokens(a, nullptr, false) == hipSuccess; }
+
+hipError_t launch_gemv_mq_tokens(const GemvArgs &a, hipStream_t s) { return mq_tokens(a, s, true); }
 
 uint32_t device_cu_count() { return device_cus(); }
 

@@ -214,10 +214,14 @@ __device__ __forceinline__ uint32_t quad_sum_u32(uint32_t v)
 //            that block (lane l: unit l % UPB of row l / UPB), so a lane's
 //            offsets are fixed and only a uniform per-slot offset moves, and
 //            a block's MFMAs can start while the next block is still landing.
-//   digits:  3 planes x DG bytes (plane p, local element e at p*DG + e)
-//   aux:     per 16-element group 16 bytes = MFMA accumulator input
-//            {-32 * sum Q (Q6_K only, else 0), 0, 0, bits of 2^(E-14)}
-//   gsum:    per group the f32 sum of x (Q4_K / Q5_K min term)
+//   digits:  per token m, 3 planes x DG bytes (plane p, local element e at
+//            (3 m + p) * DG + e)
+//   aux:     per token and 16-element group 16 bytes = MFMA accumulator
+//            input {-32 * sum Q (Q6_K only, else 0), 0, 0, bits of 2^(E-14)}
+//   gsum:    per token and group the f32 sum of x (Q4_K / Q5_K min term)
+// MT tokens (rows of x) share every weight block: the multi-token form
+// (MT > 1) encodes each token's slice and runs one MFMA per token and k-set
+// on the same B operand.
 // Waves of a workgroup for K columns at BPW super-blocks per wave (at least
 // 4, one per SIMD).  The launchers size the workgroup with it and the kernel
 // derives its wave count from it: reading blockDim.x would cost a dependent
@@ -227,7 +231,7 @@ __host__ __device__ constexpr uint32_t mq_waves(uint32_t K, uint32_t BPW)
     return (K / 256 + BPW - 1) / BPW > 4u ? (K / 256 + BPW - 1) / BPW : 4u;
 }
 
-template <class Q, int BPW>
+template <class Q, int BPW, int MT = 1>
 struct MwGeom {
     static constexpr uint32_t UPB = (Q::BS + 15) / 16;            // 16-byte units per block piece
     static constexpr uint32_t LB = 16 * UPB;
@@ -236,9 +240,9 @@ struct MwGeom {
     static constexpr uint32_t DG = BPW * 256;
     static constexpr uint32_t NGW = BPW * 16;
     static constexpr uint32_t D_OFF = 16 * RS;
-    static constexpr uint32_t A_OFF = D_OFF + 3 * DG;
-    static constexpr uint32_t G_OFF = A_OFF + 16 * NGW;
-    static constexpr uint32_t BYTES = G_OFF + 4 * NGW;            // multiple of 16
+    static constexpr uint32_t A_OFF = D_OFF + MT * 3 * DG;
+    static constexpr uint32_t G_OFF = A_OFF + MT * 16 * NGW;
+    static constexpr uint32_t BYTES = G_OFF + MT * 4 * NGW;       // multiple of 16
 };
 
 // Odd Q6_K blocks (210 bytes) start 2 bytes past a 4-byte boundary, and
@@ -313,18 +317,22 @@ __device__ __forceinline__ uint64_t phase_stamp(float dep)
     return t;
 }
 
+// MT > 1: the multi-token form (plain activations; a.M <= MT tokens, rows m
+// of x at x + m K, outputs at y + m N; tokens past a.M read the last row and
+// store nothing).
 template <class Q, int BPW, int ACT, bool MULTI, int TR = 16, bool PAIR = false, bool ROPE = false,
-          bool STAMPS = false>
+          bool STAMPS = false, int MT = 1>
 __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint32_t tr)
 {
     extern __shared__ float smem[];
-    using G = MwGeom<Q, BPW>;
+    using G = MwGeom<Q, BPW, MT>;
     static_assert(TR >= 1 && TR <= 16, "tile rows");
+    static_assert(MT == 1 || (ACT == ACT_PLAIN && !PAIR && !ROPE && !STAMPS), "multi-token form: plain rows");
     constexpr int SB = (TR + (int)G::RPS - 1) / (int)G::RPS;     // load slots of one block
     // A operands in registers, except in the persistent two-block form, whose
     // next-tile prefetch registers leave no room for them (it reads them from
     // LDS before each MFMA)
-    constexpr bool AREG = BPW == 1 || !MULTI;
+    constexpr bool AREG = (BPW == 1 || !MULTI) && MT == 1;
     constexpr int AJ = AREG ? BPW : 1;
     const uint32_t K = a.K, B = K / 256;
     const uint32_t W = mq_waves(K, BPW), NT = 64 * W;   // the launch's workgroup
@@ -347,7 +355,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     const uint32_t ntl = MULTI ? (PAIR ? 2 * nown : nown) : 1u;                    // tiles of this workgroup
     uint8_t *L = (uint8_t *)smem + wave * G::BYTES;              // this wave's region
     float *red = (float *)((uint8_t *)smem + W * G::BYTES);      // 16: RMSNorm slice sums
-    float *part = red + 16;                                      // ntl x W x 16 per-wave row partials
+    float *part = red + 16;                                      // ntl x MT x W x 16 per-wave row partials
 
     const uint32_t row_bytes = B * Q::BS;
     // every buffer has RRR_READ_SLACK readable bytes past its end: a Q6_K
@@ -395,11 +403,20 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     // the residual of this thread's first output row, read now rather than
     // on the kernel's tail (a clamped row when there is none)
     const uint32_t row_first = PAIR ? 0u : min((tile0 + (t >> 4) * GR) * tr + (t & 15), a.N - 1);
-    const float yres = PAIR ? 0.0f : a.y[row_first];
-    // 1. this wave's activation inputs: float4 lane + 64 j of its slice
-    float4 xa[BPW], xb[BPW];
+    const float yres = PAIR || MT > 1 ? 0.0f : a.y[row_first];
+    // 1. this wave's activation inputs: float4 lane + 64 j of its slice, of
+    // each token
+    float4 xa[MT][BPW], xb[MT][BPW];
 #pragma unroll
-    for (int j = 0; j < BPW; j++) src_load4<ACT>(a, min(b0 * 256 + 4 * (lane + 64 * j), K - 4), xa[j], xb[j]);
+    for (int j = 0; j < BPW; j++) {
+        const uint32_t k4 = min(b0 * 256 + 4 * (lane + 64 * j), K - 4);
+        if constexpr (MT == 1) {
+            src_load4<ACT>(a, k4, xa[0][j], xb[0][j]);
+        } else {
+#pragma unroll
+            for (int m = 0; m < MT; m++) xa[m][j] = *(const float4 *)(a.x + (size_t)min((uint32_t)m, a.M - 1) * K + k4);
+        }
+    }
 
     // every wave's activation loads enter the memory pipeline before any
     // weight load of the workgroup (a bare barrier: no wait on the loads)
@@ -415,12 +432,12 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     // for K <= 8192); the slice sums are added in wave order (waves without
     // a super-block add +0)
     float inv = 1.0f;
-    mark(1, xa[0].x);
+    mark(1, xa[0][0].x);
     if constexpr (ACT == ACT_RMSNORM) {
         float sq = 0.0f;
 #pragma unroll
         for (int j = 0; j < BPW; j++)
-            if (j < (int)nb) sq = sumsq4(xa[j], sq);
+            if (j < (int)nb) sq = sumsq4(xa[0][j], sq);
         sq = wave_sum(sq);
         if (lane == 0) red[wave] = sq;
         __syncthreads();
@@ -429,12 +446,15 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         inv = rms_inv(ordered_sum<16>(red, W, 1), K, a.eps);
     }
 
-    mark(2, xa[0].x + inv);
-    // 3. activation staging of this wave's slice
+    mark(2, xa[0][0].x + inv);
+    // 3. activation staging of this wave's slice (of each token)
 #pragma unroll
-    for (int j = 0; j < BPW; j++) {
+    for (int mj = 0; mj < MT * BPW; mj++) {
+        const int m = mj / BPW, j = mj % BPW;
         const uint32_t f = lane + 64 * j;                        // local float4 index
-        const float4 v = xform4<ACT>(xa[j], xb[j], inv);
+        uint8_t *Lm = L + m * (3 * G::DG);                       // token m's digit planes
+        const uint32_t am = m * (16 * G::NGW), gm = m * (4 * G::NGW);   // its aux and group sums
+        const float4 v = xform4<ACT>(xa[m][j], xb[m][j], inv);
         const float mx = quad_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         int e = 0;
         if (mx > 0.0f && __builtin_isfinite(mx)) {
@@ -444,9 +464,9 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         }
         uint32_t p0, p1, p2, qb;
         encode4(v, ldexpf(1.0f, 14 - e), p0, p1, p2, qb);
-        *(uint32_t *)(L + G::D_OFF + 4 * f) = p0;
-        *(uint32_t *)(L + G::D_OFF + G::DG + 4 * f) = p1;
-        *(uint32_t *)(L + G::D_OFF + 2 * G::DG + 4 * f) = p2;
+        *(uint32_t *)(Lm + G::D_OFF + 4 * f) = p0;
+        *(uint32_t *)(Lm + G::D_OFF + G::DG + 4 * f) = p1;
+        *(uint32_t *)(Lm + G::D_OFF + 2 * G::DG + 4 * f) = p2;
         i32x4 ax = {0, 0, 0, 0};
         if constexpr (Q::OFF32) {
             // sum (q - 32) Q = sum q Q - 32 sum Q: the second term enters the
@@ -455,10 +475,10 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
             ax[0] = -32 * (int)(quad_sum_u32(qb) - 16u * 0x00808080u);
         } else {
             const float sv = quad_sum((v.x + v.y) + (v.z + v.w));
-            if ((lane & 3) == 0) *(float *)(L + G::G_OFF + f) = sv;  // group f / 4
+            if ((lane & 3) == 0) *(float *)(L + G::G_OFF + gm + f) = sv;  // group f / 4
         }
         ax[3] = __float_as_int(__builtin_isfinite(mx) ? ldexpf(1.0f, e - 14) : __builtin_nanf(""));
-        if ((lane & 3) == 0) *(i32x4 *)(L + G::A_OFF + 4 * f) = ax;
+        if ((lane & 3) == 0) *(i32x4 *)(L + G::A_OFF + am + 4 * f) = ax;
     }
     wave_lds_sync();
     mark(3, 0.0f);
@@ -500,7 +520,9 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     // then take the next tile's loads of the block), its MFMAs; row partials
     // to part[]
     auto process = [&](uint32_t tl) {
-        float acc = 0.0f;
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; m++) acc[m] = 0.0f;
 #pragma unroll
         for (int j = 0; j < BPW; j++) {
             wave_lds_sync();
@@ -521,38 +543,44 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
                 i32x4 bq[4];
                 float sc[4], mn[4], d, dmin;
                 Q::decode(raw, g, bq, sc, mn, d, dmin);
-                float acc_s = 0.0f, acc_m = 0.0f;
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    i32x4 A, C;
-                    float gsum;
-                    if constexpr (AREG) {
-                        A = av[j][u];
-                        C = aux[j][u];
-                        gsum = gs[j][u];
-                    } else {
-                        const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
-                        A = i32x4{0, 0, 0, 0};
-                        if (a_live) A = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
-                        C = *(const i32x4 *)(L + G::A_OFF + 16 * grp);
-                        gsum = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + 4 * grp) : 0.0f;
+                for (int m = 0; m < MT; m++) {
+                    float acc_s = 0.0f, acc_m = 0.0f;
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        i32x4 A, C;
+                        float gsum;
+                        if constexpr (AREG) {
+                            A = av[j][u];
+                            C = aux[j][u];
+                            gsum = gs[j][u];
+                        } else {
+                            const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
+                            A = i32x4{0, 0, 0, 0};
+                            if (a_live) A = *(const i32x4 *)(L + m * (3 * G::DG) + a_base + j * 256 + Q::koff(g, u));
+                            C = *(const i32x4 *)(L + G::A_OFF + m * (16 * G::NGW) + 16 * grp);
+                            gsum = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + m * (4 * G::NGW) + 4 * grp) : 0.0f;
+                        }
+                        const i32x4 cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            __builtin_bit_cast(i8x16, A), __builtin_bit_cast(i8x16, bq[u]), C, 0, 0, 0);
+                        const int T = cc[0] + cc[1] * 256 + cc[2] * 65536;
+                        acc_s = fmaf(sc[u], __int_as_float(cc[3]) * (float)T, acc_s);
+                        if constexpr (Q::HAS_MIN) acc_m = fmaf(mn[u], gsum, acc_m);
                     }
-                    const i32x4 cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i8x16, A),
-                                                                           __builtin_bit_cast(i8x16, bq[u]), C, 0, 0, 0);
-                    const int T = cc[0] + cc[1] * 256 + cc[2] * 65536;
-                    acc_s = fmaf(sc[u], __int_as_float(cc[3]) * (float)T, acc_s);
-                    if constexpr (Q::HAS_MIN) acc_m = fmaf(mn[u], gsum, acc_m);
+                    acc[m] = fmaf(d, acc_s, acc[m]);
+                    if constexpr (Q::HAS_MIN) acc[m] = fmaf(-dmin, acc_m, acc[m]);
                 }
-                acc = fmaf(d, acc_s, acc);
-                if constexpr (Q::HAS_MIN) acc = fmaf(-dmin, acc_m, acc);
             }
-            if (tl == 0) mark(5 + 2 * j, acc);
-            else if (tl + 1 == ntl) mark(9 + 2 * j, acc);
+            if (tl == 0) mark(5 + 2 * j, acc[0]);
+            else if (tl + 1 == ntl) mark(9 + 2 * j, acc[0]);
         }
         // the 4 k-groups of a row (lanes n, n+16, n+32, n+48), by lane swaps
-        acc = lanes4_sum(acc);
-        if (lane < 16) part[(tl * W + wave) * 16 + lane] = acc;
-        if (tl + 1 == ntl) mark(12, acc);
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            acc[m] = lanes4_sum(acc[m]);
+            if (lane < 16) part[((tl * MT + m) * W + wave) * 16 + lane] = acc[m];
+        }
+        if (tl + 1 == ntl) mark(12, acc[0]);
     };
     if constexpr (MULTI) {
         for (uint32_t tl = 0; tl < ntl; tl++) process(tl);
@@ -594,12 +622,13 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         }
         return;
     }
-    for (uint32_t i = t; i < ntl * 16; i += NT) {
-        const uint32_t tl = i >> 4, r = i & 15, row = (tile0 + tl * GR) * tr + r;
-        if (r < tr && row < a.N) {
-            float v = waves_sum(part + tl * W * 16 + r, W);
-            if (a.residual) v = (i == t ? yres : a.y[row]) + v;
-            a.y[row] = v;
+    for (uint32_t i = t; i < ntl * MT * 16; i += NT) {
+        const uint32_t tm = i >> 4, tl = tm / MT, m = tm % MT, r = i & 15, row = (tile0 + tl * GR) * tr + r;
+        if (r < tr && row < a.N && m < a.M) {
+            float *yo = a.y + (size_t)m * a.N + row;
+            float v = waves_sum(part + tm * W * 16 + r, W);
+            if (a.residual) v = (MT == 1 && i == t ? yres : *yo) + v;
+            *yo = v;
         }
     }
     if constexpr (STAMPS) {

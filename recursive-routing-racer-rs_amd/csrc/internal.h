@@ -62,6 +62,11 @@ hipError_t launch_gemv_mfma(const GemvArgs &a, uint32_t act, hipStream_t s);
 // the same launch with phase timestamps into a.stamps (16 u64 per wave of
 // each workgroup); returns the grid and the waves per workgroup
 hipError_t launch_gemv_mfma_stamped(const GemvArgs &a, uint32_t act, hipStream_t s, uint32_t &grid, uint32_t &waves);
+// the same int8-MFMA GEMV for 2 <= M <= MQ_TOKENS_MAX rows of x sharing each
+// weight block (plain activations; gemv_mfma.hip)
+constexpr uint32_t MQ_TOKENS_MAX = 4;
+bool gemv_mq_tokens_supported(const GemvArgs &a);
+hipError_t launch_gemv_mq_tokens(const GemvArgs &a, hipStream_t s);
 // fp16-MFMA batched GEMV for 2 <= M <= 32, Q4_K / Q5_K (skinny.hip)
 bool skinny_supported(const GemvArgs &a);
 hipError_t launch_skinny(const GemvArgs &a, hipStream_t s);
