@@ -180,8 +180,10 @@ static hipError_t go_mq_tokens_b(const GemvArgs &a, hipStream_t s, bool launch)
     return hipGetLastError();
 }
 
-// K <= 3072 (at most 12 waves): 2 or 4 tokens a launch; K <= 8192 (16
-// waves of two super-blocks): 2 (more tokens would spill at 128 registers)
+// K <= 3072 (at most 12 waves): 2 or 4 tokens a launch (8 ran slower than
+// the skinny kernel: every token's A and C operands are LDS reads per
+// MFMA); K <= 8192 (16 waves of two super-blocks): 2 (more tokens would
+// spill at 128 registers)
 template <class Q>
 static hipError_t go_mq_tokens(const GemvArgs &a, hipStream_t s, bool launch)
 {

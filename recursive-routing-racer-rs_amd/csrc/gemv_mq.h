@@ -219,6 +219,9 @@ __device__ __forceinline__ uint32_t quad_sum_u32(uint32_t v)
 //   aux:     per token and 16-element group 16 bytes = MFMA accumulator
 //            input {-32 * sum Q (Q6_K only, else 0), 0, 0, bits of 2^(E-14)}
 //   gsum:    per token and group the f32 sum of x (Q4_K / Q5_K min term)
+//   zero:    (MT > 1) 16 zero bytes, the A operand of the lanes that supply
+//            no digit row when A is read from LDS before each MFMA (one read
+//            for every lane, no branch)
 // MT tokens (rows of x) share every weight block: the multi-token form
 // (MT > 1) encodes each token's slice and runs one MFMA per token and k-set
 // on the same B operand.
@@ -242,7 +245,8 @@ struct MwGeom {
     static constexpr uint32_t D_OFF = 16 * RS;
     static constexpr uint32_t A_OFF = D_OFF + MT * 3 * DG;
     static constexpr uint32_t G_OFF = A_OFF + MT * 16 * NGW;
-    static constexpr uint32_t BYTES = G_OFF + MT * 4 * NGW;       // multiple of 16
+    static constexpr uint32_t Z_OFF = G_OFF + MT * 4 * NGW;       // 16 zero bytes (A of the lanes without a digit row)
+    static constexpr uint32_t BYTES = Z_OFF + (MT > 1 ? 16 : 0);  // multiple of 16
 };
 
 // Odd Q6_K blocks (210 bytes) start 2 bytes past a 4-byte boundary, and
@@ -480,6 +484,9 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         ax[3] = __float_as_int(__builtin_isfinite(mx) ? ldexpf(1.0f, e - 14) : __builtin_nanf(""));
         if ((lane & 3) == 0) *(i32x4 *)(L + G::A_OFF + am + 4 * f) = ax;
     }
+    if constexpr (MT > 1) {
+        if (lane == 0) *(i32x4 *)(L + G::Z_OFF) = i32x4{0, 0, 0, 0};
+    }
     wave_lds_sync();
     mark(3, 0.0f);
 
@@ -505,6 +512,18 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
         for (int j = 0; j < AJ; j++)
 #pragma unroll
             for (int u = 0; u < 4; u++) av[j][u] = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
+    }
+    // multi-token form, one super-block a wave: every token's A operands in
+    // registers for all tiles (the accumulator inputs and group sums are read
+    // per MFMA: four more registers per token and k-set would not fit)
+    constexpr bool AREGT = MT > 1 && BPW == 1;
+    i32x4 avt[AREGT ? MT : 1][4];
+    if constexpr (AREGT) {
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                avt[m][u] = *(const i32x4 *)(L + (a_live ? m * (3 * G::DG) + a_base + Q::koff(g, u) : G::Z_OFF));
     }
 
     // ROPE: the position's rotation coefficients (pair j by thread j, j + NT,
@@ -549,22 +568,39 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
                         i32x4 A, C;
-                        float gsum;
+                        float gsum, fac = 0.0f;
                         if constexpr (AREG) {
                             A = av[j][u];
                             C = aux[j][u];
                             gsum = gs[j][u];
                         } else {
                             const uint32_t grp = j * 16 + Q::koff(g, u) / 16;
-                            A = i32x4{0, 0, 0, 0};
-                            if (a_live) A = *(const i32x4 *)(L + m * (3 * G::DG) + a_base + j * 256 + Q::koff(g, u));
-                            C = *(const i32x4 *)(L + G::A_OFF + m * (16 * G::NGW) + 16 * grp);
+                            if constexpr (AREGT) {
+                                A = avt[m][u];
+                            } else if constexpr (MT == 1) {
+                                A = i32x4{0, 0, 0, 0};
+                                if (a_live) A = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
+                            } else {
+                                A = *(const i32x4 *)(L + (a_live ? m * (3 * G::DG) + a_base + j * 256 + Q::koff(g, u)
+                                                                 : G::Z_OFF));
+                            }
+                            const uint8_t *cp = L + G::A_OFF + m * (16 * G::NGW) + 16 * grp;
+                            // Q4_K / Q5_K: the accumulator input {0, 0, 0, factor}
+                            // becomes the constant 0 and the factor a plain
+                            // read (the value the MFMA would pass through)
+                            if constexpr (Q::OFF32)
+                                C = *(const i32x4 *)cp;
+                            else {
+                                C = i32x4{0, 0, 0, 0};
+                                fac = *(const float *)(cp + 12);
+                            }
                             gsum = Q::HAS_MIN ? *(const float *)(L + G::G_OFF + m * (4 * G::NGW) + 4 * grp) : 0.0f;
                         }
                         const i32x4 cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                             __builtin_bit_cast(i8x16, A), __builtin_bit_cast(i8x16, bq[u]), C, 0, 0, 0);
                         const int T = cc[0] + cc[1] * 256 + cc[2] * 65536;
-                        acc_s = fmaf(sc[u], __int_as_float(cc[3]) * (float)T, acc_s);
+                        if (AREG || Q::OFF32) fac = __int_as_float(cc[3]);
+                        acc_s = fmaf(sc[u], fac * (float)T, acc_s);
                         if constexpr (Q::HAS_MIN) acc_m = fmaf(mn[u], gsum, acc_m);
                     }
                     acc[m] = fmaf(d, acc_s, acc[m]);
@@ -624,7 +660,7 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
     }
     for (uint32_t i = t; i < ntl * MT * 16; i += NT) {
         const uint32_t tm = i >> 4, tl = tm / MT, m = tm % MT, r = i & 15, row = (tile0 + tl * GR) * tr + r;
-        if (r < tr && row < a.N && m < a.M) {
+        if (r < tr && row < a.N && (MT == 1 || m < a.M)) {
             float *yo = a.y + (size_t)m * a.N + row;
             float v = waves_sum(part + tm * W * 16 + r, W);
             if (a.residual) v = (MT == 1 && i == t ? yres : *yo) + v;
