@@ -514,8 +514,9 @@ __device__ __forceinline__ void mq_body(const GemvArgs &a, uint32_t ntiles, uint
             for (int u = 0; u < 4; u++) av[j][u] = *(const i32x4 *)(L + a_base + j * 256 + Q::koff(g, u));
     }
     // multi-token form, one super-block a wave: every token's A operands in
-    // registers for all tiles (the accumulator inputs and group sums are read
-    // per MFMA: four more registers per token and k-set would not fit)
+    // registers for all tiles (the group factors or accumulator inputs and
+    // the group sums are read from LDS per MFMA: kept in registers too, they
+    // would not fit)
     constexpr bool AREGT = MT > 1 && BPW == 1;
     i32x4 avt[AREGT ? MT : 1][4];
     if constexpr (AREGT) {
