@@ -226,6 +226,32 @@ def test_batched_rows_extreme_scales(ctx):
     W.free(); Xb.free(); Yb.free()
 
 
+@pytest.mark.parametrize("qtype,K,N,M", [(12, 3072, 1024, 4), (13, 3072, 640, 3), (14, 3072, 512, 2), (12, 3072, 1024, 8)])
+def test_batched_small_rows_extreme_values(ctx, qtype, K, N, M):
+    """A few rows on the matrix cores (2 to 4 on the int8 GEMV's multi-token
+    form, 8 on the skinny kernel): a row of ~1e30, a zero row and a row
+    holding inf keep to themselves; the others match the oracle at the GEMV
+    bar."""
+    raw = weights(qtype, K, N, seed=19, stream=2)
+    X = synth.normal_f32(19, 3 + M, M * K).reshape(M, K)
+    X[0] *= np.float32(1e30)
+    X[1] = 0.0
+    X[M - 1, 100] = np.inf
+    W = ctx.weight_upload(qtype, K, N, raw)
+    Xb, Yb = ctx.to_device(X.reshape(-1)), ctx.alloc(M * N * 4)
+    ctx.gemv(Xb, W, qtype, Yb, K, N, M)
+    Y = ctx.download(Yb).reshape(M, N)
+    fin = list(range(M - 1))
+    ref = orc.gemv(qtype, raw, np.ascontiguousarray(X[fin]).reshape(-1), K, N, len(fin), THREADS, f64=True)
+    for i, m in enumerate(fin):
+        if m == 1:
+            assert np.all(Y[m] == 0.0)
+        else:
+            assert err(Y[m], ref[i]) < TOL, m
+    assert not np.any(np.isfinite(Y[M - 1]))
+    W.free(); Xb.free(); Yb.free()
+
+
 # ---- RMSNorm, SwiGLU glue, residual ---------------------------------------------
 
 @pytest.mark.parametrize("rows,d", [(1, 3072), (5, 3072), (1, 8192), (3, 1000), (1, 1)])
