@@ -34,7 +34,6 @@ template <class Q, int BPW>
 static void mq_plan(const GemvArgs &a, uint32_t &W, uint32_t &grid, size_t &lds, uint32_t &tr, uint32_t &ntiles)
 {
     using G = MwGeom<Q, BPW>;
-    const uint32_t B = a.K / 256;
     W = mq_waves(a.K, BPW);
     const size_t fixed = W * G::BYTES + 64;
     const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64));
@@ -63,7 +62,6 @@ template <class Q, int BPW, bool ST = false>
 static hipError_t go_mq_pair(const GemvArgs &a, hipStream_t s, MqShape *sh = nullptr)
 {
     using G = MwGeom<Q, BPW>;
-    const uint32_t B = a.K / 256;
     const uint32_t W = mq_waves(a.K, BPW);
     const size_t fixed = W * G::BYTES + 64;
     const uint32_t per_max = (uint32_t)((160 * 1024 - fixed) / (W * 64)) / 2;   // pairs: two tiles each
